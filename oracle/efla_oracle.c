@@ -1,0 +1,506 @@
+/*
+ * CPU oracle for the EFLA hot path — TEST INFRASTRUCTURE ONLY.
+ *
+ * This file restates, on the CPU, the arithmetic of the reference's EFLA,
+ * LayerNorm, GELU and AdamW kernels.  It is the checker for the HIP library
+ * (ceo_amd/csrc) and the timed CPU baseline of bench.py.  Only tests/,
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg may load it; the
+ * product path never calls it and fails loudly when the HIP library is absent.
+ *
+ * Parity pins for each function (what checks it besides itself) are listed in
+ * the Python wrapper oracle/oracle.py and exercised by tests/test_oracle_*.py.
+ *
+ * Two families of EFLA functions live here:
+ *   Mode R  — the reference ABI exactly: no q, scalar beta, d_k == d_v, a bf16
+ *             state updated in place and re-rounded to bf16 after every token,
+ *             readout o_t = S_t k_t, backward returning dk, dv, dS_0 only.
+ *             Restates kernels/cuda/efla.cu:93-128, 154-233, 235-313, 315-454,
+ *             456-476 and the host validation at 482-748.
+ *   Mode Q  — the same recurrence generalised to a query readout
+ *             o_t = S_t^T q_t, per-token beta, d_k != d_v, an optional fp32
+ *             initial/final state and varlen packing (cu_seqlens).  Restates
+ *             efla.cu:154-233 (forward) and efla.cu:315-454 (BPTT backward),
+ *             generalised, in fp64 (the parity reference) and in fp32 (the CPU
+ *             baseline), token-sequential per (sequence, head), with the
+ *             backward recomputing states from checkpoints every 64 tokens.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* hipError_t codes the reference returns (same numeric values as cudaError_t). */
+#define OR_SUCCESS 0
+#define OR_INVALID_VALUE 1
+#define OR_INVALID_CONFIGURATION 9
+
+/* ------------------------------------------------------------------------ */
+/* bf16: round-to-nearest-even, NaN forced quiet (src/tensor/dtype.zig:370-390) */
+/* ------------------------------------------------------------------------ */
+uint16_t or_f32_to_bf16(float val) {
+    uint32_t bits;
+    memcpy(&bits, &val, 4);
+    if (isnan(val)) return (uint16_t)((bits >> 16) | 1u);
+    uint32_t round_bit = (bits >> 15) & 1u;
+    uint32_t sticky = (bits & 0x7FFFu) != 0u;
+    uint32_t even = (bits >> 16) & 1u;
+    uint32_t upper = bits >> 16;
+    if (round_bit && (sticky || even)) upper += 1u;
+    return (uint16_t)upper;
+}
+
+float or_bf16_to_f32(uint16_t h) {
+    uint32_t bits = ((uint32_t)h) << 16;
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* When set, the Mode R functions keep the running state in fp32 instead of
+ * re-rounding it to bf16 after every token (used only to pin the Mode R
+ * formulas against fp64 autograd, where rounding would swamp the check). */
+static int g_r_exact = 0;
+void or_set_r_exact(int flag) { g_r_exact = flag; }
+
+static inline float rbf(float x) {
+    return g_r_exact ? x : or_bf16_to_f32(or_f32_to_bf16(x));
+}
+
+void or_f32_to_bf16_array(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = or_f32_to_bf16(src[i]);
+}
+
+void or_bf16_to_f32_array(const uint16_t* src, float* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = or_bf16_to_f32(src[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Seeded portable generator: splitmix64 -> uniform -> Box-Muller (fp64).     */
+/* Every element is a pure function of (seed, index), so any slice of a       */
+/* tensor can be regenerated on its own, on any host.                         */
+/* ------------------------------------------------------------------------ */
+static inline uint64_t splitmix64(uint64_t* s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* Normal deviates: element i uses the two uniforms at counter 2i and 2i+1 of
+ * the stream started at `seed`, so any slice can be regenerated on its own. */
+void or_randn(uint64_t seed, uint64_t offset, double* out, size_t n) {
+#pragma omp parallel for schedule(static)
+    for (long long ii = 0; ii < (long long)n; ++ii) {
+        const size_t i = (size_t)ii;
+        uint64_t s = seed + 2u * (offset + i) * 0x9E3779B97F4A7C15ull;
+        uint64_t a = splitmix64(&s);
+        uint64_t b = splitmix64(&s);
+        double u1 = ((double)(a >> 11) + 1.0) * (1.0 / 9007199254740993.0); /* (0,1] */
+        double u2 = (double)(b >> 11) * (1.0 / 9007199254740992.0);         /* [0,1) */
+        out[i] = sqrt(-2.0 * log(u1)) * cos(6.283185307179586476925286766559 * u2);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* EFLA coefficient c(beta, lambda) = (1 - exp(-beta*lambda)) / lambda and   */
+/* dc/dlambda.  fp32 form restates efla.cu:93-115 (4-term Taylor series for   */
+/* lambda <= 1e-6).                                                           */
+/* ------------------------------------------------------------------------ */
+void or_efla_coeff_f32(float lambda, float beta, float* c, float* dc_dlambda) {
+    if (lambda <= 1.0e-6f) {
+        const float b2 = beta * beta, b3 = b2 * beta, b4 = b3 * beta, b5 = b4 * beta;
+        const float l2 = lambda * lambda, l3 = l2 * lambda;
+        *c = beta - 0.5f * b2 * lambda + (1.0f / 6.0f) * b3 * l2 - (1.0f / 24.0f) * b4 * l3;
+        *dc_dlambda = -0.5f * b2 + (1.0f / 3.0f) * b3 * lambda - (1.0f / 8.0f) * b4 * l2 +
+                      (1.0f / 30.0f) * b5 * l3;
+        return;
+    }
+    const float x = beta * lambda;
+    const float e = expf(-x);
+    *c = (1.0f - e) / lambda;
+    *dc_dlambda = (beta * lambda * e - 1.0f + e) / (lambda * lambda);
+}
+
+/* fp64 form of the same function, evaluated without cancellation:
+ *   c = -expm1(-x)/lambda, x = beta*lambda
+ *   dc/dlambda = (x e^{-x} + expm1(-x)) / lambda^2
+ *   dc/dbeta   = e^{-x}
+ * For |x| < 1e-2 the power series c = sum_{n>=1} (-1)^{n+1} beta^n lambda^{n-1}/n!
+ * and its lambda-derivative are summed to 12 terms. */
+void or_efla_coeff_f64(double lambda, double beta, double* c, double* dc_dlambda, double* dc_dbeta) {
+    const double x = beta * lambda;
+    if (fabs(x) < 1.0e-2) {
+        double cs = 0.0, ds = 0.0;
+        double bn = beta;        /* beta^n */
+        double ln = 1.0;         /* lambda^(n-1) */
+        double lnm2 = 0.0;       /* lambda^(n-2) for n>=2 */
+        double fact = 1.0;       /* n! */
+        for (int n = 1; n <= 12; ++n) {
+            fact *= (double)n;
+            const double sgn = (n % 2) ? 1.0 : -1.0;
+            cs += sgn * bn * ln / fact;
+            if (n >= 2) ds += sgn * bn * (double)(n - 1) * lnm2 / fact;
+            lnm2 = (n == 1) ? 1.0 : lnm2 * lambda;
+            ln *= lambda;
+            bn *= beta;
+        }
+        *c = cs;
+        if (dc_dlambda) *dc_dlambda = ds;
+    } else {
+        const double em1 = expm1(-x);
+        *c = -em1 / lambda;
+        if (dc_dlambda) *dc_dlambda = (x * exp(-x) + em1) / (lambda * lambda);
+    }
+    if (dc_dbeta) *dc_dbeta = exp(-x);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Mode R: the reference ABI, restated with its arithmetic.                   */
+/* ------------------------------------------------------------------------ */
+#define R_BLOCK 256
+
+/* Shared-memory tree sum over 256 per-thread partials (efla.cu:117-128). */
+static float tree_sum_256(float* buf) {
+    for (int stride = R_BLOCK >> 1; stride > 0; stride >>= 1)
+        for (int t = 0; t < stride; ++t) buf[t] += buf[t + stride];
+    return buf[0];
+}
+
+/* lambda = ||k||^2 formed as in efla.cu:190-195: thread t sums d = t, t+256, ... */
+static float r_lambda(const float* kv, size_t d) {
+    float buf[R_BLOCK];
+    for (int t = 0; t < R_BLOCK; ++t) {
+        float p = 0.0f;
+        for (size_t i = (size_t)t; i < d; i += R_BLOCK) p = fmaf(kv[i], kv[i], p);
+        buf[t] = p;
+    }
+    return tree_sum_256(buf);
+}
+
+static int checked_mul(size_t a, size_t b, size_t* out) {
+    if (a != 0 && b > SIZE_MAX / a) return 0;
+    *out = a * b;
+    return 1;
+}
+
+/* One token of the reference state update on a bf16 state held as rounded
+ * floats: u = S^T k; S <- bf16(S + c k (v-u)^T)  (efla.cu:204-221, 282-311). */
+static void r_step(float* S, const float* kf, const float* vf, float* u, size_t d, float c) {
+    for (size_t col = 0; col < d; ++col) {
+        float s = 0.0f;
+        for (size_t row = 0; row < d; ++row) s = fmaf(kf[row], S[row * d + col], s);
+        u[col] = s;
+    }
+    for (size_t row = 0; row < d; ++row) {
+        const float ck = c * kf[row];
+        for (size_t col = 0; col < d; ++col) {
+            S[row * d + col] = rbf(fmaf(ck, vf[col] - u[col], S[row * d + col]));
+        }
+    }
+}
+
+/* efla_forward_cuda + efla_forward_kernel_impl (efla.cu:482-541, 154-233).
+ * k, v, output: (B,T,H,d) bf16; state: (B*H,d,d) bf16 updated in place. */
+int or_efla_r_forward(const uint16_t* k, const uint16_t* v, uint16_t* state, uint16_t* output,
+                      size_t B, size_t T, size_t H, size_t d, float beta) {
+    if (B == 0 || H == 0 || d == 0) return OR_INVALID_VALUE;
+    if (T == 0) return OR_SUCCESS;
+    if (!k || !v || !state || !output) return OR_INVALID_VALUE;
+    size_t nbh;
+    if (!checked_mul(B, H, &nbh) || nbh > 0xFFFFFFFFull) return OR_INVALID_CONFIGURATION;
+    size_t sh;
+    if (!checked_mul(3, d, &sh) || !checked_mul(sh + R_BLOCK, sizeof(float), &sh))
+        return OR_INVALID_CONFIGURATION;
+#pragma omp parallel for schedule(dynamic)
+    for (long long bh = 0; bh < (long long)nbh; ++bh) {
+        const size_t b = (size_t)bh / H, h = (size_t)bh % H;
+        float* S = (float*)malloc(d * d * sizeof(float));
+        float* kf = (float*)malloc(3 * d * sizeof(float));
+        float* vf = kf + d;
+        float* u = kf + 2 * d;
+        uint16_t* st = state + (size_t)bh * d * d;
+        for (size_t i = 0; i < d * d; ++i) S[i] = or_bf16_to_f32(st[i]);
+        for (size_t t = 0; t < T; ++t) {
+            const size_t base = ((b * T + t) * H + h) * d;
+            for (size_t i = 0; i < d; ++i) {
+                kf[i] = or_bf16_to_f32(k[base + i]);
+                vf[i] = or_bf16_to_f32(v[base + i]);
+            }
+            float c, dc;
+            or_efla_coeff_f32(r_lambda(kf, d), beta, &c, &dc);
+            r_step(S, kf, vf, u, d, c);
+            for (size_t row = 0; row < d; ++row) {
+                float s = 0.0f;
+                for (size_t col = 0; col < d; ++col) s = fmaf(S[row * d + col], kf[col], s);
+                output[base + row] = or_f32_to_bf16(s);
+            }
+        }
+        for (size_t i = 0; i < d * d; ++i) st[i] = or_f32_to_bf16(S[i]);
+        free(kf);
+        free(S);
+    }
+    return OR_SUCCESS;
+}
+
+/* efla_backward_cuda: build_state_history_kernel + efla_backward_kernel +
+ * convert_float_to_bf16_kernel (efla.cu:543-709, 235-313, 315-454, 456-464).
+ * state is S_0 (bf16, (B*H,d,d)); outputs grad_k, grad_v (B,T,H,d) and
+ * grad_state (B*H,d,d), all bf16.  The full bf16 history is rebuilt per
+ * (b,h), exactly as the reference does (memory: (T+1)*d*d floats). */
+int or_efla_r_backward(const uint16_t* grad_output, const uint16_t* k, const uint16_t* v,
+                       const uint16_t* state, uint16_t* grad_k, uint16_t* grad_v,
+                       uint16_t* grad_state, size_t B, size_t T, size_t H, size_t d,
+                       float beta) {
+    if (B == 0 || H == 0 || d == 0) return OR_INVALID_VALUE;
+    if (!state || !grad_state) return OR_INVALID_VALUE;
+    size_t nbh, gse, tmp;
+    if (!checked_mul(B, H, &nbh) || nbh > 0xFFFFFFFFull) return OR_INVALID_CONFIGURATION;
+    if (!checked_mul(nbh, d, &gse) || !checked_mul(gse, d, &gse) ||
+        !checked_mul(gse, 2, &tmp))
+        return OR_INVALID_CONFIGURATION;
+    if (T == 0) {
+        memset(grad_state, 0, gse * 2);
+        return OR_SUCCESS;
+    }
+    if (!grad_output || !k || !v || !grad_k || !grad_v) return OR_INVALID_VALUE;
+    if (!checked_mul(gse, T + 1, &tmp) || !checked_mul(tmp, 2, &tmp))
+        return OR_INVALID_CONFIGURATION;
+#pragma omp parallel for schedule(dynamic)
+    for (long long bh = 0; bh < (long long)nbh; ++bh) {
+        const size_t b = (size_t)bh / H, h = (size_t)bh % H;
+        const size_t dd = d * d;
+        float* hist = (float*)malloc((T + 1) * dd * sizeof(float));
+        float* G = (float*)malloc(dd * sizeof(float));
+        float* vec = (float*)malloc(7 * d * sizeof(float));
+        float *kf = vec, *vf = vec + d, *go = vec + 2 * d, *w1 = vec + 3 * d, *w2 = vec + 4 * d,
+              *gk = vec + 5 * d, *u = vec + 6 * d;
+        const uint16_t* s0 = state + (size_t)bh * dd;
+        for (size_t i = 0; i < dd; ++i) hist[i] = or_bf16_to_f32(s0[i]);
+        for (size_t t = 0; t < T; ++t) {
+            const size_t base = ((b * T + t) * H + h) * d;
+            for (size_t i = 0; i < d; ++i) {
+                kf[i] = or_bf16_to_f32(k[base + i]);
+                vf[i] = or_bf16_to_f32(v[base + i]);
+            }
+            float c, dc;
+            or_efla_coeff_f32(r_lambda(kf, d), beta, &c, &dc);
+            memcpy(hist + (t + 1) * dd, hist + t * dd, dd * sizeof(float));
+            r_step(hist + (t + 1) * dd, kf, vf, u, d, c);
+        }
+        memset(G, 0, dd * sizeof(float));
+        for (size_t t = T; t-- > 0;) {
+            const size_t base = ((b * T + t) * H + h) * d;
+            const float* Sp = hist + t * dd;
+            const float* Sn = hist + (t + 1) * dd;
+            for (size_t i = 0; i < d; ++i) {
+                kf[i] = or_bf16_to_f32(k[base + i]);
+                vf[i] = or_bf16_to_f32(v[base + i]);
+                go[i] = or_bf16_to_f32(grad_output[base + i]);
+            }
+            float c, dc;
+            or_efla_coeff_f32(r_lambda(kf, d), beta, &c, &dc);
+            for (size_t col = 0; col < d; ++col) {
+                float s = 0.0f;
+                for (size_t row = 0; row < d; ++row) s = fmaf(kf[row], Sp[row * d + col], s);
+                w1[col] = s;
+                w2[col] = vf[col] - s;
+            }
+            for (size_t col = 0; col < d; ++col) {
+                float s = 0.0f;
+                for (size_t row = 0; row < d; ++row) s = fmaf(Sn[row * d + col], go[row], s);
+                gk[col] = s;
+            }
+            for (size_t col = 0; col < d; ++col) {
+                float s = 0.0f;
+                for (size_t row = 0; row < d; ++row) {
+                    const float g = fmaf(go[row], kf[col], G[row * d + col]);
+                    s = fmaf(g, kf[row], s);
+                }
+                w1[col] = c * s;
+            }
+            float buf[R_BLOCK];
+            for (int th = 0; th < R_BLOCK; ++th) {
+                float p = 0.0f;
+                for (size_t idx = (size_t)th; idx < dd; idx += R_BLOCK) {
+                    const size_t row = idx / d, col = idx - row * d;
+                    const float g = fmaf(go[row], kf[col], G[idx]);
+                    p = fmaf(g * kf[row], w2[col], p);
+                }
+                buf[th] = p;
+            }
+            const float grad_lambda = tree_sum_256(buf) * dc;
+            for (size_t row = 0; row < d; ++row) {
+                float ex = 0.0f, up = 0.0f;
+                for (size_t col = 0; col < d; ++col) {
+                    const float g = fmaf(go[row], kf[col], G[row * d + col]);
+                    ex = fmaf(g, w2[col], ex);
+                    up = fmaf(Sp[row * d + col], w1[col], up);
+                }
+                gk[row] = fmaf(2.0f * grad_lambda, kf[row], fmaf(c, ex, gk[row]) - up);
+            }
+            for (size_t i = 0; i < d; ++i) {
+                grad_v[base + i] = or_f32_to_bf16(w1[i]);
+                grad_k[base + i] = or_f32_to_bf16(gk[i]);
+            }
+            for (size_t row = 0; row < d; ++row)
+                for (size_t col = 0; col < d; ++col) {
+                    const size_t idx = row * d + col;
+                    const float g = fmaf(go[row], kf[col], G[idx]);
+                    G[idx] = fmaf(-kf[row], w1[col], g);
+                }
+        }
+        uint16_t* gs = grad_state + (size_t)bh * dd;
+        for (size_t i = 0; i < dd; ++i) gs[i] = or_f32_to_bf16(G[i]);
+        free(vec);
+        free(G);
+        free(hist);
+    }
+    return OR_SUCCESS;
+}
+
+/* efla_chunked_scan_cuda + add_state_kernel (efla.cu:711-748, 466-476):
+ * chunk_states[i] <- bf16(chunk_states[i-1] + chunk_states[i]) for i = 1..n-1,
+ * each chunk holding H*d*d bf16 values.  An inclusive prefix sum, kept for
+ * ABI parity; it is not a composition of EFLA transitions. */
+int or_efla_r_chunked_scan(uint16_t** chunk_states, size_t num_chunks, size_t H, size_t d) {
+    if (num_chunks == 0 || H == 0 || d == 0) return OR_INVALID_VALUE;
+    if (!chunk_states) return OR_INVALID_VALUE;
+    size_t n;
+    if (!checked_mul(H, d, &n) || !checked_mul(n, d, &n)) return OR_INVALID_CONFIGURATION;
+    for (size_t i = 0; i < num_chunks; ++i)
+        if (!chunk_states[i]) return OR_INVALID_VALUE;
+    for (size_t i = 1; i < num_chunks; ++i)
+        for (size_t j = 0; j < n; ++j)
+            chunk_states[i][j] = or_f32_to_bf16(or_bf16_to_f32(chunk_states[i - 1][j]) +
+                                                or_bf16_to_f32(chunk_states[i][j]));
+    return OR_SUCCESS;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Mode Q: generalised recurrence in fp64 and fp32 (one body, two types).     */
+/* ------------------------------------------------------------------------ */
+#define REAL double
+#define SFX f64
+#include "efla_q_body.h"
+#undef REAL
+#undef SFX
+#define REAL float
+#define SFX f32
+#include "efla_q_body.h"
+#undef REAL
+#undef SFX
+
+int or_num_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+void or_set_num_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n);
+#else
+    (void)n;
+#endif
+}
+
+/* ------------------------------------------------------------------------ */
+/* LayerNorm forward (layernorm.cu:133-183): one-pass sum / sum of squares,   */
+/* var = E[x^2] - mean^2, inv_std = 1/sqrt(var + eps), optional bias.        */
+/* Sums are accumulated in fp64 here; inputs/outputs are fp32 arrays holding */
+/* whatever precision the caller chose.  mean/rstd are optional outputs.     */
+/* ------------------------------------------------------------------------ */
+void or_layernorm_fwd(const float* x, const float* w, const float* b, float* y, float* mean_out,
+                      float* rstd_out, size_t rows, size_t D, float eps) {
+#pragma omp parallel for schedule(static)
+    for (long long r = 0; r < (long long)rows; ++r) {
+        const float* xr = x + (size_t)r * D;
+        double s = 0.0, s2 = 0.0;
+        for (size_t j = 0; j < D; ++j) {
+            s += xr[j];
+            s2 += (double)xr[j] * xr[j];
+        }
+        const double mean = s / (double)D;
+        double var = s2 / (double)D - mean * mean;
+        const double rstd = 1.0 / sqrt(var + (double)eps);
+        for (size_t j = 0; j < D; ++j) {
+            const double yn = ((double)xr[j] - mean) * rstd;
+            y[(size_t)r * D + j] = (float)(yn * w[j] + (b ? b[j] : 0.0));
+        }
+        if (mean_out) mean_out[r] = (float)mean;
+        if (rstd_out) rstd_out[r] = (float)rstd;
+    }
+}
+
+/* LayerNorm backward (no reference counterpart; textbook gradient of the
+ * forward above):  xhat = (x-mean)*rstd, g = dy*w,
+ * dx = rstd * (g - mean(g) - xhat * mean(g*xhat)), dw = sum_r dy*xhat,
+ * db = sum_r dy.  dw/db accumulate in fp64 over rows. */
+void or_layernorm_bwd(const float* dy, const float* x, const float* w, const float* mean,
+                      const float* rstd, float* dx, double* dw, double* db, size_t rows,
+                      size_t D) {
+    memset(dw, 0, D * sizeof(double));
+    memset(db, 0, D * sizeof(double));
+    for (size_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * D;
+        const float* gr = dy + r * D;
+        double sg = 0.0, sgx = 0.0;
+        for (size_t j = 0; j < D; ++j) {
+            const double xh = ((double)xr[j] - mean[r]) * rstd[r];
+            const double g = (double)gr[j] * w[j];
+            sg += g;
+            sgx += g * xh;
+            dw[j] += (double)gr[j] * xh;
+            db[j] += gr[j];
+        }
+        sg /= (double)D;
+        sgx /= (double)D;
+        for (size_t j = 0; j < D; ++j) {
+            const double xh = ((double)xr[j] - mean[r]) * rstd[r];
+            const double g = (double)gr[j] * w[j];
+            dx[r * D + j] = (float)(rstd[r] * (g - sg - xh * sgx));
+        }
+    }
+}
+
+/* GELU, tanh approximation and its derivative (layernorm.cu:189-250), fp64. */
+void or_gelu_fwd(const float* x, float* y, size_t n) {
+    const double k0 = 0.7978845608028654, k1 = 0.044715;
+    for (size_t i = 0; i < n; ++i) {
+        const double v = x[i];
+        y[i] = (float)(0.5 * v * (1.0 + tanh(k0 * (v + k1 * v * v * v))));
+    }
+}
+
+void or_gelu_bwd(const float* dy, const float* x, float* dx, size_t n) {
+    const double k0 = 0.7978845608028654, k1 = 0.044715;
+    for (size_t i = 0; i < n; ++i) {
+        const double v = x[i];
+        const double th = tanh(k0 * (v + k1 * v * v * v));
+        const double sech2 = 1.0 - th * th;
+        const double inner = k0 * (1.0 + 3.0 * k1 * v * v);
+        dx[i] = (float)(dy[i] * (0.5 * (1.0 + th) + 0.5 * v * sech2 * inner));
+    }
+}
+
+/* AdamW with fp32 master weights (optim.cu:147-178, 657-709): bias
+ * corrections 1 - beta^step formed in double on the host. */
+void or_adamw_step(float* p, const float* g, float* m, float* v, size_t n, float lr, float b1,
+                   float b2, float eps, float wd, size_t step) {
+    const float bc1 = (float)(1.0 - pow((double)b1, (double)step));
+    const float bc2 = (float)(1.0 - pow((double)b2, (double)step));
+    for (size_t i = 0; i < n; ++i) {
+        const float mn = b1 * m[i] + (1.0f - b1) * g[i];
+        const float vn = b2 * v[i] + (1.0f - b2) * g[i] * g[i];
+        const float mh = mn / bc1, vh = vn / bc2;
+        const float den = sqrtf(fmaxf(vh, 0.0f)) + eps;
+        p[i] = p[i] * (1.0f - lr * wd) - lr * (mh / den);
+        m[i] = mn;
+        v[i] = vn;
+    }
+}
