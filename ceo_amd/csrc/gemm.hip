@@ -1,0 +1,359 @@
+// Row-major GEMM for gfx950 on MFMA, replacing the reference's cuBLAS calls
+// (kernels/cuda/gemm.cu:182-234, 303-548).
+//
+//   forward:  C[m,n] = sum_k A[m,k] B[k,n] (+ bias[n])     any of fp32/fp16/bf16
+//   backward: dA = dC B^T, dB = A^T dC, dbias = column sums of dC   (bf16)
+//
+// One kernel template covers all three products.  Operands are described as
+// (m,k) and (k,n) matrices whose contiguous index is either k ("K-major") or
+// the other one; tiles are staged in LDS k-contiguous so MFMA fragments are
+// single 16-byte reads, transposing on the way in when the source is not
+// K-major.  Workgroup tile 128x128x32, 4 waves each owning 64x64 (16 MFMA
+// 16x16 tiles), one-stage register prefetch of the next k-tile, fp32
+// accumulation, bias fused into the epilogue (the reference adds it in a
+// second pass with a second rounding).  Tiles are ordered in groups of 8 rows
+// of tiles, and consecutive tile ids are spread so that each XCD works on a
+// contiguous band of C (its own L2 then holds the A rows / B columns it
+// re-reads).  Matching dtypes run on bf16 / fp16 MFMA; mixed dtypes on fp32
+// MFMA after conversion.
+#include <hip/hip_runtime.h>
+
+#include "../../include/efla_hip.h"
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace efla {
+namespace gm {
+
+constexpr int NTH = 256, BM = 128, BN = 128, BK = 32;
+
+template <typename MT>
+constexpr int lpad() {
+    return 16 / (int)sizeof(MT);
+}
+
+// Loads a (LINES x BK) operand tile into registers as 8-element runs.
+//   KM:  element(line, k) = src[line * ld + k]   (runs along k)
+//   !KM: element(line, k) = src[k * ld + line]   (runs along line)
+// Out-of-range elements read as zero.
+template <typename T, int LINES, bool KM>
+struct TileLoader {
+    static constexpr int RUNS = LINES * BK / 8 / NTH;  // runs per thread
+    float v[RUNS][8];
+    __device__ __forceinline__ void load(const T* __restrict__ src, long ld, long line0,
+                                         long k0, long nlines, long nk, bool vec_ok) {
+#pragma unroll
+        for (int r = 0; r < RUNS; ++r) {
+            const int id = threadIdx.x + r * NTH;
+            int line, kk;
+            if (KM) {
+                line = id / (BK / 8);
+                kk = (id % (BK / 8)) * 8;
+            } else {
+                kk = id / (LINES / 8);
+                line = (id % (LINES / 8)) * 8;
+            }
+            const long gl = line0 + line, gk = k0 + kk;
+            const T* p = KM ? src + gl * ld + gk : src + gk * ld + gl;
+            const bool full = KM ? (gl < nlines && gk + 8 <= nk) : (gk < nk && gl + 8 <= nlines);
+            if (vec_ok && full) {
+                if constexpr (sizeof(T) == 2) {
+                    typedef __attribute__((__vector_size__(16))) short s8;
+                    const s8 raw = *reinterpret_cast<const s8*>(p);
+                    const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) v[r][i] = to_f(e[i]);
+                } else {
+                    const floatx4 a = *reinterpret_cast<const floatx4*>(p);
+                    const floatx4 b = *reinterpret_cast<const floatx4*>(p + 4);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        v[r][i] = to_f(a[i]);
+                        v[r][4 + i] = to_f(b[i]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const long l2 = KM ? gl : gl + i;
+                    const long k2 = KM ? gk + i : gk;
+                    v[r][i] = (l2 < nlines && k2 < nk) ? to_f(KM ? src[l2 * ld + k2]
+                                                                 : src[k2 * ld + l2])
+                                                       : 0.f;
+                }
+            }
+        }
+    }
+    // store into LDS tile dst[line * LD + k] (element type MT)
+    template <typename MT, int LD>
+    __device__ __forceinline__ void store(MT* dst) const {
+#pragma unroll
+        for (int r = 0; r < RUNS; ++r) {
+            const int id = threadIdx.x + r * NTH;
+            if (KM) {
+                const int line = id / (BK / 8), kk = (id % (BK / 8)) * 8;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dst[line * LD + kk + i] = from_f<MT>(v[r][i]);
+            } else {
+                const int kk = id / (LINES / 8), line = (id % (LINES / 8)) * 8;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) dst[(line + i) * LD + kk] = from_f<MT>(v[r][i]);
+            }
+        }
+    }
+};
+
+// C[m, n] = sum_k opA(m, k) opB(k, n) (+ bias[n]); ldc is C's row stride.
+//   opA(m, k) = AKM ? A[m*lda + k] : A[k*lda + m]
+//   opB(k, n) = BKM ? B[n*ldb + k] : B[k*ldb + n]
+template <typename TA, typename TB, typename TC, typename MT, bool AKM, bool BKM>
+__global__ void __launch_bounds__(NTH) gemm_kernel(const TA* __restrict__ A,
+                                                   const TB* __restrict__ B,
+                                                   const TC* __restrict__ bias,
+                                                   TC* __restrict__ C, long M, long N, long K,
+                                                   long lda, long ldb, long ldc, int vec_a,
+                                                   int vec_b) {
+    constexpr int LD = BK + lpad<MT>();
+    __shared__ __attribute__((aligned(16))) MT As[BM * LD];
+    __shared__ __attribute__((aligned(16))) MT Bs[BN * LD];
+    // tile order: XCD-banded, then grouped by 8 tile rows
+    const long tm_n = (M + BM - 1) / BM, tn_n = (N + BN - 1) / BN;
+    const long ntiles = tm_n * tn_n;
+    long pid = blockIdx.x;
+    if (ntiles % 8 == 0) pid = (pid % 8) * (ntiles / 8) + pid / 8;
+    constexpr long GROUP = 8;
+    const long group_span = GROUP * tn_n;
+    const long g = pid / group_span;
+    const long first_m = g * GROUP;
+    const long gsize = (tm_n - first_m) < GROUP ? (tm_n - first_m) : GROUP;
+    const long tm = first_m + (pid % group_span) % gsize;
+    const long tn = (pid % group_span) / gsize;
+    const long m0 = tm * BM, n0 = tn * BN;
+
+    const int w = wave_id(), lane = lane_id();
+    const int wm = (w >> 1) * 64, wn = (w & 1) * 64;
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    TileLoader<TA, BM, AKM> la;
+    TileLoader<TB, BN, BKM> lb;
+    const long nk = (K + BK - 1) / BK;
+    la.load(A, lda, m0, 0, M, K, vec_a);
+    lb.load(B, ldb, n0, 0, N, K, vec_b);
+    for (long kt = 0; kt < nk; ++kt) {
+        la.template store<MT, LD>(As);
+        lb.template store<MT, LD>(Bs);
+        __syncthreads();
+        if (kt + 1 < nk) {
+            la.load(A, lda, m0, (kt + 1) * BK, M, K, vec_a);
+            lb.load(B, ldb, n0, (kt + 1) * BK, N, K, vec_b);
+        }
+#pragma unroll
+        for (int ks = 0; ks < BK; ks += Mfma<MT>::KS) {
+            typename Mfma<MT>::frag fa[4], fb[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                fa[i] = load_frag<MT>(view_k((const MT*)As, LD), wm + 16 * i, ks, lane);
+                fb[i] = load_frag<MT>(view_k((const MT*)Bs, LD), wn + 16 * i, ks, lane);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<MT>::mma(fa[i], fb[j], acc[i][j]);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const long r = m0 + wm + 16 * i + 4 * (lane >> 4);
+            const long c = n0 + wn + 16 * j + (lane & 15);
+            if (c >= N) continue;
+            const float bb = bias ? to_f(bias[c]) : 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (r + e < M) C[(r + e) * ldc + c] = from_f<TC>(acc[i][j][e] + bb);
+        }
+}
+
+// grad_bias[n] = sum_m dC[m, n]: each workgroup owns 64 columns; its 4 waves
+// stride over rows, 64 lanes over columns, then combine in LDS.
+__global__ void __launch_bounds__(NTH) colsum_kernel(const bf16* __restrict__ x,
+                                                     bf16* __restrict__ y, long M, long N) {
+    __shared__ float part[4][64];
+    const long c = (long)blockIdx.x * 64 + lane_id();
+    float s = 0.f;
+    if (c < N)
+        for (long r = wave_id(); r < M; r += 4) s += (float)x[r * N + c];
+    part[wave_id()][lane_id()] = s;
+    __syncthreads();
+    if (threadIdx.x < 64 && c < N)
+        y[c] = (bf16)(part[0][threadIdx.x] + part[1][threadIdx.x] + part[2][threadIdx.x] +
+                      part[3][threadIdx.x]);
+}
+
+// k == 0: C = bias (broadcast) or 0
+template <typename TC>
+__global__ void __launch_bounds__(NTH) bias_fill_kernel(TC* __restrict__ C,
+                                                        const TC* __restrict__ bias, long M,
+                                                        long N) {
+    const long total = M * N, stride = (long)gridDim.x * blockDim.x;
+    for (long i = (long)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride)
+        C[i] = bias ? bias[i % N] : from_f<TC>(0.f);
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <typename TA, typename TB, typename TC, typename MT, bool AKM, bool BKM>
+static int launch(const void* a, const void* b, const void* bias, void* c, long M, long N,
+                  long K, long lda, long ldb, long ldc, const char* name, hipStream_t st) {
+    const long tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    if (tiles > 0x7FFFFFFFL) return kInvalidConfiguration;
+    // 16-byte runs need an aligned base and a row stride that keeps them aligned
+    const int va = aligned16(a) && (lda * (long)sizeof(TA)) % 16 == 0;
+    const int vb = aligned16(b) && (ldb * (long)sizeof(TB)) % 16 == 0;
+    EFLA_LAUNCH(name, (gemm_kernel<TA, TB, TC, MT, AKM, BKM>), dim3((unsigned)tiles), dim3(NTH),
+                st, (const TA*)a, (const TB*)b, (const TC*)bias, (TC*)c, M, N, K, lda, ldb, ldc,
+                va, vb);
+    return (int)hipPeekAtLastError();
+}
+
+template <typename TA, typename TB, typename TC>
+static int fwd_typed(const void* a, const void* b, const void* bias, void* c, long M, long K,
+                     long N, hipStream_t st) {
+    if constexpr (__is_same(TA, TB) && !__is_same(TA, float))
+        return launch<TA, TB, TC, TA, true, false>(a, b, bias, c, M, N, K, K, N, N,
+                                                   "gemm_fwd", st);
+    else
+        return launch<TA, TB, TC, float, true, false>(a, b, bias, c, M, N, K, K, N, N,
+                                                      "gemm_fwd", st);
+}
+
+template <typename TA, typename TB>
+static int fwd_c(int dc, const void* a, const void* b, const void* bias, void* c, long M,
+                 long K, long N, hipStream_t st) {
+    switch (dc) {
+        case kDtypeF32: return fwd_typed<TA, TB, float>(a, b, bias, c, M, K, N, st);
+        case kDtypeF16: return fwd_typed<TA, TB, f16>(a, b, bias, c, M, K, N, st);
+        case kDtypeBF16: return fwd_typed<TA, TB, bf16>(a, b, bias, c, M, K, N, st);
+    }
+    return kInvalidValue;
+}
+
+template <typename TA>
+static int fwd_b(int db, int dc, const void* a, const void* b, const void* bias, void* c,
+                 long M, long K, long N, hipStream_t st) {
+    switch (db) {
+        case kDtypeF32: return fwd_c<TA, float>(dc, a, b, bias, c, M, K, N, st);
+        case kDtypeF16: return fwd_c<TA, f16>(dc, a, b, bias, c, M, K, N, st);
+        case kDtypeBF16: return fwd_c<TA, bf16>(dc, a, b, bias, c, M, K, N, st);
+    }
+    return kInvalidValue;
+}
+
+static size_t dsize(int dt) {
+    switch (dt) {
+        case kDtypeF32: return 4;
+        case kDtypeF16: return 2;
+        case kDtypeBF16: return 2;
+    }
+    return 0;
+}
+
+template <typename TC>
+static int launch_bias_fill(void* c, const void* bias, long M, long N, hipStream_t st) {
+    long g = (M * N + NTH - 1) / NTH;
+    if (g > 8192) g = 8192;
+    EFLA_LAUNCH("gemm_bias_fill", bias_fill_kernel<TC>, dim3((unsigned)g), dim3(NTH), st, (TC*)c,
+                (const TC*)bias, M, N);
+    return (int)hipPeekAtLastError();
+}
+
+}  // namespace gm
+}  // namespace efla
+
+using namespace efla;
+using namespace efla::gm;
+
+extern "C" int gemm_forward_hip(const void* a, const void* b, const void* bias, void* c,
+                                size_t m, size_t k, size_t n, int dtype_a, int dtype_b,
+                                int dtype_c, hipStream_t stream) {
+    if (!a || !b || !c) return kInvalidValue;
+    if (!dsize(dtype_a) || !dsize(dtype_b) || !dsize(dtype_c)) return kInvalidValue;
+    size_t mn;
+    if (!mul_ok(m, n, &mn)) return kInvalidValue;
+    if (m == 0 || n == 0) return kSuccess;
+    if (m > ((size_t)1 << 40) || n > ((size_t)1 << 40) || k > ((size_t)1 << 40))
+        return kInvalidValue;
+    if (k == 0) {
+        switch (dtype_c) {
+            case kDtypeF32: return launch_bias_fill<float>(c, bias, (long)m, (long)n, stream);
+            case kDtypeF16: return launch_bias_fill<f16>(c, bias, (long)m, (long)n, stream);
+            default: return launch_bias_fill<bf16>(c, bias, (long)m, (long)n, stream);
+        }
+    }
+    switch (dtype_a) {
+        case kDtypeF32:
+            return fwd_b<float>(dtype_b, dtype_c, a, b, bias, c, (long)m, (long)k, (long)n, stream);
+        case kDtypeF16:
+            return fwd_b<f16>(dtype_b, dtype_c, a, b, bias, c, (long)m, (long)k, (long)n, stream);
+        case kDtypeBF16:
+            return fwd_b<bf16>(dtype_b, dtype_c, a, b, bias, c, (long)m, (long)k, (long)n, stream);
+    }
+    return kInvalidValue;
+}
+
+extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* b, void* grad_a,
+                                 void* grad_b, void* grad_bias, size_t m, size_t k, size_t n,
+                                 hipStream_t stream) {
+    size_t ea, eb;
+    if (!mul_ok(m, k, &ea) || !mul_ok(k, n, &eb)) return kInvalidValue;
+    const bool need_a = grad_a != nullptr, need_b = grad_b != nullptr,
+               need_bias = grad_bias != nullptr;
+    if (!need_a && !need_b && !need_bias) return kSuccess;
+    // validation and zero-fills in the reference's order (gemm.cu:424-466)
+    if (need_a) {
+        if (m == 0 || k == 0 || n == 0) {
+            EFLA_CHECK((hipError_t)fill_zero(grad_a, ea * 2, stream));
+        } else if (!grad_c || !b) {
+            return kInvalidValue;
+        }
+    }
+    if (need_b) {
+        if (k == 0 || n == 0 || m == 0) {
+            EFLA_CHECK((hipError_t)fill_zero(grad_b, eb * 2, stream));
+        } else if (!a || !grad_c) {
+            return kInvalidValue;
+        }
+    }
+    if (need_bias) {
+        if (n == 0) return kSuccess;
+        if (m == 0) {
+            EFLA_CHECK((hipError_t)fill_zero(grad_bias, n * 2, stream));
+        } else if (!grad_c) {
+            return kInvalidValue;
+        }
+    }
+    const long M = (long)m, K = (long)k, N = (long)n;
+    if (need_a && m && k && n) {
+        // dA[m, k] = sum_n dC[m, n] B[k, n]
+        int rc = launch<bf16, bf16, bf16, bf16, true, true>(grad_c, b, nullptr, grad_a, M, K, N,
+                                                            N, N, K, "gemm_bwd_da", stream);
+        if (rc != kSuccess) return rc;
+    }
+    if (need_b && m && k && n) {
+        // dB[k, n] = sum_m A[m, k] dC[m, n]
+        int rc = launch<bf16, bf16, bf16, bf16, false, false>(a, grad_c, nullptr, grad_b, K, N, M,
+                                                              K, N, N, "gemm_bwd_db", stream);
+        if (rc != kSuccess) return rc;
+    }
+    if (need_bias && m && n) {
+        EFLA_LAUNCH("gemm_bwd_dbias", colsum_kernel, dim3((unsigned)((N + 63) / 64)), dim3(NTH),
+                    stream, (const bf16*)grad_c, (bf16*)grad_bias, M, N);
+    }
+    return (int)hipPeekAtLastError();
+}

@@ -1,0 +1,277 @@
+// LayerNorm forward / backward for gfx950, bf16 rows with fp32 statistics.
+//
+// Forward (replaces layernorm_forward_cuda, layernorm.cu:133-183, 359-383):
+//   y = (x - mean) * rsqrt(var + eps) * w + b,  bias optional.
+// One row per wavefront.  When D is a multiple of 512 and at most 4096 the
+// row stays in registers (8 bf16 per lane per 512 columns, 16-byte coalesced
+// loads), so HBM sees one read of x and one write of y; the variance is taken
+// about the mean from those registers instead of the reference's
+// E[x^2] - mean^2, which cancels when |mean| >> std.  Other widths take a
+// looped path that re-reads the row (from cache for typical widths).
+//
+// Backward (no reference counterpart): with xhat = (x - mean) * rstd, g = dy*w
+//   dx = rstd * (g - mean(g) - xhat * mean(g * xhat))
+//   dw = sum_rows dy * xhat,  db = sum_rows dy      (fp32)
+// Each workgroup accumulates dw/db for its rows in LDS and writes one partial
+// row; a second kernel sums the partials (D <= 8192 when dw/db are wanted).
+#include <hip/hip_runtime.h>
+
+#include "../../include/efla_hip.h"
+#include "common.hpp"
+#include "internal.hpp"
+
+namespace efla {
+namespace ln {
+
+constexpr int NTH = 256;
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off);
+    return x;
+}
+
+// Row held in registers: lane owns columns (j*64 + lane)*8 .. +8 for j < NV.
+template <int NV>
+__global__ void __launch_bounds__(NTH) fwd_reg_kernel(const bf16* __restrict__ x,
+                                                      const bf16* __restrict__ w,
+                                                      const bf16* __restrict__ b,
+                                                      bf16* __restrict__ y,
+                                                      float* __restrict__ mean_out,
+                                                      float* __restrict__ rstd_out, long rows,
+                                                      float eps) {
+    constexpr int D = NV * 512;
+    const long row = (long)blockIdx.x * (NTH / kWave) + wave_id();
+    if (row >= rows) return;
+    const int lane = lane_id();
+    const bf16* xr = x + row * D;
+    bf16x8 xv[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) xv[j] = *reinterpret_cast<const bf16x8*>(xr + (j * 64 + lane) * 8);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s += (float)xv[j][i];
+    const float mean = wave_sum(s) * (1.0f / D);
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float d = (float)xv[j][i] - mean;
+            ss += d * d;
+        }
+    const float var = wave_sum(ss) * (1.0f / D);
+    const float rstd = 1.0f / sqrtf(var + eps);
+    bf16* yr = y + row * D;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = (j * 64 + lane) * 8;
+        const bf16x8 wv = *reinterpret_cast<const bf16x8*>(w + c);
+        bf16x8 bv;
+        if (b) bv = *reinterpret_cast<const bf16x8*>(b + c);
+        bf16x8 o;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const float bb = b ? (float)bv[i] : 0.f;
+            o[i] = (bf16)(((float)xv[j][i] - mean) * rstd * (float)wv[i] + bb);
+        }
+        *reinterpret_cast<bf16x8*>(yr + c) = o;
+    }
+    if (lane == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+// Any width: three passes over the row with stride-64 scalar access.
+__global__ void __launch_bounds__(NTH) fwd_loop_kernel(const bf16* __restrict__ x,
+                                                       const bf16* __restrict__ w,
+                                                       const bf16* __restrict__ b,
+                                                       bf16* __restrict__ y,
+                                                       float* __restrict__ mean_out,
+                                                       float* __restrict__ rstd_out, long rows,
+                                                       long D, float eps) {
+    const long row = (long)blockIdx.x * (NTH / kWave) + wave_id();
+    if (row >= rows) return;
+    const int lane = lane_id();
+    const bf16* xr = x + row * D;
+    float s = 0.f;
+    for (long c = lane; c < D; c += kWave) s += (float)xr[c];
+    const float mean = wave_sum(s) / (float)D;
+    float ss = 0.f;
+    for (long c = lane; c < D; c += kWave) {
+        const float d = (float)xr[c] - mean;
+        ss += d * d;
+    }
+    const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)D + eps);
+    bf16* yr = y + row * D;
+    for (long c = lane; c < D; c += kWave) {
+        const float bb = b ? (float)b[c] : 0.f;
+        yr[c] = (bf16)(((float)xr[c] - mean) * rstd * (float)w[c] + bb);
+    }
+    if (lane == 0) {
+        if (mean_out) mean_out[row] = mean;
+        if (rstd_out) rstd_out[row] = rstd;
+    }
+}
+
+// dx per row; dw/db partials per workgroup in LDS (2*D floats), written to
+// part[blockIdx.x][0..D) (dw) and part[blockIdx.x][D..2D) (db).
+__global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
+                                                  const bf16* __restrict__ x,
+                                                  const bf16* __restrict__ w,
+                                                  const float* __restrict__ mean,
+                                                  const float* __restrict__ rstd,
+                                                  bf16* __restrict__ dx,
+                                                  float* __restrict__ part, long rows, int D,
+                                                  int want_params) {
+    extern __shared__ float acc[];  // 2*D when want_params
+    const int lane = lane_id();
+    if (want_params)
+        for (int i = threadIdx.x; i < 2 * D; i += NTH) acc[i] = 0.f;
+    __syncthreads();
+    const long waves = (long)gridDim.x * (NTH / kWave);
+    for (long row = (long)blockIdx.x * (NTH / kWave) + wave_id(); row < rows; row += waves) {
+        const bf16* xr = x + row * D;
+        const bf16* gr = dy + row * D;
+        const float mu = mean[row], rs = rstd[row];
+        float sg = 0.f, sgx = 0.f;
+        for (int c = lane; c < D; c += kWave) {
+            const float xh = ((float)xr[c] - mu) * rs;
+            const float g = (float)gr[c] * (float)w[c];
+            sg += g;
+            sgx += g * xh;
+        }
+        sg = wave_sum(sg) / (float)D;
+        sgx = wave_sum(sgx) / (float)D;
+        bf16* dxr = dx + row * D;
+        for (int c = lane; c < D; c += kWave) {
+            const float xh = ((float)xr[c] - mu) * rs;
+            const float gy = (float)gr[c];
+            const float g = gy * (float)w[c];
+            dxr[c] = (bf16)(rs * (g - sg - xh * sgx));
+            if (want_params) {
+                atomicAdd(&acc[c], gy * xh);
+                atomicAdd(&acc[D + c], gy);
+            }
+        }
+    }
+    if (!want_params) return;
+    __syncthreads();
+    float* pr = part + (long)blockIdx.x * 2 * D;
+    for (int i = threadIdx.x; i < 2 * D; i += NTH) pr[i] = acc[i];
+}
+
+__global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ part, int nblk,
+                                                     int D, float* __restrict__ dw,
+                                                     float* __restrict__ db) {
+    const int c = blockIdx.x * NTH + threadIdx.x;
+    if (c >= 2 * D) return;
+    float s = 0.f;
+    for (int b = 0; b < nblk; ++b) s += part[(long)b * 2 * D + c];
+    if (c < D) {
+        if (dw) dw[c] = s;
+    } else if (db) {
+        db[c - D] = s;
+    }
+}
+
+static int forward(const void* input, const void* weight, const void* bias, void* output,
+                   float* mean, float* rstd, size_t numel, size_t D, float eps,
+                   hipStream_t stream) {
+    if (D == 0) return kInvalidValue;
+    const size_t rows = numel / D;
+    if (rows == 0) return kSuccess;
+    if (!input || !weight || !output) return kInvalidValue;
+    if (rows > ((size_t)1 << 40)) return kInvalidConfiguration;
+    const size_t rpb = NTH / kWave;
+    const size_t grid = (rows + rpb - 1) / rpb;
+    if (grid > 0x7FFFFFFFull) return kInvalidConfiguration;
+    const bf16* x = (const bf16*)input;
+    const bf16* w = (const bf16*)weight;
+    const bf16* b = (const bf16*)bias;
+    bf16* y = (bf16*)output;
+    const bool aligned = (((uintptr_t)x | (uintptr_t)w | (uintptr_t)y |
+                           (uintptr_t)(b ? b : w)) & 15u) == 0;
+    const dim3 g((unsigned)grid), bl(NTH);
+    if (aligned && D % 512 == 0 && D <= 4096) {
+        switch (D / 512) {
+#define LN_CASE(nv)                                                                            \
+    case nv:                                                                                   \
+        EFLA_LAUNCH("layernorm_fwd", fwd_reg_kernel<nv>, g, bl, stream, x, w, b, y, mean, rstd, \
+                    (long)rows, eps);                                                          \
+        return (int)hipPeekAtLastError();
+            LN_CASE(1) LN_CASE(2) LN_CASE(3) LN_CASE(4) LN_CASE(5) LN_CASE(6) LN_CASE(7)
+            LN_CASE(8)
+#undef LN_CASE
+        }
+    }
+    EFLA_LAUNCH("layernorm_fwd_loop", fwd_loop_kernel, g, bl, stream, x, w, b, y, mean, rstd,
+                (long)rows, (long)D, eps);
+    return (int)hipPeekAtLastError();
+}
+
+}  // namespace ln
+}  // namespace efla
+
+using namespace efla;
+
+extern "C" int layernorm_forward_hip(const void* input, const void* weight, const void* bias,
+                                     void* output, size_t numel, size_t normalized_shape,
+                                     float eps, hipStream_t stream) {
+    return ln::forward(input, weight, bias, output, nullptr, nullptr, numel, normalized_shape,
+                       eps, stream);
+}
+
+extern "C" int layernorm_forward_stats_hip(const void* input, const void* weight,
+                                           const void* bias, void* output, float* mean,
+                                           float* rstd, size_t numel, size_t normalized_shape,
+                                           float eps, hipStream_t stream) {
+    if (!mean || !rstd) return kInvalidValue;
+    return ln::forward(input, weight, bias, output, mean, rstd, numel, normalized_shape, eps,
+                       stream);
+}
+
+extern "C" int layernorm_backward_hip(const void* grad_output, const void* input,
+                                      const void* weight, const float* mean, const float* rstd,
+                                      void* grad_input, float* grad_weight, float* grad_bias,
+                                      size_t numel, size_t normalized_shape,
+                                      hipStream_t stream) {
+    const size_t D = normalized_shape;
+    if (D == 0) return kInvalidValue;
+    const size_t rows = numel / D;
+    const bool params = grad_weight || grad_bias;
+    if (rows == 0) {
+        if (grad_weight) EFLA_CHECK((hipError_t)fill_zero(grad_weight, D * 4, stream));
+        if (grad_bias) EFLA_CHECK((hipError_t)fill_zero(grad_bias, D * 4, stream));
+        return kSuccess;
+    }
+    if (!grad_output || !input || !weight || !mean || !rstd || !grad_input) return kInvalidValue;
+    if ((params && D > 8192) || rows > ((size_t)1 << 40)) return kInvalidConfiguration;
+    size_t nblk = (rows + 3) / 4;
+    if (nblk > 1024) nblk = 1024;
+    float* part = nullptr;
+    if (params) {
+        void* ws = nullptr;
+        int rc = workspace_acquire(nblk * 2 * D * sizeof(float), stream, &ws);
+        if (rc != kSuccess) return rc;
+        part = (float*)ws;
+    }
+    const size_t smem = params ? 2 * D * sizeof(float) : 0;
+    {
+        ::efla::ProfScope ps("layernorm_bwd", stream);
+        hipLaunchKernelGGL(ln::bwd_kernel, dim3((unsigned)nblk), dim3(ln::NTH), smem, stream,
+                           (const bf16*)grad_output, (const bf16*)input, (const bf16*)weight,
+                           mean, rstd, (bf16*)grad_input, part, (long)rows, (int)D,
+                           params ? 1 : 0);
+    }
+    EFLA_CHECK(hipPeekAtLastError());
+    if (params) {
+        const unsigned g = (unsigned)((2 * D + ln::NTH - 1) / ln::NTH);
+        EFLA_LAUNCH("layernorm_bwd_reduce", ln::reduce_kernel, dim3(g), dim3(ln::NTH), stream,
+                    (const float*)part, (int)nblk, (int)D, grad_weight, grad_bias);
+    }
+    return (int)hipPeekAtLastError();
+}

@@ -1,0 +1,86 @@
+"""LayerNorm and GEMM around EFLA: torch-facing wrappers over the C ABI.
+
+Mirror the reference's ``layerNormForwardCuda`` / ``gemmForwardCuda`` /
+``gemmBackwardCuda`` externs (src/kernels/nn_kernels.zig:28-76) and their
+callers ``LayerNorm.forward`` (src/nn/layers.zig:226-245, eps 1e-5) and
+``Linear.forward`` (src/nn/layers.zig:561-586, weight (in, out) row-major).
+"""
+from __future__ import annotations
+
+import torch
+
+from ._lib import check, lib
+from .efla import DTYPE_CODES, _p, _require, _stream
+
+
+def layernorm_forward(x: torch.Tensor, weight: torch.Tensor, bias=None, eps: float = 1e-5,
+                      save_stats: bool = False):
+    """y = LayerNorm(x) over the last dim (bf16); with save_stats also (mean, rstd) fp32."""
+    D = x.shape[-1]
+    _require(x, "x", torch.bfloat16)
+    _require(weight, "weight", torch.bfloat16, x.device)
+    if bias is not None:
+        _require(bias, "bias", torch.bfloat16, x.device)
+    y = torch.empty_like(x)
+    if save_stats:
+        rows = x.numel() // D
+        mean = torch.empty(rows, dtype=torch.float32, device=x.device)
+        rstd = torch.empty(rows, dtype=torch.float32, device=x.device)
+        rc = lib().layernorm_forward_stats_hip(_p(x), _p(weight), _p(bias), _p(y), _p(mean),
+                                               _p(rstd), x.numel(), D, float(eps), _stream(x))
+        check(rc, "layernorm_forward_stats_hip")
+        return y, mean, rstd
+    rc = lib().layernorm_forward_hip(_p(x), _p(weight), _p(bias), _p(y), x.numel(), D,
+                                     float(eps), _stream(x))
+    check(rc, "layernorm_forward_hip")
+    return y
+
+
+def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True):
+    """(dx bf16, dweight fp32 or None, dbias fp32 or None)."""
+    D = x.shape[-1]
+    for t, n in ((dy, "dy"), (x, "x"), (weight, "weight")):
+        _require(t, n, torch.bfloat16, x.device)
+    _require(mean, "mean", torch.float32, x.device)
+    _require(rstd, "rstd", torch.float32, x.device)
+    dx = torch.empty_like(x)
+    dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
+    db = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
+    rc = lib().layernorm_backward_hip(_p(dy), _p(x), _p(weight), _p(mean), _p(rstd), _p(dx),
+                                      _p(dw), _p(db), x.numel(), D, _stream(x))
+    check(rc, "layernorm_backward_hip")
+    return dx, dw, db
+
+
+def gemm_forward(a: torch.Tensor, b: torch.Tensor, bias=None, out_dtype=None) -> torch.Tensor:
+    """c = a @ b (+ bias), a (m,k), b (k,n) row-major; fp32 accumulation."""
+    m, k = a.shape
+    k2, n = b.shape
+    if k2 != k:
+        raise ValueError("gemm_forward: inner dimensions differ")
+    _require(a, "a")
+    _require(b, "b", device=a.device)
+    out_dtype = out_dtype or a.dtype
+    c = torch.empty(m, n, dtype=out_dtype, device=a.device)
+    if bias is not None:
+        _require(bias, "bias", out_dtype, a.device)
+    rc = lib().gemm_forward_hip(_p(a), _p(b), _p(bias), _p(c), m, k, n, DTYPE_CODES[a.dtype],
+                                DTYPE_CODES[b.dtype], DTYPE_CODES[out_dtype], _stream(a))
+    check(rc, "gemm_forward_hip")
+    return c
+
+
+def gemm_backward(dc: torch.Tensor, a: torch.Tensor, b: torch.Tensor, need_a=True, need_b=True,
+                  need_bias=False):
+    """(da, db, dbias) for c = a @ b + bias, all bf16."""
+    m, k = a.shape
+    n = b.shape[1]
+    for t, nme in ((dc, "dc"), (a, "a"), (b, "b")):
+        _require(t, nme, torch.bfloat16, a.device)
+    da = torch.empty_like(a) if need_a else None
+    dbm = torch.empty_like(b) if need_b else None
+    dbias = torch.empty(n, dtype=torch.bfloat16, device=a.device) if need_bias else None
+    rc = lib().gemm_backward_hip(_p(dc), _p(a), _p(b), _p(da), _p(dbm), _p(dbias), m, k, n,
+                                 _stream(a))
+    check(rc, "gemm_backward_hip")
+    return da, dbm, dbias

@@ -1,0 +1,168 @@
+/*
+ * efla_hip.h -- C ABI of the MI355X (gfx950) EFLA hot path.
+ *
+ * Drop-in for the reference's kernel ABI (kernels/cuda/include/kernels.h):
+ * same argument order, meaning, tensor layouts and error behaviour, with
+ * hipStream_t in place of cudaStream_t.  Every entry returns a hipError_t code
+ * as int; the codes the reference returns keep their numbers
+ * (0 success, 1 invalid value, 2 out of memory, 9 invalid configuration).
+ * Pointers are caller-owned device pointers to contiguous row-major buffers;
+ * calls are asynchronous on `stream`.  No entry point allocates per call: the
+ * Mode Q entries take a caller workspace (or use one cached per device,
+ * allocated once and grown only when a larger problem arrives).
+ *
+ * Layouts:
+ *   tokens      (B, T, H, D) row-major, i.e. token-major with heads interleaved
+ *   Mode R state (B*H, d, d) bf16, row index = key dim, column = value dim
+ *   Mode Q state (N, H, d_k, d_v) fp32
+ *   beta        (B, T, H), same dtype as q/k/v
+ *   cu_seqlens  int32 (N+1) device array of packed sequence offsets, or NULL
+ */
+#ifndef EFLA_HIP_H
+#define EFLA_HIP_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes: hipDataType values, equal to the reference's cudaDataType codes */
+#define EFLA_DTYPE_F32 0
+#define EFLA_DTYPE_F16 2
+#define EFLA_DTYPE_BF16 14
+
+/* ========================================================================
+ * EFLA, reference ABI ("Mode R")
+ * ======================================================================== */
+
+/*
+ * Replaces efla_forward_cuda (kernels/cuda/include/kernels.h:35-47,
+ * kernels/cuda/efla.cu:482-541).  Per (b, h), token-sequential:
+ *   lambda = |k_t|^2, c = (1 - exp(-beta lambda)) / lambda,
+ *   S <- bf16(S + c k_t (v_t - S^T k_t)^T), o_t = S k_t   (requires d_k == d_v)
+ * k, v, output: (B, T, H, d) bf16.  state: (B*H, d, d) bf16, read as S_0 and
+ * overwritten with S_T.  chunk_size is accepted and ignored, as in the
+ * reference.  Validation order: B, H or d == 0 -> 1; T == 0 -> 0; any null
+ * pointer -> 1; B*H or sizes overflowing -> 9.
+ */
+int efla_forward_hip(const void* k, const void* v, void* state, void* output,
+                     size_t batch_size, size_t seq_len, size_t num_heads, size_t head_dim,
+                     float beta, size_t chunk_size, hipStream_t stream);
+
+/*
+ * Replaces efla_backward_cuda (kernels.h:52-66, efla.cu:543-709).  `state` is
+ * S_0.  Outputs grad_k, grad_v (B, T, H, d) bf16 and grad_state = dL/dS_0
+ * (B*H, d, d) bf16 for the loss sum(output * grad_output).  T == 0 zeroes
+ * grad_state and returns 0.  State history is recomputed from checkpoints in a
+ * cached workspace instead of the reference's per-call (T+1)*d*d allocation.
+ */
+int efla_backward_hip(const void* grad_output, const void* k, const void* v, const void* state,
+                      void* grad_k, void* grad_v, void* grad_state, size_t batch_size,
+                      size_t seq_len, size_t num_heads, size_t head_dim, float beta,
+                      hipStream_t stream);
+
+/*
+ * Replaces efla_chunked_scan_cuda (kernels.h:71-77, efla.cu:711-748).
+ * chunk_states is a HOST array of num_chunks device pointers, each to H*d*d
+ * bf16 values; chunk_states[i] <- bf16(chunk_states[i-1] + chunk_states[i])
+ * for i = 1..num_chunks-1 (an inclusive prefix sum, as in the reference).
+ */
+int efla_chunked_scan_hip(void** chunk_states, size_t num_chunks, size_t num_heads,
+                          size_t head_dim, hipStream_t stream);
+
+/* ========================================================================
+ * EFLA, chunked query-readout form ("Mode Q")
+ *
+ * No reference counterpart: the benchmark configurations need a query
+ * readout o_t = S_t^T q_t, per-token beta, d_k != d_v, dq, dbeta and varlen
+ * packing, none of which the reference ABI expresses.  The state recurrence
+ * is the reference's (efla.cu:154-233) with beta per token.
+ *
+ * q, k (B, T, H, d_k); v, output (B, T, H, d_v); beta (B, T, H); all of
+ * `dtype` (EFLA_DTYPE_BF16 or EFLA_DTYPE_F32), fp32 accumulation.  With
+ * cu_seqlens != NULL the batch must be 1 and `seq_len` is the packed token
+ * count; num_seqs gives the number of sequences (cu_seqlens has num_seqs+1
+ * entries); otherwise num_seqs must equal batch_size.  initial_state /
+ * final_state (num_seqs, H, d_k, d_v) fp32, either may be NULL.
+ * Supported: chunk_size 64 (0 selects 64); (d_k, d_v) in
+ * {64,128} x {64,128,256} for bf16, d_k = d_v = 64 for fp32.
+ * Workspace: pass NULL to use the library's cached per-device buffer, or a
+ * buffer of at least efla_chunk_*_workspace_size() bytes.
+ * ======================================================================== */
+size_t efla_chunk_fwd_workspace_size(size_t batch_size, size_t seq_len, size_t num_seqs,
+                                     size_t num_heads, size_t head_dim_k, size_t head_dim_v,
+                                     int dtype);
+
+int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, const void* beta,
+                       const float* initial_state, void* output, float* final_state,
+                       const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                       size_t num_seqs, size_t num_heads, size_t head_dim_k,
+                       size_t head_dim_v, size_t chunk_size, int dtype, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+size_t efla_chunk_bwd_workspace_size(size_t batch_size, size_t seq_len, size_t num_seqs,
+                                     size_t num_heads, size_t head_dim_k, size_t head_dim_v,
+                                     int dtype);
+
+/* Gradients of sum(output * grad_output) + sum(final_state * grad_final_state);
+ * grad_final_state and grad_initial_state may be NULL.  Chunk states are
+ * recomputed, not read from the forward. */
+int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, const void* beta,
+                       const float* initial_state, const void* grad_output,
+                       const float* grad_final_state, void* grad_q, void* grad_k,
+                       void* grad_v, void* grad_beta, float* grad_initial_state,
+                       const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                       size_t num_seqs, size_t num_heads, size_t head_dim_k,
+                       size_t head_dim_v, size_t chunk_size, int dtype, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/* ========================================================================
+ * LayerNorm
+ * ======================================================================== */
+
+/* Replaces layernorm_forward_cuda (kernels.h:153-162, layernorm.cu:359-383):
+ * rows = numel / normalized_shape; y = (x - mean) * rsqrt(var + eps) * w + b,
+ * bias may be NULL.  bf16 in/out, fp32 statistics. */
+int layernorm_forward_hip(const void* input, const void* weight, const void* bias, void* output,
+                          size_t numel, size_t normalized_shape, float eps, hipStream_t stream);
+
+/* No reference counterpart (the reference has no LayerNorm backward): the
+ * forward above that also stores per-row fp32 mean and rstd for the backward. */
+int layernorm_forward_stats_hip(const void* input, const void* weight, const void* bias,
+                                void* output, float* mean, float* rstd, size_t numel,
+                                size_t normalized_shape, float eps, hipStream_t stream);
+
+/* No reference counterpart.  grad_input bf16; grad_weight / grad_bias fp32
+ * (either may be NULL).  Uses the cached workspace for per-block partials. */
+int layernorm_backward_hip(const void* grad_output, const void* input, const void* weight,
+                           const float* mean, const float* rstd, void* grad_input,
+                           float* grad_weight, float* grad_bias, size_t numel,
+                           size_t normalized_shape, hipStream_t stream);
+
+/* ========================================================================
+ * GEMM (row-major)
+ * ======================================================================== */
+
+/* Replaces gemm_forward_cuda (kernels.h:211-223, gemm.cu:303-398):
+ * c[m x n] = a[m x k] * b[k x n] (+ bias[n]), fp32 accumulation; dtypes are
+ * EFLA_DTYPE_* codes for each operand.  m or n == 0 -> 0; k == 0 -> c = bias
+ * (or 0). */
+int gemm_forward_hip(const void* a, const void* b, const void* bias, void* c, size_t m,
+                     size_t k, size_t n, int dtype_a, int dtype_b, int dtype_c,
+                     hipStream_t stream);
+
+/* Replaces gemm_backward_cuda (kernels.h:228-239, gemm.cu:400-548), bf16:
+ * grad_a = grad_c * b^T, grad_b = a^T * grad_c, grad_bias = column sums of
+ * grad_c; a NULL gradient pointer skips that product. */
+int gemm_backward_hip(const void* grad_c, const void* a, const void* b, void* grad_a,
+                      void* grad_b, void* grad_bias, size_t m, size_t k, size_t n,
+                      hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* EFLA_HIP_H */

@@ -1,0 +1,114 @@
+"""The C ABI without a GPU: the library loads, exports every symbol the public
+headers declare, and rejects bad arguments before touching a device, with the
+reference's codes (0 success, 1 invalid value, 9 invalid configuration)."""
+import ctypes
+
+import pytest
+
+from ceo_amd import _lib
+
+NULL = None
+
+
+@pytest.fixture(scope="module")
+def L():
+    return _lib.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    names = _lib.header_functions()
+    assert len(names) >= 40
+    for n in names:
+        assert hasattr(L, n), n
+        assert n in _lib._SIGS, f"{n} has no ctypes signature"
+
+
+def test_efla_forward_validation_order(L):
+    p = ctypes.c_void_p(16)
+    # B, H or d == 0 -> InvalidValue, before the T == 0 early return (efla.cu:497-502)
+    assert L.efla_forward_hip(p, p, p, p, 0, 0, 1, 1, 1.0, 64, NULL) == 1
+    assert L.efla_forward_hip(p, p, p, p, 1, 4, 0, 1, 1.0, 64, NULL) == 1
+    assert L.efla_forward_hip(p, p, p, p, 1, 4, 1, 0, 1.0, 64, NULL) == 1
+    # T == 0 -> success even with null pointers
+    assert L.efla_forward_hip(NULL, NULL, NULL, NULL, 1, 0, 1, 1, 1.0, 64, NULL) == 0
+    assert L.efla_forward_hip(p, NULL, p, p, 1, 1, 1, 1, 1.0, 64, NULL) == 1
+    # B*H beyond the 32-bit grid -> InvalidConfiguration (efla.cu:507-513)
+    assert L.efla_forward_hip(p, p, p, p, 1 << 31, 1, 4, 1, 1.0, 64, NULL) == 9
+
+
+def test_efla_backward_validation_order(L):
+    p = ctypes.c_void_p(16)
+    assert L.efla_backward_hip(p, p, p, p, p, p, p, 0, 1, 1, 1, 1.0, NULL) == 1
+    assert L.efla_backward_hip(p, p, p, NULL, p, p, p, 1, 1, 1, 1, 1.0, NULL) == 1
+    assert L.efla_backward_hip(p, p, p, p, p, p, NULL, 1, 1, 1, 1, 1.0, NULL) == 1
+    assert L.efla_backward_hip(NULL, p, p, p, p, p, p, 1, 1, 1, 2, 1.0, NULL) == 1
+    assert L.efla_backward_hip(p, p, p, p, p, p, p, 1 << 31, 1, 4, 1, 1.0, NULL) == 9
+
+
+def test_efla_chunked_scan_validation(L):
+    arr = (ctypes.c_void_p * 2)(16, None)
+    assert L.efla_chunked_scan_hip(arr, 0, 1, 1, NULL) == 1
+    assert L.efla_chunked_scan_hip(arr, 2, 0, 1, NULL) == 1
+    assert L.efla_chunked_scan_hip(NULL, 2, 1, 1, NULL) == 1
+    assert L.efla_chunked_scan_hip(arr, 2, 1, 4, NULL) == 1  # a null chunk
+    one = (ctypes.c_void_p * 1)(16)
+    assert L.efla_chunked_scan_hip(one, 1, 1, 4, NULL) == 0  # nothing to add
+
+
+def _fwd(L, **kw):
+    a = dict(q=16, k=16, v=16, beta=16, s0=None, o=16, st=None, cu=None, B=2, T=128, N=0,
+             H=2, K=64, V=64, C=64, dt=14, ws=None, wsb=0)
+    a.update(kw)
+    vp = ctypes.c_void_p
+    return L.efla_chunk_fwd_hip(vp(a["q"]), vp(a["k"]), vp(a["v"]), vp(a["beta"]), a["s0"],
+                                vp(a["o"]) if a["o"] else None, a["st"], a["cu"], a["B"], a["T"],
+                                a["N"], a["H"], a["K"], a["V"], a["C"], a["dt"], a["ws"],
+                                a["wsb"], None)
+
+
+def test_chunk_fwd_validation(L):
+    assert _fwd(L, H=0) == 1
+    assert _fwd(L, K=0) == 1
+    assert _fwd(L, C=32) == 1          # only 64-token chunks
+    assert _fwd(L, K=96) == 1          # unsupported head dim
+    assert _fwd(L, dt=0, K=128) == 1   # fp32 only at 64 x 64
+    assert _fwd(L, dt=2) == 1          # fp16 not supported
+    assert _fwd(L, B=0) == 1
+    assert _fwd(L, N=3) == 1           # num_seqs must match batch without cu_seqlens
+    assert _fwd(L, cu=ctypes.c_void_p(16), B=2, N=2) == 1  # packed input has batch 1
+    assert _fwd(L, T=0) == 0           # nothing to do, no final state requested
+    assert _fwd(L, q=0) == 1
+    assert _fwd(L, o=0) == 1
+    assert _fwd(L, ws=ctypes.c_void_p(256), wsb=16) == 1   # workspace too small
+
+
+def test_workspace_sizes(L):
+    f = L.efla_chunk_fwd_workspace_size
+    b = L.efla_chunk_bwd_workspace_size
+    # cfg3: B=4, T=8192, H=32, K=V=128 bf16
+    fw = f(4, 8192, 0, 32, 128, 128, 14)
+    bw = b(4, 8192, 0, 32, 128, 128, 14)
+    ntok = 4 * 8192
+    per_tok = 32 * 128 * 2
+    assert fw >= 3 * ntok * per_tok          # W, U, Vn
+    assert bw > fw
+    assert bw < 16 * 2**30                   # fits comfortably in 288 GB
+    assert f(4, 8192, 0, 32, 96, 128, 14) == 0
+    assert f(1, 65536, 40, 16, 128, 256, 14) > 0   # packed, cfg5 shape
+
+
+def test_gemm_validation(L):
+    p = ctypes.c_void_p(16)
+    assert L.gemm_forward_hip(NULL, p, NULL, p, 4, 4, 4, 14, 14, 14, NULL) == 1
+    assert L.gemm_forward_hip(p, p, NULL, p, 4, 4, 4, 14, 14, 99, NULL) == 1
+    assert L.gemm_forward_hip(p, p, NULL, p, 0, 4, 4, 14, 14, 14, NULL) == 0
+    assert L.gemm_backward_hip(p, p, p, NULL, NULL, NULL, 4, 4, 4, NULL) == 0
+    assert L.gemm_backward_hip(NULL, p, p, p, NULL, NULL, 4, 4, 4, NULL) == 1
+
+
+def test_layernorm_validation(L):
+    p = ctypes.c_void_p(16)
+    assert L.layernorm_forward_hip(p, p, NULL, p, 1024, 0, 1e-5, NULL) == 1
+    assert L.layernorm_forward_hip(p, p, NULL, p, 0, 1024, 1e-5, NULL) == 0
+    assert L.layernorm_forward_hip(NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1
+    assert L.layernorm_forward_stats_hip(p, p, NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1

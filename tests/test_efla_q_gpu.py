@@ -1,0 +1,132 @@
+"""Chunked query-readout EFLA on the GPU against the fp64 oracle.
+
+Tolerances: rel-L2 <= 1e-4 for the fp32 path,
+<= 2e-2 for bf16 inputs with fp32 accumulation, on O, dq, dk, dv, dbeta (and
+the final / initial state and their gradients when present).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce, rel_l2, to_dev
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
+
+
+def _case(oracle, seed, B, T, H, K, V, dtype, *, s0=False, dst=False, cu=None):
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd
+
+    announce(f"chunk_efla B={B} T={T} H={H} K={K} V={V} {dtype} s0={s0} dst={dst} "
+             f"varlen={cu is not None}")
+    ntok = B * T
+    x = oracle.make_efla_inputs(seed, ntok, H, K, V, bf16=dtype == torch.bfloat16)
+    N = B if cu is None else len(cu) - 1
+    rng = np.random.default_rng(seed)
+    S0 = (rng.standard_normal((N, H, K, V)) * 0.3).astype(np.float32) if s0 else None
+    dST = rng.standard_normal((N, H, K, V)).astype(np.float32) if dst else None
+    g = {n: to_dev(a, dtype, (B, T, H, K) if n in "qk" else
+                   (B, T, H) if n == "beta" else (B, T, H, V)) for n, a in x.items()}
+    cu_t = None if cu is None else torch.tensor(cu, dtype=torch.int32, device="cuda:0")
+    s0_t = None if S0 is None else torch.from_numpy(S0).cuda()
+    dst_t = None if dST is None else torch.from_numpy(dST).cuda()
+    o, st = chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], s0_t, True, cu_t)
+    dq, dk, dv, db, ds0 = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], s0_t,
+                                         dst_t, cu_t)
+    torch.cuda.synchronize()
+    kw = dict(cu_seqlens=cu) if cu is not None else dict(T=T)
+    ro, rst = oracle.q_forward(x["q"], x["k"], x["v"], x["beta"], S0=S0, **kw)
+    rg = oracle.q_backward(x["q"], x["k"], x["v"], x["beta"], x["do"], S0=S0, dST=dST, **kw)
+    errs = {"o": rel_l2(o, ro), "S_T": rel_l2(st, rst), "dq": rel_l2(dq, rg[0]),
+            "dk": rel_l2(dk, rg[1]), "dv": rel_l2(dv, rg[2]), "dbeta": rel_l2(db, rg[3])}
+    if s0:
+        errs["dS0"] = rel_l2(ds0, rg[4])
+    print("  rel-L2:", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    tol = TOL[dtype]
+    bad = {k: v for k, v in errs.items() if not v <= tol}
+    assert not bad, bad
+
+
+def test_cfg1_fp32(oracle):
+    # B=2, T=256, H=4, d_k=d_v=64, chunk 64, fp32
+    _case(oracle, 0xEF1A0000, 2, 256, 4, 64, 64, torch.float32)
+
+
+def test_fp32_ragged_with_states(oracle):
+    _case(oracle, 11, 2, 200, 3, 64, 64, torch.float32, s0=True, dst=True)
+
+
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 128), (128, 256), (64, 128), (128, 64),
+                                 (64, 256)])
+def test_bf16_shapes(oracle, K, V):
+    _case(oracle, 100 + K + V, 2, 192, 2, K, V, torch.bfloat16)
+
+
+def test_bf16_ragged_states(oracle):
+    _case(oracle, 21, 2, 301, 2, 128, 128, torch.bfloat16, s0=True, dst=True)
+
+
+@pytest.mark.parametrize("T", [1, 63, 64, 65])
+def test_bf16_short_sequences(oracle, T):
+    _case(oracle, 30 + T, 3, T, 2, 64, 64, torch.bfloat16, s0=True, dst=True)
+
+
+def test_varlen_bf16(oracle):
+    lens = [1, 63, 64, 65, 130, 7, 0, 200]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    _case(oracle, 41, 1, int(cu[-1]), 2, 128, 256, torch.bfloat16, s0=True, dst=True,
+          cu=cu)
+
+
+def test_varlen_fp32(oracle):
+    lens = [17, 64, 100]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    _case(oracle, 42, 1, int(cu[-1]), 2, 64, 64, torch.float32, s0=True, dst=True, cu=cu)
+
+
+def test_empty_sequence_passes_state_through(oracle):
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd
+
+    announce("chunk_efla T=0")
+    q = torch.zeros(2, 0, 2, 64, dtype=torch.bfloat16, device="cuda:0")
+    beta = torch.zeros(2, 0, 2, dtype=torch.bfloat16, device="cuda:0")
+    s0 = torch.randn(2, 2, 64, 64, device="cuda:0")
+    o, st = chunk_efla_fwd(q, q, q, beta, s0, True)
+    assert o.numel() == 0
+    assert torch.equal(st, s0)
+    dht = torch.randn_like(s0)
+    *_, dh0 = chunk_efla_bwd(q, q, q, beta, q, s0, dht)
+    assert torch.equal(dh0, dht)
+
+
+def test_caller_workspace_matches_cached(oracle):
+    from ceo_amd.efla import chunk_efla_fwd, workspace_bytes
+
+    announce("chunk_efla caller workspace")
+    B, T, H, K, V = 2, 128, 2, 128, 128
+    x = oracle.make_efla_inputs(77, B * T, H, K, V, bf16=True)
+    g = {n: to_dev(a, torch.bfloat16, (B, T, H, K) if n in "qk" else
+                   (B, T, H) if n == "beta" else (B, T, H, V)) for n, a in x.items()}
+    o1, _ = chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"])
+    nbytes = workspace_bytes("fwd", B, T, H, K, V, torch.bfloat16)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    o2, _ = chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], workspace=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
+
+
+def test_autograd_function(oracle):
+    from ceo_amd.efla import chunk_efla
+
+    announce("chunk_efla autograd")
+    B, T, H, K, V = 1, 130, 2, 64, 64
+    x = oracle.make_efla_inputs(88, B * T, H, K, V, bf16=False)
+    g = {n: to_dev(a, torch.float32, (B, T, H, K) if n in "qk" else
+                   (B, T, H) if n == "beta" else (B, T, H, V)).requires_grad_(n != "do")
+         for n, a in x.items()}
+    o, _ = chunk_efla(g["q"], g["k"], g["v"], g["beta"])
+    (o * g["do"]).sum().backward()
+    rg = oracle.q_backward(x["q"], x["k"], x["v"], x["beta"], x["do"], T=T)
+    for name, ref in zip(("q", "k", "v", "beta"), rg[:4]):
+        assert rel_l2(g[name].grad, ref) <= 1e-4, name

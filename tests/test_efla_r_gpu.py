@@ -1,0 +1,122 @@
+"""Reference-ABI EFLA (efla_forward_hip / efla_backward_hip /
+efla_chunked_scan_hip) on the GPU against the oracle's restatement of
+kernels/cuda/efla.cu, including its per-token bf16 state rounding.
+
+The GPU sums in a different order than the reference's serial loops, so the
+bf16 trajectories can part by one ulp where a value sits on a rounding
+boundary; the bound is the bf16 path's rel-L2 <= 2e-2 (measured values are
+printed and are far below it)."""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _u16_to_dev(a):
+    return torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).cuda()
+
+
+def _dev_to_u16(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _inputs(oracle, seed, B, T, H, d, s0_scale):
+    x = oracle.make_efla_inputs(seed, B * T, H, d, d, bf16=True, with_q=False)
+    k = oracle.f32_to_bf16(x["k"]).reshape(B, T, H, d)
+    v = oracle.f32_to_bf16(x["v"]).reshape(B, T, H, d)
+    do = oracle.f32_to_bf16(x["do"]).reshape(B, T, H, d)
+    rng = np.random.default_rng(seed)
+    s0 = oracle.f32_to_bf16((rng.standard_normal((B * H, d, d)) * s0_scale).astype(np.float32))
+    return k, v, do, s0
+
+
+@pytest.mark.parametrize("B,T,H,d", [(2, 100, 2, 64), (1, 130, 3, 128), (1, 40, 1, 256),
+                                     (2, 1, 2, 32), (1, 70, 2, 96)])
+def test_forward_matches_reference(oracle, B, T, H, d):
+    from ceo_amd.efla import efla_forward
+
+    announce(f"efla_forward_hip B={B} T={T} H={H} d={d}")
+    k, v, _, s0 = _inputs(oracle, 500 + d, B, T, H, d, 0.2)
+    beta = 0.8
+    st_ref = s0.copy()
+    rc, o_ref = oracle.r_forward(k, v, st_ref, B, T, H, d, beta)
+    assert rc == 0
+    st = _u16_to_dev(s0)
+    o = efla_forward(_u16_to_dev(k), _u16_to_dev(v), st, beta)
+    torch.cuda.synchronize()
+    eo = rel_l2(oracle.bf16_to_f32(_dev_to_u16(o)), oracle.bf16_to_f32(o_ref))
+    es = rel_l2(oracle.bf16_to_f32(_dev_to_u16(st)), oracle.bf16_to_f32(st_ref))
+    print(f"  rel-L2 o={eo:.2e} state={es:.2e}", flush=True)
+    assert eo <= 2e-2 and es <= 2e-2
+
+
+@pytest.mark.parametrize("B,T,H,d", [(2, 100, 2, 64), (1, 150, 2, 128), (1, 70, 1, 256),
+                                     (1, 64, 2, 48)])
+def test_backward_matches_reference(oracle, B, T, H, d):
+    from ceo_amd.efla import efla_backward
+
+    announce(f"efla_backward_hip B={B} T={T} H={H} d={d}")
+    k, v, do, s0 = _inputs(oracle, 600 + d, B, T, H, d, 0.2)
+    beta = 0.7
+    rc, gk_ref, gv_ref, gs_ref = oracle.r_backward(do, k, v, s0, B, T, H, d, beta)
+    assert rc == 0
+    gk, gv, gs = efla_backward(_u16_to_dev(do), _u16_to_dev(k), _u16_to_dev(v),
+                               _u16_to_dev(s0), beta)
+    torch.cuda.synchronize()
+    errs = {n: rel_l2(oracle.bf16_to_f32(_dev_to_u16(a)), oracle.bf16_to_f32(r))
+            for n, a, r in (("grad_k", gk, gk_ref), ("grad_v", gv, gv_ref),
+                            ("grad_state", gs, gs_ref))}
+    print("  rel-L2:", {k: f"{e:.2e}" for k, e in errs.items()}, flush=True)
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_backward_zero_length_zeroes_grad_state(oracle):
+    from ceo_amd._lib import lib
+
+    announce("efla_backward_hip T=0")
+    gs = torch.full((4, 8, 8), 3.0, dtype=torch.bfloat16, device="cuda:0")
+    st = torch.zeros_like(gs)
+    rc = lib().efla_backward_hip(None, None, None, ctypes.c_void_p(st.data_ptr()), None, None,
+                                 ctypes.c_void_p(gs.data_ptr()), 2, 0, 2, 8, 1.0, None)
+    torch.cuda.synchronize()
+    assert rc == 0 and not gs.any()
+
+
+def test_chunked_scan_bit_exact(oracle):
+    from ceo_amd.efla import efla_chunked_scan
+
+    announce("efla_chunked_scan_hip")
+    H, d, n = 3, 16, 6
+    rng = np.random.default_rng(5)
+    host = [oracle.f32_to_bf16(rng.standard_normal((H, d, d)).astype(np.float32))
+            for _ in range(n)]
+    dev = [_u16_to_dev(h) for h in host]
+    efla_chunked_scan(dev, H, d)
+    assert oracle.r_chunked_scan(host, H, d) == 0
+    torch.cuda.synchronize()
+    for i in range(n):
+        assert np.array_equal(_dev_to_u16(dev[i]), host[i]), i
+
+
+def test_forward_state_carry_equals_one_call(oracle):
+    # Two calls on halves of the sequence with the state carried in place
+    # equal one call over the whole sequence (the ABI's in/out state).
+    from ceo_amd.efla import efla_forward
+
+    announce("efla_forward_hip state carry")
+    B, T, H, d = 1, 128, 2, 64
+    k, v, _, s0 = _inputs(oracle, 700, B, T, H, d, 0.0)
+    kd, vd = _u16_to_dev(k), _u16_to_dev(v)
+    st1 = _u16_to_dev(s0)
+    o_full = efla_forward(kd, vd, st1, 0.5)
+    st2 = _u16_to_dev(s0)
+    o_a = efla_forward(kd[:, :64].contiguous(), vd[:, :64].contiguous(), st2, 0.5)
+    o_b = efla_forward(kd[:, 64:].contiguous(), vd[:, 64:].contiguous(), st2, 0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(torch.cat([o_a, o_b], 1), o_full)
+    assert torch.equal(st1, st2)

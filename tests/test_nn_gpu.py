@@ -1,0 +1,114 @@
+"""LayerNorm and GEMM kernels on the GPU against the oracle / an fp64 reference."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import announce, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("rows,D,bias", [(64, 1024, True), (37, 512, False), (16, 4096, True),
+                                         (9, 1000, True), (5, 96, False)])
+def test_layernorm_forward(oracle, rows, D, bias):
+    from ceo_amd.nn import layernorm_forward
+
+    announce(f"layernorm_forward rows={rows} D={D} bias={bias}")
+    rng = np.random.default_rng(rows + D)
+    x = _bf(rng.standard_normal((rows, D)) * 2 + 0.5)
+    w = _bf(1 + 0.1 * rng.standard_normal(D))
+    b = _bf(0.1 * rng.standard_normal(D)) if bias else None
+    y, mean, rstd = layernorm_forward(x.cuda(), w.cuda(), None if b is None else b.cuda(),
+                                      1e-5, save_stats=True)
+    torch.cuda.synchronize()
+    ry, rm, rr = oracle.layernorm_fwd(x.float().numpy(), w.float().numpy(),
+                                      None if b is None else b.float().numpy(), 1e-5)
+    e = rel_l2(y, ry)
+    print(f"  rel-L2 y={e:.2e}", flush=True)
+    assert e <= 1e-2
+    assert rel_l2(mean, rm) <= 1e-5 and rel_l2(rstd, rr) <= 1e-5
+    # invariant: with w = 1, b = 0 each row has mean 0 and variance 1
+    y1 = layernorm_forward(x.cuda(), torch.ones(D, dtype=torch.bfloat16, device="cuda"))
+    y1 = y1.float().cpu().numpy()
+    assert np.abs(y1.mean(1)).max() < 2e-2 and np.abs(y1.var(1) - 1).max() < 3e-2
+
+
+@pytest.mark.parametrize("rows,D", [(64, 1024), (50, 96)])
+def test_layernorm_backward(oracle, rows, D):
+    from ceo_amd.nn import layernorm_backward, layernorm_forward
+
+    announce(f"layernorm_backward rows={rows} D={D}")
+    rng = np.random.default_rng(7)
+    x = _bf(rng.standard_normal((rows, D)))
+    w = _bf(1 + 0.1 * rng.standard_normal(D))
+    dy = _bf(rng.standard_normal((rows, D)))
+    _, mean, rstd = layernorm_forward(x.cuda(), w.cuda(), None, 1e-5, save_stats=True)
+    dx, dw, db = layernorm_backward(dy.cuda(), x.cuda(), w.cuda(), mean, rstd)
+    torch.cuda.synchronize()
+    _, rm, rr = oracle.layernorm_fwd(x.float().numpy(), w.float().numpy(), None, 1e-5)
+    rdx, rdw, rdb = oracle.layernorm_bwd(dy.float().numpy(), x.float().numpy(),
+                                         w.float().numpy(), rm, rr)
+    errs = (rel_l2(dx, rdx), rel_l2(dw, rdw), rel_l2(db, rdb))
+    print("  rel-L2 dx,dw,db:", errs, flush=True)
+    assert errs[0] <= 1e-2 and errs[1] <= 1e-4 and errs[2] <= 1e-5
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (1, 64, 8), (300, 1024, 260)])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+def test_gemm_forward(m, k, n, dt):
+    from ceo_amd.nn import gemm_forward
+
+    announce(f"gemm_forward {m}x{k}x{n} {dt}")
+    g = torch.Generator().manual_seed(m * 7 + n)
+    a = torch.randn(m, k, generator=g).to(dt)
+    b = torch.randn(k, n, generator=g).to(dt)
+    bias = torch.randn(n, generator=g).to(dt)
+    c = gemm_forward(a.cuda(), b.cuda(), bias.cuda())
+    torch.cuda.synchronize()
+    ref = a.double() @ b.double() + bias.double()
+    e = rel_l2(c, ref.numpy())
+    print(f"  rel-L2={e:.2e}", flush=True)
+    assert e <= (1e-5 if dt == torch.float32 else 1e-2)
+
+
+def test_gemm_forward_mixed_dtypes():
+    from ceo_amd.nn import gemm_forward
+
+    announce("gemm_forward mixed")
+    a = torch.randn(70, 48).to(torch.bfloat16)
+    b = torch.randn(48, 90)
+    c = gemm_forward(a.cuda(), b.cuda(), None, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_l2(c, (a.double() @ b.double()).numpy()) <= 1e-5
+
+
+def test_gemm_k0_gives_bias():
+    from ceo_amd.nn import gemm_forward
+
+    announce("gemm_forward k=0")
+    a = torch.empty(5, 0, dtype=torch.bfloat16, device="cuda")
+    b = torch.empty(0, 7, dtype=torch.bfloat16, device="cuda")
+    bias = torch.arange(7, dtype=torch.bfloat16, device="cuda")
+    c = gemm_forward(a, b, bias)
+    torch.cuda.synchronize()
+    assert torch.equal(c, bias.expand(5, 7))
+
+
+@pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (513, 200, 129)])
+def test_gemm_backward(m, k, n):
+    from ceo_amd.nn import gemm_backward
+
+    announce(f"gemm_backward {m}x{k}x{n}")
+    g = torch.Generator().manual_seed(m + k + n)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    b = torch.randn(k, n, generator=g).to(torch.bfloat16)
+    dc = torch.randn(m, n, generator=g).to(torch.bfloat16)
+    da, db, dbias = gemm_backward(dc.cuda(), a.cuda(), b.cuda(), need_bias=True)
+    torch.cuda.synchronize()
+    assert rel_l2(da, (dc.double() @ b.double().T).numpy()) <= 1e-2
+    assert rel_l2(db, (a.double().T @ dc.double()).numpy()) <= 1e-2
+    assert rel_l2(dbias, dc.double().sum(0).numpy()) <= 1e-2
