@@ -1,0 +1,310 @@
+"""EFLA fwd+bwd throughput on one MI355X (the headline benchmark).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg2|cfg5]
+                    [--no-cpu] [--cpu-budget SECONDS]
+
+A step is one chunked EFLA forward plus one backward (the backward recomputes
+the chunk states; nothing is carried over from the forward) over one batch of
+synthetic inputs already resident in HBM.  Default workload: configs[2] of the
+benchmark definition, B=4, T=8192, H=32, d_k=d_v=128, chunk 64, bf16 storage
+with fp32 accumulation.  W untimed steps, then K timed steps bracketed by
+torch.cuda.synchronize() and hipEvents on the launch stream.
+
+Prints ONE JSON line with the metric, the per-kernel timing from the library's
+own launch events (recorded on the launch stream during the timed steps), the
+roofline of the dominant kernel and the step, and a CPU baseline: the scalar
+fp32 restatement of the same recurrence (oracle/, OpenMP over (sequence,
+head)) timed on a bounded sample of the same workload on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+C = 64  # chunk length
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+PEAK_HBM_GBS = 8000.0
+
+CONFIGS = {
+    # name: (B, T, H, K, V, dtype, fwd+bwd?, varlen?)
+    "cfg3": dict(B=4, T=8192, H=32, K=128, V=128, dtype="bf16", bwd=True, varlen=False),
+    "cfg2": dict(B=8, T=2048, H=16, K=128, V=128, dtype="bf16", bwd=False, varlen=False),
+    "cfg5": dict(B=1, T=65536, H=16, K=128, V=256, dtype="bf16", bwd=True, varlen=True),
+}
+
+
+# ---------------------------------------------------------------------------
+# FLOP model (algorithmic; recompute is not counted)
+# ---------------------------------------------------------------------------
+def f_fwd_per_token_head(K: int, V: int, c: int = C) -> float:
+    """C(6K + 4V) + 6KV + (2/3)C^2 per (token, head): per chunk the products
+    KK^T, W = T(bK), U = T(bV), QK^T (2C^2K each but U, 2C^2V), P Vn (2C^2V),
+    WS, QS, K^T Vn (2CKV each) and the UT solve (2/3)C^3."""
+    return c * (6 * K + 4 * V) + 6 * K * V + (2.0 / 3.0) * c * c
+
+
+def kernel_flops_per_chunk(K: int, V: int, c: int = C) -> dict:
+    """Algorithmic FLOPs of each library kernel per (chunk, head).  The
+    backward's re-run of prep and the state scan is recompute (0)."""
+    c2, c3, ckv = c * c, c ** 3, c * K * V
+    return {
+        "efla_q_fwd_prep": 4 * c2 * K + 2 * c2 * V + (2.0 / 3.0) * c3,
+        "efla_q_fwd_state": 4 * ckv,
+        "efla_q_fwd_o": 2 * c2 * K + 2 * c2 * V + 2 * ckv,
+        "efla_q_bwd_re_prep": 0.0,
+        "efla_q_bwd_re_state": 0.0,
+        "efla_q_bwd_dvloc": 2 * c2 * K + 2 * c2 * V,
+        "efla_q_bwd_state": 6 * ckv,
+        "efla_q_bwd_dqkw": 4 * c2 * K + 2 * c2 * V + 6 * ckv,
+        "efla_q_bwd_wy": 6 * c2 * K + 4 * c2 * V + 4 * c3,
+    }
+
+
+def io_bytes(ntok: int, H: int, K: int, V: int, bwd: bool, esize: int = 2) -> float:
+    """Algorithmic HBM bytes: fwd reads q, k, v, beta and writes o; bwd reads
+    q, k, v, beta, dO and writes dq, dk, dv, dbeta."""
+    per_tok = H * (2 * K + 2 * V + 1) * esize  # fwd: q k (K each) v o (V each) beta
+    if bwd:
+        per_tok += H * (2 * K + V + 1 + V + 2 * K + V + 1) * esize
+    return float(ntok) * per_tok
+
+
+# ---------------------------------------------------------------------------
+# inputs
+# ---------------------------------------------------------------------------
+def varlen_lengths(total: int, seed: int):
+    """Log-uniform lengths in [64, 8192], the last one truncated to fill `total`."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    lens = []
+    while sum(lens) < total:
+        lens.append(int(math.floor(math.exp(rng.uniform(math.log(64), math.log(8192))))))
+    lens[-1] -= sum(lens) - total
+    return [x for x in lens if x > 0]
+
+
+def make_inputs(cfg: dict, seed: int, device):
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    B, T, H, K, V = cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"]
+    dt = torch.bfloat16 if cfg["dtype"] == "bf16" else torch.float32
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
+
+    q = randn(B, T, H, K)
+    k = randn(B, T, H, K)
+    k = k / k.norm(dim=-1, keepdim=True)
+    v = randn(B, T, H, V)
+    beta = torch.sigmoid(randn(B, T, H))
+    do = randn(B, T, H, V)
+    out = {n: t.to(dt).contiguous() for n, t in
+           (("q", q), ("k", k), ("v", v), ("beta", beta), ("do", do))}
+    out["cu"] = None
+    if cfg["varlen"]:
+        lens = varlen_lengths(B * T, seed)
+        cu = [0]
+        for x in lens:
+            cu.append(cu[-1] + x)
+        out["cu"] = torch.tensor(cu, dtype=torch.int32, device=device)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline
+# ---------------------------------------------------------------------------
+def cpu_baseline(cfg: dict, seed: int, budget_s: float) -> dict:
+    """Scalar fp32 restatement of the same recurrence (oracle/efla_q_body.h),
+    OpenMP over (sequence, head), on whole sequences of the workload's shape
+    until `budget_s` is spent (at least one).  Scaled to the metric's unit:
+    workload tokens (all H heads) per second."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle  # the checker / baseline only; never on the measured GPU path
+
+    oracle.lib()
+    T, H, K, V = cfg["T"], cfg["H"], cfg["K"], cfg["V"]
+    if cfg["varlen"]:
+        T = 8192  # the longest sequence length the varlen draw allows
+    n_seq = cfg["B"] if not cfg["varlen"] else max(1, cfg["B"] * cfg["T"] // T)
+    done, elapsed = 0, 0.0
+    for s in range(n_seq):
+        x = oracle.make_efla_inputs(seed + s, T, H, K, V, bf16=cfg["dtype"] == "bf16",
+                                    with_do=cfg["bwd"])
+        t0 = time.perf_counter()
+        oracle.q_forward(x["q"], x["k"], x["v"], x["beta"], T=T, dtype=np.float32)
+        if cfg["bwd"]:
+            oracle.q_backward(x["q"], x["k"], x["v"], x["beta"], x["do"], T=T,
+                              dtype=np.float32)
+        elapsed += time.perf_counter() - t0
+        done += 1
+        print(f"[bench] cpu baseline: sequence {done}/{n_seq} ({elapsed:.1f} s)",
+              file=sys.stderr, flush=True)
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": done * T / elapsed,
+        "unit": "tokens/s",
+        "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": f"{done} of {n_seq} sequences of T={T}, H={H}, d_k={K}, d_v={V} "
+                  f"({'fwd+bwd' if cfg['bwd'] else 'fwd'}, fp32 math on "
+                  f"{'bf16-rounded ' if cfg['dtype'] == 'bf16' else ''}inputs), "
+                  f"{elapsed:.2f} s",
+    }
+
+
+# ---------------------------------------------------------------------------
+# main
+# ---------------------------------------------------------------------------
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="seconds of CPU-baseline work (whole sequences, at least one)")
+    ap.add_argument("--seed", type=int, default=0xEF1A0002)
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU: the EFLA path here has no multi-GPU mode "
+              f"(--gpus {args.gpus}, WORLD_SIZE={world} requested)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from ceo_amd import efla, runtime
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = CONFIGS[args.config]
+    B, T, H, K, V = cfg["B"], cfg["T"], cfg["H"], cfg["K"], cfg["V"]
+    ntok = B * T
+    x = make_inputs(cfg, args.seed, dev)
+    cu = x["cu"]
+    print(f"[bench] {args.config}: B={B} T={T} H={H} K={K} V={V} {cfg['dtype']} "
+          f"{'fwd+bwd' if cfg['bwd'] else 'fwd'}{' varlen' if cu is not None else ''}",
+          file=sys.stderr, flush=True)
+
+    def step():
+        o, _ = efla.chunk_efla_fwd(x["q"], x["k"], x["v"], x["beta"], cu_seqlens=cu)
+        if cfg["bwd"]:
+            efla.chunk_efla_bwd(x["q"], x["k"], x["v"], x["beta"], x["do"], cu_seqlens=cu)
+        return o
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
+
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    prof = runtime.Profiler()
+    torch.cuda.synchronize()
+    with prof:
+        ev0.record(stream)
+        for _ in range(args.steps):
+            step()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_total = ev0.elapsed_time(ev1)
+    ms_step = ms_total / args.steps
+    kern = prof.results()
+    print(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step", file=sys.stderr,
+          flush=True)
+
+    # FLOPs / bytes
+    if cu is not None:
+        lens = (cu[1:] - cu[:-1]).tolist()
+        n_chunks = sum((L + C - 1) // C for L in lens)
+        fwd_flops = float(sum(lens)) * H * f_fwd_per_token_head(K, V)
+    else:
+        n_chunks = B * ((T + C - 1) // C)
+        fwd_flops = float(ntok) * H * f_fwd_per_token_head(K, V)
+    step_flops = fwd_flops * (3 if cfg["bwd"] else 1)
+    per_chunk = kernel_flops_per_chunk(K, V)
+    kernels = {}
+    for name, (launches, tot_ms) in sorted(kern.items(), key=lambda kv: -kv[1][1]):
+        avg_ms = tot_ms / max(launches, 1)
+        fl = per_chunk.get(name, 0.0) * n_chunks * H
+        kernels[name] = {
+            "launches": launches, "avg_ms": round(avg_ms, 4),
+            "share": round(tot_ms / max(ms_total, 1e-9), 4),
+            "tflops": round(fl / (avg_ms * 1e-3) / 1e12, 2) if fl else None,
+        }
+    dom = max(kern.items(), key=lambda kv: kv[1][1])[0] if kern else None
+    roof = None
+    if dom is not None:
+        launches, tot_ms = kern[dom]
+        avg_ms = tot_ms / launches
+        fl = per_chunk.get(dom, 0.0) * n_chunks * H
+        ach = fl / (avg_ms * 1e-3) / 1e12
+        roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "avg_ms": round(avg_ms, 4),
+                "flops_per_launch": fl}
+    step_tflops = step_flops / (ms_step * 1e-3) / 1e12
+    io = io_bytes(ntok, H, K, V, cfg["bwd"])
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(cfg, args.seed, args.cpu_budget)
+
+    info = runtime.device_info(0)
+    tokens_per_s = ntok / (ms_step * 1e-3)
+    line = {
+        "metric": "EFLA fwd+bwd tokens/s at H=32,d=128,T=8192 bf16; % bf16 MFMA peak"
+                  if args.config == "cfg3" else f"EFLA {args.config} tokens/s",
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": cfg["dtype"],
+        "data": "synthetic (seeded torch N(0,1) q/k/v/dO, k L2-normalised, "
+                "beta=sigmoid(N(0,1)))",
+        "config": {"workload": f"{args.config}: EFLA {'fwd+bwd' if cfg['bwd'] else 'fwd'} "
+                               f"B={B} T={T} H={H} d_k={K} d_v={V} chunk={C} "
+                               f"{cfg['dtype']}{' varlen' if cu is not None else ''}",
+                   "tokens_per_step": ntok, "parallelism": "single GPU"},
+        "pct_bf16_mfma_peak": round(100 * step_tflops / PEAK_BF16_TFLOPS, 3),
+        "step_tflops": round(step_tflops, 2),
+        "step_flops": step_flops,
+        "step_io_gbs": round(io / (ms_step * 1e-3) / 1e9, 1),
+        "roofline": roof,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+        "device": {"arch": info["arch"], "cus": info["compute_units"],
+                   "clock_mhz": info["clock_khz"] // 1000},
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -948,9 +948,10 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
     EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, st));
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
-    EFLA_LAUNCH("efla_q_fwd_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH), st,
-                k, v, beta, si, H, w.bco, w.W, w.U);
-    EFLA_LAUNCH("efla_q_fwd_state", (fwd_state_kernel<T, K, V, VS, false>),
+    // forward recompute: W, U, chunk states and Vn (nothing is kept from the forward)
+    EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH),
+                st, k, v, beta, si, H, w.bco, w.W, w.U);
+    EFLA_LAUNCH("efla_q_bwd_re_state", (fwd_state_kernel<T, K, V, VS, false>),
                 dim3(p.N * H, V / VS), dim3(NTH), st, k, w.W, w.U, si, H, S0,
                 (float*)nullptr, w.h, w.Vn);
     EFLA_LAUNCH("efla_q_bwd_dvloc", (bwd_dvloc_kernel<T, K, V, VO>), dim3(p.slots, H, V / VO),

@@ -87,15 +87,27 @@ def test_gemm_forward_mixed_dtypes():
 
 
 def test_gemm_k0_gives_bias():
-    from ceo_amd.nn import gemm_forward
-
     announce("gemm_forward k=0")
-    a = torch.empty(5, 0, dtype=torch.bfloat16, device="cuda")
-    b = torch.empty(0, 7, dtype=torch.bfloat16, device="cuda")
-    bias = torch.arange(7, dtype=torch.bfloat16, device="cuda")
-    c = gemm_forward(a, b, bias)
+    import ctypes
+
+    from ceo_amd._lib import lib
+
+    # gemm.cu:316-318 rejects null a/b even when k == 0 (torch hands out null
+    # data pointers for empty tensors), so the C ABI gets real allocations
+    m, n = 5, 7
+    buf = torch.empty(8, dtype=torch.bfloat16, device="cuda")
+    bias = torch.arange(n, dtype=torch.bfloat16, device="cuda")
+    c = torch.full((m, n), 3.0, dtype=torch.bfloat16, device="cuda")
+    P = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib().gemm_forward_hip(P(buf), P(buf), P(bias), P(c), m, 0, n, 14, 14, 14, st) == 0
     torch.cuda.synchronize()
-    assert torch.equal(c, bias.expand(5, 7))
+    assert torch.equal(c, bias.expand(m, n))
+    assert lib().gemm_forward_hip(P(buf), P(buf), None, P(c), m, 0, n, 14, 14, 14, st) == 0
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(c) == 0
+    # null operands: InvalidValue (1), as the reference
+    assert lib().gemm_forward_hip(None, P(buf), None, P(c), m, 0, n, 14, 14, 14, st) == 1
 
 
 @pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (513, 200, 129)])
