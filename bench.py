@@ -59,6 +59,8 @@ def kernel_flops_per_chunk(K: int, V: int, c: int = C) -> dict:
         "efla_q_fwd_prep": 4 * c2 * K + 2 * c2 * V + (2.0 / 3.0) * c3,
         "efla_q_fwd_state": 4 * ckv,
         "efla_q_fwd_o": 2 * c2 * K + 2 * c2 * V + 2 * ckv,
+        # fused state scan + output (WS, K^T Vn, QS, QK^T, P Vn)
+        "efla_q_fwd_scan": 6 * ckv + 2 * c2 * K + 2 * c2 * V,
         "efla_q_bwd_re_prep": 0.0,
         "efla_q_bwd_re_state": 0.0,
         "efla_q_bwd_dvloc": 2 * c2 * K + 2 * c2 * V,

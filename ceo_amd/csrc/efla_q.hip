@@ -23,11 +23,12 @@
 #include "common.hpp"
 #include "efla_coeff.hpp"
 #include "internal.hpp"
+#include "efla_q_seq.hpp"
+#include "efla_q_fast.hpp"
 
 namespace efla {
 namespace q {
 
-constexpr int BT = 64;    // chunk length
 constexpr int NTH = 256;  // threads per workgroup
 constexpr int NW = 4;     // waves per workgroup
 constexpr int LDF = 68;   // row stride of the 64x64 fp32 LDS matrices
@@ -35,54 +36,6 @@ constexpr int LDF = 68;   // row stride of the 64x64 fp32 LDS matrices
 template <typename T>
 constexpr int pad() {
     return 16 / (int)sizeof(T);
-}
-
-// Where the tokens of each sequence live.  Without cu_seqlens there are N
-// sequences of T tokens back to back; with it, `cu` is a sanitised copy of
-// cu_seqlens and `coff[i]` the index of sequence i's first chunk.
-struct SeqInfo {
-    const int32_t* cu;
-    const int32_t* coff;
-    int N;
-    long T;
-    int nt;  // chunks per sequence (fixed-length case)
-};
-
-__device__ __forceinline__ void seq_bounds(const SeqInfo& s, int seq, long& bos, long& len,
-                                           int& slot0) {
-    if (s.cu == nullptr) {
-        bos = (long)seq * s.T;
-        len = s.T;
-        slot0 = seq * s.nt;
-    } else {
-        bos = s.cu[seq];
-        len = (long)s.cu[seq + 1] - bos;
-        slot0 = s.coff[seq];
-    }
-}
-
-// Chunk slot -> first token and length; false for slots past the last chunk.
-__device__ __forceinline__ bool locate_chunk(const SeqInfo& s, int slot, long& bos, int& len) {
-    if (s.cu == nullptr) {
-        const int seq = slot / s.nt, n = slot - seq * s.nt;
-        if (seq >= s.N) return false;
-        bos = (long)seq * s.T + (long)n * BT;
-        const long rem = s.T - (long)n * BT;
-        len = (int)(rem < BT ? rem : BT);
-        return true;
-    }
-    if (slot >= s.coff[s.N]) return false;
-    int lo = 0, hi = s.N - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s.coff[mid] <= slot) lo = mid;
-        else hi = mid - 1;
-    }
-    const int n = slot - s.coff[lo];
-    bos = (long)s.cu[lo] + (long)n * BT;
-    const long rem = (long)s.cu[lo + 1] - bos;
-    len = (int)(rem < BT ? rem : BT);
-    return true;
 }
 
 // Sanitise cu_seqlens into [0, ntok] (non-decreasing) and build chunk offsets.
@@ -930,6 +883,14 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
     EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, st));
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
+    if constexpr (__is_same(T, bf16)) {
+        EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K, V>), dim3(p.slots, H),
+                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U);
+        EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
+                    dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, w.W, w.U, si, H, S0,
+                    ST, o);
+        return (int)hipPeekAtLastError();
+    }
     EFLA_LAUNCH("efla_q_fwd_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH), st,
                 k, v, beta, si, H, w.bco, w.W, w.U);
     EFLA_LAUNCH("efla_q_fwd_state", (fwd_state_kernel<T, K, V, VS, true>),
@@ -949,8 +910,13 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
     // forward recompute: W, U, chunk states and Vn (nothing is kept from the forward)
-    EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH),
-                st, k, v, beta, si, H, w.bco, w.W, w.U);
+    if constexpr (__is_same(T, bf16)) {
+        EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(p.slots, H),
+                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U);
+    } else {
+        EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H),
+                    dim3(NTH), st, k, v, beta, si, H, w.bco, w.W, w.U);
+    }
     EFLA_LAUNCH("efla_q_bwd_re_state", (fwd_state_kernel<T, K, V, VS, false>),
                 dim3(p.N * H, V / VS), dim3(NTH), st, k, w.W, w.U, si, H, S0,
                 (float*)nullptr, w.h, w.Vn);

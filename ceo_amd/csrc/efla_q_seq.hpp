@@ -1,0 +1,60 @@
+// Sequence / chunk bookkeeping shared by the chunked EFLA kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace efla {
+namespace q {
+
+constexpr int BT = 64;  // chunk length
+
+// Where the tokens of each sequence live.  Without cu_seqlens there are N
+// sequences of T tokens back to back; with it, `cu` is a sanitised copy of
+// cu_seqlens and `coff[i]` the index of sequence i's first chunk.
+struct SeqInfo {
+    const int32_t* cu;
+    const int32_t* coff;
+    int N;
+    long T;
+    int nt;  // chunks per sequence (fixed-length case)
+};
+
+__device__ __forceinline__ void seq_bounds(const SeqInfo& s, int seq, long& bos, long& len,
+                                           int& slot0) {
+    if (s.cu == nullptr) {
+        bos = (long)seq * s.T;
+        len = s.T;
+        slot0 = seq * s.nt;
+    } else {
+        bos = s.cu[seq];
+        len = (long)s.cu[seq + 1] - bos;
+        slot0 = s.coff[seq];
+    }
+}
+
+// Chunk slot -> first token and length; false for slots past the last chunk.
+__device__ __forceinline__ bool locate_chunk(const SeqInfo& s, int slot, long& bos, int& len) {
+    if (s.cu == nullptr) {
+        const int seq = slot / s.nt, n = slot - seq * s.nt;
+        if (seq >= s.N) return false;
+        bos = (long)seq * s.T + (long)n * BT;
+        const long rem = s.T - (long)n * BT;
+        len = (int)(rem < BT ? rem : BT);
+        return true;
+    }
+    if (slot >= s.coff[s.N]) return false;
+    int lo = 0, hi = s.N - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s.coff[mid] <= slot) lo = mid;
+        else hi = mid - 1;
+    }
+    const int n = slot - s.coff[lo];
+    bos = (long)s.cu[lo] + (long)n * BT;
+    const long rem = (long)s.cu[lo + 1] - bos;
+    len = (int)(rem < BT ? rem : BT);
+    return true;
+}
+
+}  // namespace q
+}  // namespace efla

@@ -72,6 +72,13 @@ def test_bf16_short_sequences(oracle, T):
     _case(oracle, 30 + T, 3, T, 2, 64, 64, torch.bfloat16, s0=True, dst=True)
 
 
+@pytest.mark.parametrize("K,V", [(128, 128), (128, 256)])
+def test_bf16_long_sequence(oracle, K, V):
+    # full benchmark sequence length: rounding must not accumulate over 128
+    # chunks of the state recurrence
+    _case(oracle, 0xEF1A0002 + V, 1, 8192, 2, K, V, torch.bfloat16, s0=True, dst=True)
+
+
 def test_varlen_bf16(oracle):
     lens = [1, 63, 64, 65, 130, 7, 0, 200]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
