@@ -67,6 +67,9 @@ def kernel_flops_per_chunk(K: int, V: int, c: int = C) -> dict:
         "efla_q_bwd_state": 6 * ckv,
         "efla_q_bwd_dqkw": 4 * c2 * K + 2 * c2 * V + 6 * ckv,
         "efla_q_bwd_wy": 6 * c2 * K + 4 * c2 * V + 4 * c3,
+        # per-chunk gradients: dVn = P^T dO (+ K dh), Dm, dq, dk', dW, WY backward
+        # (dvloc + dqkw + wy above, excluding the recomputed KK^T, T, P, R, Vn)
+        "efla_q_bwd_grad": 12 * c2 * K + 6 * c2 * V + 6 * ckv + 4 * c3,
     }
 
 

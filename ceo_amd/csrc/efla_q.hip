@@ -25,6 +25,7 @@
 #include "internal.hpp"
 #include "efla_q_seq.hpp"
 #include "efla_q_fast.hpp"
+#include "efla_q_bwd.hpp"
 
 namespace efla {
 namespace q {
@@ -911,8 +912,16 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const int H = p.H;
     // forward recompute: W, U, chunk states and Vn (nothing is kept from the forward)
     if constexpr (__is_same(T, bf16)) {
+        const dim3 scan_grid(p.N * H * (V / fast::VS));
         EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(p.slots, H),
                     dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U);
+        EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
+                    dim3(fast::NT), st, k, w.W, w.U, si, H, S0, w.h);
+        EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V>), scan_grid,
+                    dim3(fast::NT), st, q, k, w.W, dO, si, H, dST, dS0, w.dh);
+        EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V>), dim3(p.slots, H),
+                    dim3(fast::NT), st, q, k, v, beta, dO, w.h, w.dh, si, H, dq, dk, dv, dbeta);
+        return (int)hipPeekAtLastError();
     } else {
         EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H),
                     dim3(NTH), st, k, v, beta, si, H, w.bco, w.W, w.U);
