@@ -52,24 +52,27 @@ def f_fwd_per_token_head(K: int, V: int, c: int = C) -> float:
 
 
 def kernel_flops_per_chunk(K: int, V: int, c: int = C) -> dict:
-    """Algorithmic FLOPs of each library kernel per (chunk, head).  The
-    backward's re-run of prep and the state scan is recompute (0)."""
+    """Algorithmic FLOPs of each library kernel per (chunk, head), assigned so
+    that the forward kernels sum to F_fwd and the backward ones to 2 F_fwd
+    (the backward's re-run of prep and of the state scan is recompute: 0)."""
     c2, c3, ckv = c * c, c ** 3, c * K * V
     return {
+        # forward: WY prep (K K^T, UT solve, W, U) and the fused scan + output
+        # (W S, K^T Vn, Q S, Q K^T, P Vn)
         "efla_q_fwd_prep": 4 * c2 * K + 2 * c2 * V + (2.0 / 3.0) * c3,
-        "efla_q_fwd_state": 4 * ckv,
-        "efla_q_fwd_o": 2 * c2 * K + 2 * c2 * V + 2 * ckv,
-        # fused state scan + output (WS, K^T Vn, QS, QK^T, P Vn)
         "efla_q_fwd_scan": 6 * ckv + 2 * c2 * K + 2 * c2 * V,
+        # backward: reverse scan (K dS, Q^T dO, W^T dVn, P^T dO) and the
+        # per-chunk gradients (the rest of 2 F_fwd)
         "efla_q_bwd_re_prep": 0.0,
         "efla_q_bwd_re_state": 0.0,
+        "efla_q_bwd_state": 6 * ckv + 2 * c2 * V,
+        "efla_q_bwd_grad": 12 * c2 * K + 6 * c2 * V + 6 * ckv + (4.0 / 3.0) * c3,
+        # fp32 path (generic kernels)
+        "efla_q_fwd_state": 4 * ckv,
+        "efla_q_fwd_o": 2 * c2 * K + 2 * c2 * V + 2 * ckv,
         "efla_q_bwd_dvloc": 2 * c2 * K + 2 * c2 * V,
-        "efla_q_bwd_state": 6 * ckv,
         "efla_q_bwd_dqkw": 4 * c2 * K + 2 * c2 * V + 6 * ckv,
         "efla_q_bwd_wy": 6 * c2 * K + 4 * c2 * V + 4 * c3,
-        # per-chunk gradients: dVn = P^T dO (+ K dh), Dm, dq, dk', dW, WY backward
-        # (dvloc + dqkw + wy above, excluding the recomputed KK^T, T, P, R, Vn)
-        "efla_q_bwd_grad": 12 * c2 * K + 6 * c2 * V + 6 * ckv + 4 * c3,
     }
 
 
@@ -172,6 +175,40 @@ def cpu_baseline(cfg: dict, seed: int, budget_s: float) -> dict:
 
 
 # ---------------------------------------------------------------------------
+# HBM traffic of the dominant kernel (from committed rocprofv3 counter runs)
+# ---------------------------------------------------------------------------
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def copy_calibration(mib: int) -> int:
+    """A plain copy of known size: FETCH_SIZE and WRITE_SIZE of its kernel
+    divided into the true byte count give the counters' scale factors."""
+    import torch
+
+    n = mib << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n}), flush=True)
+    return 0
+
+
+def measured_traffic(config: str, kernel: str):
+    """HBM bytes per launch of `kernel` recorded in profiles/traffic.json by the
+    FETCH_SIZE / WRITE_SIZE runs (already scaled by the copy calibration), or
+    None when that file does not cover this kernel and workload."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+        k = rec[config]["kernels"][kernel]
+        return float(k["fetch_bytes"]) + float(k["write_bytes"])
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
+# ---------------------------------------------------------------------------
 # main
 # ---------------------------------------------------------------------------
 def main() -> int:
@@ -184,7 +221,13 @@ def main() -> int:
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (whole sequences, at least one)")
     ap.add_argument("--seed", type=int, default=0xEF1A0002)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB five times "
+                         "(the known-size kernel that calibrates rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE readings) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -266,7 +309,8 @@ def main() -> int:
         ach = fl / (avg_ms * 1e-3) / 1e12
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                "traffic": measured_traffic(args.config, dom),
                 "avg_ms": round(avg_ms, 4),
                 "flops_per_launch": fl}
     step_tflops = step_flops / (ms_step * 1e-3) / 1e12

@@ -817,6 +817,7 @@ struct BwdWs {
     float* bco;
     T *W, *U, *h, *Vn, *dvloc, *dh, *dVn, *dW;
     float* dKp;
+    T* Tc;  // per-chunk bf16 T of the WY prep (bf16 path)
 };
 
 template <typename T>
@@ -850,6 +851,7 @@ static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
     w.dVn = c.take<T>((size_t)p.ntok * p.H * p.V);
     w.dW = c.take<T>((size_t)p.ntok * p.H * p.K);
     w.dKp = c.take<float>((size_t)p.ntok * p.H * p.K);
+    w.Tc = c.take<T>((size_t)p.slots * p.H * 64 * 64);
     if (out) *out = w;
     return c.off + 256;
 }
@@ -886,7 +888,7 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const int H = p.H;
     if constexpr (__is_same(T, bf16)) {
         EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K, V>), dim3(p.slots, H),
-                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U);
+                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, (bf16*)nullptr);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
                     dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, w.W, w.U, si, H, S0,
                     ST, o);
@@ -914,13 +916,14 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
     if constexpr (__is_same(T, bf16)) {
         const dim3 scan_grid(p.N * H * (V / fast::VS));
         EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(p.slots, H),
-                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U);
+                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, w.Tc);
         EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
                     dim3(fast::NT), st, k, w.W, w.U, si, H, S0, w.h);
         EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V>), scan_grid,
                     dim3(fast::NT), st, q, k, w.W, dO, si, H, dST, dS0, w.dh);
         EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V>), dim3(p.slots, H),
-                    dim3(fast::NT), st, q, k, v, beta, dO, w.h, w.dh, si, H, dq, dk, dv, dbeta);
+                    dim3(fast::NT), st, q, k, v, beta, dO, (const bf16*)w.Tc, w.h, w.dh, si,
+                    H, dq, dk, dv, dbeta);
         return (int)hipPeekAtLastError();
     } else {
         EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H),

@@ -262,14 +262,9 @@ struct GradSmem {
     bf16 Qs[64 * ldb<K>()];
     bf16 Ks[64 * ldb<K>()];
     bf16 Ps[64 * LD64];  // P[t][t'] (t' <= t)
-    bf16 Tb[64 * LD64];  // bf16(T)[t][t'] (t' <= t)
-    float b[64], dcl[64], dcb[64], db[64];
+    bf16 Tb[64 * LD64];  // bf16(T)[t][t'] (t' <= t), from the WY prep
+    float lam[64], b[64], dcl[64], dcb[64];
     union {
-        struct {  // WY recompute
-            float G[64 * LDF];
-            float T[64 * LDF];
-            float lam[64];
-        } a;
         struct {  // one 64-wide value slice
             bf16 V[64 * LD64];   // v[:, slice]; each wave's rows later hold D Y
             bf16 dO[64 * LD64];  // dO[:, slice]
@@ -290,9 +285,10 @@ struct GradSmem {
 template <int K, int V>
 __global__ void __launch_bounds__(NT) grad_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const bf16* __restrict__ beta, const bf16* __restrict__ dO, const bf16* __restrict__ hist,
-    const bf16* __restrict__ dhist, SeqInfo si, int H, bf16* __restrict__ dq,
-    bf16* __restrict__ dk, bf16* __restrict__ dv, bf16* __restrict__ dbeta) {
+    const bf16* __restrict__ beta, const bf16* __restrict__ dO, const bf16* __restrict__ Tws,
+    const bf16* __restrict__ hist, const bf16* __restrict__ dhist, SeqInfo si, int H,
+    bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
+    bf16* __restrict__ dbeta) {
     constexpr int LDK = ldb<K>(), NS = V / VS;
     __shared__ __attribute__((aligned(16))) GradSmem<K> sm;
     const int slot = blockIdx.x, h = blockIdx.y;
@@ -303,110 +299,6 @@ __global__ void __launch_bounds__(NT) grad_kernel(
     const int t = 16 * w + r;  // this lane's token (column of the transposed tiles)
     const long chb = ((long)slot * H + h) * V * K;  // this chunk's h / dh block
 
-    // ---- WY recompute: b, G, T; P; bf16 T ----
-    {
-        mf::TileRegs<64, K, NT> rq, rk;
-        rq.load(q + (bos * H + h) * K, (long)H * K, len);
-        rk.load(k + (bos * H + h) * K, (long)H * K, len);
-        rq.store_rows(sm.Qs, LDK);
-        rk.store_rows(sm.Ks, LDK);
-#pragma unroll
-        for (int j = 0; j < rk.TPT; ++j) {
-            const float s = rk.row_sumsq(j);
-            if (rk.fg() == 0) sm.u.a.lam[rk.t0() + j] = s;
-        }
-        for (int i = threadIdx.x; i < 64 * LD64; i += NT) {
-            sm.Ps[i] = (bf16)0.f;
-            sm.Tb[i] = (bf16)0.f;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const int tt = threadIdx.x;
-        float c = 0.f, dcl = 0.f, dcb = 0.f;
-        if (tt < len) efla_coeff(sm.u.a.lam[tt], (float)beta[(bos + tt) * H + h], c, dcl, dcb);
-        sm.b[tt] = c;
-        sm.dcl[tt] = dcl;
-        sm.dcb[tt] = dcb;
-    }
-    for (int n = w; n < 10; n += 4) {
-        int I, J;
-        lower_tile(n, I, J);
-        floatx4 acc = zero4(), accp = zero4();
-#pragma unroll
-        for (int k0 = 0; k0 < K; k0 += 32) {
-            const bf16x8 kj = frag_nat(sm.Ks, LDK, 16 * J, k0);
-            acc = mma(frag_nat(sm.Ks, LDK, 16 * I, k0), kj, acc);
-            accp = mma(kj, frag_nat(sm.Qs, LDK, 16 * I, k0), accp);
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sm.u.a.G[(16 * I + 4 * g + i) * LDF + 16 * J + r] = acc[i];
-        const int tq = 16 * I + r, tk = 16 * J + 4 * g;
-        *reinterpret_cast<bf16x4*>(sm.Ps + tq * LD64 + tk) =
-            bf16x4{(bf16)(tk + 0 <= tq ? accp[0] : 0.f), (bf16)(tk + 1 <= tq ? accp[1] : 0.f),
-                   (bf16)(tk + 2 <= tq ? accp[2] : 0.f), (bf16)(tk + 3 <= tq ? accp[3] : 0.f)};
-    }
-    __syncthreads();
-    float* T = sm.u.a.T;
-    if (l < 16) {
-        const int base = 16 * w;
-        float x[16];
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float s = 0.f;
-#pragma unroll
-            for (int j = 0; j < i; ++j) s += sm.u.a.G[(base + i) * LDF + base + j] * x[j];
-            x[i] = (i == l ? 1.f : 0.f) - sm.b[base + i] * s;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) T[(base + i) * LDF + base + l] = x[i];
-    }
-    __syncthreads();
-    for (int d = 1; d < 4; ++d) {
-        if (w < 4 - d) {
-            const int I = w + d, J = w;
-            const float bi = sm.b[16 * I + r];
-            floatx4 y = zero4();
-            for (int m = 16 * J; m < 16 * I; m += 4)
-                y = mma_f32(bi * sm.u.a.G[(16 * I + r) * LDF + m + g], T[(m + g) * LDF + 16 * J + r], y);
-            floatx4 tt = zero4();
-#pragma unroll
-            for (int i = 0; i < 4; ++i) tt = mma_f32(T[(16 * I + r) * LDF + 16 * I + 4 * g + i], y[i], tt);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) T[(16 * I + 4 * g + i) * LDF + 16 * J + r] = -tt[i];
-        }
-        __syncthreads();
-    }
-    // B operand (line t, k = t') of T, and the bf16 copy of T
-    bf16x8 tfr[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int k0 = 32 * ks + 8 * g;
-        const floatx4 t0 = *reinterpret_cast<const floatx4*>(T + t * LDF + k0);
-        const floatx4 t1 = *reinterpret_cast<const floatx4*>(T + t * LDF + k0 + 4);
-        bf16x8 f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            f[s] = (bf16)((k0 + s <= t) ? t0[s] : 0.f);
-            f[4 + s] = (bf16)((k0 + 4 + s <= t) ? t1[s] : 0.f);
-        }
-        tfr[ks] = f;
-    }
-    for (int i = threadIdx.x; i < 64 * 64; i += NT) {
-        const int rr = i >> 6, cc = i & 63;
-        if (cc <= rr) sm.Tb[rr * LD64 + cc] = (bf16)T[rr * LDF + cc];
-    }
-    const float bt = sm.b[t];
-    const int nks = w >= 2 ? 1 : 0;  // first k-step (of 32) that reaches t'' >= t
-    __syncthreads();  // the value slices overwrite G / T from here
-
-    // ---- value slices ----
-    floatx4 dqa[K / 16], dka[K / 16], dma[4], dta[4];
-#pragma unroll
-    for (int fb = 0; fb < K / 16; ++fb) dqa[fb] = dka[fb] = zero4();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dma[j] = dta[j] = zero4();
-    float dbp = 0.f;
     mf::TileRegs<64, VS, NT> rv, rd;
     mf::TileRegs<64, K, NT> rh, rdh;
     auto prefetch = [&](int s) {
@@ -416,7 +308,58 @@ __global__ void __launch_bounds__(NT) grad_kernel(
         rh.load(hist + chb + (long)vv * K, K, 64);
         rdh.load(dhist + chb + (long)vv * K, K, 64);
     };
-    prefetch(0);
+    // ---- chunk setup: q, k, T, b, P ----
+    {
+        mf::TileRegs<64, K, NT> rq, rk;
+        mf::TileRegs<64, 64, NT> rt;
+        rq.load(q + (bos * H + h) * K, (long)H * K, len);
+        rk.load(k + (bos * H + h) * K, (long)H * K, len);
+        rt.load(Tws + ((long)slot * H + h) * 64 * 64, 64, 64);
+        prefetch(0);
+        rq.store_rows(sm.Qs, LDK);
+        rk.store_rows(sm.Ks, LDK);
+        rt.store_rows(sm.Tb, LD64);
+#pragma unroll
+        for (int j = 0; j < rk.TPT; ++j) {
+            const float s = rk.row_sumsq(j);
+            if (rk.fg() == 0) sm.lam[rk.t0() + j] = s;
+        }
+        for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.Ps[i] = (bf16)0.f;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int tt = threadIdx.x;
+        float c = 0.f, dcl = 0.f, dcb = 0.f;
+        if (tt < len) efla_coeff(sm.lam[tt], (float)beta[(bos + tt) * H + h], c, dcl, dcb);
+        sm.b[tt] = c;
+        sm.dcl[tt] = dcl;
+        sm.dcb[tt] = dcb;
+    }
+    for (int n = w; n < 10; n += 4) {
+        int I, J;
+        lower_tile(n, I, J);
+        floatx4 accp = zero4();
+#pragma unroll
+        for (int k0 = 0; k0 < K; k0 += 32)
+            accp = mma(frag_nat(sm.Ks, LDK, 16 * J, k0), frag_nat(sm.Qs, LDK, 16 * I, k0), accp);
+        const int tq = 16 * I + r, tk = 16 * J + 4 * g;
+        *reinterpret_cast<bf16x4*>(sm.Ps + tq * LD64 + tk) =
+            bf16x4{(bf16)(tk + 0 <= tq ? accp[0] : 0.f), (bf16)(tk + 1 <= tq ? accp[1] : 0.f),
+                   (bf16)(tk + 2 <= tq ? accp[2] : 0.f), (bf16)(tk + 3 <= tq ? accp[3] : 0.f)};
+    }
+    // B operand (line t, k = t') of T
+    const bf16x8 tfr[2] = {frag_nat(sm.Tb, LD64, 16 * w, 0), frag_nat(sm.Tb, LD64, 16 * w, 32)};
+    __syncthreads();
+    const float bt = sm.b[t];
+    const int nks = w >= 2 ? 1 : 0;  // first k-step (of 32) that reaches t'' >= t
+
+    // ---- value slices ----
+    floatx4 dqa[K / 16], dka[K / 16], dma[4], dta[4];
+#pragma unroll
+    for (int fb = 0; fb < K / 16; ++fb) dqa[fb] = dka[fb] = zero4();
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma[j] = dta[j] = zero4();
+    float dbp = 0.f;
     for (int s = 0; s < NS; ++s) {
         const int vv = s * VS;
         if (s > 0) __syncthreads();

@@ -69,7 +69,8 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
                                                   const bf16* __restrict__ v,
                                                   const bf16* __restrict__ beta, SeqInfo si,
                                                   int H, bf16* __restrict__ Wout,
-                                                  bf16* __restrict__ Uout) {
+                                                  bf16* __restrict__ Uout,
+                                                  bf16* __restrict__ Tout) {
     constexpr int LDK = ldb<K>(), LDV = ldb<V>();
     __shared__ __attribute__((aligned(16))) PrepSmem<K, V> sm;
     const int slot = blockIdx.x, h = blockIdx.y;
@@ -140,6 +141,19 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
             for (int i = 0; i < 4; ++i) T[(16 * I + 4 * g + i) * LDF + 16 * J + r] = -t[i];
         }
         __syncthreads();
+    }
+    // optional bf16 copy of T for the backward: [t][t'], zero above the diagonal
+    if (Tout) {
+        const int tr = threadIdx.x >> 2, c0 = 16 * (threadIdx.x & 3);
+        bf16x8 lo, hi;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            lo[c] = (bf16)(c0 + c <= tr ? T[tr * LDF + c0 + c] : 0.f);
+            hi[c] = (bf16)(c0 + 8 + c <= tr ? T[tr * LDF + c0 + 8 + c] : 0.f);
+        }
+        bf16* dst = Tout + ((long)slot * H + h) * 64 * 64 + tr * 64 + c0;
+        *reinterpret_cast<bf16x8*>(dst) = lo;
+        *reinterpret_cast<bf16x8*>(dst + 8) = hi;
     }
     // W^T = K^T (T diag(b))^T and U^T likewise, for token block w.  B operand
     // (k = t', column t = 16w + r): (T diag(b))[t][t'], zero above the diagonal.

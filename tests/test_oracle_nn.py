@@ -1,0 +1,83 @@
+"""Pins for the oracle's LayerNorm, GELU and AdamW (CPU only).
+
+LayerNorm follows layernorm.cu:133-183 (eps inside the rsqrt, optional bias);
+its gradient is the textbook one.  GELU is the tanh approximation of
+layernorm.cu:189-250.  AdamW is optim.cu:147-178 with fp32 master weights.
+Each is checked against an independent statement: numpy fp64 formulas, torch
+fp64 autograd / torch's own GELU, invariants and a one-step closed form.
+"""
+import numpy as np
+import pytest
+import torch
+
+
+def test_layernorm_forward_formula_and_invariants(oracle):
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((7, 96)) * 3 + 2).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(96)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(96)).astype(np.float32)
+    y, mean, rstd = oracle.layernorm_fwd(x, w, b, 1e-5)
+    xd = x.astype(np.float64)
+    mu = xd.mean(1, keepdims=True)
+    var = ((xd - mu) ** 2).mean(1, keepdims=True)
+    ref = (xd - mu) / np.sqrt(var + 1e-5) * w + b
+    assert np.abs(y - ref).max() < 1e-5
+    assert np.allclose(mean, mu[:, 0], rtol=1e-6)
+    assert np.allclose(rstd, 1 / np.sqrt(var[:, 0] + 1e-5), rtol=1e-5)
+    # w = 1, b = 0: each row has mean 0 and variance var / (var + eps)
+    y1, _, _ = oracle.layernorm_fwd(x, np.ones(96, np.float32), None, 1e-5)
+    assert np.abs(y1.mean(1)).max() < 1e-6
+    assert np.abs(y1.var(1) - var[:, 0] / (var[:, 0] + 1e-5)).max() < 1e-5
+
+
+def test_layernorm_backward_matches_autograd(oracle):
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((5, 48)).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(48)).astype(np.float32)
+    b = (0.1 * rng.standard_normal(48)).astype(np.float32)
+    dy = rng.standard_normal((5, 48)).astype(np.float32)
+    _, mean, rstd = oracle.layernorm_fwd(x, w, b, 1e-5)
+    dx, dw, db = oracle.layernorm_bwd(dy, x, w, mean, rstd)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    wt = torch.tensor(w, dtype=torch.float64, requires_grad=True)
+    bt = torch.tensor(b, dtype=torch.float64, requires_grad=True)
+    yt = torch.nn.functional.layer_norm(xt, (48,), wt, bt, 1e-5)
+    (yt * torch.tensor(dy, dtype=torch.float64)).sum().backward()
+    assert np.abs(dx - xt.grad.numpy()).max() < 1e-4
+    assert np.abs(dw - wt.grad.numpy()).max() < 1e-4
+    assert np.abs(db - bt.grad.numpy()).max() < 1e-6
+
+
+def test_gelu_matches_torch_tanh_gelu(oracle):
+    x = np.linspace(-8, 8, 1001).astype(np.float32)
+    y = oracle.gelu_fwd(x)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    yt = torch.nn.functional.gelu(xt, approximate="tanh")
+    assert np.abs(y - yt.detach().numpy()).max() < 1e-6
+    dy = np.cos(x).astype(np.float32)
+    (yt * torch.tensor(dy, dtype=torch.float64)).sum().backward()
+    assert np.abs(oracle.gelu_bwd(dy, x) - xt.grad.numpy()).max() < 1e-6
+    # special values: gelu(0) = 0, gelu(x) -> x for large x, -> 0 for very negative x
+    assert oracle.gelu_fwd(np.array([0.0, 30.0, -30.0], np.float32)).tolist() == [0.0, 30.0, 0.0]
+
+
+@pytest.mark.parametrize("step", [1, 7])
+def test_adamw_step_closed_form(oracle, step):
+    rng = np.random.default_rng(3)
+    n = 64
+    p = rng.standard_normal(n).astype(np.float32)
+    g = rng.standard_normal(n).astype(np.float32)
+    m = (0.1 * rng.standard_normal(n)).astype(np.float32) if step > 1 else np.zeros(n, np.float32)
+    v = np.abs(0.1 * rng.standard_normal(n)).astype(np.float32) if step > 1 else np.zeros(n, np.float32)
+    lr, b1, b2, eps, wd = 3e-4, 0.9, 0.999, 1e-8, 0.1
+    p0, m0, v0 = p.astype(np.float64), m.astype(np.float64), v.astype(np.float64)
+    mn = b1 * m0 + (1 - b1) * g
+    vn = b2 * v0 + (1 - b2) * g.astype(np.float64) ** 2
+    ref = p0 * (1 - lr * wd) - lr * (mn / (1 - b1 ** step)) / (np.sqrt(vn / (1 - b2 ** step)) + eps)
+    oracle.adamw_step(p, g, m, v, lr, b1, b2, eps, wd, step)
+    assert np.abs(p - ref).max() < 1e-6
+    assert np.abs(m - mn).max() < 1e-7 and np.abs(v - vn).max() < 1e-7
+    if step == 1:
+        # from a zero state one step is p(1 - lr wd) - lr g / (|g| + eps)
+        kat = p0 * (1 - lr * wd) - lr * g / (np.abs(g) + eps)
+        assert np.abs(p - kat).max() < 1e-6
