@@ -887,7 +887,7 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
     if constexpr (__is_same(T, bf16)) {
-        EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K, V>), dim3(p.slots, H),
+        EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K, V>), dim3(H, p.slots),
                     dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, (bf16*)nullptr);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
                     dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, w.W, w.U, si, H, S0,
@@ -915,14 +915,14 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
     // forward recompute: W, U, chunk states and Vn (nothing is kept from the forward)
     if constexpr (__is_same(T, bf16)) {
         const dim3 scan_grid(p.N * H * (V / fast::VS));
-        EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(p.slots, H),
+        EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(H, p.slots),
                     dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, w.Tc);
         EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
                     dim3(fast::NT), st, k, w.W, w.U, si, H, S0, w.h);
         EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V>), scan_grid,
                     dim3(fast::NT), st, q, k, w.W, dO, si, H, dST, dS0, w.dh);
-        EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V>), dim3(p.slots, H),
-                    dim3(fast::NT), st, q, k, v, beta, dO, (const bf16*)w.Tc, w.h, w.dh, si,
+        EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V>), dim3(H, p.slots),
+                    dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc, w.h, w.dh, si,
                     H, dq, dk, dv, dbeta);
         return (int)hipPeekAtLastError();
     } else {

@@ -67,10 +67,15 @@ __device__ __forceinline__ void store_state_vf(bf16* __restrict__ hist, const fl
 // forward recompute: chunk start states
 // ---------------------------------------------------------------------------
 template <int K>
-struct ScanHSmem {
+struct ScanHBuf {
     bf16 W[64 * ldb<K>()];
     bf16 Kr[64 * ldb<K>()];
     bf16 U[64 * LD64];
+};
+
+template <int K>
+struct ScanHSmem {
+    ScanHBuf<K> buf[2];  // chunk n in buf[n & 1]
 };
 
 template <int K, int V>
@@ -109,14 +114,19 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
         rk.load(k + (bos * H + h) * K, (long)H * K, len);
         ru.load(U + (bos * H + h) * V + v0, (long)H * V, len);
     };
-    if (nch > 0) prefetch(0);
+    auto stage = [&](ScanHBuf<K>& b) {
+        rw.store_rows(b.W, LDK);
+        rk.store_rows(b.Kr, LDK);
+        ru.store_rows(b.U, LD64);
+    };
+    if (nch > 0) {
+        prefetch(0);
+        stage(sm.buf[0]);
+        if (nch > 1) prefetch(1);
+    }
     for (int n = 0; n < nch; ++n) {
-        __syncthreads();
-        rw.store_rows(sm.W, LDK);
-        rk.store_rows(sm.Kr, LDK);
-        ru.store_rows(sm.U, LD64);
-        __syncthreads();
-        if (n + 1 < nch) prefetch(n + 1);
+        const ScanHBuf<K>& cb = sm.buf[n & 1];
+        __syncthreads();  // chunk n staged; everyone is done with chunk n - 1
         store_state_vf<K>(hist + ((long)(slot0 + n) * H + h) * V * K, S, vcol);
         bf16x8 sb[K / 32];
 #pragma unroll
@@ -124,19 +134,23 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
         floatx4 vn[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-            const bf16x4 u = tr_rows4(sm.U, LD64, 32 * (tb >> 1) + 4 * (tb & 1), 16 * w, 4);
+            const bf16x4 u = tr_rows4(cb.U, LD64, 32 * (tb >> 1) + 4 * (tb & 1), 16 * w, 4);
             vn[tb] = floatx4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]};
             const int row = pim(tb, r);
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb)
-                vn[tb] = mma(frag_row(sm.W, LDK, row, 32 * kb), sb[kb], vn[tb]);
+                vn[tb] = mma(frag_row(cb.W, LDK, row, 32 * kb), sb[kb], vn[tb]);
         }
         const bf16x8 vb0 = frag_from_c(vn[0], vn[1]), vb1 = frag_from_c(vn[2], vn[3]);
 #pragma unroll
         for (int fb = 0; fb < K / 16; ++fb) {
             const int c0 = 32 * (fb >> 1) + 4 * (fb & 1);
-            S[fb] = mma(frag_tr(sm.Kr, LDK, 0, c0, 8), vb0, S[fb]);
-            S[fb] = mma(frag_tr(sm.Kr, LDK, 32, c0, 8), vb1, S[fb]);
+            S[fb] = mma(frag_tr(cb.Kr, LDK, 0, c0, 8), vb0, S[fb]);
+            S[fb] = mma(frag_tr(cb.Kr, LDK, 32, c0, 8), vb1, S[fb]);
+        }
+        if (n + 1 < nch) {
+            stage(sm.buf[(n + 1) & 1]);
+            if (n + 2 < nch) prefetch(n + 2);
         }
     }
 }
@@ -145,12 +159,17 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
 // reverse scan: chunk end-state gradients
 // ---------------------------------------------------------------------------
 template <int K>
-struct ScanDhSmem {
+struct ScanDhBuf {
     bf16 Q[64 * ldb<K>()];
     bf16 Kr[64 * ldb<K>()];
     bf16 W[64 * ldb<K>()];
     bf16 dO[64 * LD64];  // dO[:, slice]
-    bf16 P[64 * LD64];   // tril(Q K^T) [t][t']
+};
+
+template <int K>
+struct ScanDhSmem {
+    ScanDhBuf<K> buf[2];  // chunk n in buf[n & 1]
+    bf16 P[64 * LD64];    // tril(Q K^T) [t][t']
 };
 
 template <int K, int V>
@@ -193,15 +212,20 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         rw.load(W + (bos * H + h) * K, (long)H * K, len);
         rd.load(dO + (bos * H + h) * V + v0, (long)H * V, len);
     };
-    if (nch > 0) prefetch(nch - 1);
+    auto stage = [&](ScanDhBuf<K>& b) {
+        rq.store_rows(b.Q, LDK);
+        rk.store_rows(b.Kr, LDK);
+        rw.store_rows(b.W, LDK);
+        rd.store_rows(b.dO, LD64);
+    };
+    if (nch > 0) {
+        prefetch(nch - 1);
+        stage(sm.buf[(nch - 1) & 1]);
+        if (nch > 1) prefetch(nch - 2);
+    }
     for (int n = nch - 1; n >= 0; --n) {
-        __syncthreads();
-        rq.store_rows(sm.Q, LDK);
-        rk.store_rows(sm.Kr, LDK);
-        rw.store_rows(sm.W, LDK);
-        rd.store_rows(sm.dO, LD64);
-        __syncthreads();
-        if (n > 0) prefetch(n - 1);
+        const ScanDhBuf<K>& cb = sm.buf[n & 1];
+        __syncthreads();  // chunk n staged; everyone is done with chunk n + 1
         store_state_vf<K>(dhist + ((long)(slot0 + n) * H + h) * V * K, dS, vcol);
         for (int nt = w; nt < 10; nt += 4) {
             int I, J;
@@ -209,7 +233,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
             floatx4 acc = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)
-                acc = mma(frag_nat(sm.Kr, LDK, 16 * J, k0), frag_nat(sm.Q, LDK, 16 * I, k0), acc);
+                acc = mma(frag_nat(cb.Kr, LDK, 16 * J, k0), frag_nat(cb.Q, LDK, 16 * I, k0), acc);
             const int tq = 16 * I + r, tk = 16 * J + 4 * g;
             *reinterpret_cast<bf16x4*>(sm.P + tq * LD64 + tk) =
                 bf16x4{(bf16)(tk + 0 <= tq ? acc[0] : 0.f), (bf16)(tk + 1 <= tq ? acc[1] : 0.f),
@@ -218,19 +242,28 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(dS[2 * kb], dS[2 * kb + 1]);
-        const bf16x8 do0 = frag_tr(sm.dO, LD64, 0, 16 * w), do1 = frag_tr(sm.dO, LD64, 32, 16 * w);
-        __syncthreads();
-        // dVn = P^T dO + K dS; tile tb row 4g + i is token pim(tb, 4g + i)
+        const bf16x8 do0 = frag_tr(cb.dO, LD64, 0, 16 * w), do1 = frag_tr(cb.dO, LD64, 32, 16 * w);
+        // K dS part of dVn (P^T dO is added once P is complete)
         floatx4 dvn[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-            const int row = pim(tb, r), c0 = 32 * (tb >> 1) + 4 * (tb & 1);
+            const int row = pim(tb, r);
             floatx4 acc = zero4();
-            if (tb < 2) acc = mma(frag_tr(sm.P, LD64, 0, c0, 8), do0, acc);
-            acc = mma(frag_tr(sm.P, LD64, 32, c0, 8), do1, acc);
 #pragma unroll
-            for (int kb = 0; kb < K / 32; ++kb) acc = mma(frag_row(sm.Kr, LDK, row, 32 * kb), sb[kb], acc);
+            for (int kb = 0; kb < K / 32; ++kb) acc = mma(frag_row(cb.Kr, LDK, row, 32 * kb), sb[kb], acc);
             dvn[tb] = acc;
+        }
+        if (n > 0) {
+            stage(sm.buf[(n - 1) & 1]);
+            if (n > 1) prefetch(n - 2);
+        }
+        __syncthreads();  // P complete
+        // dVn += P^T dO; tile tb row 4g + i is token pim(tb, 4g + i)
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const int c0 = 32 * (tb >> 1) + 4 * (tb & 1);
+            if (tb < 2) dvn[tb] = mma(frag_tr(sm.P, LD64, 0, c0, 8), do0, dvn[tb]);
+            dvn[tb] = mma(frag_tr(sm.P, LD64, 32, c0, 8), do1, dvn[tb]);
         }
         const bf16x8 nd0 = mf::neg(frag_from_c(dvn[0], dvn[1]));
         const bf16x8 nd1 = mf::neg(frag_from_c(dvn[2], dvn[3]));
@@ -239,10 +272,10 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         for (int fb = 0; fb < K / 16; ++fb) {
             const int c0 = 32 * (fb >> 1) + 4 * (fb & 1);
             floatx4 acc = dS[fb];
-            acc = mma(frag_tr(sm.Q, LDK, 0, c0, 8), do0, acc);
-            acc = mma(frag_tr(sm.Q, LDK, 32, c0, 8), do1, acc);
-            acc = mma(frag_tr(sm.W, LDK, 0, c0, 8), nd0, acc);
-            acc = mma(frag_tr(sm.W, LDK, 32, c0, 8), nd1, acc);
+            acc = mma(frag_tr(cb.Q, LDK, 0, c0, 8), do0, acc);
+            acc = mma(frag_tr(cb.Q, LDK, 32, c0, 8), do1, acc);
+            acc = mma(frag_tr(cb.W, LDK, 0, c0, 8), nd0, acc);
+            acc = mma(frag_tr(cb.W, LDK, 32, c0, 8), nd1, acc);
             dS[fb] = acc;
         }
     }
@@ -264,9 +297,10 @@ struct GradSmem {
     bf16 Ps[64 * LD64];  // P[t][t'] (t' <= t)
     bf16 Tb[64 * LD64];  // bf16(T)[t][t'] (t' <= t), from the WY prep
     float lam[64], b[64], dcl[64], dcb[64];
+    float dbh[2][64];    // per-half partial dL/db
     union {
         struct {  // one 64-wide value slice
-            bf16 V[64 * LD64];   // v[:, slice]; each wave's rows later hold D Y
+            bf16 V[64 * LD64];   // v[:, slice]; each wave's (rows, value tiles) later hold D Y
             bf16 dO[64 * LD64];  // dO[:, slice]
             bf16 h[64 * ldb<K>()];   // h[v][f] for the slice's v
             bf16 dh[64 * ldb<K>()];  // dh[v][f]
@@ -276,31 +310,41 @@ struct GradSmem {
         } s;
         struct {  // closing products
             bf16 Dm[64 * LD64];  // Dm [t][t']
+            bf16 dT[64 * LD64];  // dT [t][t'] (t' < t)
             bf16 X[64 * LD64];   // dT T^T [t][t'']
-            bf16 dG[64 * LD64];  // dG [i][j]
+            bf16 dG[64 * LD64];  // dG [i][j] (j < i)
         } e;
     } u;
 };
 
+constexpr int NT8 = 512;  // grad_kernel: 8 waves
+
+// Wave (tb, hf): tb = wave & 3 owns tokens 16tb .. 16tb+15 (the columns of
+// every transposed tile it computes); hf = wave >> 2 picks half of the value
+// tiles (slice phase), of the key tiles (dq / dk) and of the 16-token blocks
+// of the 64 x 64 chunk matrices.
 template <int K, int V>
-__global__ void __launch_bounds__(NT) grad_kernel(
+__global__ void __launch_bounds__(NT8) grad_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ beta, const bf16* __restrict__ dO, const bf16* __restrict__ Tws,
     const bf16* __restrict__ hist, const bf16* __restrict__ dhist, SeqInfo si, int H,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
     bf16* __restrict__ dbeta) {
-    constexpr int LDK = ldb<K>(), NS = V / VS;
+    constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 32;  // NF key tiles per half
     __shared__ __attribute__((aligned(16))) GradSmem<K> sm;
-    const int slot = blockIdx.x, h = blockIdx.y;
+    const int h = blockIdx.x, slot = blockIdx.y;  // heads fastest: one chunk's rows stay together
     long bos;
     int len;
     if (!locate_chunk(si, slot, bos, len)) return;
-    const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
-    const int t = 16 * w + r;  // this lane's token (column of the transposed tiles)
+    const int w8 = mf::wave(), tb = w8 & 3, hf = w8 >> 2;
+    const int l = mf::lane(), g = l >> 4, r = l & 15;
+    const int t = 16 * tb + r;  // this lane's token (column of the transposed tiles)
     const long chb = ((long)slot * H + h) * V * K;  // this chunk's h / dh block
+    const int nks = tb >= 2 ? 1 : 0;  // first k-step (of 32) that reaches t'' >= t
+    const int f0 = hf * NF;            // first key tile of this half
 
-    mf::TileRegs<64, VS, NT> rv, rd;
-    mf::TileRegs<64, K, NT> rh, rdh;
+    mf::TileRegs<64, VS, NT8> rv, rd;
+    mf::TileRegs<64, K, NT8> rh, rdh;
     auto prefetch = [&](int s) {
         const int vv = s * VS;
         rv.load(v + (bos * H + h) * V + vv, (long)H * V, len);
@@ -310,8 +354,8 @@ __global__ void __launch_bounds__(NT) grad_kernel(
     };
     // ---- chunk setup: q, k, T, b, P ----
     {
-        mf::TileRegs<64, K, NT> rq, rk;
-        mf::TileRegs<64, 64, NT> rt;
+        mf::TileRegs<64, K, NT8> rq, rk;
+        mf::TileRegs<64, 64, NT8> rt;
         rq.load(q + (bos * H + h) * K, (long)H * K, len);
         rk.load(k + (bos * H + h) * K, (long)H * K, len);
         rt.load(Tws + ((long)slot * H + h) * 64 * 64, 64, 64);
@@ -324,7 +368,7 @@ __global__ void __launch_bounds__(NT) grad_kernel(
             const float s = rk.row_sumsq(j);
             if (rk.fg() == 0) sm.lam[rk.t0() + j] = s;
         }
-        for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.Ps[i] = (bf16)0.f;
+        for (int i = threadIdx.x; i < 64 * LD64; i += NT8) sm.Ps[i] = (bf16)0.f;
     }
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -335,7 +379,7 @@ __global__ void __launch_bounds__(NT) grad_kernel(
         sm.dcl[tt] = dcl;
         sm.dcb[tt] = dcb;
     }
-    for (int n = w; n < 10; n += 4) {
+    for (int n = w8; n < 10; n += 8) {
         int I, J;
         lower_tile(n, I, J);
         floatx4 accp = zero4();
@@ -348,17 +392,16 @@ __global__ void __launch_bounds__(NT) grad_kernel(
                    (bf16)(tk + 2 <= tq ? accp[2] : 0.f), (bf16)(tk + 3 <= tq ? accp[3] : 0.f)};
     }
     // B operand (line t, k = t') of T
-    const bf16x8 tfr[2] = {frag_nat(sm.Tb, LD64, 16 * w, 0), frag_nat(sm.Tb, LD64, 16 * w, 32)};
+    const bf16x8 tfr0 = frag_nat(sm.Tb, LD64, 16 * tb, 0), tfr1 = frag_nat(sm.Tb, LD64, 16 * tb, 32);
     __syncthreads();
     const float bt = sm.b[t];
-    const int nks = w >= 2 ? 1 : 0;  // first k-step (of 32) that reaches t'' >= t
 
     // ---- value slices ----
-    floatx4 dqa[K / 16], dka[K / 16], dma[4], dta[4];
+    floatx4 dqa[NF], dka[NF], dma[2], dta[2];
 #pragma unroll
-    for (int fb = 0; fb < K / 16; ++fb) dqa[fb] = dka[fb] = zero4();
-#pragma unroll
-    for (int j = 0; j < 4; ++j) dma[j] = dta[j] = zero4();
+    for (int fb = 0; fb < NF; ++fb) dqa[fb] = dka[fb] = zero4();
+    dma[0] = dma[1] = dta[0] = dta[1] = zero4();
+    const bool jlive = hf == 0 || tb >= 2;  // this half's t' blocks reach t' <= t
     float dbp = 0.f;
     for (int s = 0; s < NS; ++s) {
         const int vv = s * VS;
@@ -369,180 +412,182 @@ __global__ void __launch_bounds__(NT) grad_kernel(
         rdh.store_rows(sm.u.s.dh, LDK);
         __syncthreads();
         if (s + 1 < NS) prefetch(s + 1);
-        // R^T = V^T - h K^T and dVn^T = dO^T P + dh K^T, tile vb: (value 16vb + 4g + i, token t)
-        floatx4 rT[4];
+        // R^T = V^T - h K^T and dVn^T = dO^T P + dh K^T for value tiles 2hf, 2hf+1:
+        // tile (value 16vb + 4g + i, token t)
+        floatx4 rT[2];
 #pragma unroll
-        for (int vb = 0; vb < 4; ++vb) {
+        for (int e = 0; e < 2; ++e) {
+            const int vb = 2 * hf + e;
             floatx4 ra = load4(sm.u.s.V + t * LD64 + 16 * vb + 4 * g);
             floatx4 da = zero4();
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb) {
-                const bf16x8 kt = frag_nat(sm.Ks, LDK, 16 * w, 32 * kb);
+                const bf16x8 kt = frag_nat(sm.Ks, LDK, 16 * tb, 32 * kb);
                 ra = mma(frag_nat(sm.u.s.h, LDK, 16 * vb, 32 * kb), mf::neg(kt), ra);
                 da = mma(frag_nat(sm.u.s.dh, LDK, 16 * vb, 32 * kb), kt, da);
             }
-            if (nks == 0) da = mma(frag_tr(sm.u.s.dO, LD64, 0, 16 * vb), frag_tr(sm.Ps, LD64, 0, 16 * w), da);
-            da = mma(frag_tr(sm.u.s.dO, LD64, 32, 16 * vb), frag_tr(sm.Ps, LD64, 32, 16 * w), da);
-            rT[vb] = ra;
+            if (nks == 0) da = mma(frag_tr(sm.u.s.dO, LD64, 0, 16 * vb), frag_tr(sm.Ps, LD64, 0, 16 * tb), da);
+            da = mma(frag_tr(sm.u.s.dO, LD64, 32, 16 * vb), frag_tr(sm.Ps, LD64, 32, 16 * tb), da);
+            rT[e] = ra;
             store4s(sm.u.s.DR + t * LD64 + 16 * vb + 4 * g, ra, bt);
             store4(sm.u.s.dVn + t * LD64 + 16 * vb + 4 * g, da);
         }
         __syncthreads();
-        // Vn^T = (D R)^T T^T; Y^T = dVn^T T; dv = D Y; db += sum_v Y R; D Y -> own rows of V
+        // Vn^T = (D R)^T T^T; Y^T = dVn^T T; dv = D Y; db += sum_v Y R; D Y -> V
         bf16* vrow = dv + ((bos + t) * H + h) * V + vv + 4 * g;
 #pragma unroll
-        for (int vb = 0; vb < 4; ++vb) {
-            floatx4 vn = mma(frag_tr(sm.u.s.DR, LD64, 0, 16 * vb), tfr[0], zero4());
-            if (w >= 2) vn = mma(frag_tr(sm.u.s.DR, LD64, 32, 16 * vb), tfr[1], vn);
+        for (int e = 0; e < 2; ++e) {
+            const int vb = 2 * hf + e;
+            floatx4 vn = mma(frag_tr(sm.u.s.DR, LD64, 0, 16 * vb), tfr0, zero4());
+            if (tb >= 2) vn = mma(frag_tr(sm.u.s.DR, LD64, 32, 16 * vb), tfr1, vn);
             store4(sm.u.s.Vn + t * LD64 + 16 * vb + 4 * g, vn);
             floatx4 y = zero4();
             if (nks == 0)
-                y = mma(frag_tr(sm.u.s.dVn, LD64, 0, 16 * vb), frag_tr(sm.Tb, LD64, 0, 16 * w), y);
-            y = mma(frag_tr(sm.u.s.dVn, LD64, 32, 16 * vb), frag_tr(sm.Tb, LD64, 32, 16 * w), y);
+                y = mma(frag_tr(sm.u.s.dVn, LD64, 0, 16 * vb), frag_tr(sm.Tb, LD64, 0, 16 * tb), y);
+            y = mma(frag_tr(sm.u.s.dVn, LD64, 32, 16 * vb), frag_tr(sm.Tb, LD64, 32, 16 * tb), y);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dbp += y[i] * rT[vb][i];
+            for (int i = 0; i < 4; ++i) dbp += y[i] * rT[e][i];
             if (t < len) store4s(vrow + 16 * vb, y, bt);
             store4s(sm.u.s.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
-        lds_fence_wave();
-        // dq^T += h^T dO^T;  dk^T -= h^T (D Y)^T;  dT^T[t'][t] += sum_v D R[t'] dVn[t]
+        __syncthreads();
+        // dq^T += h^T dO^T; dk^T += dh^T Vn^T - h^T (D Y)^T  (key tiles f0 .. f0+NF-1)
+        // dT^T[t'][t] += sum_v D R[t'] dVn[t]; Dm^T[t'][t] += sum_v Vn[t'] dO[t]
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 dob = frag_nat(sm.u.s.dO, LD64, 16 * w, 32 * ks);
-            const bf16x8 dyb = mf::neg(frag_nat(sm.u.s.V, LD64, 16 * w, 32 * ks));
-            const bf16x8 dvb = frag_nat(sm.u.s.dVn, LD64, 16 * w, 32 * ks);
+            const bf16x8 dob = frag_nat(sm.u.s.dO, LD64, 16 * tb, 32 * ks);
+            const bf16x8 dyb = mf::neg(frag_nat(sm.u.s.V, LD64, 16 * tb, 32 * ks));
+            const bf16x8 vnb = frag_nat(sm.u.s.Vn, LD64, 16 * tb, 32 * ks);
 #pragma unroll
-            for (int fb = 0; fb < K / 16; ++fb) {
-                const bf16x8 ha = frag_tr(sm.u.s.h, LDK, 32 * ks, 16 * fb);
+            for (int fb = 0; fb < NF; ++fb) {
+                const bf16x8 ha = frag_tr(sm.u.s.h, LDK, 32 * ks, 16 * (f0 + fb));
                 dqa[fb] = mma(ha, dob, dqa[fb]);
                 dka[fb] = mma(ha, dyb, dka[fb]);
+                dka[fb] = mma(frag_tr(sm.u.s.dh, LDK, 32 * ks, 16 * (f0 + fb)), vnb, dka[fb]);
             }
+            if (jlive) {
+                const bf16x8 dvb = frag_nat(sm.u.s.dVn, LD64, 16 * tb, 32 * ks);
 #pragma unroll
-            for (int J = 0; J < 4; ++J)
-                if (J < 2 || w >= 2)
-                    dta[J] = mma(frag_row(sm.u.s.DR, LD64, pim(J, r), 32 * ks), dvb, dta[J]);
-        }
-        __syncthreads();
-        // Dm^T[t'][t] += sum_v Vn[t'] dO[t];  dk^T += dh^T Vn^T
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 dob = frag_nat(sm.u.s.dO, LD64, 16 * w, 32 * ks);
-            const bf16x8 vnb = frag_nat(sm.u.s.Vn, LD64, 16 * w, 32 * ks);
-#pragma unroll
-            for (int J = 0; J < 4; ++J)
-                if (J < 2 || w >= 2)
-                    dma[J] = mma(frag_row(sm.u.s.Vn, LD64, pim(J, r), 32 * ks), dob, dma[J]);
-#pragma unroll
-            for (int fb = 0; fb < K / 16; ++fb)
-                dka[fb] = mma(frag_tr(sm.u.s.dh, LDK, 32 * ks, 16 * fb), vnb, dka[fb]);
+                for (int e = 0; e < 2; ++e) {
+                    const int J = 2 * hf + e;
+                    dta[e] = mma(frag_row(sm.u.s.DR, LD64, pim(J, r), 32 * ks), dvb, dta[e]);
+                    dma[e] = mma(frag_row(sm.u.s.Vn, LD64, pim(J, r), 32 * ks), dob, dma[e]);
+                }
+            }
         }
     }
-    // db from Y o R: sum over the 4 lane groups holding token t
+    // db from Y o R: sum over the 4 lane groups holding token t, then the halves
     dbp += __shfl_xor(dbp, 16);
     dbp += __shfl_xor(dbp, 32);
+    if (g == 0) sm.dbh[hf][t] = dbp;
     __syncthreads();  // slice buffers are free
 
     // ---- closing products ----
-    // masks: Dm[t][t'] needs t' <= t, dT[t][t'] needs t' < t
+    // Dm[t][t'] keeps t' <= t, dT[t][t'] keeps t' < t; share both [t][t']
 #pragma unroll
-    for (int J = 0; J < 4; ++J)
+    for (int e = 0; e < 2; ++e) {
+        const int J = 2 * hf + e;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tp = pim(J, 4 * g + i);
-            if (tp > t) dma[J][i] = 0.f;
-            if (tp >= t) dta[J][i] = 0.f;
+            if (tp > t) dma[e][i] = 0.f;
+            if (tp >= t) dta[e][i] = 0.f;
         }
-    // dq^T += K^T Dm^T (k = t'), Dm from registers
-    {
-        const bf16x8 m0 = frag_from_c(dma[0], dma[1]), m1 = frag_from_c(dma[2], dma[3]);
-#pragma unroll
-        for (int fb = 0; fb < K / 16; ++fb) {
-            dqa[fb] = mma(frag_tr(sm.Ks, LDK, 0, 16 * fb), m0, dqa[fb]);
-            if (w >= 2) dqa[fb] = mma(frag_tr(sm.Ks, LDK, 32, 16 * fb), m1, dqa[fb]);
-        }
+        store4(sm.u.e.Dm + t * LD64 + pim(J, 4 * g), dma[e]);
+        store4(sm.u.e.dT + t * LD64 + pim(J, 4 * g), dta[e]);
     }
-    // share Dm [t][t'] and X^T: X[t][t''] = sum_t' dT[t][t'] T[t''][t']
-#pragma unroll
-    for (int J = 0; J < 4; ++J) store4(sm.u.e.Dm + t * LD64 + pim(J, 4 * g), dma[J]);
+    __syncthreads();
+    // X^T[t''][t] = sum_t' T[t''][t'] dT[t][t'] for t'' blocks 2hf, 2hf+1
     {
-        const bf16x8 d0 = frag_from_c(dta[0], dta[1]), d1 = frag_from_c(dta[2], dta[3]);
+        const bf16x8 d0 = frag_nat(sm.u.e.dT, LD64, 16 * tb, 0), d1 = frag_nat(sm.u.e.dT, LD64, 16 * tb, 32);
 #pragma unroll
-        for (int J = 0; J < 4; ++J) {
+        for (int e = 0; e < 2; ++e) {
+            const int J = 2 * hf + e;
             floatx4 x = mma(frag_nat(sm.Tb, LD64, 16 * J, 0), d0, zero4());
             x = mma(frag_nat(sm.Tb, LD64, 16 * J, 32), d1, x);
             store4(sm.u.e.X + t * LD64 + 16 * J + 4 * g, x);
         }
     }
-    __syncthreads();
-    // dk^T += Q^T Dm (token t' = t owned here, k = t >= t')
+    // dq^T += K^T Dm^T (k = t' <= t);  dk^T += Q^T Dm (token t' = t, k = t >= t')
+    {
+        const bf16x8 m0 = frag_nat(sm.u.e.Dm, LD64, 16 * tb, 0), m1 = frag_nat(sm.u.e.Dm, LD64, 16 * tb, 32);
+        const bf16x8 c1 = frag_tr(sm.u.e.Dm, LD64, 32, 16 * tb);
+        bf16x8 c0 = c1;
+        if (nks == 0) c0 = frag_tr(sm.u.e.Dm, LD64, 0, 16 * tb);
 #pragma unroll
-    for (int fb = 0; fb < K / 16; ++fb) {
-        if (nks == 0)
-            dka[fb] = mma(frag_tr(sm.Qs, LDK, 0, 16 * fb), frag_tr(sm.u.e.Dm, LD64, 0, 16 * w), dka[fb]);
-        dka[fb] = mma(frag_tr(sm.Qs, LDK, 32, 16 * fb), frag_tr(sm.u.e.Dm, LD64, 32, 16 * w), dka[fb]);
+        for (int fb = 0; fb < NF; ++fb) {
+            const int fc = 16 * (f0 + fb);
+            dqa[fb] = mma(frag_tr(sm.Ks, LDK, 0, fc), m0, dqa[fb]);
+            if (tb >= 2) dqa[fb] = mma(frag_tr(sm.Ks, LDK, 32, fc), m1, dqa[fb]);
+            if (nks == 0) dka[fb] = mma(frag_tr(sm.Qs, LDK, 0, fc), c0, dka[fb]);
+            dka[fb] = mma(frag_tr(sm.Qs, LDK, 32, fc), c1, dka[fb]);
+        }
     }
-    // M^T[j][i] = sum_t X[t][j] T[t][i] for i = t owned here, rows j = pim(J, .) < i;
-    // dA = -M (strict lower), G recomputed; db += sum_j dA G; dG = b_i dA
+    __syncthreads();
+    // M^T[j][i] = sum_t X[t][j] T[t][i] (i = t owned here, j in blocks 2hf, 2hf+1, j < i);
+    // dA = -M, G recomputed: db += sum_j dA G; dG = b_i dA -> shared [i][j]
     float dbg = 0.f;
-    floatx4 dgt[4];
 #pragma unroll
-    for (int J = 0; J < 4; ++J) {
-        dgt[J] = zero4();
-        if (J < 2 || w >= 2) {
+    for (int e = 0; e < 2; ++e) {
+        const int J = 2 * hf + e;
+        floatx4 dg = zero4();
+        if (jlive) {
             const int c0 = 32 * (J >> 1) + 4 * (J & 1);
             floatx4 m = zero4();
-            if (nks == 0) m = mma(frag_tr(sm.u.e.X, LD64, 0, c0, 8), frag_tr(sm.Tb, LD64, 0, 16 * w), m);
-            m = mma(frag_tr(sm.u.e.X, LD64, 32, c0, 8), frag_tr(sm.Tb, LD64, 32, 16 * w), m);
+            if (nks == 0) m = mma(frag_tr(sm.u.e.X, LD64, 0, c0, 8), frag_tr(sm.Tb, LD64, 0, 16 * tb), m);
+            m = mma(frag_tr(sm.u.e.X, LD64, 32, c0, 8), frag_tr(sm.Tb, LD64, 32, 16 * tb), m);
             floatx4 gg = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)
-                gg = mma(frag_row(sm.Ks, LDK, pim(J, r), k0), frag_nat(sm.Ks, LDK, 16 * w, k0), gg);
+                gg = mma(frag_row(sm.Ks, LDK, pim(J, r), k0), frag_nat(sm.Ks, LDK, 16 * tb, k0), gg);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int j = pim(J, 4 * g + i);
                 const float da = (j < t) ? -m[i] : 0.f;
                 dbg += da * gg[i];
-                dgt[J][i] = bt * da;
+                dg[i] = bt * da;
             }
         }
+        store4(sm.u.e.dG + t * LD64 + pim(J, 4 * g), dg);
     }
     dbg += __shfl_xor(dbg, 16);
     dbg += __shfl_xor(dbg, 32);
-    const float dbt = dbp + dbg;  // dL/db for token t (all lanes of the column)
-    // dk^T += K^T dG^T (k = j < i = t), from registers; share dG [i][j]
+    __syncthreads();
+    if (g == 0) sm.dbh[hf][t] += dbg;
+    // dk^T += K^T dG^T (k = j < i = t) + K^T dG (token j = t, k = i > j)
     {
-        const bf16x8 g0 = frag_from_c(dgt[0], dgt[1]), g1 = frag_from_c(dgt[2], dgt[3]);
+        const bf16x8 a0 = frag_nat(sm.u.e.dG, LD64, 16 * tb, 0), a1 = frag_nat(sm.u.e.dG, LD64, 16 * tb, 32);
+        const bf16x8 b1 = frag_tr(sm.u.e.dG, LD64, 32, 16 * tb);
+        bf16x8 b0 = b1;
+        if (nks == 0) b0 = frag_tr(sm.u.e.dG, LD64, 0, 16 * tb);
 #pragma unroll
-        for (int fb = 0; fb < K / 16; ++fb) {
-            dka[fb] = mma(frag_tr(sm.Ks, LDK, 0, 16 * fb), g0, dka[fb]);
-            if (w >= 2) dka[fb] = mma(frag_tr(sm.Ks, LDK, 32, 16 * fb), g1, dka[fb]);
+        for (int fb = 0; fb < NF; ++fb) {
+            const int fc = 16 * (f0 + fb);
+            const bf16x8 k0 = frag_tr(sm.Ks, LDK, 0, fc), k1 = frag_tr(sm.Ks, LDK, 32, fc);
+            dka[fb] = mma(k0, a0, dka[fb]);
+            if (tb >= 2) dka[fb] = mma(k1, a1, dka[fb]);
+            if (nks == 0) dka[fb] = mma(k0, b0, dka[fb]);
+            dka[fb] = mma(k1, b1, dka[fb]);
         }
     }
-#pragma unroll
-    for (int J = 0; J < 4; ++J) store4(sm.u.e.dG + t * LD64 + pim(J, 4 * g), dgt[J]);
     __syncthreads();
-    // dk^T += K^T dG (token j = t owned here, k = i > j)
-#pragma unroll
-    for (int fb = 0; fb < K / 16; ++fb) {
-        if (nks == 0)
-            dka[fb] = mma(frag_tr(sm.Ks, LDK, 0, 16 * fb), frag_tr(sm.u.e.dG, LD64, 0, 16 * w), dka[fb]);
-        dka[fb] = mma(frag_tr(sm.Ks, LDK, 32, 16 * fb), frag_tr(sm.u.e.dG, LD64, 32, 16 * w), dka[fb]);
-    }
-    // dk += 2 db c'(lambda) k; write dq, dk, dbeta
+    const float dbt = sm.dbh[0][t] + sm.dbh[1][t];  // dL/db for token t
+    // dk += 2 db c'(lambda) k; write dq, dk (this half's key tiles), dbeta
     if (t < len) {
         const float s2 = 2.f * dbt * sm.dcl[t];
         bf16* qrow = dq + ((bos + t) * H + h) * K + 4 * g;
         bf16* krow = dk + ((bos + t) * H + h) * K + 4 * g;
 #pragma unroll
-        for (int fb = 0; fb < K / 16; ++fb) {
-            store4(qrow + 16 * fb, dqa[fb]);
-            const floatx4 kk = load4(sm.Ks + t * LDK + 16 * fb + 4 * g);
+        for (int fb = 0; fb < NF; ++fb) {
+            const int fc = 16 * (f0 + fb);
+            store4(qrow + fc, dqa[fb]);
+            const floatx4 kk = load4(sm.Ks + t * LDK + fc + 4 * g);
             floatx4 a = dka[fb];
 #pragma unroll
             for (int i = 0; i < 4; ++i) a[i] += s2 * kk[i];
-            store4(krow + 16 * fb, a);
+            store4(krow + fc, a);
         }
-        if (g == 0) dbeta[(bos + t) * H + h] = (bf16)(dbt * sm.dcb[t]);
+        if (hf == 0 && g == 0) dbeta[(bos + t) * H + h] = (bf16)(dbt * sm.dcb[t]);
     }
 }
 

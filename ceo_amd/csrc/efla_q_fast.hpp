@@ -73,7 +73,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
                                                   bf16* __restrict__ Tout) {
     constexpr int LDK = ldb<K>(), LDV = ldb<V>();
     __shared__ __attribute__((aligned(16))) PrepSmem<K, V> sm;
-    const int slot = blockIdx.x, h = blockIdx.y;
+    const int h = blockIdx.x, slot = blockIdx.y;  // heads fastest: one chunk's rows stay together
     long bos;
     int len;
     if (!locate_chunk(si, slot, bos, len)) return;
@@ -202,11 +202,16 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
 constexpr int VS = 64;  // value slice per workgroup
 
 template <int K>
-struct ScanSmem {
+struct ScanBuf {
     bf16 W[64 * ldb<K>()];
     bf16 Q[64 * ldb<K>()];
     bf16 Kr[64 * ldb<K>()];
     bf16 U[64 * ldb<VS>()];  // U[:, slice]
+};
+
+template <int K>
+struct ScanSmem {
+    ScanBuf<K> buf[2];       // chunk n in buf[n & 1]; chunk n + 1 is stored meanwhile
     bf16 P[64 * ldb<64>()];  // tril(Q K^T) [t][t'] (upper tiles stay zero)
 };
 
@@ -267,17 +272,22 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         rk.load(k + (bos * H + h) * K, (long)H * K, len);
         ru.load(U + (bos * H + h) * V + v0, (long)H * V, len);
     };
-    if (nch > 0) prefetch(0);
+    auto stage = [&](ScanBuf<K>& b) {
+        rw.store_rows(b.W, LDK);
+        rq.store_rows(b.Q, LDK);
+        rk.store_rows(b.Kr, LDK);
+        ru.store_rows(b.U, LDU);
+    };
+    if (nch > 0) {
+        prefetch(0);
+        stage(sm.buf[0]);
+        if (nch > 1) prefetch(1);
+    }
     for (int n = 0; n < nch; ++n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
-        __syncthreads();
-        rw.store_rows(sm.W, LDK);
-        rq.store_rows(sm.Q, LDK);
-        rk.store_rows(sm.Kr, LDK);
-        ru.store_rows(sm.U, LDU);
-        __syncthreads();
-        if (n + 1 < nch) prefetch(n + 1);
+        const ScanBuf<K>& cb = sm.buf[n & 1];
+        __syncthreads();  // chunk n staged; everyone is done with chunk n - 1
         // P[t][t'] = q_t . k_t' for t' <= t, lower 16x16 tiles (I = t block,
         // J = t' block) computed transposed so each lane writes 4 consecutive t'
         for (int nt = w; nt < 10; nt += 4) {
@@ -286,7 +296,7 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
             floatx4 acc = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)
-                acc = mma(frag_nat(sm.Kr, LDK, 16 * J, k0), frag_nat(sm.Q, LDK, 16 * I, k0), acc);
+                acc = mma(frag_nat(cb.Kr, LDK, 16 * J, k0), frag_nat(cb.Q, LDK, 16 * I, k0), acc);
             const int tq = 16 * I + r, tk = 16 * J + 4 * g;
             *reinterpret_cast<bf16x4*>(sm.P + tq * LDP + tk) =
                 bf16x4{(bf16)(tk + 0 <= tq ? acc[0] : 0.f), (bf16)(tk + 1 <= tq ? acc[1] : 0.f),
@@ -299,14 +309,19 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         floatx4 vn[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-            const bf16x4 u = mf::tr_rows4(sm.U, LDU, 32 * (tb >> 1) + 4 * (tb & 1), 16 * w, 4);
+            const bf16x4 u = mf::tr_rows4(cb.U, LDU, 32 * (tb >> 1) + 4 * (tb & 1), 16 * w, 4);
             vn[tb] = floatx4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]};
             const int row = pim(tb, r);
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb)
-                vn[tb] = mma(mf::frag_row(sm.W, LDK, row, 32 * kb), mf::neg(sb[kb]), vn[tb]);
+                vn[tb] = mma(mf::frag_row(cb.W, LDK, row, 32 * kb), mf::neg(sb[kb]), vn[tb]);
         }
-        __syncthreads();
+        // stage chunk n + 1 (its loads were issued one chunk ago), fetch n + 2
+        if (n + 1 < nch) {
+            stage(sm.buf[(n + 1) & 1]);
+            if (n + 2 < nch) prefetch(n + 2);
+        }
+        __syncthreads();  // P complete
         const bf16x8 vb0 = frag_from_c(vn[0], vn[1]), vb1 = frag_from_c(vn[2], vn[3]);
         // o^T = S^T Q^T + Vn^T P^T: tile tb holds (value 16w + 4g + i, token 16tb + r)
         bf16* orow = o + (bos * H + h) * V + v0 + 16 * w + 4 * g;
@@ -315,7 +330,7 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
             floatx4 acc = zero4();
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb)
-                acc = mma(sb[kb], frag_nat(sm.Q, LDK, 16 * tb, 32 * kb), acc);
+                acc = mma(sb[kb], frag_nat(cb.Q, LDK, 16 * tb, 32 * kb), acc);
             acc = mma(vb0, frag_nat(sm.P, LDP, 16 * tb, 0), acc);
             if (tb >= 2) acc = mma(vb1, frag_nat(sm.P, LDP, 16 * tb, 32), acc);
             const int t = 16 * tb + r;
@@ -327,8 +342,8 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
 #pragma unroll
         for (int fb = 0; fb < K / 16; ++fb) {
             const int c0 = 32 * (fb >> 1) + 4 * (fb & 1);
-            S[fb] = mma(mf::frag_tr(sm.Kr, LDK, 0, c0, 8), vb0, S[fb]);
-            S[fb] = mma(mf::frag_tr(sm.Kr, LDK, 32, c0, 8), vb1, S[fb]);
+            S[fb] = mma(mf::frag_tr(cb.Kr, LDK, 0, c0, 8), vb0, S[fb]);
+            S[fb] = mma(mf::frag_tr(cb.Kr, LDK, 32, c0, 8), vb1, S[fb]);
         }
     }
     if (ST) {
