@@ -253,10 +253,16 @@ def main() -> int:
           f"{'fwd+bwd' if cfg['bwd'] else 'fwd'}{' varlen' if cu is not None else ''}",
           file=sys.stderr, flush=True)
 
+    # one workspace for both calls: the backward takes the forward's per-chunk
+    # WY factors (W, U, T) from it and recomputes the chunk states
+    ws = efla.new_workspace(x["q"], x["v"], cu)
+
     def step():
-        o, _ = efla.chunk_efla_fwd(x["q"], x["k"], x["v"], x["beta"], cu_seqlens=cu)
+        o, _ = efla.chunk_efla_fwd(x["q"], x["k"], x["v"], x["beta"], cu_seqlens=cu,
+                                   workspace=ws)
         if cfg["bwd"]:
-            efla.chunk_efla_bwd(x["q"], x["k"], x["v"], x["beta"], x["do"], cu_seqlens=cu)
+            efla.chunk_efla_bwd(x["q"], x["k"], x["v"], x["beta"], x["do"], cu_seqlens=cu,
+                                workspace=ws, reuse_forward=True)
         return o
 
     for _ in range(args.warmup):

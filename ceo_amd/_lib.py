@@ -77,7 +77,7 @@ _SIGS = {
     "efla_chunk_fwd_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz,
                                  i32, vp, sz, vp]),
     "efla_chunk_bwd_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz,
-                                 sz, sz, sz, sz, sz, i32, vp, sz, vp]),
+                                 sz, sz, sz, sz, sz, i32, vp, sz, ctypes.c_uint, vp]),
     # LayerNorm
     "layernorm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, f32, vp]),
     "layernorm_forward_stats_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, f32, vp]),

@@ -804,33 +804,49 @@ struct Problem {
     int nt;         // chunks per sequence (fixed-length case)
 };
 
+// Workspace layouts.  Both start with the same prefix (sequence offsets, W, U
+// and, on the bf16 path, the per-chunk T), so a backward call given the
+// forward's workspace finds the forward's W, U, T in place.
 template <typename T>
 struct FwdWs {
     int32_t *cu_s, *coff;
-    float* bco;
-    T *W, *U, *h, *Vn;
+    T *W, *U;
+    T* Tc;      // per-chunk bf16 T (bf16 path)
+    float* bco; // generic path
+    T *h, *Vn;  // generic path
 };
 
 template <typename T>
 struct BwdWs {
     int32_t *cu_s, *coff;
-    float* bco;
-    T *W, *U, *h, *Vn, *dvloc, *dh, *dVn, *dW;
+    T *W, *U;
+    T* Tc;                                 // bf16 path
+    T *h, *dh;                             // chunk states / end-state gradients
+    float* bco;                            // generic path from here on
+    T *Vn, *dvloc, *dVn, *dW;
     float* dKp;
-    T* Tc;  // per-chunk bf16 T of the WY prep (bf16 path)
 };
+
+template <typename T>
+static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** coff, T** W,
+                         T** U, T** Tc) {
+    *cu_s = c.take<int32_t>(p.N + 1);
+    *coff = c.take<int32_t>(p.N + 1);
+    *W = c.take<T>((size_t)p.ntok * p.H * p.K);
+    *U = c.take<T>((size_t)p.ntok * p.H * p.V);
+    *Tc = __is_same(T, bf16) ? c.take<T>((size_t)p.slots * p.H * 64 * 64) : nullptr;
+}
 
 template <typename T>
 static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out) {
     Carve c(base);
-    FwdWs<T> w;
-    w.cu_s = c.take<int32_t>(p.N + 1);
-    w.coff = c.take<int32_t>(p.N + 1);
-    w.bco = c.take<float>((size_t)p.ntok * p.H);
-    w.W = c.take<T>((size_t)p.ntok * p.H * p.K);
-    w.U = c.take<T>((size_t)p.ntok * p.H * p.V);
-    w.h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
-    w.Vn = c.take<T>((size_t)p.ntok * p.H * p.V);
+    FwdWs<T> w{};
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc);
+    if (!__is_same(T, bf16)) {
+        w.bco = c.take<float>((size_t)p.ntok * p.H);
+        w.h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
+        w.Vn = c.take<T>((size_t)p.ntok * p.H * p.V);
+    }
     if (out) *out = w;
     return c.off + 256;
 }
@@ -838,20 +854,18 @@ static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out) {
 template <typename T>
 static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
     Carve c(base);
-    BwdWs<T> w;
-    w.cu_s = c.take<int32_t>(p.N + 1);
-    w.coff = c.take<int32_t>(p.N + 1);
-    w.bco = c.take<float>((size_t)p.ntok * p.H);
-    w.W = c.take<T>((size_t)p.ntok * p.H * p.K);
-    w.U = c.take<T>((size_t)p.ntok * p.H * p.V);
+    BwdWs<T> w{};
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc);
     w.h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
-    w.Vn = c.take<T>((size_t)p.ntok * p.H * p.V);
-    w.dvloc = c.take<T>((size_t)p.ntok * p.H * p.V);
     w.dh = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
-    w.dVn = c.take<T>((size_t)p.ntok * p.H * p.V);
-    w.dW = c.take<T>((size_t)p.ntok * p.H * p.K);
-    w.dKp = c.take<float>((size_t)p.ntok * p.H * p.K);
-    w.Tc = c.take<T>((size_t)p.slots * p.H * 64 * 64);
+    if (!__is_same(T, bf16)) {
+        w.bco = c.take<float>((size_t)p.ntok * p.H);
+        w.Vn = c.take<T>((size_t)p.ntok * p.H * p.V);
+        w.dvloc = c.take<T>((size_t)p.ntok * p.H * p.V);
+        w.dVn = c.take<T>((size_t)p.ntok * p.H * p.V);
+        w.dW = c.take<T>((size_t)p.ntok * p.H * p.K);
+        w.dKp = c.take<float>((size_t)p.ntok * p.H * p.K);
+    }
     if (out) *out = w;
     return c.off + 256;
 }
@@ -888,7 +902,7 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const int H = p.H;
     if constexpr (__is_same(T, bf16)) {
         EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K, V>), dim3(H, p.slots),
-                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, (bf16*)nullptr);
+                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, w.Tc);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
                     dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, w.W, w.U, si, H, S0,
                     ST, o);
@@ -906,17 +920,20 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
 template <typename T, int K, int V>
 static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T* beta,
                    const float* S0, const T* dO, const float* dST, T* dq, T* dk, T* dv,
-                   T* dbeta, float* dS0, const int32_t* cu, void* ws, hipStream_t st) {
+                   T* dbeta, float* dS0, const int32_t* cu, void* ws, bool reuse,
+                   hipStream_t st) {
     BwdWs<T> w;
     carve_bwd<T>(p, ws, &w);
     EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, st));
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
-    // forward recompute: W, U, chunk states and Vn (nothing is kept from the forward)
+    // forward recompute: W, U, T unless the forward's are in the workspace
+    // (reuse), then always the chunk states
     if constexpr (__is_same(T, bf16)) {
         const dim3 scan_grid(p.N * H * (V / fast::VS));
-        EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(H, p.slots),
-                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, w.Tc);
+        if (!reuse)
+            EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(H, p.slots),
+                        dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, w.Tc);
         EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
                     dim3(fast::NT), st, k, w.W, w.U, si, H, S0, w.h);
         EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V>), scan_grid,
@@ -925,7 +942,7 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
                     dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc, w.h, w.dh, si,
                     H, dq, dk, dv, dbeta);
         return (int)hipPeekAtLastError();
-    } else {
+    } else if (!reuse) {
         EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H),
                     dim3(NTH), st, k, v, beta, si, H, w.bco, w.W, w.U);
     }
@@ -1103,13 +1120,16 @@ extern "C" int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, c
                                   const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
                                   size_t num_seqs, size_t num_heads, size_t head_dim_k,
                                   size_t head_dim_v, size_t chunk_size, int dtype,
-                                  void* workspace, size_t workspace_bytes,
+                                  void* workspace, size_t workspace_bytes, unsigned flags,
                                   hipStream_t stream) {
     Problem p;
     bool empty;
     int rc = make_problem(q, k, v, beta, cu_seqlens, batch_size, seq_len, num_seqs, num_heads,
                           head_dim_k, head_dim_v, chunk_size, dtype, &p, &empty);
     if (rc != kSuccess) return rc;
+    if ((flags & ~(unsigned)EFLA_BWD_REUSE_FORWARD) != 0) return kInvalidValue;
+    const bool reuse = (flags & EFLA_BWD_REUSE_FORWARD) != 0;
+    if (reuse && workspace == nullptr) return kInvalidValue;
     const size_t sbytes = (size_t)p.N * p.H * p.K * p.V * sizeof(float);
     if (empty) {
         if (grad_initial_state == nullptr) return kSuccess;
@@ -1132,14 +1152,14 @@ extern "C" int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, c
         EFLA_Q_DISPATCH_BF16(run_bwd, p, (const bf16*)q, (const bf16*)k, (const bf16*)v,
                              (const bf16*)beta, initial_state, (const bf16*)grad_output,
                              grad_final_state, (bf16*)grad_q, (bf16*)grad_k, (bf16*)grad_v,
-                             (bf16*)grad_beta, grad_initial_state, cu_seqlens, ws, stream);
+                             (bf16*)grad_beta, grad_initial_state, cu_seqlens, ws, reuse, stream);
     } else {
         return run_bwd<float, 64, 64>(p, (const float*)q, (const float*)k, (const float*)v,
                                       (const float*)beta, initial_state,
                                       (const float*)grad_output, grad_final_state,
                                       (float*)grad_q, (float*)grad_k, (float*)grad_v,
                                       (float*)grad_beta, grad_initial_state, cu_seqlens, ws,
-                                      stream);
+                                      reuse, stream);
     }
     return kInvalidValue;
 }

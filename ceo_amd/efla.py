@@ -135,9 +135,18 @@ def chunk_efla_fwd(q, k, v, beta, initial_state=None, output_final_state=False,
     return o, st
 
 
+REUSE_FORWARD = 1  # EFLA_BWD_REUSE_FORWARD
+
+
 def chunk_efla_bwd(q, k, v, beta, do, initial_state=None, dht=None, cu_seqlens=None,
-                   workspace=None):
-    """Returns (dq, dk, dv, dbeta, dh0 or None)."""
+                   workspace=None, reuse_forward=False):
+    """Returns (dq, dk, dv, dbeta, dh0 or None).
+
+    With ``reuse_forward`` the ``workspace`` must be the one the forward call on
+    the same inputs used (untouched since): the per-chunk WY factors are taken
+    from it instead of being recomputed."""
+    if reuse_forward and workspace is None:
+        raise ValueError("reuse_forward needs the forward's workspace")
     B, T, H, K, V, N, dt = _q_shapes(q, k, v, beta, cu_seqlens)
     _require(do, "do", q.dtype, q.device)
     if do.shape != v.shape:
@@ -157,23 +166,39 @@ def chunk_efla_bwd(q, k, v, beta, do, initial_state=None, dht=None, cu_seqlens=N
     rc = lib().efla_chunk_bwd_hip(_p(q), _p(k), _p(v), _p(beta), _p(initial_state), _p(do),
                                   _p(dht), _p(dq), _p(dk), _p(dv), _p(db), _p(dh0),
                                   _p(cu_seqlens), B, T, N if cu_seqlens is not None else 0, H,
-                                  K, V, 64, dt, _p(workspace), ws_bytes, _stream(q))
+                                  K, V, 64, dt, _p(workspace), ws_bytes,
+                                  REUSE_FORWARD if reuse_forward else 0, _stream(q))
     check(rc, "efla_chunk_bwd_hip")
     return dq, dk, dv, db, dh0
 
 
+def new_workspace(q, v, cu_seqlens=None) -> torch.Tensor:
+    """A workspace large enough for the backward of this problem (and so for its
+    forward), for passing to both calls with reuse_forward."""
+    B, T, H, K = q.shape
+    N = 0 if cu_seqlens is None else cu_seqlens.numel() - 1
+    n = workspace_bytes("bwd", B, T, H, K, v.shape[-1], q.dtype, N)
+    return torch.empty(n, dtype=torch.uint8, device=q.device)
+
+
 class ChunkEflaFunction(torch.autograd.Function):
+    """Keeps the forward's workspace (W, U, T per chunk) for the backward,
+    which still recomputes the chunk states."""
+
     @staticmethod
     def forward(ctx, q, k, v, beta, initial_state, output_final_state, cu_seqlens):
-        o, st = chunk_efla_fwd(q, k, v, beta, initial_state, output_final_state, cu_seqlens)
-        ctx.save_for_backward(q, k, v, beta, initial_state, cu_seqlens)
+        ws = new_workspace(q, v, cu_seqlens)
+        o, st = chunk_efla_fwd(q, k, v, beta, initial_state, output_final_state, cu_seqlens,
+                               workspace=ws)
+        ctx.save_for_backward(q, k, v, beta, initial_state, cu_seqlens, ws)
         return o, st
 
     @staticmethod
     def backward(ctx, do, dht):
-        q, k, v, beta, s0, cu = ctx.saved_tensors
+        q, k, v, beta, s0, cu, ws = ctx.saved_tensors
         dq, dk, dv, db, dh0 = chunk_efla_bwd(q, k, v, beta, do.contiguous(), s0,
-                                             None if dht is None else dht.contiguous(), cu)
+                                             None if dht is None else dht.contiguous(), cu,
+                                             workspace=ws, reuse_forward=True)
         return dq, dk, dv, db, dh0, None, None
 
 

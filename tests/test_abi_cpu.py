@@ -82,6 +82,22 @@ def test_chunk_fwd_validation(L):
     assert _fwd(L, ws=ctypes.c_void_p(256), wsb=16) == 1   # workspace too small
 
 
+def _bwd(L, flags=0, ws=None, wsb=0, T=128, **kw):
+    vp = ctypes.c_void_p
+    p = vp(16)
+    return L.efla_chunk_bwd_hip(p, p, p, p, None, p, None, p, p, p, p, None, None, 2, T, 0, 2,
+                                64, 64, 64, 14, ws, wsb, flags, None)
+
+
+def test_chunk_bwd_flags(L):
+    # unknown flag bits, and reusing the forward's factors without a workspace
+    assert _bwd(L, flags=2) == 1
+    assert _bwd(L, flags=1) == 1
+    assert _bwd(L, flags=1, ws=ctypes.c_void_p(256), wsb=16) == 1  # workspace too small
+    assert _bwd(L, flags=1, T=0) == 1   # flags are checked before the empty case
+    assert _bwd(L, flags=0, T=0) == 0
+
+
 def test_workspace_sizes(L):
     f = L.efla_chunk_fwd_workspace_size
     b = L.efla_chunk_bwd_workspace_size
@@ -90,7 +106,7 @@ def test_workspace_sizes(L):
     bw = b(4, 8192, 0, 32, 128, 128, 14)
     ntok = 4 * 8192
     per_tok = 32 * 128 * 2
-    assert fw >= 3 * ntok * per_tok          # W, U, Vn
+    assert fw >= 2 * ntok * per_tok          # W, U
     assert bw > fw
     assert bw < 16 * 2**30                   # fits comfortably in 288 GB
     assert f(4, 8192, 0, 32, 96, 128, 14) == 0

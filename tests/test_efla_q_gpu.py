@@ -137,3 +137,27 @@ def test_autograd_function(oracle):
     rg = oracle.q_backward(x["q"], x["k"], x["v"], x["beta"], x["do"], T=T)
     for name, ref in zip(("q", "k", "v", "beta"), rg[:4]):
         assert rel_l2(g[name].grad, ref) <= 1e-4, name
+
+
+@pytest.mark.parametrize("dtype,K,V", [(torch.bfloat16, 128, 128), (torch.bfloat16, 64, 256),
+                                       (torch.float32, 64, 64)])
+def test_backward_reusing_forward_factors(oracle, dtype, K, V):
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd, new_workspace
+
+    announce(f"chunk_efla reuse_forward {dtype} K={K} V={V}")
+    B, T, H = 2, 200, 2
+    x = oracle.make_efla_inputs(91, B * T, H, K, V, bf16=dtype == torch.bfloat16)
+    g = {n: to_dev(a, dtype, (B, T, H, K) if n in "qk" else
+                   (B, T, H) if n == "beta" else (B, T, H, V)) for n, a in x.items()}
+    ws = new_workspace(g["q"], g["v"])
+    chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], workspace=ws)
+    got = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], workspace=ws,
+                         reuse_forward=True)
+    ref = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"])
+    torch.cuda.synchronize()
+    for a, b, n in zip(got[:4], ref[:4], ("dq", "dk", "dv", "dbeta")):
+        if dtype == torch.bfloat16:
+            assert torch.equal(a, b), n  # same kernels, same order: bit-identical
+        else:
+            # the generic fp32 path sums dL/db with LDS float atomics, whose order varies
+            assert rel_l2(a, b.float().cpu().numpy()) <= 1e-6, n
