@@ -804,23 +804,26 @@ struct Problem {
     int nt;         // chunks per sequence (fixed-length case)
 };
 
-// Workspace layouts.  Both start with the same prefix (sequence offsets, W, U
-// and, on the bf16 path, the per-chunk T), so a backward call given the
-// forward's workspace finds the forward's W, U, T in place.
+// Workspace layouts.  Both start with the same prefix (sequence offsets and
+// the per-chunk WY data: bf16 T and fp32 b on the bf16 path, W and U on the
+// generic path), so a backward call given the forward's workspace finds the
+// forward's factors in place.
 template <typename T>
 struct FwdWs {
     int32_t *cu_s, *coff;
-    T *W, *U;
-    T* Tc;      // per-chunk bf16 T (bf16 path)
-    float* bco; // generic path
-    T *h, *Vn;  // generic path
+    T *W, *U;     // generic path
+    bf16* Tc;     // bf16 path
+    float* bc;    // bf16 path
+    float* bco;   // generic path
+    T *h, *Vn;    // generic path
 };
 
 template <typename T>
 struct BwdWs {
     int32_t *cu_s, *coff;
     T *W, *U;
-    T* Tc;                                 // bf16 path
+    bf16* Tc;
+    float* bc;
     T *h, *dh;                             // chunk states / end-state gradients
     float* bco;                            // generic path from here on
     T *Vn, *dvloc, *dVn, *dW;
@@ -829,19 +832,26 @@ struct BwdWs {
 
 template <typename T>
 static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** coff, T** W,
-                         T** U, T** Tc) {
+                         T** U, bf16** Tc, float** bc) {
     *cu_s = c.take<int32_t>(p.N + 1);
     *coff = c.take<int32_t>(p.N + 1);
-    *W = c.take<T>((size_t)p.ntok * p.H * p.K);
-    *U = c.take<T>((size_t)p.ntok * p.H * p.V);
-    *Tc = __is_same(T, bf16) ? c.take<T>((size_t)p.slots * p.H * 64 * 64) : nullptr;
+    if (__is_same(T, bf16)) {
+        *W = *U = nullptr;
+        *Tc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
+        *bc = c.take<float>((size_t)p.slots * p.H * 64);
+    } else {
+        *W = c.take<T>((size_t)p.ntok * p.H * p.K);
+        *U = c.take<T>((size_t)p.ntok * p.H * p.V);
+        *Tc = nullptr;
+        *bc = nullptr;
+    }
 }
 
 template <typename T>
 static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out) {
     Carve c(base);
     FwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc);
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc);
     if (!__is_same(T, bf16)) {
         w.bco = c.take<float>((size_t)p.ntok * p.H);
         w.h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
@@ -855,7 +865,7 @@ template <typename T>
 static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
     Carve c(base);
     BwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc);
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc);
     w.h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
     w.dh = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
     if (!__is_same(T, bf16)) {
@@ -901,11 +911,11 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
     if constexpr (__is_same(T, bf16)) {
-        EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K, V>), dim3(H, p.slots),
-                    dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, w.Tc);
+        EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
+                    dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
-                    dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, w.W, w.U, si, H, S0,
-                    ST, o);
+                    dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, v, w.Tc, w.bc, si,
+                    H, S0, ST, o);
         return (int)hipPeekAtLastError();
     }
     EFLA_LAUNCH("efla_q_fwd_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH), st,
@@ -932,12 +942,14 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
     if constexpr (__is_same(T, bf16)) {
         const dim3 scan_grid(p.N * H * (V / fast::VS));
         if (!reuse)
-            EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K, V>), dim3(H, p.slots),
-                        dim3(fast::NT), st, k, v, beta, si, H, w.W, w.U, w.Tc);
+            EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
+                        dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc);
         EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
-                    dim3(fast::NT), st, k, w.W, w.U, si, H, S0, w.h);
+                    dim3(fast::NT), st, k, v, (const bf16*)w.Tc, (const float*)w.bc, si, H, S0,
+                    w.h);
         EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V>), scan_grid,
-                    dim3(fast::NT), st, q, k, w.W, dO, si, H, dST, dS0, w.dh);
+                    dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc, si, H,
+                    dST, dS0, w.dh);
         EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V>), dim3(H, p.slots),
                     dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc, w.h, w.dh, si,
                     H, dq, dk, dv, dbeta);

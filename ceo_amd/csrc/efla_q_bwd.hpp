@@ -21,7 +21,8 @@
 //   S through the chunks as in scan_o_kernel; writes each chunk's start state
 //   h_n to `hist` as bf16 [chunk][head][v][f].
 // scan_dh_kernel  (reverse, same grid)
-//   dS through the chunks backwards; writes each chunk's end-state gradient to
+//   dS through the chunks backwards (dVn = P^T dO + K dS, Z = D T^T dVn,
+//   dS <- dS + Q^T dO - K^T Z); writes each chunk's end-state gradient to
 //   `dhist` in the same layout, and dS_0.
 // grad_kernel     (grid: chunk slots x H)
 //   everything above for one chunk from q, k, v, beta, dO, h, dh, looping over
@@ -68,9 +69,10 @@ __device__ __forceinline__ void store_state_vf(bf16* __restrict__ hist, const fl
 // ---------------------------------------------------------------------------
 template <int K>
 struct ScanHBuf {
-    bf16 W[64 * ldb<K>()];
     bf16 Kr[64 * ldb<K>()];
-    bf16 U[64 * LD64];
+    bf16 Vs[64 * LD64];  // v[:, slice]
+    bf16 T[64 * LD64];
+    float b[64];
 };
 
 template <int K>
@@ -80,8 +82,9 @@ struct ScanHSmem {
 
 template <int K, int V>
 __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
-                                                    const bf16* __restrict__ W,
-                                                    const bf16* __restrict__ U, SeqInfo si,
+                                                    const bf16* __restrict__ v,
+                                                    const bf16* __restrict__ Tc,
+                                                    const float* __restrict__ bc, SeqInfo si,
                                                     int H, const float* __restrict__ S0,
                                                     bf16* __restrict__ hist) {
     constexpr int LDK = ldb<K>(), NVS = V / VS;
@@ -105,23 +108,15 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
 #pragma unroll
             for (int i = 0; i < 4; ++i) S[fb][i] = S0[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
     }
-    mf::TileRegs<64, K, NT> rw, rk;
-    mf::TileRegs<64, VS, NT> ru;
+    ChunkRegs<K, false, true> pre;
     auto prefetch = [&](int n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
-        rw.load(W + (bos * H + h) * K, (long)H * K, len);
-        rk.load(k + (bos * H + h) * K, (long)H * K, len);
-        ru.load(U + (bos * H + h) * V + v0, (long)H * V, len);
-    };
-    auto stage = [&](ScanHBuf<K>& b) {
-        rw.store_rows(b.W, LDK);
-        rk.store_rows(b.Kr, LDK);
-        ru.store_rows(b.U, LD64);
+        pre.load(nullptr, k, v, Tc, bc, bos, len, H, h, V, v0, (long)(slot0 + n) * H + h);
     };
     if (nch > 0) {
         prefetch(0);
-        stage(sm.buf[0]);
+        pre.stage(sm.buf[0]);
         if (nch > 1) prefetch(1);
     }
     for (int n = 0; n < nch; ++n) {
@@ -130,17 +125,9 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
         store_state_vf<K>(hist + ((long)(slot0 + n) * H + h) * V * K, S, vcol);
         bf16x8 sb[K / 32];
 #pragma unroll
-        for (int kb = 0; kb < K / 32; ++kb) sb[kb] = mf::neg(frag_from_c(S[2 * kb], S[2 * kb + 1]));
+        for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(S[2 * kb], S[2 * kb + 1]);
         floatx4 vn[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-            const bf16x4 u = tr_rows4(cb.U, LD64, 32 * (tb >> 1) + 4 * (tb & 1), 16 * w, 4);
-            vn[tb] = floatx4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]};
-            const int row = pim(tb, r);
-#pragma unroll
-            for (int kb = 0; kb < K / 32; ++kb)
-                vn[tb] = mma(frag_row(cb.W, LDK, row, 32 * kb), sb[kb], vn[tb]);
-        }
+        chunk_vn<K>(cb, w, sb, vn);
         const bf16x8 vb0 = frag_from_c(vn[0], vn[1]), vb1 = frag_from_c(vn[2], vn[3]);
 #pragma unroll
         for (int fb = 0; fb < K / 16; ++fb) {
@@ -149,7 +136,7 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
             S[fb] = mma(frag_tr(cb.Kr, LDK, 32, c0, 8), vb1, S[fb]);
         }
         if (n + 1 < nch) {
-            stage(sm.buf[(n + 1) & 1]);
+            pre.stage(sm.buf[(n + 1) & 1]);
             if (n + 2 < nch) prefetch(n + 2);
         }
     }
@@ -162,8 +149,9 @@ template <int K>
 struct ScanDhBuf {
     bf16 Q[64 * ldb<K>()];
     bf16 Kr[64 * ldb<K>()];
-    bf16 W[64 * ldb<K>()];
-    bf16 dO[64 * LD64];  // dO[:, slice]
+    bf16 Vs[64 * LD64];  // dO[:, slice]
+    bf16 T[64 * LD64];
+    float b[64];
 };
 
 template <int K>
@@ -175,8 +163,9 @@ struct ScanDhSmem {
 template <int K, int V>
 __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
                                                      const bf16* __restrict__ k,
-                                                     const bf16* __restrict__ W,
-                                                     const bf16* __restrict__ dO, SeqInfo si,
+                                                     const bf16* __restrict__ dO,
+                                                     const bf16* __restrict__ Tc,
+                                                     const float* __restrict__ bc, SeqInfo si,
                                                      int H, const float* __restrict__ dST,
                                                      float* __restrict__ dS0,
                                                      bf16* __restrict__ dhist) {
@@ -202,25 +191,15 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
             for (int i = 0; i < 4; ++i) dS[fb][i] = dST[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
     }
     for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;
-    mf::TileRegs<64, K, NT> rq, rk, rw;
-    mf::TileRegs<64, VS, NT> rd;
+    ChunkRegs<K, true, true> pre;
     auto prefetch = [&](int n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
-        rq.load(q + (bos * H + h) * K, (long)H * K, len);
-        rk.load(k + (bos * H + h) * K, (long)H * K, len);
-        rw.load(W + (bos * H + h) * K, (long)H * K, len);
-        rd.load(dO + (bos * H + h) * V + v0, (long)H * V, len);
-    };
-    auto stage = [&](ScanDhBuf<K>& b) {
-        rq.store_rows(b.Q, LDK);
-        rk.store_rows(b.Kr, LDK);
-        rw.store_rows(b.W, LDK);
-        rd.store_rows(b.dO, LD64);
+        pre.load(q, k, dO, Tc, bc, bos, len, H, h, V, v0, (long)(slot0 + n) * H + h);
     };
     if (nch > 0) {
         prefetch(nch - 1);
-        stage(sm.buf[(nch - 1) & 1]);
+        pre.stage(sm.buf[(nch - 1) & 1]);
         if (nch > 1) prefetch(nch - 2);
     }
     for (int n = nch - 1; n >= 0; --n) {
@@ -242,8 +221,9 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(dS[2 * kb], dS[2 * kb + 1]);
-        const bf16x8 do0 = frag_tr(cb.dO, LD64, 0, 16 * w), do1 = frag_tr(cb.dO, LD64, 32, 16 * w);
-        // K dS part of dVn (P^T dO is added once P is complete)
+        const bf16x8 do0 = frag_tr(cb.Vs, LD64, 0, 16 * w), do1 = frag_tr(cb.Vs, LD64, 32, 16 * w);
+        // K dS part of dVn (P^T dO is added once P is complete); tile tb row
+        // 4g + i is token pim(tb, 4g + i)
         floatx4 dvn[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
@@ -254,28 +234,40 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
             dvn[tb] = acc;
         }
         if (n > 0) {
-            stage(sm.buf[(n - 1) & 1]);
+            pre.stage(sm.buf[(n - 1) & 1]);
             if (n > 1) prefetch(n - 2);
         }
         __syncthreads();  // P complete
-        // dVn += P^T dO; tile tb row 4g + i is token pim(tb, 4g + i)
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
             const int c0 = 32 * (tb >> 1) + 4 * (tb & 1);
             if (tb < 2) dvn[tb] = mma(frag_tr(sm.P, LD64, 0, c0, 8), do0, dvn[tb]);
             dvn[tb] = mma(frag_tr(sm.P, LD64, 32, c0, 8), do1, dvn[tb]);
         }
-        const bf16x8 nd0 = mf::neg(frag_from_c(dvn[0], dvn[1]));
-        const bf16x8 nd1 = mf::neg(frag_from_c(dvn[2], dvn[3]));
-        // dS <- dS + Q^T dO - W^T dVn
+        // Z = D T^T dVn (k = t'' >= t)
+        const bf16x8 dv0 = frag_from_c(dvn[0], dvn[1]), dv1 = frag_from_c(dvn[2], dvn[3]);
+        floatx4 z[4];
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const int c0 = 32 * (tb >> 1) + 4 * (tb & 1);
+            floatx4 acc = zero4();
+            if (tb < 2) acc = mma(frag_tr(cb.T, LD64, 0, c0, 8), dv0, acc);
+            acc = mma(frag_tr(cb.T, LD64, 32, c0, 8), dv1, acc);
+            const floatx4 bb = *reinterpret_cast<const floatx4*>(cb.b + pim(tb, 4 * g));
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] *= -bb[i];  // -D Y
+            z[tb] = acc;
+        }
+        const bf16x8 nz0 = frag_from_c(z[0], z[1]), nz1 = frag_from_c(z[2], z[3]);
+        // dS <- dS + Q^T dO - K^T Z
 #pragma unroll
         for (int fb = 0; fb < K / 16; ++fb) {
             const int c0 = 32 * (fb >> 1) + 4 * (fb & 1);
             floatx4 acc = dS[fb];
             acc = mma(frag_tr(cb.Q, LDK, 0, c0, 8), do0, acc);
             acc = mma(frag_tr(cb.Q, LDK, 32, c0, 8), do1, acc);
-            acc = mma(frag_tr(cb.W, LDK, 0, c0, 8), nd0, acc);
-            acc = mma(frag_tr(cb.W, LDK, 32, c0, 8), nd1, acc);
+            acc = mma(frag_tr(cb.Kr, LDK, 0, c0, 8), nz0, acc);
+            acc = mma(frag_tr(cb.Kr, LDK, 32, c0, 8), nz1, acc);
             dS[fb] = acc;
         }
     }

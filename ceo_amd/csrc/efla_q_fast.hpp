@@ -1,17 +1,20 @@
 // bf16 chunked EFLA kernels tuned for gfx950 (included by efla_q.hip after
-// the SeqInfo helpers).  Same algorithm and workspace layout as the generic
-// kernels in efla_q.hip; these keep operands in MFMA fragment registers
-// instead of re-staging them, read LDS with 8/16-byte vectors, write global
-// memory in 16-byte row segments, and prefetch the next chunk while the
-// current one computes.
+// the SeqInfo helpers).  These keep operands in MFMA fragment registers
+// instead of re-staging them, read LDS with 16-byte and transposing reads,
+// write global memory in 8/16-byte pieces, and prefetch the next chunk while
+// the current one computes.
 //
-// prep_kernel   (grid: chunk slots x H)
-//   b = c(beta, |k|^2); T = (I + strict_lower(diag(b) K K^T))^{-1} in fp32;
-//   W = T diag(b) K, U = T diag(b) V (bf16, token layout like k / v).
-// scan_kernel   (grid: sequences x H x V/64, one 64-wide value slice each)
+// With b = c(beta, |k|^2), D = diag(b), T = (I + strict_lower(D K K^T))^{-1}
+// the chunk's effective values are Vn = T D (V - K S) (= U - W S with the WY
+// factors W = T D K, U = T D V, which are never materialised).
+//
+// prep_kernel   (grid: H x chunk slots)
+//   b and T (fp32 solve) for one chunk; writes bf16 T [64][64] (zero above the
+//   diagonal) and fp32 b [64].
+// scan_o_kernel (grid: sequences x H x V/64, one 64-wide value slice each)
 //   carries S[:, slice] (K x 64, fp32) through the chunks of one sequence in
 //   MFMA accumulators (wave w owns value columns 16w..16w+15) and per chunk
-//     Vn = U - W S,  o = Q S + tril(Q K^T) Vn,  S <- S + K^T Vn.
+//     R = V - K S,  Vn = T D R,  o = Q S + tril(Q K^T) Vn,  S <- S + K^T Vn.
 #pragma once
 #include "mfma.hpp"
 
@@ -54,37 +57,34 @@ constexpr int ldb() {  // bf16 row stride: D + 16 keeps b128, b64 and tr16 reads
 // ---------------------------------------------------------------------------
 // prep
 // ---------------------------------------------------------------------------
-template <int K, int V>
+template <int K>
 struct PrepSmem {
-    bf16 Kr[64 * ldb<K>()];
-    bf16 Vr[64 * ldb<V>()];
+    union {
+        bf16 Kr[64 * ldb<K>()];  // k, until K K^T is formed
+        float T[64 * LDF];       // (I + A)^{-1}
+    } u;
     float G[64 * LDF];  // K K^T (lower tiles)
-    float T[64 * LDF];  // (I + A)^{-1}
     float lam[64];
     float b[64];
 };
 
-template <int K, int V>
+template <int K>
 __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
-                                                  const bf16* __restrict__ v,
                                                   const bf16* __restrict__ beta, SeqInfo si,
-                                                  int H, bf16* __restrict__ Wout,
-                                                  bf16* __restrict__ Uout,
-                                                  bf16* __restrict__ Tout) {
-    constexpr int LDK = ldb<K>(), LDV = ldb<V>();
-    __shared__ __attribute__((aligned(16))) PrepSmem<K, V> sm;
+                                                  int H, bf16* __restrict__ Tout,
+                                                  float* __restrict__ bout) {
+    constexpr int LDK = ldb<K>();
+    __shared__ __attribute__((aligned(16))) PrepSmem<K> sm;
     const int h = blockIdx.x, slot = blockIdx.y;  // heads fastest: one chunk's rows stay together
     long bos;
     int len;
     if (!locate_chunk(si, slot, bos, len)) return;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
+    const long cid = (long)slot * H + h;
     {
         mf::TileRegs<64, K, NT> kt;
-        mf::TileRegs<64, V, NT> vt;
         kt.load(k + (bos * H + h) * K, (long)H * K, len);
-        vt.load(v + (bos * H + h) * V, (long)H * V, len);
-        kt.store_rows(sm.Kr, LDK);
-        vt.store_rows(sm.Vr, LDV);
+        kt.store_rows(sm.u.Kr, LDK);
 #pragma unroll
         for (int j = 0; j < kt.TPT; ++j) {
             const float s = kt.row_sumsq(j);
@@ -97,6 +97,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
         float c = 0.f, dcl, dcb;
         if (t < len) efla_coeff(sm.lam[t], (float)beta[(bos + t) * H + h], c, dcl, dcb);
         sm.b[t] = c;
+        bout[cid * 64 + t] = c;
     }
     // G = K K^T, lower tiles
     for (int n = w; n < 10; n += 4) {
@@ -105,12 +106,12 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
         floatx4 acc = zero4();
 #pragma unroll
         for (int k0 = 0; k0 < K; k0 += 32)
-            acc = mma(frag_nat(sm.Kr, LDK, 16 * I, k0), frag_nat(sm.Kr, LDK, 16 * J, k0), acc);
+            acc = mma(frag_nat(sm.u.Kr, LDK, 16 * I, k0), frag_nat(sm.u.Kr, LDK, 16 * J, k0), acc);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sm.G[(16 * I + 4 * g + i) * LDF + 16 * J + r] = acc[i];
     }
-    __syncthreads();
-    float* T = sm.T;
+    __syncthreads();  // k is dead from here; T takes its place
+    float* T = sm.u.T;
     // diagonal 16x16 blocks of T by forward substitution (lane = column)
     if (l < 16) {
         const int base = 16 * w;
@@ -142,8 +143,8 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
         }
         __syncthreads();
     }
-    // optional bf16 copy of T for the backward: [t][t'], zero above the diagonal
-    if (Tout) {
+    // bf16 T [t][t'], zero above the diagonal
+    {
         const int tr = threadIdx.x >> 2, c0 = 16 * (threadIdx.x & 3);
         bf16x8 lo, hi;
 #pragma unroll
@@ -151,48 +152,9 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
             lo[c] = (bf16)(c0 + c <= tr ? T[tr * LDF + c0 + c] : 0.f);
             hi[c] = (bf16)(c0 + 8 + c <= tr ? T[tr * LDF + c0 + 8 + c] : 0.f);
         }
-        bf16* dst = Tout + ((long)slot * H + h) * 64 * 64 + tr * 64 + c0;
+        bf16* dst = Tout + cid * 64 * 64 + tr * 64 + c0;
         *reinterpret_cast<bf16x8*>(dst) = lo;
         *reinterpret_cast<bf16x8*>(dst + 8) = hi;
-    }
-    // W^T = K^T (T diag(b))^T and U^T likewise, for token block w.  B operand
-    // (k = t', column t = 16w + r): (T diag(b))[t][t'], zero above the diagonal.
-    const int t = 16 * w + r;
-    const int nks = w >= 2 ? 2 : 1;
-    bf16x8 tb[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int k0 = 32 * ks + 8 * g;
-        const floatx4 t0 = *reinterpret_cast<const floatx4*>(T + t * LDF + k0);
-        const floatx4 t1 = *reinterpret_cast<const floatx4*>(T + t * LDF + k0 + 4);
-        const floatx4 b0 = *reinterpret_cast<const floatx4*>(sm.b + k0);
-        const floatx4 b1 = *reinterpret_cast<const floatx4*>(sm.b + k0 + 4);
-        bf16x8 f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-            f[s] = (bf16)((k0 + s <= t) ? t0[s] * b0[s] : 0.f);
-            f[4 + s] = (bf16)((k0 + 4 + s <= t) ? t1[s] * b1[s] : 0.f);
-        }
-        tb[ks] = f;
-    }
-    const bool live = t < len;
-    bf16* wrow = Wout + ((bos + t) * H + h) * K + 4 * g;
-    bf16* urow = Uout + ((bos + t) * H + h) * V + 4 * g;
-#pragma unroll
-    for (int fb = 0; fb < K / 16; ++fb) {
-        floatx4 acc = mma(mf::frag_tr(sm.Kr, LDK, 0, 16 * fb), tb[0], zero4());
-        if (nks > 1) acc = mma(mf::frag_tr(sm.Kr, LDK, 32, 16 * fb), tb[1], acc);
-        if (live)
-            *reinterpret_cast<bf16x4*>(wrow + 16 * fb) =
-                bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
-    }
-#pragma unroll
-    for (int vb = 0; vb < V / 16; ++vb) {
-        floatx4 acc = mma(mf::frag_tr(sm.Vr, LDV, 0, 16 * vb), tb[0], zero4());
-        if (nks > 1) acc = mma(mf::frag_tr(sm.Vr, LDV, 32, 16 * vb), tb[1], acc);
-        if (live)
-            *reinterpret_cast<bf16x4*>(urow + 16 * vb) =
-                bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
     }
 }
 
@@ -203,10 +165,11 @@ constexpr int VS = 64;  // value slice per workgroup
 
 template <int K>
 struct ScanBuf {
-    bf16 W[64 * ldb<K>()];
     bf16 Q[64 * ldb<K>()];
     bf16 Kr[64 * ldb<K>()];
-    bf16 U[64 * ldb<VS>()];  // U[:, slice]
+    bf16 Vs[64 * ldb<VS>()];  // v[:, slice]
+    bf16 T[64 * ldb<64>()];   // bf16 T [t][t']
+    float b[64];
 };
 
 template <int K>
@@ -217,7 +180,7 @@ struct ScanSmem {
 
 // Workgroup -> (sequence * H + head, value slice).  When the head count
 // allows, the slices of one head get ids that are equal modulo 8 so they run
-// on the same XCD and share its L2 for the W / Q / K tiles they all read.
+// on the same XCD and share its L2 for the Q / K / T tiles they all read.
 __device__ __forceinline__ void scan_map(int id, int NH, int nvs, int& bh, int& vs) {
     if ((NH & 7) == 0) {
         const int grp = id / (8 * nvs), rem = id % (8 * nvs);
@@ -229,17 +192,76 @@ __device__ __forceinline__ void scan_map(int id, int NH, int nvs, int& bh, int& 
     }
 }
 
+// Per-chunk inputs of the scans, loaded one chunk ahead into registers.
+template <int K, bool WITH_Q, bool VALUES>
+struct ChunkRegs {
+    mf::TileRegs<64, K, NT> rq, rk;
+    mf::TileRegs<64, VS, NT> rv;  // v (VALUES) or dO slice
+    mf::TileRegs<64, 64, NT> rt;
+    float b;                      // thread < 64: b of token threadIdx.x
+    __device__ __forceinline__ void load(const bf16* q, const bf16* k, const bf16* vsl,
+                                         const bf16* Tc, const float* bc, long bos, int len,
+                                         int H, int h, int V, int v0, long cid) {
+        if (WITH_Q) rq.load(q + (bos * H + h) * K, (long)H * K, len);
+        rk.load(k + (bos * H + h) * K, (long)H * K, len);
+        rv.load(vsl + (bos * H + h) * V + v0, (long)H * V, len);
+        rt.load(Tc + cid * 64 * 64, 64, 64);
+        if (threadIdx.x < 64) b = bc[cid * 64 + threadIdx.x];
+    }
+    template <typename Buf>
+    __device__ __forceinline__ void stage(Buf& bf) {
+        if constexpr (WITH_Q) rq.store_rows(bf.Q, ldb<K>());
+        rk.store_rows(bf.Kr, ldb<K>());
+        rv.store_rows(bf.Vs, ldb<VS>());
+        rt.store_rows(bf.T, ldb<64>());
+        if (threadIdx.x < 64) bf.b[threadIdx.x] = b;
+    }
+};
+
 // State layout in registers: S[fb] is a C tile whose row r = 4g + i is key
 // index pim(fb, r) and whose column is value v0 + 16 w + (lane & 15).
+// Token tiles (R, Vn) use the same map for their rows: tile tb row 4g + i is
+// token pim(tb, 4g + i).
+// Vn = T D (V - K S) for the chunk staged in `cb` (Kr, Vs, T, b); S is given as
+// natural-order B fragments sb[kb] (k = key index) of this wave's 16 value
+// columns.  Vn tile tb row 4g + i is token pim(tb, 4g + i).
+template <int K, typename Buf>
+__device__ __forceinline__ void chunk_vn(const Buf& cb, int w, const bf16x8* sb, floatx4* vn) {
+    constexpr int LDK = ldb<K>(), LDV = ldb<VS>(), LDT = ldb<64>();
+    const int l = mf::lane(), g = l >> 4, r = l & 15;
+    floatx4 R[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const bf16x4 u = mf::tr_rows4(cb.Vs, LDV, 32 * (tb >> 1) + 4 * (tb & 1), 16 * w, 4);
+        floatx4 acc = floatx4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]};
+        const int row = pim(tb, r);
+#pragma unroll
+        for (int kb = 0; kb < K / 32; ++kb)
+            acc = mma(mf::frag_row(cb.Kr, LDK, row, 32 * kb), mf::neg(sb[kb]), acc);
+        const floatx4 bb = *reinterpret_cast<const floatx4*>(cb.b + pim(tb, 4 * g));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] *= bb[i];  // D R
+        R[tb] = acc;
+    }
+    const bf16x8 dr0 = frag_from_c(R[0], R[1]), dr1 = frag_from_c(R[2], R[3]);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int row = pim(tb, r);
+        vn[tb] = mma(mf::frag_row(cb.T, LDT, row, 0), dr0, zero4());
+        if (tb >= 2) vn[tb] = mma(mf::frag_row(cb.T, LDT, row, 32), dr1, vn[tb]);
+    }
+}
+
 template <int K, int V>
 __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
                                                     const bf16* __restrict__ k,
-                                                    const bf16* __restrict__ W,
-                                                    const bf16* __restrict__ U, SeqInfo si,
+                                                    const bf16* __restrict__ v,
+                                                    const bf16* __restrict__ Tc,
+                                                    const float* __restrict__ bc, SeqInfo si,
                                                     int H, const float* __restrict__ S0,
                                                     float* __restrict__ ST,
                                                     bf16* __restrict__ o) {
-    constexpr int LDK = ldb<K>(), LDU = ldb<VS>(), LDP = ldb<64>(), NVS = V / VS;
+    constexpr int LDK = ldb<K>(), LDV = ldb<VS>(), LDP = ldb<64>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanSmem<K> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
     int bh, vsl;
@@ -262,25 +284,15 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
     }
     for (int i = threadIdx.x; i < 64 * LDP; i += NT) sm.P[i] = (bf16)0.f;
 
-    mf::TileRegs<64, K, NT> rw, rq, rk;
-    mf::TileRegs<64, VS, NT> ru;
+    ChunkRegs<K, true, true> pre;
     auto prefetch = [&](int n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
-        rw.load(W + (bos * H + h) * K, (long)H * K, len);
-        rq.load(q + (bos * H + h) * K, (long)H * K, len);
-        rk.load(k + (bos * H + h) * K, (long)H * K, len);
-        ru.load(U + (bos * H + h) * V + v0, (long)H * V, len);
-    };
-    auto stage = [&](ScanBuf<K>& b) {
-        rw.store_rows(b.W, LDK);
-        rq.store_rows(b.Q, LDK);
-        rk.store_rows(b.Kr, LDK);
-        ru.store_rows(b.U, LDU);
+        pre.load(q, k, v, Tc, bc, bos, len, H, h, V, v0, (long)(slot0 + n) * H + h);
     };
     if (nch > 0) {
         prefetch(0);
-        stage(sm.buf[0]);
+        pre.stage(sm.buf[0]);
         if (nch > 1) prefetch(1);
     }
     for (int n = 0; n < nch; ++n) {
@@ -305,20 +317,11 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(S[2 * kb], S[2 * kb + 1]);
-        // Vn = U - W S; tile tb row 4g + i is token pim(tb, 4g + i)
         floatx4 vn[4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-            const bf16x4 u = mf::tr_rows4(cb.U, LDU, 32 * (tb >> 1) + 4 * (tb & 1), 16 * w, 4);
-            vn[tb] = floatx4{(float)u[0], (float)u[1], (float)u[2], (float)u[3]};
-            const int row = pim(tb, r);
-#pragma unroll
-            for (int kb = 0; kb < K / 32; ++kb)
-                vn[tb] = mma(mf::frag_row(cb.W, LDK, row, 32 * kb), mf::neg(sb[kb]), vn[tb]);
-        }
+        chunk_vn<K>(cb, w, sb, vn);
         // stage chunk n + 1 (its loads were issued one chunk ago), fetch n + 2
         if (n + 1 < nch) {
-            stage(sm.buf[(n + 1) & 1]);
+            pre.stage(sm.buf[(n + 1) & 1]);
             if (n + 2 < nch) prefetch(n + 2);
         }
         __syncthreads();  // P complete
