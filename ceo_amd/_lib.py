@@ -75,7 +75,7 @@ _SIGS = {
     "efla_chunk_fwd_workspace_size": (sz, [sz, sz, sz, sz, sz, sz, i32]),
     "efla_chunk_bwd_workspace_size": (sz, [sz, sz, sz, sz, sz, sz, i32]),
     "efla_chunk_fwd_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz,
-                                 i32, vp, sz, vp]),
+                                 i32, vp, sz, ctypes.c_uint, vp]),
     "efla_chunk_bwd_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz,
                                  sz, sz, sz, sz, sz, i32, vp, sz, ctypes.c_uint, vp]),
     # LayerNorm

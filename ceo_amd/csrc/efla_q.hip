@@ -804,10 +804,11 @@ struct Problem {
     int nt;         // chunks per sequence (fixed-length case)
 };
 
-// Workspace layouts.  Both start with the same prefix (sequence offsets and
-// the per-chunk WY data: bf16 T and fp32 b on the bf16 path, W and U on the
-// generic path), so a backward call given the forward's workspace finds the
-// forward's factors in place.
+// Workspace layouts.  The forward's layout is a prefix of the backward's:
+// sequence offsets, the per-chunk WY data (bf16 T and fp32 b on the bf16 path;
+// W, U and per-token b on the generic path), then the chunk states h (and, on
+// the generic path, Vn).  A backward call given the forward's workspace finds
+// the forward's factors, and its saved states, in place.
 template <typename T>
 struct FwdWs {
     int32_t *cu_s, *coff;
@@ -815,7 +816,8 @@ struct FwdWs {
     bf16* Tc;     // bf16 path
     float* bc;    // bf16 path
     float* bco;   // generic path
-    T *h, *Vn;    // generic path
+    T* h;         // generic path; bf16 path when the states are saved
+    T* Vn;        // generic path
 };
 
 template <typename T>
@@ -824,39 +826,46 @@ struct BwdWs {
     T *W, *U;
     bf16* Tc;
     float* bc;
-    T *h, *dh;                             // chunk states / end-state gradients
-    float* bco;                            // generic path from here on
-    T *Vn, *dvloc, *dVn, *dW;
-    float* dKp;
+    float* bco;  // generic path
+    T* h;        // chunk start states
+    T* Vn;       // generic path
+    T* dh;       // chunk end-state gradients
+    T *dvloc, *dVn, *dW;  // generic path
+    float* dKp;           // generic path
 };
 
+// Takes the common prefix; returns with `c` at the end of h (and Vn).
 template <typename T>
 static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** coff, T** W,
-                         T** U, bf16** Tc, float** bc) {
+                         T** U, bf16** Tc, float** bc, float** bco, T** h, T** Vn,
+                         bool with_h) {
     *cu_s = c.take<int32_t>(p.N + 1);
     *coff = c.take<int32_t>(p.N + 1);
+    *W = *U = nullptr;
+    *Tc = nullptr;
+    *bc = *bco = nullptr;
+    *h = *Vn = nullptr;
     if (__is_same(T, bf16)) {
-        *W = *U = nullptr;
         *Tc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
         *bc = c.take<float>((size_t)p.slots * p.H * 64);
+        if (with_h) *h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
     } else {
         *W = c.take<T>((size_t)p.ntok * p.H * p.K);
         *U = c.take<T>((size_t)p.ntok * p.H * p.V);
-        *Tc = nullptr;
-        *bc = nullptr;
+        *bco = c.take<float>((size_t)p.ntok * p.H);
+        *h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
+        *Vn = c.take<T>((size_t)p.ntok * p.H * p.V);
     }
 }
 
+// with_states: room for the bf16 path's chunk states (the generic path always
+// keeps them)
 template <typename T>
-static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out) {
+static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out, bool with_states) {
     Carve c(base);
     FwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc);
-    if (!__is_same(T, bf16)) {
-        w.bco = c.take<float>((size_t)p.ntok * p.H);
-        w.h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
-        w.Vn = c.take<T>((size_t)p.ntok * p.H * p.V);
-    }
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Vn,
+                    with_states);
     if (out) *out = w;
     return c.off + 256;
 }
@@ -865,12 +874,10 @@ template <typename T>
 static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
     Carve c(base);
     BwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc);
-    w.h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Vn,
+                    true);
     w.dh = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
     if (!__is_same(T, bf16)) {
-        w.bco = c.take<float>((size_t)p.ntok * p.H);
-        w.Vn = c.take<T>((size_t)p.ntok * p.H * p.V);
         w.dvloc = c.take<T>((size_t)p.ntok * p.H * p.V);
         w.dVn = c.take<T>((size_t)p.ntok * p.H * p.V);
         w.dW = c.take<T>((size_t)p.ntok * p.H * p.K);
@@ -904,9 +911,9 @@ static int build_offsets(const Problem& p, const int32_t* cu, int32_t* cu_s, int
 template <typename T, int K, int V>
 static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T* beta,
                    const float* S0, T* o, float* ST, const int32_t* cu, void* ws,
-                   hipStream_t st) {
+                   bool save_states, hipStream_t st) {
     FwdWs<T> w;
-    carve_fwd<T>(p, ws, &w);
+    carve_fwd<T>(p, ws, &w, save_states);
     EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, st));
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
@@ -915,7 +922,7 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
                     dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
                     dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, v, w.Tc, w.bc, si,
-                    H, S0, ST, o);
+                    H, S0, ST, o, w.h);
         return (int)hipPeekAtLastError();
     }
     EFLA_LAUNCH("efla_q_fwd_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH), st,
@@ -931,22 +938,23 @@ template <typename T, int K, int V>
 static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T* beta,
                    const float* S0, const T* dO, const float* dST, T* dq, T* dk, T* dv,
                    T* dbeta, float* dS0, const int32_t* cu, void* ws, bool reuse,
-                   hipStream_t st) {
+                   bool reuse_states, hipStream_t st) {
     BwdWs<T> w;
     carve_bwd<T>(p, ws, &w);
     EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, st));
     const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
     const int H = p.H;
-    // forward recompute: W, U, T unless the forward's are in the workspace
-    // (reuse), then always the chunk states
+    // forward recompute: the WY factors unless the forward's are in the
+    // workspace (reuse), the chunk states unless the forward saved them
     if constexpr (__is_same(T, bf16)) {
         const dim3 scan_grid(p.N * H * (V / fast::VS));
         if (!reuse)
             EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
                         dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc);
-        EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
-                    dim3(fast::NT), st, k, v, (const bf16*)w.Tc, (const float*)w.bc, si, H, S0,
-                    w.h);
+        if (!reuse_states)
+            EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
+                        dim3(fast::NT), st, k, v, (const bf16*)w.Tc, (const float*)w.bc, si, H,
+                        S0, w.h);
         EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V>), scan_grid,
                     dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc, si, H,
                     dST, dS0, w.dh);
@@ -958,9 +966,11 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
         EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H),
                     dim3(NTH), st, k, v, beta, si, H, w.bco, w.W, w.U);
     }
+    // the generic forward keeps its states transposed for its output kernel,
+    // so this path recomputes them whatever reuse_states says
     EFLA_LAUNCH("efla_q_bwd_re_state", (fwd_state_kernel<T, K, V, VS, false>),
-                dim3(p.N * H, V / VS), dim3(NTH), st, k, w.W, w.U, si, H, S0,
-                (float*)nullptr, w.h, w.Vn);
+                dim3(p.N * H, V / VS), dim3(NTH), st, k, w.W, w.U, si, H, S0, (float*)nullptr,
+                w.h, w.Vn);
     EFLA_LAUNCH("efla_q_bwd_dvloc", (bwd_dvloc_kernel<T, K, V, VO>), dim3(p.slots, H, V / VO),
                 dim3(NTH), st, q, k, dO, si, H, w.dvloc);
     EFLA_LAUNCH("efla_q_bwd_state", (bwd_state_kernel<T, K, V, VS>), dim3(p.N * H, V / VS),
@@ -1068,8 +1078,8 @@ extern "C" size_t efla_chunk_fwd_workspace_size(size_t batch_size, size_t seq_le
     Problem p;
     if (!ws_problem(batch_size, seq_len, num_seqs, num_heads, head_dim_k, head_dim_v, dtype, &p))
         return 0;
-    return dtype == kDtypeBF16 ? carve_fwd<bf16>(p, nullptr, nullptr)
-                               : carve_fwd<float>(p, nullptr, nullptr);
+    return dtype == kDtypeBF16 ? carve_fwd<bf16>(p, nullptr, nullptr, false)
+                               : carve_fwd<float>(p, nullptr, nullptr, false);
 }
 
 extern "C" size_t efla_chunk_bwd_workspace_size(size_t batch_size, size_t seq_len,
@@ -1088,13 +1098,16 @@ extern "C" int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, c
                                   const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
                                   size_t num_seqs, size_t num_heads, size_t head_dim_k,
                                   size_t head_dim_v, size_t chunk_size, int dtype,
-                                  void* workspace, size_t workspace_bytes,
+                                  void* workspace, size_t workspace_bytes, unsigned flags,
                                   hipStream_t stream) {
     Problem p;
     bool empty;
     int rc = make_problem(q, k, v, beta, cu_seqlens, batch_size, seq_len, num_seqs, num_heads,
                           head_dim_k, head_dim_v, chunk_size, dtype, &p, &empty);
     if (rc != kSuccess) return rc;
+    if ((flags & ~(unsigned)EFLA_FWD_SAVE_STATES) != 0) return kInvalidValue;
+    const bool save = (flags & EFLA_FWD_SAVE_STATES) != 0;
+    if (save && workspace == nullptr) return kInvalidValue;
     const size_t sbytes = (size_t)p.N * p.H * p.K * p.V * sizeof(float);
     if (empty) {
         if (final_state == nullptr) return kSuccess;
@@ -1104,8 +1117,8 @@ extern "C" int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, c
         return fill_zero(final_state, sbytes, stream);
     }
     if (output == nullptr) return kInvalidValue;
-    const size_t need = dtype == kDtypeBF16 ? carve_fwd<bf16>(p, nullptr, nullptr)
-                                            : carve_fwd<float>(p, nullptr, nullptr);
+    const size_t need = dtype == kDtypeBF16 ? carve_fwd<bf16>(p, nullptr, nullptr, save)
+                                            : carve_fwd<float>(p, nullptr, nullptr, save);
     void* ws = workspace;
     if (ws == nullptr) {
         rc = workspace_acquire(need, stream, &ws);
@@ -1116,11 +1129,11 @@ extern "C" int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, c
     if (dtype == kDtypeBF16) {
         EFLA_Q_DISPATCH_BF16(run_fwd, p, (const bf16*)q, (const bf16*)k, (const bf16*)v,
                              (const bf16*)beta, initial_state, (bf16*)output, final_state,
-                             cu_seqlens, ws, stream);
+                             cu_seqlens, ws, save, stream);
     } else {
         return run_fwd<float, 64, 64>(p, (const float*)q, (const float*)k, (const float*)v,
                                       (const float*)beta, initial_state, (float*)output,
-                                      final_state, cu_seqlens, ws, stream);
+                                      final_state, cu_seqlens, ws, save, stream);
     }
     return kInvalidValue;
 }
@@ -1139,9 +1152,12 @@ extern "C" int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, c
     int rc = make_problem(q, k, v, beta, cu_seqlens, batch_size, seq_len, num_seqs, num_heads,
                           head_dim_k, head_dim_v, chunk_size, dtype, &p, &empty);
     if (rc != kSuccess) return rc;
-    if ((flags & ~(unsigned)EFLA_BWD_REUSE_FORWARD) != 0) return kInvalidValue;
+    if ((flags & ~(unsigned)(EFLA_BWD_REUSE_FORWARD | EFLA_BWD_REUSE_STATES)) != 0)
+        return kInvalidValue;
     const bool reuse = (flags & EFLA_BWD_REUSE_FORWARD) != 0;
-    if (reuse && workspace == nullptr) return kInvalidValue;
+    const bool reuse_states = (flags & EFLA_BWD_REUSE_STATES) != 0;
+    if ((reuse || reuse_states) && workspace == nullptr) return kInvalidValue;
+    if (reuse_states && !reuse) return kInvalidValue;
     const size_t sbytes = (size_t)p.N * p.H * p.K * p.V * sizeof(float);
     if (empty) {
         if (grad_initial_state == nullptr) return kSuccess;
@@ -1164,14 +1180,15 @@ extern "C" int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, c
         EFLA_Q_DISPATCH_BF16(run_bwd, p, (const bf16*)q, (const bf16*)k, (const bf16*)v,
                              (const bf16*)beta, initial_state, (const bf16*)grad_output,
                              grad_final_state, (bf16*)grad_q, (bf16*)grad_k, (bf16*)grad_v,
-                             (bf16*)grad_beta, grad_initial_state, cu_seqlens, ws, reuse, stream);
+                             (bf16*)grad_beta, grad_initial_state, cu_seqlens, ws, reuse,
+                             reuse_states, stream);
     } else {
         return run_bwd<float, 64, 64>(p, (const float*)q, (const float*)k, (const float*)v,
                                       (const float*)beta, initial_state,
                                       (const float*)grad_output, grad_final_state,
                                       (float*)grad_q, (float*)grad_k, (float*)grad_v,
                                       (float*)grad_beta, grad_initial_state, cu_seqlens, ws,
-                                      reuse, stream);
+                                      reuse, reuse_states, stream);
     }
     return kInvalidValue;
 }

@@ -40,9 +40,6 @@ using mf::tr_rows4;
 
 constexpr int LD64 = ldb<64>();
 
-__device__ __forceinline__ void store4(bf16* p, floatx4 a) {
-    *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
-}
 __device__ __forceinline__ void store4s(bf16* p, floatx4 a, float s) {
     *reinterpret_cast<bf16x4*>(p) =
         bf16x4{(bf16)(a[0] * s), (bf16)(a[1] * s), (bf16)(a[2] * s), (bf16)(a[3] * s)};
@@ -54,15 +51,6 @@ __device__ __forceinline__ floatx4 load4(const bf16* p) {
 // keep the compiler from moving LDS accesses across this point and wait for
 // this wave's outstanding LDS operations (a wave reads back what it wrote)
 __device__ __forceinline__ void lds_fence_wave() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-// Write the C tiles of a K x 64 state slice (S[fb] rows pim(fb, 4g + i),
-// column v0 + 16 w + r) to hist[v][f] (row stride K) as bf16, 8 bytes a lane.
-template <int K>
-__device__ __forceinline__ void store_state_vf(bf16* __restrict__ hist, const floatx4* S, int vcol) {
-    const int g = mf::lane() >> 4;
-#pragma unroll
-    for (int fb = 0; fb < K / 16; ++fb) store4(hist + (long)vcol * K + pim(fb, 4 * g), S[fb]);
-}
 
 // ---------------------------------------------------------------------------
 // forward recompute: chunk start states

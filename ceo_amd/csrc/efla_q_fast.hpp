@@ -14,7 +14,9 @@
 // scan_o_kernel (grid: sequences x H x V/64, one 64-wide value slice each)
 //   carries S[:, slice] (K x 64, fp32) through the chunks of one sequence in
 //   MFMA accumulators (wave w owns value columns 16w..16w+15) and per chunk
-//     R = V - K S,  Vn = T D R,  o = Q S + tril(Q K^T) Vn,  S <- S + K^T Vn.
+//     R = V - K S,  Vn = T D R,  o = Q S + tril(Q K^T) Vn,  S <- S + K^T Vn;
+//   optionally writes each chunk's start state to `hist` (bf16 [chunk][head]
+//   [v][f], as the backward reads it) so the backward need not recompute it.
 #pragma once
 #include "mfma.hpp"
 
@@ -52,6 +54,19 @@ __device__ __forceinline__ int pim(int tile, int r) {
 template <int D>
 constexpr int ldb() {  // bf16 row stride: D + 16 keeps b128, b64 and tr16 reads conflict-free
     return D + 16;
+}
+
+__device__ __forceinline__ void store4(bf16* p, floatx4 a) {
+    *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
+}
+
+// Write the C tiles of a K x 64 state slice (S[fb] rows pim(fb, 4g + i),
+// column v0 + 16 w + r) to hist[v][f] (row stride K) as bf16, 8 bytes a lane.
+template <int K>
+__device__ __forceinline__ void store_state_vf(bf16* __restrict__ hist, const floatx4* S, int vcol) {
+    const int g = mf::lane() >> 4;
+#pragma unroll
+    for (int fb = 0; fb < K / 16; ++fb) store4(hist + (long)vcol * K + pim(fb, 4 * g), S[fb]);
 }
 
 // ---------------------------------------------------------------------------
@@ -260,7 +275,8 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
                                                     const float* __restrict__ bc, SeqInfo si,
                                                     int H, const float* __restrict__ S0,
                                                     float* __restrict__ ST,
-                                                    bf16* __restrict__ o) {
+                                                    bf16* __restrict__ o,
+                                                    bf16* __restrict__ hist) {
     constexpr int LDK = ldb<K>(), LDV = ldb<VS>(), LDP = ldb<64>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanSmem<K> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
@@ -300,6 +316,7 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         const int len = (int)min((long)64, slen - (long)n * 64);
         const ScanBuf<K>& cb = sm.buf[n & 1];
         __syncthreads();  // chunk n staged; everyone is done with chunk n - 1
+        if (hist) store_state_vf<K>(hist + ((long)(slot0 + n) * H + h) * V * K, S, vcol);
         // P[t][t'] = q_t . k_t' for t' <= t, lower 16x16 tiles (I = t block,
         // J = t' block) computed transposed so each lane writes 4 consecutive t'
         for (int nt = w; nt < 10; nt += 4) {

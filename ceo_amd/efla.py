@@ -116,9 +116,18 @@ def _q_shapes(q, k, v, beta, cu_seqlens):
     return B, T, H, K, V, N, DTYPE_CODES[dt]
 
 
+SAVE_STATES = 1  # EFLA_FWD_SAVE_STATES
+
+
 def chunk_efla_fwd(q, k, v, beta, initial_state=None, output_final_state=False,
-                   cu_seqlens=None, workspace=None):
-    """Returns (o, final_state or None)."""
+                   cu_seqlens=None, workspace=None, save_states=False):
+    """Returns (o, final_state or None).
+
+    With ``save_states`` the chunk start states are also written into
+    ``workspace`` (which must then be a backward-sized one, ``new_workspace``),
+    for a backward call with ``reuse_states``."""
+    if save_states and workspace is None:
+        raise ValueError("save_states needs a caller workspace")
     B, T, H, K, V, N, dt = _q_shapes(q, k, v, beta, cu_seqlens)
     if initial_state is not None:
         _require(initial_state, "initial_state", torch.float32, q.device)
@@ -130,23 +139,29 @@ def chunk_efla_fwd(q, k, v, beta, initial_state=None, output_final_state=False,
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     rc = lib().efla_chunk_fwd_hip(_p(q), _p(k), _p(v), _p(beta), _p(initial_state), _p(o),
                                   _p(st), _p(cu_seqlens), B, T, N if cu_seqlens is not None
-                                  else 0, H, K, V, 64, dt, _p(workspace), ws_bytes, _stream(q))
+                                  else 0, H, K, V, 64, dt, _p(workspace), ws_bytes,
+                                  SAVE_STATES if save_states else 0, _stream(q))
     check(rc, "efla_chunk_fwd_hip")
     return o, st
 
 
 REUSE_FORWARD = 1  # EFLA_BWD_REUSE_FORWARD
+REUSE_STATES = 2  # EFLA_BWD_REUSE_STATES
 
 
 def chunk_efla_bwd(q, k, v, beta, do, initial_state=None, dht=None, cu_seqlens=None,
-                   workspace=None, reuse_forward=False):
+                   workspace=None, reuse_forward=False, reuse_states=False):
     """Returns (dq, dk, dv, dbeta, dh0 or None).
 
     With ``reuse_forward`` the ``workspace`` must be the one the forward call on
     the same inputs used (untouched since): the per-chunk WY factors are taken
-    from it instead of being recomputed."""
-    if reuse_forward and workspace is None:
-        raise ValueError("reuse_forward needs the forward's workspace")
+    from it instead of being recomputed.  ``reuse_states`` (with
+    ``reuse_forward``, after a forward with ``save_states``) takes the chunk
+    states from it too."""
+    if (reuse_forward or reuse_states) and workspace is None:
+        raise ValueError("reuse_forward / reuse_states need the forward's workspace")
+    if reuse_states and not reuse_forward:
+        raise ValueError("reuse_states needs reuse_forward")
     B, T, H, K, V, N, dt = _q_shapes(q, k, v, beta, cu_seqlens)
     _require(do, "do", q.dtype, q.device)
     if do.shape != v.shape:
@@ -167,14 +182,15 @@ def chunk_efla_bwd(q, k, v, beta, do, initial_state=None, dht=None, cu_seqlens=N
                                   _p(dht), _p(dq), _p(dk), _p(dv), _p(db), _p(dh0),
                                   _p(cu_seqlens), B, T, N if cu_seqlens is not None else 0, H,
                                   K, V, 64, dt, _p(workspace), ws_bytes,
-                                  REUSE_FORWARD if reuse_forward else 0, _stream(q))
+                                  (REUSE_FORWARD if reuse_forward else 0)
+                                  | (REUSE_STATES if reuse_states else 0), _stream(q))
     check(rc, "efla_chunk_bwd_hip")
     return dq, dk, dv, db, dh0
 
 
 def new_workspace(q, v, cu_seqlens=None) -> torch.Tensor:
     """A workspace large enough for the backward of this problem (and so for its
-    forward), for passing to both calls with reuse_forward."""
+    forward), for passing to both calls with save_states / reuse_forward."""
     B, T, H, K = q.shape
     N = 0 if cu_seqlens is None else cu_seqlens.numel() - 1
     n = workspace_bytes("bwd", B, T, H, K, v.shape[-1], q.dtype, N)
@@ -182,14 +198,14 @@ def new_workspace(q, v, cu_seqlens=None) -> torch.Tensor:
 
 
 class ChunkEflaFunction(torch.autograd.Function):
-    """Keeps the forward's workspace (W, U, T per chunk) for the backward,
-    which still recomputes the chunk states."""
+    """Keeps the forward's workspace (the per-chunk WY factors and chunk start
+    states) for the backward, which then recomputes nothing of the forward."""
 
     @staticmethod
     def forward(ctx, q, k, v, beta, initial_state, output_final_state, cu_seqlens):
         ws = new_workspace(q, v, cu_seqlens)
         o, st = chunk_efla_fwd(q, k, v, beta, initial_state, output_final_state, cu_seqlens,
-                               workspace=ws)
+                               workspace=ws, save_states=True)
         ctx.save_for_backward(q, k, v, beta, initial_state, cu_seqlens, ws)
         return o, st
 
@@ -198,7 +214,8 @@ class ChunkEflaFunction(torch.autograd.Function):
         q, k, v, beta, s0, cu, ws = ctx.saved_tensors
         dq, dk, dv, db, dh0 = chunk_efla_bwd(q, k, v, beta, do.contiguous(), s0,
                                              None if dht is None else dht.contiguous(), cu,
-                                             workspace=ws, reuse_forward=True)
+                                             workspace=ws, reuse_forward=True,
+                                             reuse_states=True)
         return dq, dk, dv, db, dh0, None, None
 
 

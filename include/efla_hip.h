@@ -96,12 +96,20 @@ size_t efla_chunk_fwd_workspace_size(size_t batch_size, size_t seq_len, size_t n
                                      size_t num_heads, size_t head_dim_k, size_t head_dim_v,
                                      int dtype);
 
+/* flags of efla_chunk_fwd_hip */
+/* Also write each chunk's start state into the caller-owned `workspace`, where
+ * a backward call with EFLA_BWD_REUSE_STATES reads it instead of recomputing
+ * the state scan.  Requires a non-NULL workspace of at least
+ * efla_chunk_bwd_workspace_size() bytes (the one the backward will get). */
+#define EFLA_FWD_SAVE_STATES 1u
+
+/* flags: 0 or EFLA_FWD_SAVE_STATES (other bits -> 1). */
 int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, const void* beta,
                        const float* initial_state, void* output, float* final_state,
                        const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
                        size_t num_seqs, size_t num_heads, size_t head_dim_k,
                        size_t head_dim_v, size_t chunk_size, int dtype, void* workspace,
-                       size_t workspace_bytes, hipStream_t stream);
+                       size_t workspace_bytes, unsigned flags, hipStream_t stream);
 
 size_t efla_chunk_bwd_workspace_size(size_t batch_size, size_t seq_len, size_t num_seqs,
                                      size_t num_heads, size_t head_dim_k, size_t head_dim_v,
@@ -112,14 +120,20 @@ size_t efla_chunk_bwd_workspace_size(size_t batch_size, size_t seq_len, size_t n
  * inputs (same q, k, v, beta, cu_seqlens, shapes) used, and nothing has
  * written to it since: the backward takes the forward's per-chunk WY factors
  * (W, U, T) from it instead of recomputing them.  The chunk states are
- * recomputed either way.  Requires a non-NULL workspace of at least
- * efla_chunk_bwd_workspace_size() bytes, also passed to the forward. */
+ * recomputed unless EFLA_BWD_REUSE_STATES is also set.  Requires a non-NULL
+ * workspace of at least efla_chunk_bwd_workspace_size() bytes, also passed to
+ * the forward. */
 #define EFLA_BWD_REUSE_FORWARD 1u
+/* With EFLA_BWD_REUSE_FORWARD only: the forward also ran with
+ * EFLA_FWD_SAVE_STATES on this workspace, so the chunk states are read from it
+ * too and the backward runs no forward recompute at all (bf16; the fp32 path
+ * accepts the flag and recomputes the states). */
+#define EFLA_BWD_REUSE_STATES 2u
 
 /* Gradients of sum(output * grad_output) + sum(final_state * grad_final_state);
- * grad_final_state and grad_initial_state may be NULL.  Chunk states are
- * recomputed, not read from the forward.  flags: 0 or EFLA_BWD_REUSE_FORWARD
- * (other bits -> 1). */
+ * grad_final_state and grad_initial_state may be NULL.  flags: 0,
+ * EFLA_BWD_REUSE_FORWARD or EFLA_BWD_REUSE_FORWARD | EFLA_BWD_REUSE_STATES
+ * (anything else -> 1). */
 int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, const void* beta,
                        const float* initial_state, const void* grad_output,
                        const float* grad_final_state, void* grad_q, void* grad_k,

@@ -57,13 +57,13 @@ def test_efla_chunked_scan_validation(L):
 
 def _fwd(L, **kw):
     a = dict(q=16, k=16, v=16, beta=16, s0=None, o=16, st=None, cu=None, B=2, T=128, N=0,
-             H=2, K=64, V=64, C=64, dt=14, ws=None, wsb=0)
+             H=2, K=64, V=64, C=64, dt=14, ws=None, wsb=0, flags=0)
     a.update(kw)
     vp = ctypes.c_void_p
     return L.efla_chunk_fwd_hip(vp(a["q"]), vp(a["k"]), vp(a["v"]), vp(a["beta"]), a["s0"],
                                 vp(a["o"]) if a["o"] else None, a["st"], a["cu"], a["B"], a["T"],
                                 a["N"], a["H"], a["K"], a["V"], a["C"], a["dt"], a["ws"],
-                                a["wsb"], None)
+                                a["wsb"], a["flags"], None)
 
 
 def test_chunk_fwd_validation(L):
@@ -96,6 +96,19 @@ def test_chunk_bwd_flags(L):
     assert _bwd(L, flags=1, ws=ctypes.c_void_p(256), wsb=16) == 1  # workspace too small
     assert _bwd(L, flags=1, T=0) == 1   # flags are checked before the empty case
     assert _bwd(L, flags=0, T=0) == 0
+    assert _bwd(L, flags=4) == 1
+    assert _bwd(L, flags=3) == 1        # no workspace
+    # saved states without the factors
+    assert _bwd(L, flags=2, ws=ctypes.c_void_p(256), wsb=1 << 40) == 1
+
+
+def test_chunk_fwd_flags(L):
+    assert _fwd(L, flags=2) == 1        # unknown bit
+    assert _fwd(L, flags=1) == 1        # saving states needs a caller workspace
+    # the fwd-sized workspace has no room for the states
+    fw = L.efla_chunk_fwd_workspace_size(2, 128, 0, 2, 64, 64, 14)
+    assert _fwd(L, flags=1, ws=ctypes.c_void_p(256), wsb=fw) == 1
+    assert _fwd(L, flags=1, T=0) == 1   # flags are checked before the empty case
 
 
 def test_workspace_sizes(L):
@@ -104,10 +117,12 @@ def test_workspace_sizes(L):
     # cfg3: B=4, T=8192, H=32, K=V=128 bf16
     fw = f(4, 8192, 0, 32, 128, 128, 14)
     bw = b(4, 8192, 0, 32, 128, 128, 14)
-    ntok = 4 * 8192
-    per_tok = 32 * 128 * 2
-    assert fw >= 2 * ntok * per_tok          # W, U
-    assert bw > fw
+    slots, H = 4 * 8192 // 64, 32
+    t_bytes = slots * H * 64 * 64 * 2        # bf16 T per chunk
+    state_bytes = slots * H * 128 * 128 * 2  # bf16 chunk states
+    assert fw >= t_bytes
+    assert fw < t_bytes + state_bytes        # no states unless asked for
+    assert bw >= fw + 2 * state_bytes        # h and dh
     assert bw < 16 * 2**30                   # fits comfortably in 288 GB
     assert f(4, 8192, 0, 32, 96, 128, 14) == 0
     assert f(1, 65536, 40, 16, 128, 256, 14) > 0   # packed, cfg5 shape

@@ -139,23 +139,28 @@ def test_autograd_function(oracle):
         assert rel_l2(g[name].grad, ref) <= 1e-4, name
 
 
+@pytest.mark.parametrize("states", [False, True], ids=["factors", "factors+states"])
 @pytest.mark.parametrize("dtype,K,V", [(torch.bfloat16, 128, 128), (torch.bfloat16, 64, 256),
                                        (torch.float32, 64, 64)])
-def test_backward_reusing_forward_factors(oracle, dtype, K, V):
+def test_backward_reusing_forward_factors(oracle, dtype, K, V, states):
     from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd, new_workspace
 
-    announce(f"chunk_efla reuse_forward {dtype} K={K} V={V}")
+    announce(f"chunk_efla reuse_forward states={states} {dtype} K={K} V={V}")
     B, T, H = 2, 200, 2
     x = oracle.make_efla_inputs(91, B * T, H, K, V, bf16=dtype == torch.bfloat16)
     g = {n: to_dev(a, dtype, (B, T, H, K) if n in "qk" else
                    (B, T, H) if n == "beta" else (B, T, H, V)) for n, a in x.items()}
+    s0 = 0.1 * torch.randn(B, H, K, V, generator=torch.Generator().manual_seed(5)).cuda()
     ws = new_workspace(g["q"], g["v"])
-    chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], workspace=ws)
-    got = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], workspace=ws,
-                         reuse_forward=True)
-    ref = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"])
+    o_ws, _ = chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], s0, workspace=ws,
+                             save_states=states)
+    got = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], s0, workspace=ws,
+                         reuse_forward=True, reuse_states=states)
+    o_ref, _ = chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], s0)
+    ref = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], s0)
     torch.cuda.synchronize()
-    for a, b, n in zip(got[:4], ref[:4], ("dq", "dk", "dv", "dbeta")):
+    assert torch.equal(o_ws, o_ref)
+    for a, b, n in zip(got, ref, ("dq", "dk", "dv", "dbeta", "dh0")):
         if dtype == torch.bfloat16:
             assert torch.equal(a, b), n  # same kernels, same order: bit-identical
         else:
