@@ -322,12 +322,18 @@ def main() -> int:
         avg_ms = tot_ms / launches
         fl = per_chunk.get(dom, 0.0) * n_chunks * H
         ach = fl / (avg_ms * 1e-3) / 1e12
+        traffic = measured_traffic(args.config, dom)
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-                "traffic": measured_traffic(args.config, dom),
+                "traffic": traffic,
                 "avg_ms": round(avg_ms, 4),
                 "flops_per_launch": fl}
+        if traffic:
+            # the same launch against the HBM roof: its measured bytes over its time
+            gbs = traffic / (avg_ms * 1e-3) / 1e9
+            roof["hbm"] = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                           "frac": round(gbs / PEAK_HBM_GBS, 4)}
     step_tflops = step_flops / (ms_step * 1e-3) / 1e12
     io = io_bytes(ntok, H, K, V, cfg["bwd"])
 
