@@ -1021,6 +1021,9 @@ static int make_problem(const void* q, const void* k, const void* v, const void*
     if (!mul_ok(batch, seq_len, &ntok)) return kInvalidConfiguration;
     if (!mul_ok(ntok, H, (K > V ? K : V), &elems) || elems > ((size_t)1 << 46))
         return kInvalidConfiguration;
+    // 64 token rows of a chunk span < 2^32 bytes (32-bit tile offsets)
+    if (H >= ((size_t)1 << 24) || H * (K > V ? K : V) >= ((size_t)1 << 24))
+        return kInvalidConfiguration;
     if (num_seqs > (size_t)INT32_MAX / 2 || ntok > (size_t)INT32_MAX)
         return kInvalidConfiguration;
     p->ntok = (long)ntok;

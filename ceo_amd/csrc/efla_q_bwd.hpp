@@ -110,10 +110,10 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
     for (int n = 0; n < nch; ++n) {
         const ScanHBuf<K>& cb = sm.buf[n & 1];
         __syncthreads();  // chunk n staged; everyone is done with chunk n - 1
-        store_state_vf<K>(hist + ((long)(slot0 + n) * H + h) * V * K, S, vcol);
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(S[2 * kb], S[2 * kb + 1]);
+        store_state_frag<K>(hist + ((long)(slot0 + n) * H + h) * V * K, sb, vcol);
         floatx4 vn[4];
         chunk_vn<K>(cb, w, sb, vn);
         const bf16x8 vb0 = frag_from_c(vn[0], vn[1]), vb1 = frag_from_c(vn[2], vn[3]);
@@ -193,7 +193,6 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
     for (int n = nch - 1; n >= 0; --n) {
         const ScanDhBuf<K>& cb = sm.buf[n & 1];
         __syncthreads();  // chunk n staged; everyone is done with chunk n + 1
-        store_state_vf<K>(dhist + ((long)(slot0 + n) * H + h) * V * K, dS, vcol);
         for (int nt = w; nt < 10; nt += 4) {
             int I, J;
             lower_tile(nt, I, J);
@@ -209,6 +208,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(dS[2 * kb], dS[2 * kb + 1]);
+        store_state_frag<K>(dhist + ((long)(slot0 + n) * H + h) * V * K, sb, vcol);
         const bf16x8 do0 = frag_tr(cb.Vs, LD64, 0, 16 * w), do1 = frag_tr(cb.Vs, LD64, 32, 16 * w);
         // K dS part of dVn (P^T dO is added once P is complete); tile tb row
         // 4g + i is token pim(tb, 4g + i)

@@ -60,13 +60,14 @@ __device__ __forceinline__ void store4(bf16* p, floatx4 a) {
     *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
 }
 
-// Write the C tiles of a K x 64 state slice (S[fb] rows pim(fb, 4g + i),
-// column v0 + 16 w + r) to hist[v][f] (row stride K) as bf16, 8 bytes a lane.
+// Write a K x 64 state slice to hist[v][f] (row stride K) as bf16 from its
+// operand fragments: sb[kb] holds keys 32 kb + 8 g .. 32 kb + 8 g + 7 of
+// column vcol, one 16-byte store each.
 template <int K>
-__device__ __forceinline__ void store_state_vf(bf16* __restrict__ hist, const floatx4* S, int vcol) {
-    const int g = mf::lane() >> 4;
+__device__ __forceinline__ void store_state_frag(bf16* __restrict__ hist, const bf16x8* sb, int vcol) {
+    bf16* p = hist + (long)vcol * K + 8 * (mf::lane() >> 4);
 #pragma unroll
-    for (int fb = 0; fb < K / 16; ++fb) store4(hist + (long)vcol * K + pim(fb, 4 * g), S[fb]);
+    for (int kb = 0; kb < K / 32; ++kb) *reinterpret_cast<bf16x8*>(p + 32 * kb) = sb[kb];
 }
 
 // ---------------------------------------------------------------------------
@@ -277,7 +278,7 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
                                                     float* __restrict__ ST,
                                                     bf16* __restrict__ o,
                                                     bf16* __restrict__ hist) {
-    constexpr int LDK = ldb<K>(), LDV = ldb<VS>(), LDP = ldb<64>(), NVS = V / VS;
+    constexpr int LDK = ldb<K>(), LDP = ldb<64>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanSmem<K> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
     int bh, vsl;
@@ -316,7 +317,6 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         const int len = (int)min((long)64, slen - (long)n * 64);
         const ScanBuf<K>& cb = sm.buf[n & 1];
         __syncthreads();  // chunk n staged; everyone is done with chunk n - 1
-        if (hist) store_state_vf<K>(hist + ((long)(slot0 + n) * H + h) * V * K, S, vcol);
         // P[t][t'] = q_t . k_t' for t' <= t, lower 16x16 tiles (I = t block,
         // J = t' block) computed transposed so each lane writes 4 consecutive t'
         for (int nt = w; nt < 10; nt += 4) {
@@ -334,6 +334,7 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(S[2 * kb], S[2 * kb + 1]);
+        if (hist) store_state_frag<K>(hist + ((long)(slot0 + n) * H + h) * V * K, sb, vcol);
         floatx4 vn[4];
         chunk_vn<K>(cb, w, sb, vn);
         // stage chunk n + 1 (its loads were issued one chunk ago), fetch n + 2

@@ -159,16 +159,22 @@ struct TileRegs {
     // mask(), which the store functions call.  Nothing here consumes the loaded
     // registers, so the loads stay in flight until the tile is stored (a
     // prefetch overlaps whatever runs in between).
+    // `src` is uniform across the workgroup and ROWS * ld * 2 < 2^32 (the
+    // host validates H * max(d_k, d_v) < 2^24), so each row is a 32-bit byte
+    // offset from a scalar base (global_load ... v_off, s_base).
     __device__ __forceinline__ void load(const bf16* __restrict__ src, long ld, int nvalid) {
         const int f = fg(), t = t0();
         valid = nvalid;
+        const char* base = reinterpret_cast<const char*>(src);
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
             const int tt = min(t + j, nvalid - 1);
-            x[j] = *reinterpret_cast<const bf16x8*>(src + (long)tt * ld + 8 * f);
+            const unsigned off = (unsigned)(tt * (int)ld + 8 * f) * 2u;
+            x[j] = *reinterpret_cast<const bf16x8*>(base + off);
         }
     }
     __device__ __forceinline__ void mask() {
+        if (__builtin_amdgcn_readfirstlane(valid) >= ROWS) return;  // full tile
         const int t = t0();
 #pragma unroll
         for (int j = 0; j < TPT; ++j)
