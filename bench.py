@@ -1,7 +1,7 @@
 """EFLA fwd+bwd throughput on one MI355X (the headline benchmark).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg2|cfg5]
-                    [--no-cpu] [--cpu-budget SECONDS]
+                    [--no-cpu] [--cpu-budget SECONDS] [--aux]
 
 A step is one chunked EFLA forward plus one backward (the backward recomputes
 the chunk states; nothing is carried over from the forward) over one batch of
@@ -217,6 +217,69 @@ def measured_traffic(config: str, kernel: str):
 
 
 # ---------------------------------------------------------------------------
+# HBM-bound kernels of the config-4 step (LayerNorm, GELU, AdamW)
+# ---------------------------------------------------------------------------
+CFG4 = {"tokens": 16384, "d_model": 1024, "mlp": 4096, "params": 368_000_000}
+
+
+def aux_bench(steps: int, warmup: int) -> int:
+    """Times the elementwise / row kernels at config-4 shapes against the HBM
+    roof: algorithmic bytes per launch (what each kernel must read and write
+    once) over its average hipEvent duration.  Prints one JSON line."""
+    import torch
+
+    from ceo_amd import nn, runtime
+
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(4)
+    N, D, F, P = CFG4["tokens"], CFG4["d_model"], CFG4["mlp"], CFG4["params"]
+
+    def bf(*shape, scale=1.0):
+        return (torch.randn(*shape, generator=g, device=dev) * scale).to(torch.bfloat16)
+
+    x, w, b, dy = bf(N, D), bf(D), bf(D, scale=0.1), bf(N, D)
+    h, dh = bf(N, F), bf(N, F)
+    p32 = torch.randn(P, generator=g, device=dev)
+    m32 = torch.zeros(P, device=dev)
+    v32 = torch.zeros(P, device=dev)
+    gp = bf(P, scale=0.01)
+    pcopy = torch.empty(P, dtype=torch.bfloat16, device=dev)
+    y, mean, rstd = nn.layernorm_forward(x, w, b, save_stats=True)
+    cases = {
+        # name: (callable, algorithmic bytes per launch, what)
+        "layernorm_fwd": (lambda: nn.layernorm_forward(x, w, b, save_stats=True),
+                          N * D * 4 + N * 8, "x in, y out (bf16), mean/rstd out"),
+        "layernorm_bwd": (lambda: nn.layernorm_backward(dy, x, w, mean, rstd),
+                          N * D * 6 + N * 8, "dy, x in, dx out (bf16), mean/rstd in"),
+        "gelu_fwd": (lambda: nn.gelu_forward(h), N * F * 4, "x in, y out (bf16)"),
+        "gelu_bwd": (lambda: nn.gelu_backward(dh, h), N * F * 6, "dy, x in, dx out (bf16)"),
+        "adamw_master": (lambda: nn.adamw_step_master(p32, gp, m32, v32, 3e-4, 0.9, 0.999,
+                                                      1e-8, 0.1, 1, param_bf16=pcopy),
+                         P * 28, "p, m, v fp32 in+out, g bf16 in, bf16 copy out"),
+    }
+    out = {}
+    for name, (fn, nbytes, what) in cases.items():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        with runtime.Profiler() as prof:
+            for _ in range(steps):
+                fn()
+        res = prof.results()
+        # the op's time: every kernel it launched (LayerNorm's backward has a
+        # second, small reduction kernel), averaged over the timed calls
+        avg_ms = sum(tot for _, tot in res.values()) / steps
+        gbs = nbytes / (avg_ms * 1e-3) / 1e9
+        out[name] = {"avg_ms": round(avg_ms, 4), "bytes": nbytes, "bytes_are": what,
+                     "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
+                     "kernels_ms": {k: round(tot / n, 4) for k, (n, tot) in res.items()}}
+        print(f"[bench] {name}: {avg_ms:.4f} ms, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
+    print(json.dumps({"aux": "config-4 HBM-bound kernels", "shapes": CFG4, "steps": steps,
+                      "kernels": out}), flush=True)
+    return 0
+
+
+# ---------------------------------------------------------------------------
 # main
 # ---------------------------------------------------------------------------
 def main() -> int:
@@ -233,9 +296,14 @@ def main() -> int:
                     help="only run a plain device-to-device copy of MIB MiB five times "
                          "(the known-size kernel that calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings) and exit")
+    ap.add_argument("--aux", action="store_true",
+                    help="only time the config-4 LayerNorm / GELU / AdamW kernels against "
+                         "the HBM roof (one JSON line) and exit")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.aux:
+        return aux_bench(args.steps, args.warmup)
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:

@@ -85,6 +85,11 @@ _SIGS = {
     # GEMM
     "gemm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, sz, i32, i32, i32, vp]),
     "gemm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),
+    # GELU, AdamW
+    "gelu_forward_hip": (i32, [vp, vp, sz, ctypes.c_bool, vp]),
+    "gelu_backward_hip": (i32, [vp, vp, vp, sz, ctypes.c_bool, vp]),
+    "adamw_step_hip": (i32, [vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, sz, vp]),
+    "adamw_step_master_hip": (i32, [vp, vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, sz, vp]),
     # runtime
     "efla_rt_device_count": (i32, [ctypes.POINTER(i32)]),
     "efla_rt_set_device": (i32, [i32]),

@@ -28,7 +28,8 @@ typedef __attribute__((__vector_size__(16))) int int4v;
 typedef __attribute__((__vector_size__(8))) int int2v;
 
 __device__ __forceinline__ int lane() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave() { return threadIdx.x >> 6; }
+// wave index as a scalar (wave-uniform branches and addresses stay in SGPRs)
+__device__ __forceinline__ int wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 __device__ __forceinline__ floatx4 zero4() { return floatx4{0.f, 0.f, 0.f, 0.f}; }
 

@@ -1,9 +1,10 @@
-"""LayerNorm and GEMM around EFLA: torch-facing wrappers over the C ABI.
+"""LayerNorm, GEMM, GELU and AdamW around EFLA: torch-facing wrappers over the C ABI.
 
 Mirror the reference's ``layerNormForwardCuda`` / ``gemmForwardCuda`` /
 ``gemmBackwardCuda`` externs (src/kernels/nn_kernels.zig:28-76) and their
 callers ``LayerNorm.forward`` (src/nn/layers.zig:226-245, eps 1e-5) and
-``Linear.forward`` (src/nn/layers.zig:561-586, weight (in, out) row-major).
+``Linear.forward`` (src/nn/layers.zig:561-586, weight (in, out) row-major),
+and the GELU / AdamW kernels of kernels/cuda/include/kernels.h:171-189, 309-322.
 """
 from __future__ import annotations
 
@@ -84,3 +85,58 @@ def gemm_backward(dc: torch.Tensor, a: torch.Tensor, b: torch.Tensor, need_a=Tru
                                  _stream(a))
     check(rc, "gemm_backward_hip")
     return da, dbm, dbias
+
+
+def gelu_forward(x: torch.Tensor, approximate: bool = True) -> torch.Tensor:
+    """GELU of a bf16 tensor (tanh form unless approximate=False)."""
+    _require(x, "x", torch.bfloat16)
+    y = torch.empty_like(x)
+    rc = lib().gelu_forward_hip(_p(x), _p(y), x.numel(), bool(approximate), _stream(x))
+    check(rc, "gelu_forward_hip")
+    return y
+
+
+def gelu_backward(dy: torch.Tensor, x: torch.Tensor, approximate: bool = True) -> torch.Tensor:
+    """dy * GELU'(x), bf16."""
+    _require(x, "x", torch.bfloat16)
+    _require(dy, "dy", torch.bfloat16, x.device)
+    if dy.shape != x.shape:
+        raise ValueError("gelu_backward: dy and x differ in shape")
+    dx = torch.empty_like(x)
+    rc = lib().gelu_backward_hip(_p(dy), _p(x), _p(dx), x.numel(), bool(approximate),
+                                 _stream(x))
+    check(rc, "gelu_backward_hip")
+    return dx
+
+
+def adamw_step(param, grad, exp_avg, exp_avg_sq, lr, beta1=0.9, beta2=0.999, eps=1e-8,
+               weight_decay=0.0, step=1) -> None:
+    """In-place AdamW step with bf16 parameters and state (the reference's layout)."""
+    for t, n in ((param, "param"), (grad, "grad"), (exp_avg, "exp_avg"),
+                 (exp_avg_sq, "exp_avg_sq")):
+        _require(t, n, torch.bfloat16, param.device)
+        if t.numel() != param.numel():
+            raise ValueError(f"adamw_step: {n} size differs from param")
+    rc = lib().adamw_step_hip(_p(param), _p(grad), _p(exp_avg), _p(exp_avg_sq), param.numel(),
+                              float(lr), float(beta1), float(beta2), float(eps),
+                              float(weight_decay), int(step), _stream(param))
+    check(rc, "adamw_step_hip")
+
+
+def adamw_step_master(param, grad, exp_avg, exp_avg_sq, lr, beta1=0.9, beta2=0.999, eps=1e-8,
+                      weight_decay=0.0, step=1, param_bf16=None) -> None:
+    """In-place AdamW step on fp32 master weights / moments with a bf16 gradient;
+    ``param_bf16`` (optional) receives the new weights in bf16."""
+    for t, n in ((param, "param"), (exp_avg, "exp_avg"), (exp_avg_sq, "exp_avg_sq")):
+        _require(t, n, torch.float32, param.device)
+    _require(grad, "grad", torch.bfloat16, param.device)
+    if param_bf16 is not None:
+        _require(param_bf16, "param_bf16", torch.bfloat16, param.device)
+    for t in (grad, exp_avg, exp_avg_sq, param_bf16):
+        if t is not None and t.numel() != param.numel():
+            raise ValueError("adamw_step_master: sizes differ")
+    rc = lib().adamw_step_master_hip(_p(param), _p(grad), _p(exp_avg), _p(exp_avg_sq),
+                                     _p(param_bf16), param.numel(), float(lr), float(beta1),
+                                     float(beta2), float(eps), float(weight_decay), int(step),
+                                     _stream(param))
+    check(rc, "adamw_step_master_hip")

@@ -22,6 +22,7 @@
 #define EFLA_HIP_H
 
 #include <hip/hip_runtime_api.h>
+#include <stdbool.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -184,6 +185,43 @@ int gemm_forward_hip(const void* a, const void* b, const void* bias, void* c, si
 int gemm_backward_hip(const void* grad_c, const void* a, const void* b, void* grad_a,
                       void* grad_b, void* grad_bias, size_t m, size_t k, size_t n,
                       hipStream_t stream);
+
+/* ========================================================================
+ * GELU and AdamW (the config-4 training step around EFLA)
+ * ======================================================================== */
+
+/* Replaces gelu_forward_cuda (kernels.h:171-177, layernorm.cu:189-214,
+ * 385-403): y = GELU(x), bf16 in / out, fp32 math; approximate selects the
+ * tanh form 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))), otherwise
+ * x Phi(x).  numel == 0 -> 9 (the reference launches an empty grid); a NULL
+ * pointer -> 1. */
+int gelu_forward_hip(const void* input, void* output, size_t numel, bool approximate,
+                     hipStream_t stream);
+
+/* Replaces gelu_backward_cuda (kernels.h:182-189, layernorm.cu:216-250,
+ * 405-425): grad_input = grad_output * GELU'(input), bf16.  Same return codes
+ * as gelu_forward_hip. */
+int gelu_backward_hip(const void* grad_output, const void* input, void* grad_input,
+                      size_t numel, bool approximate, hipStream_t stream);
+
+/* Replaces adamw_step_cuda (kernels.h:309-322, optim.cu:147-178, 657-709):
+ * bf16 param, grad, exp_avg, exp_avg_sq updated in place with fp32 math,
+ *   m = b1 m + (1 - b1) g,  v = b2 v + (1 - b2) g^2,
+ *   p = p (1 - lr wd) - lr (m / bc1) / (sqrt(v / bc2) + eps),
+ * bc = 1 - beta^step in double.  numel == 0 -> 0; a NULL pointer -> 1;
+ * non-finite hyper-parameters, beta outside [0, 1), eps <= 0 or step == 0
+ * -> 1. */
+int adamw_step_hip(void* param, const void* grad, void* exp_avg, void* exp_avg_sq, size_t numel,
+                   float lr, float beta1, float beta2, float eps, float weight_decay, size_t step,
+                   hipStream_t stream);
+
+/* No reference counterpart (the reference keeps bf16 optimizer state): the
+ * same step on fp32 master weights and fp32 moments with a bf16 gradient;
+ * param_bf16, if not NULL, receives the new weights rounded to bf16.  Same
+ * return codes as adamw_step_hip. */
+int adamw_step_master_hip(float* param, const void* grad, float* exp_avg, float* exp_avg_sq,
+                          void* param_bf16, size_t numel, float lr, float beta1, float beta2,
+                          float eps, float weight_decay, size_t step, hipStream_t stream);
 
 #ifdef __cplusplus
 }

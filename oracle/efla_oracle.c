@@ -468,23 +468,48 @@ void or_layernorm_bwd(const float* dy, const float* x, const float* w, const flo
     }
 }
 
-/* GELU, tanh approximation and its derivative (layernorm.cu:189-250), fp64. */
-void or_gelu_fwd(const float* x, float* y, size_t n) {
+/* GELU, tanh approximation and its derivative (layernorm.cu:189-250), fp64.
+ * 0.5 (1 + tanh u) is evaluated as 1 / (1 + e^(-2u)) (the same function):
+ * 1 + tanh u cancels for u << 0 even in fp64, and the kernel under test is
+ * accurate there.  The erf form uses Phi(x) = erfc(-x / sqrt 2) / 2 for the
+ * same reason. */
+static double gelu_s(double x, double* du) {
     const double k0 = 0.7978845608028654, k1 = 0.044715;
-    for (size_t i = 0; i < n; ++i) {
-        const double v = x[i];
-        y[i] = (float)(0.5 * v * (1.0 + tanh(k0 * (v + k1 * v * v * v))));
-    }
+    const double u = k0 * (x + k1 * x * x * x);
+    *du = k0 * (1.0 + 3.0 * k1 * x * x);
+    return 1.0 / (1.0 + exp(-2.0 * u));
+}
+
+void or_gelu_fwd(const float* x, float* y, size_t n) {
+    double du;
+    for (size_t i = 0; i < n; ++i) y[i] = (float)(x[i] * gelu_s(x[i], &du));
 }
 
 void or_gelu_bwd(const float* dy, const float* x, float* dx, size_t n) {
-    const double k0 = 0.7978845608028654, k1 = 0.044715;
+    for (size_t i = 0; i < n; ++i) {
+        double du;
+        const double v = x[i], s = gelu_s(v, &du);
+        /* 0.5 (1 + tanh) + 0.5 x sech^2 u', with 1 - tanh^2 = 4 s (1 - s) */
+        dx[i] = (float)(dy[i] * (s + 2.0 * v * s * (1.0 - s) * du));
+    }
+}
+
+/* GELU, exact erf form and its derivative (layernorm.cu:196-200, 241-246),
+ * fp64: y = x Phi(x), dy/dx = Phi(x) + x phi(x). */
+void or_gelu_exact_fwd(const float* x, float* y, size_t n) {
     for (size_t i = 0; i < n; ++i) {
         const double v = x[i];
-        const double th = tanh(k0 * (v + k1 * v * v * v));
-        const double sech2 = 1.0 - th * th;
-        const double inner = k0 * (1.0 + 3.0 * k1 * v * v);
-        dx[i] = (float)(dy[i] * (0.5 * (1.0 + th) + 0.5 * v * sech2 * inner));
+        y[i] = (float)(0.5 * v * erfc(-v / sqrt(2.0)));
+    }
+}
+
+void or_gelu_exact_bwd(const float* dy, const float* x, float* dx, size_t n) {
+    const double inv_sqrt_2pi = 0.3989422804014327;
+    for (size_t i = 0; i < n; ++i) {
+        const double v = x[i];
+        const double cdf = 0.5 * erfc(-v / sqrt(2.0));
+        const double pdf = exp(-0.5 * v * v) * inv_sqrt_2pi;
+        dx[i] = (float)(dy[i] * (cdf + v * pdf));
     }
 }
 

@@ -30,6 +30,12 @@ Contents and what pins each part (tests/test_oracle_*.py):
 * ``layernorm_fwd`` / ``layernorm_bwd`` -- layernorm.cu:133-183 and the
   textbook gradient.  Pinned by the per-row mean 0 / variance 1 invariant and
   torch fp64 autograd.
+* ``gelu_fwd`` / ``gelu_bwd`` -- layernorm.cu:189-250, tanh and erf forms.
+  Pinned by torch's own GELU (both forms) and its autograd, and special values.
+* ``adamw_step`` / ``adamw_step_bf16`` -- optim.cu:147-178, 657-709 with fp32
+  and with bf16 state.  Pinned by an fp64 closed form at steps 1 and 7 and the
+  zero-state identity p1 = p0 (1 - lr wd) - lr g / (|g| + eps); the bf16 form
+  adds only the bf16 round trip, pinned by the reference's KAT (dtype.zig:654).
 """
 from __future__ import annotations
 
@@ -105,6 +111,8 @@ def lib():
                                    c_f64p, sz, sz]
     L.or_gelu_fwd.argtypes = [c_f32p, c_f32p, sz]
     L.or_gelu_bwd.argtypes = [c_f32p, c_f32p, c_f32p, sz]
+    L.or_gelu_exact_fwd.argtypes = [c_f32p, c_f32p, sz]
+    L.or_gelu_exact_bwd.argtypes = [c_f32p, c_f32p, c_f32p, sz]
     L.or_adamw_step.argtypes = [c_f32p, c_f32p, c_f32p, c_f32p, sz, ctypes.c_float,
                                 ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                 ctypes.c_float, sz]
@@ -400,18 +408,23 @@ def layernorm_bwd(dy, x, w, mean, rstd):
     return dx, dw, db
 
 
-def gelu_fwd(x):
+def gelu_fwd(x, approximate=True):
+    """GELU in fp64, rounded to fp32: the tanh form (layernorm.cu:189-194) or,
+    with approximate=False, the erf form (layernorm.cu:196-200)."""
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
-    lib().or_gelu_fwd(_p(x, c_f32p), _p(y, c_f32p), x.size)
+    fn = lib().or_gelu_fwd if approximate else lib().or_gelu_exact_fwd
+    fn(_p(x, c_f32p), _p(y, c_f32p), x.size)
     return y
 
 
-def gelu_bwd(dy, x):
+def gelu_bwd(dy, x, approximate=True):
+    """dy * GELU'(x) in fp64 (layernorm.cu:216-250), rounded to fp32."""
     dy = np.ascontiguousarray(dy, dtype=np.float32)
     x = np.ascontiguousarray(x, dtype=np.float32)
     dx = np.empty_like(x)
-    lib().or_gelu_bwd(_p(dy, c_f32p), _p(x, c_f32p), _p(dx, c_f32p), x.size)
+    fn = lib().or_gelu_bwd if approximate else lib().or_gelu_exact_bwd
+    fn(_p(dy, c_f32p), _p(x, c_f32p), _p(dx, c_f32p), x.size)
     return dx
 
 
@@ -422,6 +435,15 @@ def adamw_step(p, g, m, v, lr, b1, b2, eps, wd, step):
     g = np.ascontiguousarray(g, dtype=np.float32)
     lib().or_adamw_step(_p(p, c_f32p), _p(g, c_f32p), _p(m, c_f32p), _p(v, c_f32p), p.size,
                         lr, b1, b2, eps, wd, step)
+
+
+def adamw_step_bf16(p, g, m, v, lr, b1, b2, eps, wd, step):
+    """The reference's bf16-state AdamW (optim.cu:147-178): bf16 p, g, m, v
+    (given as uint16 bit patterns) read as fp32, the fp32 step above, each
+    result rounded to bf16.  Returns the new (p, m, v) bit patterns."""
+    pf, gf, mf, vf = (bf16_to_f32(a) for a in (p, g, m, v))
+    adamw_step(pf, gf, mf, vf, lr, b1, b2, eps, wd, step)
+    return f32_to_bf16(pf), f32_to_bf16(mf), f32_to_bf16(vf)
 
 
 def num_threads() -> int:

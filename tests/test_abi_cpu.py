@@ -143,3 +143,34 @@ def test_layernorm_validation(L):
     assert L.layernorm_forward_hip(p, p, NULL, p, 0, 1024, 1e-5, NULL) == 0
     assert L.layernorm_forward_hip(NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1
     assert L.layernorm_forward_stats_hip(p, p, NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1
+
+
+def test_gelu_validation(L):
+    p = ctypes.c_void_p(16)
+    # numel == 0: the reference launches an empty grid -> InvalidConfiguration
+    assert L.gelu_forward_hip(p, p, 0, True, NULL) == 9
+    assert L.gelu_backward_hip(p, p, p, 0, False, NULL) == 9
+    assert L.gelu_forward_hip(NULL, p, 8, True, NULL) == 1
+    assert L.gelu_backward_hip(p, NULL, p, 8, True, NULL) == 1
+
+
+def test_adamw_validation(L):
+    p = ctypes.c_void_p(16)
+    ok = (3e-4, 0.9, 0.999, 1e-8, 0.1, 1)
+
+    def bf(*hp, n=8, ptrs=(p, p, p, p)):
+        return L.adamw_step_hip(*ptrs, n, *hp, NULL)
+
+    def ms(*hp, n=8, ptrs=(p, p, p, p, NULL)):
+        return L.adamw_step_master_hip(*ptrs, n, *hp, NULL)
+
+    for fn in (bf, ms):
+        # optim.cu:671-690: numel == 0 first, then nulls, then hyper-parameters
+        assert fn(*ok, n=0, ptrs=(NULL,) * (4 if fn is bf else 5)) == 0
+        assert fn(*ok, ptrs=(p, NULL, p, p) if fn is bf else (p, NULL, p, p, NULL)) == 1
+        assert fn(float("nan"), 0.9, 0.999, 1e-8, 0.1, 1) == 1
+        assert fn(3e-4, 1.0, 0.999, 1e-8, 0.1, 1) == 1      # beta1 >= 1
+        assert fn(3e-4, 0.9, -0.1, 1e-8, 0.1, 1) == 1       # beta2 < 0
+        assert fn(3e-4, 0.9, 0.999, 0.0, 0.1, 1) == 1       # eps <= 0
+        assert fn(3e-4, 0.9, 0.999, 1e-8, float("inf"), 1) == 1
+        assert fn(3e-4, 0.9, 0.999, 1e-8, 0.1, 0) == 1      # step == 0

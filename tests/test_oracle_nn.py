@@ -81,3 +81,35 @@ def test_adamw_step_closed_form(oracle, step):
         # from a zero state one step is p(1 - lr wd) - lr g / (|g| + eps)
         kat = p0 * (1 - lr * wd) - lr * g / (np.abs(g) + eps)
         assert np.abs(p - kat).max() < 1e-6
+
+
+def test_gelu_erf_form_matches_torch(oracle):
+    x = np.linspace(-8, 8, 1001).astype(np.float32)
+    xt = torch.tensor(x, dtype=torch.float64, requires_grad=True)
+    yt = torch.nn.functional.gelu(xt, approximate="none")
+    assert np.abs(oracle.gelu_fwd(x, approximate=False) - yt.detach().numpy()).max() < 1e-6
+    dy = np.sin(x).astype(np.float32)
+    (yt * torch.tensor(dy, dtype=torch.float64)).sum().backward()
+    assert np.abs(oracle.gelu_bwd(dy, x, approximate=False) - xt.grad.numpy()).max() < 1e-6
+    # Phi(0) = 1/2: gelu(0) = 0 with slope 1/2; the two forms agree to ~1e-3
+    assert oracle.gelu_bwd(np.ones(1, np.float32), np.zeros(1, np.float32), False)[0] == 0.5
+    assert np.abs(oracle.gelu_fwd(x, False) - oracle.gelu_fwd(x, True)).max() < 2e-3
+
+
+def test_adamw_bf16_state_is_the_fp32_step_rounded(oracle):
+    rng = np.random.default_rng(4)
+    n = 257
+    f = [rng.standard_normal(n).astype(np.float32) for _ in range(2)]
+    m = (0.01 * rng.standard_normal(n)).astype(np.float32)
+    v = (1e-4 * np.abs(rng.standard_normal(n))).astype(np.float32)
+    bits = [oracle.f32_to_bf16(a) for a in (f[0], f[1], m, v)]
+    p2, m2, v2 = oracle.adamw_step_bf16(*bits, 1e-3, 0.9, 0.999, 1e-8, 0.1, 5)
+    # independent: fp64 closed form on the bf16 values, then bf16 rounding
+    pf, gf, mf, vf = (oracle.bf16_to_f32(b).astype(np.float64) for b in bits)
+    mn = 0.9 * mf + 0.1 * gf
+    vn = 0.999 * vf + 0.001 * gf * gf
+    pn = pf * (1 - 1e-4) - 1e-3 * (mn / (1 - 0.9 ** 5)) / (np.sqrt(vn / (1 - 0.999 ** 5)) + 1e-8)
+    for got, ref in ((p2, pn), (m2, mn), (v2, vn)):
+        g = oracle.bf16_to_f32(got).astype(np.float64)
+        # one bf16 step at most (the fp32 step can sit on the other side of a boundary)
+        assert np.all(np.abs(g - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
