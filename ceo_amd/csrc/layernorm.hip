@@ -12,8 +12,13 @@
 // Backward (no reference counterpart): with xhat = (x - mean) * rstd, g = dy*w
 //   dx = rstd * (g - mean(g) - xhat * mean(g * xhat))
 //   dw = sum_rows dy * xhat,  db = sum_rows dy      (fp32)
-// Each workgroup accumulates dw/db for its rows in LDS and writes one partial
-// row; a second kernel sums the partials (D <= 8192 when dw/db are wanted).
+// One row per wavefront, grid-stride over rows.  For D a multiple of 512 up
+// to 2048 the rows of x and dy stay in registers (16-byte loads, one HBM pass)
+// and each lane accumulates dw/db for its own columns in registers across its
+// rows; the 4 waves of a workgroup combine theirs in LDS and write one partial
+// row.  Other widths loop over the row and accumulate with LDS atomics.  A
+// second kernel sums the per-workgroup partials, 16 row groups per column
+// block (D <= 8192 when dw/db are wanted).
 #include <hip/hip_runtime.h>
 
 #include "../../include/efla_hip.h"
@@ -164,17 +169,132 @@ __global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
     for (int i = threadIdx.x; i < 2 * D; i += NTH) pr[i] = acc[i];
 }
 
+// Register-resident backward for D = NV * 512 (NV <= 4): lane owns columns
+// (j * 64 + lane) * 8 + i.  part[blockIdx.x][0..D) = dw, [D..2D) = db partials.
+template <int NV>
+__global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ dy,
+                                                      const bf16* __restrict__ x,
+                                                      const bf16* __restrict__ w,
+                                                      const float* __restrict__ mean,
+                                                      const float* __restrict__ rstd,
+                                                      bf16* __restrict__ dx,
+                                                      float* __restrict__ part, long rows,
+                                                      int want_params) {
+    constexpr int D = NV * 512;
+    __shared__ float red[NTH / kWave][2 * D];  // 32 KB per 1024 columns
+    const int lane = lane_id(), wv = wave_id();
+    float wf[NV][8], dwa[NV][8], dba[NV][8];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const bf16x8 t = *reinterpret_cast<const bf16x8*>(w + (j * 64 + lane) * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            wf[j][i] = (float)t[i];
+            dwa[j][i] = dba[j][i] = 0.f;
+        }
+    }
+    const long waves = (long)gridDim.x * (NTH / kWave);
+    long row = (long)blockIdx.x * (NTH / kWave) + wv;
+    // the next row's x, dy are loaded while this one computes
+    bf16x8 xn[NV], gn[NV];
+    auto fetch = [&](long r) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            xn[j] = *reinterpret_cast<const bf16x8*>(x + r * D + (j * 64 + lane) * 8);
+            gn[j] = *reinterpret_cast<const bf16x8*>(dy + r * D + (j * 64 + lane) * 8);
+        }
+    };
+    if (row < rows) fetch(row);
+    for (; row < rows; row += waves) {
+        bf16x8 xv[NV], gv[NV];
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            xv[j] = xn[j];
+            gv[j] = gn[j];
+        }
+        if (row + waves < rows) fetch(row + waves);
+        const float mu = mean[row], rs = rstd[row];
+        float sg = 0.f, sgx = 0.f;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float g = (float)gv[j][i] * wf[j][i];
+                sg += g;
+                sgx += g * (((float)xv[j][i] - mu) * rs);
+            }
+        sg = wave_sum(sg) * (1.0f / D);
+        sgx = wave_sum(sgx) * (1.0f / D);
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            bf16x8 o;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float xh = ((float)xv[j][i] - mu) * rs;
+                const float gy = (float)gv[j][i];
+                o[i] = (bf16)(rs * (gy * wf[j][i] - sg - xh * sgx));
+                dwa[j][i] += gy * xh;
+                dba[j][i] += gy;
+            }
+            *reinterpret_cast<bf16x8*>(dx + row * D + (j * 64 + lane) * 8) = o;
+        }
+    }
+    if (!want_params) return;
+    // combine the 4 waves' column sums, then one partial row per workgroup
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            red[wv][(j * 64 + lane) * 8 + i] = dwa[j][i];
+            red[wv][D + (j * 64 + lane) * 8 + i] = dba[j][i];
+        }
+    __syncthreads();
+    float* pr = part + (long)blockIdx.x * 2 * D;
+    for (int c = threadIdx.x; c < 2 * D; c += NTH) {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < NTH / kWave; ++k) s += red[k][c];
+        pr[c] = s;
+    }
+}
+
+// out[c] = sum_b part[b][c] for c < 2D (dw = out[0..D), db = out[D..2D)).
+// Workgroup: 16 row groups x 16 lanes of 4 columns (16-byte loads); grid over
+// 64-column blocks (2D is a multiple of 4 when D is even; odd D reads scalars).
 __global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ part, int nblk,
                                                      int D, float* __restrict__ dw,
                                                      float* __restrict__ db) {
-    const int c = blockIdx.x * NTH + threadIdx.x;
-    if (c >= 2 * D) return;
-    float s = 0.f;
-    for (int b = 0; b < nblk; ++b) s += part[(long)b * 2 * D + c];
-    if (c < D) {
-        if (dw) dw[c] = s;
-    } else if (db) {
-        db[c - D] = s;
+    __shared__ float acc[16][64 + 1];
+    const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
+    const int c0 = blockIdx.x * 64 + 4 * q;
+    const int W = 2 * D;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    if (W % 4 == 0 && c0 + 4 <= W) {
+#pragma unroll 4
+        for (int b = rg; b < nblk; b += 16) {
+            const floatx4 v = *reinterpret_cast<const floatx4*>(part + (long)b * W + c0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) s[i] += v[i];
+        }
+    } else {
+        for (int b = rg; b < nblk; b += 16)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (c0 + i < W) s[i] += part[(long)b * W + c0 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[rg][4 * q + i] = s[i];
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        const int c = blockIdx.x * 64 + threadIdx.x;
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) t += acc[k][threadIdx.x];
+        if (c < D) {
+            if (dw) dw[c] = t;
+        } else if (c < W && db) {
+            db[c - D] = t;
+        }
     }
 }
 
@@ -250,8 +370,13 @@ extern "C" int layernorm_backward_hip(const void* grad_output, const void* input
     }
     if (!grad_output || !input || !weight || !mean || !rstd || !grad_input) return kInvalidValue;
     if ((params && D > 8192) || rows > ((size_t)1 << 40)) return kInvalidConfiguration;
+    const bool aligned = ((uintptr_t)grad_output | (uintptr_t)input | (uintptr_t)weight |
+                          (uintptr_t)grad_input) % 16 == 0;
+    const int nv = (aligned && D % 512 == 0 && D <= 2048) ? (int)(D / 512) : 0;
+    // two workgroups per CU; each wave then takes several rows, which keeps the
+    // per-workgroup dw/db partials (and their reduction) small
     size_t nblk = (rows + 3) / 4;
-    if (nblk > 1024) nblk = 1024;
+    if (nblk > 512) nblk = 512;
     float* part = nullptr;
     if (params) {
         void* ws = nullptr;
@@ -259,18 +384,28 @@ extern "C" int layernorm_backward_hip(const void* grad_output, const void* input
         if (rc != kSuccess) return rc;
         part = (float*)ws;
     }
-    const size_t smem = params ? 2 * D * sizeof(float) : 0;
-    {
-        ::efla::ProfScope ps("layernorm_bwd", stream);
-        hipLaunchKernelGGL(ln::bwd_kernel, dim3((unsigned)nblk), dim3(ln::NTH), smem, stream,
-                           (const bf16*)grad_output, (const bf16*)input, (const bf16*)weight,
-                           mean, rstd, (bf16*)grad_input, part, (long)rows, (int)D,
-                           params ? 1 : 0);
+    const bf16 *g = (const bf16*)grad_output, *x = (const bf16*)input, *w = (const bf16*)weight;
+    bf16* dx = (bf16*)grad_input;
+    const dim3 grid((unsigned)nblk), block(ln::NTH);
+    switch (nv) {
+#define LN_BWD_CASE(n)                                                                        \
+    case n:                                                                                   \
+        EFLA_LAUNCH("layernorm_bwd", ln::bwd_reg_kernel<n>, grid, block, stream, g, x, w, mean, \
+                    rstd, dx, part, (long)rows, params ? 1 : 0);                              \
+        break;
+        LN_BWD_CASE(1) LN_BWD_CASE(2) LN_BWD_CASE(3) LN_BWD_CASE(4)
+#undef LN_BWD_CASE
+        default: {
+            const size_t smem = params ? 2 * D * sizeof(float) : 0;
+            ::efla::ProfScope ps("layernorm_bwd_loop", stream);
+            hipLaunchKernelGGL(ln::bwd_kernel, grid, block, smem, stream, g, x, w, mean, rstd, dx,
+                               part, (long)rows, (int)D, params ? 1 : 0);
+        }
     }
     EFLA_CHECK(hipPeekAtLastError());
     if (params) {
-        const unsigned g = (unsigned)((2 * D + ln::NTH - 1) / ln::NTH);
-        EFLA_LAUNCH("layernorm_bwd_reduce", ln::reduce_kernel, dim3(g), dim3(ln::NTH), stream,
+        const unsigned gr = (unsigned)((2 * D + 63) / 64);
+        EFLA_LAUNCH("layernorm_bwd_reduce", ln::reduce_kernel, dim3(gr), dim3(ln::NTH), stream,
                     (const float*)part, (int)nblk, (int)D, grad_weight, grad_bias);
     }
     return (int)hipPeekAtLastError();

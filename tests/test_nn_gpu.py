@@ -37,7 +37,8 @@ def test_layernorm_forward(oracle, rows, D, bias):
     assert np.abs(y1.mean(1)).max() < 2e-2 and np.abs(y1.var(1) - 1).max() < 3e-2
 
 
-@pytest.mark.parametrize("rows,D", [(64, 1024), (50, 96)])
+@pytest.mark.parametrize("rows,D", [(64, 1024), (50, 96), (5000, 1024), (33, 1536), (300, 2048),
+                                    (17, 4096)])
 def test_layernorm_backward(oracle, rows, D):
     from ceo_amd.nn import layernorm_backward, layernorm_forward
 
