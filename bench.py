@@ -223,9 +223,11 @@ CFG4 = {"tokens": 16384, "d_model": 1024, "mlp": 4096, "params": 368_000_000}
 
 
 def aux_bench(steps: int, warmup: int) -> int:
-    """Times the elementwise / row kernels at config-4 shapes against the HBM
-    roof: algorithmic bytes per launch (what each kernel must read and write
-    once) over its average hipEvent duration.  Prints one JSON line."""
+    """Times the kernels around EFLA at config-4 shapes: the GEMMs of one layer
+    and the LM head against the bf16 MFMA roof (their FLOPs over the average
+    hipEvent duration), LayerNorm / GELU / AdamW against the HBM roof
+    (algorithmic bytes per launch: what each must read and write once).
+    Prints one JSON line."""
     import torch
 
     from ceo_amd import nn, runtime
@@ -257,7 +259,34 @@ def aux_bench(steps: int, warmup: int) -> int:
                                                       1e-8, 0.1, 1, param_bf16=pcopy),
                          P * 28, "p, m, v fp32 in+out, g bf16 in, bf16 copy out"),
     }
+    # GEMMs of one config-4 layer and the LM head (MFMA-bound: FLOPs, not bytes)
+    wq, wu, wd, wh = bf(D, 3 * D, scale=0.03), bf(D, F, scale=0.03), bf(F, D, scale=0.02), \
+        bf(D, 32000, scale=0.03)
+    xu = bf(N, F)
+    dcu = bf(N, F)
+    gemms = {
+        "gemm_qkv_fwd": (lambda: nn.gemm_forward(x, wq), 2.0 * N * D * 3 * D),
+        "gemm_up_fwd": (lambda: nn.gemm_forward(x, wu), 2.0 * N * D * F),
+        "gemm_down_fwd": (lambda: nn.gemm_forward(xu, wd), 2.0 * N * F * D),
+        "gemm_lm_head_fwd": (lambda: nn.gemm_forward(x, wh), 2.0 * N * D * 32000),
+        "gemm_up_bwd": (lambda: nn.gemm_backward(dcu, x, wu, need_bias=False), 4.0 * N * D * F),
+    }
     out = {}
+    for name, (fn, flops) in gemms.items():
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        with runtime.Profiler() as prof:
+            for _ in range(steps):
+                fn()
+        res = prof.results()
+        avg_ms = sum(tot for _, tot in res.values()) / steps
+        tf = flops / (avg_ms * 1e-3) / 1e12
+        out[name] = {"avg_ms": round(avg_ms, 4), "flops": flops, "TFLOP/s": round(tf, 1),
+                     "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                     "kernels_ms": {k: round(tot / n, 4) for k, (n, tot) in res.items()}}
+        print(f"[bench] {name}: {avg_ms:.4f} ms, {tf:.0f} TFLOP/s", file=sys.stderr, flush=True)
+    del xu, dcu
     for name, (fn, nbytes, what) in cases.items():
         for _ in range(warmup):
             fn()
@@ -274,7 +303,7 @@ def aux_bench(steps: int, warmup: int) -> int:
                      "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
                      "kernels_ms": {k: round(tot / n, 4) for k, (n, tot) in res.items()}}
         print(f"[bench] {name}: {avg_ms:.4f} ms, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
-    print(json.dumps({"aux": "config-4 HBM-bound kernels", "shapes": CFG4, "steps": steps,
+    print(json.dumps({"aux": "config-4 kernels around EFLA", "shapes": CFG4, "steps": steps,
                       "kernels": out}), flush=True)
     return 0
 

@@ -106,6 +106,7 @@ _SIGS = {
     "efla_rt_memcpy_async": (i32, [vp, vp, sz, i32, vp]),
     "efla_rt_mem_get_info": (i32, [ctypes.POINTER(sz), ctypes.POINTER(sz)]),
     "efla_rt_fill": (i32, [vp, f32, sz, i32, vp]),
+    "efla_rt_set_gemm_backend": (i32, [i32]),
     "efla_rt_stream_create": (i32, [ctypes.POINTER(vp)]),
     "efla_rt_stream_destroy": (i32, [vp]),
     "efla_rt_stream_synchronize": (i32, [vp]),

@@ -1,5 +1,15 @@
-// Row-major GEMM for gfx950 on MFMA, replacing the reference's cuBLAS calls
+// Row-major GEMM for gfx950, replacing the reference's cuBLAS calls
 // (kernels/cuda/gemm.cu:182-234, 303-548).
+//
+// Matching bf16 / fp16 / fp32 operands go to hipBLASLt (a plain library GEMM,
+// as the reference's cuBLAS call is): one handle and one 32 MiB workspace per
+// device, created on first use and kept; the chosen algorithm and descriptors
+// are cached per (shape, transposes, dtype, bias) so a steady-state call does
+// no heuristic query and no device allocation.  The row-major product
+// C = A B is issued as the column-major C^T = B^T A^T, the bias as the
+// epilogue's per-row bias of C^T.  Mixed dtypes, shapes for which hipBLASLt
+// offers no algorithm, and efla_rt_set_gemm_backend(1) take the hand-written
+// MFMA kernel below.
 //
 //   forward:  C[m,n] = sum_k A[m,k] B[k,n] (+ bias[n])     any of fp32/fp16/bf16
 //   backward: dA = dC B^T, dB = A^T dC, dbias = column sums of dC   (bf16)
@@ -17,8 +27,14 @@
 // re-reads).  Matching dtypes run on bf16 / fp16 MFMA; mixed dtypes on fp32
 // MFMA after conversion.
 #include <hip/hip_runtime.h>
+#include <hipblaslt/hipblaslt.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
 
 #include "../../include/efla_hip.h"
+#include "../../include/efla_runtime.h"
 #include "common.hpp"
 #include "internal.hpp"
 
@@ -273,11 +289,154 @@ static int launch_bias_fill(void* c, const void* bias, long M, long N, hipStream
     return (int)hipPeekAtLastError();
 }
 
+// ---------------------------------------------------------------------------
+// hipBLASLt path
+// ---------------------------------------------------------------------------
+constexpr size_t kLtWorkspace = (size_t)32 << 20;
+constexpr int kMaxDev = 64;
+
+struct LtDevice {
+    hipblasLtHandle_t handle = nullptr;
+    void* ws = nullptr;
+    bool broken = false;  // creation failed: always use the native kernel
+};
+
+// (opA, opB, M, N, K, lda, ldb, ldd, dtype, has_bias)
+typedef std::tuple<int, int, long, long, long, long, long, long, int, int> LtKey;
+
+struct LtPlan {
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+    hipblasLtMatmulAlgo_t algo;
+    size_t ws_bytes = 0;
+    bool ok = false;  // false: hipBLASLt offers no algorithm for this problem
+};
+
+static std::mutex g_lt_mu;
+static LtDevice g_lt_dev[kMaxDev];
+static std::map<std::pair<int, LtKey>, LtPlan> g_lt_plans;
+static int g_backend = 0;  // 0: hipBLASLt where possible, 1: native kernel only
+
+static hipDataType lt_type(int dt) {
+    return dt == kDtypeF32 ? HIP_R_32F : dt == kDtypeF16 ? HIP_R_16F : HIP_R_16BF;
+}
+
+// Caller holds g_lt_mu.  nullptr when hipBLASLt is unusable on this device.
+static LtDevice* lt_device(int dev) {
+    if (dev < 0 || dev >= kMaxDev) return nullptr;
+    LtDevice& d = g_lt_dev[dev];
+    if (d.broken) return nullptr;
+    if (!d.handle) {
+        if (hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) {
+            d.handle = nullptr;
+            d.broken = true;
+            return nullptr;
+        }
+        if (hipMalloc(&d.ws, kLtWorkspace) != hipSuccess) {
+            hipblasLtDestroy(d.handle);
+            d.handle = nullptr;
+            d.ws = nullptr;
+            d.broken = true;
+            return nullptr;
+        }
+    }
+    return &d;
+}
+
+static bool lt_plan(LtDevice* d, const LtKey& k, LtPlan* p) {
+    const hipblasOperation_t ta = (hipblasOperation_t)std::get<0>(k);
+    const hipblasOperation_t tb = (hipblasOperation_t)std::get<1>(k);
+    const long M = std::get<2>(k), N = std::get<3>(k), K = std::get<4>(k);
+    const long lda = std::get<5>(k), ldb = std::get<6>(k), ldd = std::get<7>(k);
+    const hipDataType t = lt_type(std::get<8>(k));
+    const bool bias = std::get<9>(k) != 0;
+    if (hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) !=
+        HIPBLAS_STATUS_SUCCESS)
+        return false;
+    int32_t opa = ta, opb = tb;
+    hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa));
+    hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb));
+    if (bias) {
+        hipblasLtEpilogue_t ep = HIPBLASLT_EPILOGUE_BIAS;
+        int32_t bt = t;
+        hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep));
+        hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt,
+                                        sizeof(bt));
+    }
+    // column-major layouts: op(A) is M x K, op(B) is K x N, D is M x N
+    const long ar = ta == HIPBLAS_OP_N ? M : K, ac = ta == HIPBLAS_OP_N ? K : M;
+    const long br = tb == HIPBLAS_OP_N ? K : N, bc = tb == HIPBLAS_OP_N ? N : K;
+    if (hipblasLtMatrixLayoutCreate(&p->a, t, ar, ac, lda) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&p->b, t, br, bc, ldb) != HIPBLAS_STATUS_SUCCESS ||
+        hipblasLtMatrixLayoutCreate(&p->d, t, M, N, ldd) != HIPBLAS_STATUS_SUCCESS)
+        return false;
+    hipblasLtMatmulPreference_t pref;
+    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
+    uint64_t wsb = kLtWorkspace;
+    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
+                                          sizeof(wsb));
+    hipblasLtMatmulHeuristicResult_t res[1];
+    int n = 0;
+    const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(d->handle, p->desc, p->a, p->b,
+                                                               p->d, p->d, pref, 1, res, &n);
+    hipblasLtMatmulPreferenceDestroy(pref);
+    if (st != HIPBLAS_STATUS_SUCCESS || n < 1 || res[0].workspaceSize > kLtWorkspace) return false;
+    p->algo = res[0].algo;
+    p->ws_bytes = res[0].workspaceSize;
+    return true;
+}
+
+// Column-major D[M x N] = op(A) op(B) (+ bias[M] per row), all of dtype dt,
+// fp32 accumulation.  Returns kSuccess, a launch error, or -1 when hipBLASLt
+// cannot take the problem (the caller then runs the native kernel).
+static int lt_matmul(hipblasOperation_t ta, hipblasOperation_t tb, long M, long N, long K,
+                     const void* A, long lda, const void* B, long ldb, void* D, long ldd,
+                     const void* bias, int dt, hipStream_t stream) {
+    std::lock_guard<std::mutex> lk(g_lt_mu);
+    if (g_backend != 0) return -1;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return -1;
+    LtDevice* d = lt_device(dev);
+    if (!d) return -1;
+    const LtKey key(ta, tb, M, N, K, lda, ldb, ldd, dt, bias ? 1 : 0);
+    auto it = g_lt_plans.find({dev, key});
+    if (it == g_lt_plans.end()) {
+        LtPlan p;
+        p.ok = lt_plan(d, key, &p);
+        it = g_lt_plans.emplace(std::make_pair(dev, key), p).first;
+    }
+    LtPlan& p = it->second;
+    if (!p.ok) return -1;
+    if (bias)
+        hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias,
+                                        sizeof(bias));
+    const float one = 1.f, zero = 0.f;
+    ::efla::ProfScope ps("gemm_hipblaslt", stream);
+    const hipblasStatus_t st = hipblasLtMatmul(d->handle, p.desc, &one, A, p.a, B, p.b, &zero, D,
+                                               p.d, D, p.d, &p.algo, d->ws, p.ws_bytes, stream);
+    if (st != HIPBLAS_STATUS_SUCCESS) return kInvalidValue;
+    return (int)hipPeekAtLastError();
+}
+
+// Row-major C[m x n] = A[m x k] B[k x n] (+ bias[n]) as column-major
+// C^T = B^T A^T: A' = B (n x k, ld n), B' = A (k x m, ld k), bias per row of C^T.
+static int lt_forward(const void* a, const void* b, const void* bias, void* c, long m, long k,
+                      long n, int dt, hipStream_t st) {
+    return lt_matmul(HIPBLAS_OP_N, HIPBLAS_OP_N, n, m, k, b, n, a, k, c, n, bias, dt, st);
+}
+
 }  // namespace gm
 }  // namespace efla
 
 using namespace efla;
 using namespace efla::gm;
+
+extern "C" int efla_rt_set_gemm_backend(int backend) {
+    if (backend != 0 && backend != 1) return kInvalidValue;
+    std::lock_guard<std::mutex> lk(g_lt_mu);
+    g_backend = backend;
+    return kSuccess;
+}
 
 extern "C" int gemm_forward_hip(const void* a, const void* b, const void* bias, void* c,
                                 size_t m, size_t k, size_t n, int dtype_a, int dtype_b,
@@ -295,6 +454,10 @@ extern "C" int gemm_forward_hip(const void* a, const void* b, const void* bias, 
             case kDtypeF16: return launch_bias_fill<f16>(c, bias, (long)m, (long)n, stream);
             default: return launch_bias_fill<bf16>(c, bias, (long)m, (long)n, stream);
         }
+    }
+    if (dtype_a == dtype_b && dtype_b == dtype_c) {
+        const int rc = lt_forward(a, b, bias, c, (long)m, (long)k, (long)n, dtype_a, stream);
+        if (rc >= 0) return rc;
     }
     switch (dtype_a) {
         case kDtypeF32:
@@ -340,14 +503,22 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
     }
     const long M = (long)m, K = (long)k, N = (long)n;
     if (need_a && m && k && n) {
-        // dA[m, k] = sum_n dC[m, n] B[k, n]
-        int rc = launch<bf16, bf16, bf16, bf16, true, true>(grad_c, b, nullptr, grad_a, M, K, N,
+        // dA[m, k] = sum_n dC[m, n] B[k, n]; column-major dA^T = op_T(B') dC^T
+        // with B' = B as (n x k, ld n) and dC^T as (n x m, ld n)
+        int rc = lt_matmul(HIPBLAS_OP_T, HIPBLAS_OP_N, K, M, N, b, N, grad_c, N, grad_a, K,
+                           nullptr, kDtypeBF16, stream);
+        if (rc < 0)
+            rc = launch<bf16, bf16, bf16, bf16, true, true>(grad_c, b, nullptr, grad_a, M, K, N,
                                                             N, N, K, "gemm_bwd_da", stream);
         if (rc != kSuccess) return rc;
     }
     if (need_b && m && k && n) {
-        // dB[k, n] = sum_m A[m, k] dC[m, n]
-        int rc = launch<bf16, bf16, bf16, bf16, false, false>(a, grad_c, nullptr, grad_b, K, N, M,
+        // dB[k, n] = sum_m A[m, k] dC[m, n]; column-major dB^T = dC^T op_T(A')
+        // with dC^T as (n x m, ld n) and A' = A as (k x m, ld k)
+        int rc = lt_matmul(HIPBLAS_OP_N, HIPBLAS_OP_T, N, K, M, grad_c, N, a, K, grad_b, N,
+                           nullptr, kDtypeBF16, stream);
+        if (rc < 0)
+            rc = launch<bf16, bf16, bf16, bf16, false, false>(a, grad_c, nullptr, grad_b, K, N, M,
                                                               K, N, N, "gemm_bwd_db", stream);
         if (rc != kSuccess) return rc;
     }

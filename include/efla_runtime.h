@@ -63,6 +63,11 @@ size_t efla_rt_workspace_bytes(void);
 /* Release the cached workspace of the current device (synchronises it). */
 int efla_rt_workspace_release(void);
 
+/* GEMM backend of gemm_forward_hip / gemm_backward_hip for this process:
+ * 0 (default) hipBLASLt where it takes the problem, else the library's own
+ * MFMA kernel; 1 the library's own kernel always.  Other values -> 1. */
+int efla_rt_set_gemm_backend(int backend);
+
 /* --- launch profiler ---
  * While enabled, each kernel the library launches is bracketed by hipEvents
  * recorded on its stream.  efla_prof_collect() waits for the recorded events

@@ -58,12 +58,23 @@ def test_layernorm_backward(oracle, rows, D):
     assert errs[0] <= 1e-2 and errs[1] <= 1e-4 and errs[2] <= 1e-5
 
 
+@pytest.fixture(params=[0, 1], ids=["hipblaslt", "native"])
+def gemm_backend(request):
+    """Runs a GEMM test on the hipBLASLt path and on the library's own MFMA
+    kernel (efla_rt_set_gemm_backend), restoring the default afterwards."""
+    from ceo_amd._lib import lib
+
+    assert lib().efla_rt_set_gemm_backend(request.param) == 0
+    yield request.param
+    assert lib().efla_rt_set_gemm_backend(0) == 0
+
+
 @pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (1, 64, 8), (300, 1024, 260)])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
-def test_gemm_forward(m, k, n, dt):
+def test_gemm_forward(m, k, n, dt, gemm_backend):
     from ceo_amd.nn import gemm_forward
 
-    announce(f"gemm_forward {m}x{k}x{n} {dt}")
+    announce(f"gemm_forward {m}x{k}x{n} {dt} backend={gemm_backend}")
     g = torch.Generator().manual_seed(m * 7 + n)
     a = torch.randn(m, k, generator=g).to(dt)
     b = torch.randn(k, n, generator=g).to(dt)
@@ -85,6 +96,22 @@ def test_gemm_forward_mixed_dtypes():
     c = gemm_forward(a.cuda(), b.cuda(), None, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert rel_l2(c, (a.double() @ b.double()).numpy()) <= 1e-5
+
+
+def test_gemm_bias_epilogue_at_layer_shape():
+    """hipBLASLt's bias epilogue on a config-4 projection shape, against torch."""
+    from ceo_amd.nn import gemm_forward
+
+    announce("gemm_forward 2048x1024x3072 bf16 + bias")
+    g = torch.Generator(device="cuda").manual_seed(3)
+    a = torch.randn(2048, 1024, generator=g, device="cuda").to(torch.bfloat16)
+    b = (0.03 * torch.randn(1024, 3072, generator=g, device="cuda")).to(torch.bfloat16)
+    bias = torch.randn(3072, generator=g, device="cuda").to(torch.bfloat16)
+    c = gemm_forward(a, b, bias)
+    ref = a.float() @ b.float() + bias.float()
+    e = rel_l2(c, ref.cpu().numpy())
+    print(f"  rel-L2={e:.2e}", flush=True)
+    assert e <= 1e-2
 
 
 def test_gemm_k0_gives_bias():
@@ -112,10 +139,10 @@ def test_gemm_k0_gives_bias():
 
 
 @pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (513, 200, 129)])
-def test_gemm_backward(m, k, n):
+def test_gemm_backward(m, k, n, gemm_backend):
     from ceo_amd.nn import gemm_backward
 
-    announce(f"gemm_backward {m}x{k}x{n}")
+    announce(f"gemm_backward {m}x{k}x{n} backend={gemm_backend}")
     g = torch.Generator().manual_seed(m + k + n)
     a = torch.randn(m, k, generator=g).to(torch.bfloat16)
     b = torch.randn(k, n, generator=g).to(torch.bfloat16)
