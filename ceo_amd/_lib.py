@@ -90,6 +90,12 @@ _SIGS = {
     "gelu_backward_hip": (i32, [vp, vp, vp, sz, ctypes.c_bool, vp]),
     "adamw_step_hip": (i32, [vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, sz, vp]),
     "adamw_step_master_hip": (i32, [vp, vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, sz, vp]),
+    # embedding, cross-entropy
+    "embedding_forward_hip": (i32, [vp, vp, vp, sz, sz, vp]),
+    "embedding_forward_checked_hip": (i32, [vp, vp, vp, sz, sz, sz, vp]),
+    "embedding_backward_hip": (i32, [vp, vp, vp, sz, sz, sz, vp]),
+    "cross_entropy_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
+    "cross_entropy_backward_hip": (i32, [vp, vp, vp, vp, sz, sz, f32, vp]),
     # runtime
     "efla_rt_device_count": (i32, [ctypes.POINTER(i32)]),
     "efla_rt_set_device": (i32, [i32]),

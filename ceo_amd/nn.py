@@ -140,3 +140,60 @@ def adamw_step_master(param, grad, exp_avg, exp_avg_sq, lr, beta1=0.9, beta2=0.9
                                      float(beta2), float(eps), float(weight_decay), int(step),
                                      _stream(param))
     check(rc, "adamw_step_master_hip")
+
+
+def embedding_forward(indices: torch.Tensor, weight: torch.Tensor,
+                      checked: bool = True) -> torch.Tensor:
+    """weight[indices] for int32 indices and a (vocab, dim) bf16 table; with
+    ``checked`` an out-of-range index gives a zero row."""
+    _require(indices, "indices", torch.int32)
+    _require(weight, "weight", torch.bfloat16, indices.device)
+    V, D = weight.shape
+    out = torch.empty(*indices.shape, D, dtype=torch.bfloat16, device=weight.device)
+    if checked:
+        rc = lib().embedding_forward_checked_hip(_p(indices), _p(weight), _p(out),
+                                                 indices.numel(), V, D, _stream(weight))
+        check(rc, "embedding_forward_checked_hip")
+    else:
+        rc = lib().embedding_forward_hip(_p(indices), _p(weight), _p(out), indices.numel(), D,
+                                         _stream(weight))
+        check(rc, "embedding_forward_hip")
+    return out
+
+
+def embedding_backward(grad_output: torch.Tensor, indices: torch.Tensor, grad_weight) -> None:
+    """grad_weight (vocab, dim) fp32 += scatter of grad_output rows by index."""
+    _require(indices, "indices", torch.int32)
+    _require(grad_output, "grad_output", torch.bfloat16, indices.device)
+    _require(grad_weight, "grad_weight", torch.float32, indices.device)
+    V, D = grad_weight.shape
+    rc = lib().embedding_backward_hip(_p(grad_output), _p(indices), _p(grad_weight),
+                                      indices.numel(), V, D, _stream(grad_weight))
+    check(rc, "embedding_backward_hip")
+
+
+def cross_entropy_forward(logits: torch.Tensor, targets: torch.Tensor,
+                          label_smoothing: float = 0.0) -> torch.Tensor:
+    """Per-row loss / batch, fp32 (B,): its sum is the mean loss."""
+    _require(logits, "logits", torch.bfloat16)
+    _require(targets, "targets", torch.int32, logits.device)
+    B, V = logits.shape
+    loss = torch.empty(B, dtype=torch.float32, device=logits.device)
+    rc = lib().cross_entropy_forward_hip(_p(logits), _p(targets), _p(loss), B, V,
+                                         float(label_smoothing), _stream(logits))
+    check(rc, "cross_entropy_forward_hip")
+    return loss
+
+
+def cross_entropy_backward(grad_loss: torch.Tensor, logits: torch.Tensor, targets: torch.Tensor,
+                           label_smoothing: float = 0.0) -> torch.Tensor:
+    """dL/dlogits (bf16) given dL/dloss[i] (fp32, (B,))."""
+    _require(logits, "logits", torch.bfloat16)
+    _require(targets, "targets", torch.int32, logits.device)
+    _require(grad_loss, "grad_loss", torch.float32, logits.device)
+    B, V = logits.shape
+    g = torch.empty_like(logits)
+    rc = lib().cross_entropy_backward_hip(_p(grad_loss), _p(logits), _p(targets), _p(g), B, V,
+                                          float(label_smoothing), _stream(logits))
+    check(rc, "cross_entropy_backward_hip")
+    return g

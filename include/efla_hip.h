@@ -223,6 +223,49 @@ int adamw_step_master_hip(float* param, const void* grad, float* exp_avg, float*
                           void* param_bf16, size_t numel, float lr, float beta1, float beta2,
                           float eps, float weight_decay, size_t step, hipStream_t stream);
 
+/* ========================================================================
+ * Token embedding and cross-entropy (the ends of the config-4 step)
+ * ======================================================================== */
+
+/* Replaces embedding_forward_cuda (kernels.h:366-373; declared only in the
+ * reference, semantics of Embedding.forward, layers.zig:658-686):
+ * output[i, :] = weight[indices[i], :], bf16, indices int32.  Like the
+ * reference entry it cannot range-check (no vocabulary size): every index
+ * must be valid.  num_indices == 0 -> 0; NULL or embedding_dim == 0 -> 1. */
+int embedding_forward_hip(const int32_t* indices, const void* weight, void* output,
+                          size_t num_indices, size_t embedding_dim, hipStream_t stream);
+
+/* No reference counterpart: embedding_forward_hip with the vocabulary size;
+ * an index outside [0, num_embeddings) gives a zero row. */
+int embedding_forward_checked_hip(const int32_t* indices, const void* weight, void* output,
+                                  size_t num_indices, size_t num_embeddings,
+                                  size_t embedding_dim, hipStream_t stream);
+
+/* No reference counterpart: grad_weight[indices[i], :] += grad_output[i, :]
+ * in fp32 (grad_weight is accumulated into, not cleared; duplicate indices
+ * add in no fixed order); indices out of range are skipped. */
+int embedding_backward_hip(const void* grad_output, const int32_t* indices, float* grad_weight,
+                           size_t num_indices, size_t num_embeddings, size_t embedding_dim,
+                           hipStream_t stream);
+
+/* Replaces cross_entropy_forward_cuda (kernels.h:248-256; declared only,
+ * semantics of crossEntropyForwardCpu, nn_kernels.zig:200-246): logits
+ * (batch, vocab) bf16, targets int32, loss (batch,) fp32 with
+ *   loss[i] = ((1 - eps) (logsumexp(z_i) - z_i,t) + eps log vocab) / batch,
+ * so sum(loss) is the mean loss.  A target outside [0, vocab) gives NaN.
+ * batch == 0 -> 0; NULL, vocab == 0 or eps outside [0, 1) -> 1. */
+int cross_entropy_forward_hip(const void* logits, const int32_t* targets, void* loss,
+                              size_t batch_size, size_t vocab_size, float label_smoothing,
+                              hipStream_t stream);
+
+/* Replaces cross_entropy_backward_cuda (kernels.h:261-270): grad_loss
+ * (batch,) fp32 is dL/dloss[i]; grad_logits (batch, vocab) bf16 =
+ * grad_loss[i] (1 - eps) (softmax(z_i) - onehot(t_i)) / batch.  Same return
+ * codes as the forward. */
+int cross_entropy_backward_hip(const void* grad_loss, const void* logits, const int32_t* targets,
+                               void* grad_logits, size_t batch_size, size_t vocab_size,
+                               float label_smoothing, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

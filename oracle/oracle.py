@@ -36,6 +36,11 @@ Contents and what pins each part (tests/test_oracle_*.py):
   and with bf16 state.  Pinned by an fp64 closed form at steps 1 and 7 and the
   zero-state identity p1 = p0 (1 - lr wd) - lr g / (|g| + eps); the bf16 form
   adds only the bf16 round trip, pinned by the reference's KAT (dtype.zig:654).
+* ``cross_entropy_fwd`` / ``cross_entropy_bwd`` -- nn_kernels.zig:200-246.
+  Pinned by torch's cross_entropy and its autograd (eps = 0), uniform logits
+  (loss log V for every eps) and zero-sum gradient rows.
+* ``embedding_fwd`` / ``embedding_bwd`` -- layers.zig:658-686 and its
+  adjoint; pinned by a dense one-hot matmul (E = onehot W, dW = onehot^T dY).
 """
 from __future__ import annotations
 
@@ -444,6 +449,56 @@ def adamw_step_bf16(p, g, m, v, lr, b1, b2, eps, wd, step):
     pf, gf, mf, vf = (bf16_to_f32(a) for a in (p, g, m, v))
     adamw_step(pf, gf, mf, vf, lr, b1, b2, eps, wd, step)
     return f32_to_bf16(pf), f32_to_bf16(mf), f32_to_bf16(vf)
+
+
+def cross_entropy_fwd(logits, targets, label_smoothing=0.0):
+    """crossEntropyForwardCpu (nn_kernels.zig:200-246) in fp64: per-row
+    ((1 - eps) (logsumexp - z_t) + eps log V) / B; NaN for a target outside
+    [0, V).  Returns the (B,) array whose sum is the mean loss."""
+    z = np.asarray(logits, dtype=np.float64)
+    B, V = z.shape
+    t = np.asarray(targets).astype(np.int64)
+    m = z.max(axis=1, keepdims=True)
+    lse = (m + np.log(np.exp(z - m).sum(axis=1, keepdims=True)))[:, 0]
+    ok = (t >= 0) & (t < V)
+    zt = np.where(ok, z[np.arange(B), np.clip(t, 0, V - 1)], 0.0)
+    loss = ((1.0 - label_smoothing) * (lse - zt) + label_smoothing * np.log(V)) / B
+    return np.where(ok, loss, np.nan)
+
+
+def cross_entropy_bwd(grad_loss, logits, targets, label_smoothing=0.0):
+    """d loss / d logits for the forward above: grad_loss[i] (1 - eps)
+    (softmax_i - onehot(t_i)) / B, zero rows for invalid targets (fp64)."""
+    z = np.asarray(logits, dtype=np.float64)
+    B, V = z.shape
+    t = np.asarray(targets).astype(np.int64)
+    p = np.exp(z - z.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    ok = (t >= 0) & (t < V)
+    p[np.arange(B)[ok], t[ok]] -= 1.0
+    coef = np.where(ok, np.asarray(grad_loss, dtype=np.float64) * (1 - label_smoothing) / B, 0.0)
+    return p * coef[:, None]
+
+
+def embedding_fwd(indices, weight):
+    """Embedding.forward (layers.zig:658-686): rows of `weight`; an index
+    outside the table gives a zero row (the checked entry's behaviour)."""
+    w = np.asarray(weight)
+    idx = np.asarray(indices).astype(np.int64)
+    ok = (idx >= 0) & (idx < w.shape[0])
+    out = np.zeros((idx.size, w.shape[1]), dtype=w.dtype)
+    out[ok] = w[idx[ok]]
+    return out
+
+
+def embedding_bwd(grad_output, indices, num_embeddings):
+    """sum of grad_output rows per index (fp64), out-of-range indices skipped."""
+    g = np.asarray(grad_output, dtype=np.float64)
+    idx = np.asarray(indices).astype(np.int64)
+    ok = (idx >= 0) & (idx < num_embeddings)
+    dw = np.zeros((num_embeddings, g.shape[1]))
+    np.add.at(dw, idx[ok], g[ok])
+    return dw
 
 
 def num_threads() -> int:

@@ -174,3 +174,20 @@ def test_adamw_validation(L):
         assert fn(3e-4, 0.9, 0.999, 0.0, 0.1, 1) == 1       # eps <= 0
         assert fn(3e-4, 0.9, 0.999, 1e-8, float("inf"), 1) == 1
         assert fn(3e-4, 0.9, 0.999, 1e-8, 0.1, 0) == 1      # step == 0
+
+
+def test_embedding_and_cross_entropy_validation(L):
+    p = ctypes.c_void_p(16)
+    assert L.embedding_forward_hip(p, p, p, 0, 8, NULL) == 0
+    assert L.embedding_forward_hip(NULL, p, p, 4, 8, NULL) == 1
+    assert L.embedding_forward_hip(p, p, p, 4, 0, NULL) == 1
+    assert L.embedding_forward_checked_hip(p, p, p, 4, 0, 8, NULL) == 1   # empty table
+    assert L.embedding_backward_hip(p, p, p, 0, 10, 8, NULL) == 0
+    assert L.embedding_backward_hip(p, NULL, p, 4, 10, 8, NULL) == 1
+    assert L.cross_entropy_forward_hip(p, p, p, 0, 100, 0.0, NULL) == 0
+    assert L.cross_entropy_forward_hip(NULL, p, p, 4, 100, 0.0, NULL) == 1
+    assert L.cross_entropy_forward_hip(p, p, p, 4, 0, 0.0, NULL) == 1
+    assert L.cross_entropy_forward_hip(p, p, p, 4, 100, 1.0, NULL) == 1   # eps outside [0, 1)
+    assert L.cross_entropy_forward_hip(p, p, NULL, 4, 100, 0.0, NULL) == 1
+    assert L.cross_entropy_backward_hip(NULL, p, p, p, 4, 100, 0.0, NULL) == 1
+    assert L.cross_entropy_backward_hip(p, p, p, p, 4, 100, float("nan"), NULL) == 1

@@ -113,3 +113,42 @@ def test_adamw_bf16_state_is_the_fp32_step_rounded(oracle):
         g = oracle.bf16_to_f32(got).astype(np.float64)
         # one bf16 step at most (the fp32 step can sit on the other side of a boundary)
         assert np.all(np.abs(g - ref) <= np.abs(ref) * 2.0 ** -7 + 1e-30)
+
+
+def test_cross_entropy_matches_torch(oracle):
+    rng = np.random.default_rng(5)
+    B, V = 7, 33
+    z = rng.standard_normal((B, V)) * 3
+    t = rng.integers(0, V, B)
+    zt = torch.tensor(z, requires_grad=True)
+    ref = torch.nn.functional.cross_entropy(zt, torch.tensor(t), reduction="mean")
+    loss = oracle.cross_entropy_fwd(z, t)
+    assert abs(loss.sum() - ref.item()) < 1e-12
+    ref.backward()
+    assert np.abs(oracle.cross_entropy_bwd(np.ones(B), z, t) - zt.grad.numpy()).max() < 1e-12
+    # label smoothing as the CPU reference: (1 - eps) loss_0 + eps log V, per row / B
+    l2 = oracle.cross_entropy_fwd(z, t, 0.1)
+    assert np.allclose(l2, 0.9 * loss + 0.1 * np.log(V) / B)
+    # uniform logits: log V for any eps; gradient rows sum to zero
+    assert np.allclose(oracle.cross_entropy_fwd(np.zeros((B, V)), t, 0.3).sum(), np.log(V))
+    g = oracle.cross_entropy_bwd(rng.standard_normal(B), z, t, 0.2)
+    assert np.abs(g.sum(axis=1)).max() < 1e-12
+    # invalid target: NaN loss, zero gradient row
+    t2 = t.copy()
+    t2[2] = V
+    assert np.isnan(oracle.cross_entropy_fwd(z, t2)[2])
+    assert not oracle.cross_entropy_bwd(np.ones(B), z, t2)[2].any()
+
+
+def test_embedding_is_a_one_hot_product(oracle):
+    rng = np.random.default_rng(6)
+    V, D, N = 11, 5, 40
+    w = rng.standard_normal((V, D))
+    idx = rng.integers(0, V, N)
+    onehot = np.eye(V)[idx]
+    assert np.array_equal(oracle.embedding_fwd(idx, w), onehot @ w)
+    dy = rng.standard_normal((N, D))
+    assert np.allclose(oracle.embedding_bwd(dy, idx, V), onehot.T @ dy)
+    bad = idx.copy()
+    bad[3] = V
+    assert not oracle.embedding_fwd(bad, w)[3].any()
