@@ -1,6 +1,6 @@
 """EFLA fwd+bwd throughput on one MI355X (the headline benchmark).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg2|cfg5]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg2|cfg4|cfg5]
                     [--no-cpu] [--cpu-budget SECONDS] [--aux]
 
 A step is one chunked EFLA forward plus one backward (the backward recomputes
@@ -309,6 +309,70 @@ def aux_bench(steps: int, warmup: int) -> int:
 
 
 # ---------------------------------------------------------------------------
+# config 4: the full training step of the decoder LM
+# ---------------------------------------------------------------------------
+def lm_bench(steps: int, warmup: int, seed: int) -> int:
+    """Times forwardStep + backwardStep + updateStep of the config-4 model
+    (random init, synthetic uniform token ids, batch 8 x 2048).  Prints one
+    JSON line: tokens/s and model FLOP utilisation, with the per-kernel split."""
+    import torch
+
+    from ceo_amd import runtime
+    from ceo_amd.lm_step import EflaLM, LMConfig, step_flops, synthetic_batch
+
+    dev = torch.device("cuda:0")
+    cfg = LMConfig()
+    B, T = 8, 2048
+    model = EflaLM(cfg, device=dev, seed=seed)
+    tokens, targets = synthetic_batch(cfg, B, T, seed=seed + 1, device=dev)
+    print(f"[bench] cfg4: {model.n_params / 1e6:.1f} M parameters, batch {B} x {T}",
+          file=sys.stderr, flush=True)
+    losses = []
+    for _ in range(warmup):
+        losses.append(model.train_step(tokens, targets))
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    prof = runtime.Profiler()
+    with prof:
+        ev0.record(stream)
+        for _ in range(steps):
+            losses.append(model.train_step(tokens, targets))
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    kern = prof.results()
+    lib_ms = sum(tot for _, tot in kern.values()) / steps
+    groups = {}
+    for name, (n, tot) in kern.items():
+        key = ("gemm" if name.startswith("gemm") else "efla" if name.startswith("efla")
+               else name.split("_")[0])
+        groups[key] = groups.get(key, 0.0) + tot / steps
+    flops = step_flops(cfg, B * T, T)
+    line = {
+        "metric": "config-4 training step tokens/s (fwd + bwd + AdamW)",
+        "value": round(B * T / (ms * 1e-3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (uniform token ids, random init)",
+        "config": {"workload": "cfg4: d_model 1024, 24 layers, 16 EFLA heads x 64, MLP 4096, "
+                               "vocab 32000, batch 8 x 2048, fp32 master + AdamW",
+                   "params": model.n_params, "tokens_per_step": B * T},
+        "model_tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+        "mfu_bf16": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "library_kernel_ms": round(lib_ms, 3),
+        "kernel_ms_by_group": {k: round(v, 3) for k, v in sorted(groups.items(),
+                                                                 key=lambda kv: -kv[1])},
+        "kernels": {k: {"launches_per_step": n / steps, "ms_per_step": round(tot / steps, 3)}
+                    for k, (n, tot) in sorted(kern.items(), key=lambda kv: -kv[1][1])},
+        "loss_first_last": [round(losses[0].item(), 4), round(losses[-1].item(), 4)],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+# ---------------------------------------------------------------------------
 # main
 # ---------------------------------------------------------------------------
 def main() -> int:
@@ -316,7 +380,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg4"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (whole sequences, at least one)")
@@ -347,6 +411,8 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.config == "cfg4":
+        return lm_bench(args.steps, args.warmup, args.seed & 0xFFFF)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     cfg = CONFIGS[args.config]

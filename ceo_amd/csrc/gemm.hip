@@ -2,7 +2,7 @@
 // (kernels/cuda/gemm.cu:182-234, 303-548).
 //
 // Matching bf16 / fp16 / fp32 operands go to hipBLASLt (a plain library GEMM,
-// as the reference's cuBLAS call is): one handle and one 32 MiB workspace per
+// as the reference's cuBLAS call is): one handle and one 128 MiB workspace per
 // device, created on first use and kept; the chosen algorithm and descriptors
 // are cached per (shape, transposes, dtype, bias) so a steady-state call does
 // no heuristic query and no device allocation.  The row-major product
@@ -212,6 +212,46 @@ __global__ void __launch_bounds__(NTH) colsum_kernel(const bf16* __restrict__ x,
                       part[3][threadIdx.x]);
 }
 
+// Column sums at full width: workgroup (blockIdx.x, blockIdx.y) sums columns
+// 128 x .. 128 x + 127 over rows y, y + RS, y + 2 RS, ... (16 row groups of 16
+// lanes, 8 bf16 columns each with 16-byte loads) into part[y][col]; a second
+// kernel adds the RS partial rows in a fixed order.  N % 8 == 0, x aligned.
+constexpr int CS_RS = 32;  // row splits
+__global__ void __launch_bounds__(NTH) colsum_part_kernel(const bf16* __restrict__ x,
+                                                          float* __restrict__ part, long M,
+                                                          long N) {
+    __shared__ float acc[16][128 + 4];
+    const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
+    const long c0 = (long)blockIdx.x * 128 + 8 * q;
+    float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (c0 < N)
+        for (long r = (long)blockIdx.y + (long)rg * CS_RS; r < M; r += 16L * CS_RS) {
+            const bf16x8 v = *reinterpret_cast<const bf16x8*>(x + r * N + c0);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s[i] += (float)v[i];
+        }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[rg][8 * q + i] = s[i];
+    __syncthreads();
+    if (threadIdx.x < 128) {
+        const long c = (long)blockIdx.x * 128 + threadIdx.x;
+        float t = 0.f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) t += acc[k][threadIdx.x];
+        if (c < N) part[(long)blockIdx.y * N + c] = t;
+    }
+}
+
+__global__ void __launch_bounds__(NTH) colsum_final_kernel(const float* __restrict__ part,
+                                                           bf16* __restrict__ y, long N) {
+    const long c = (long)blockIdx.x * NTH + threadIdx.x;
+    if (c >= N) return;
+    float t = 0.f;
+#pragma unroll 8
+    for (int k = 0; k < CS_RS; ++k) t += part[(long)k * N + c];
+    y[c] = (bf16)t;
+}
+
 // k == 0: C = bias (broadcast) or 0
 template <typename TC>
 __global__ void __launch_bounds__(NTH) bias_fill_kernel(TC* __restrict__ C,
@@ -292,7 +332,7 @@ static int launch_bias_fill(void* c, const void* bias, long M, long N, hipStream
 // ---------------------------------------------------------------------------
 // hipBLASLt path
 // ---------------------------------------------------------------------------
-constexpr size_t kLtWorkspace = (size_t)32 << 20;
+constexpr size_t kLtWorkspace = (size_t)128 << 20;
 constexpr int kMaxDev = 64;
 
 struct LtDevice {
@@ -375,15 +415,20 @@ static bool lt_plan(LtDevice* d, const LtKey& k, LtPlan* p) {
     uint64_t wsb = kLtWorkspace;
     hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
                                           sizeof(wsb));
-    hipblasLtMatmulHeuristicResult_t res[1];
+    hipblasLtMatmulHeuristicResult_t res[8];
     int n = 0;
     const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(d->handle, p->desc, p->a, p->b,
-                                                               p->d, p->d, pref, 1, res, &n);
+                                                               p->d, p->d, pref, 8, res, &n);
     hipblasLtMatmulPreferenceDestroy(pref);
-    if (st != HIPBLAS_STATUS_SUCCESS || n < 1 || res[0].workspaceSize > kLtWorkspace) return false;
-    p->algo = res[0].algo;
-    p->ws_bytes = res[0].workspaceSize;
-    return true;
+    if (st != HIPBLAS_STATUS_SUCCESS) return false;
+    for (int i = 0; i < n; ++i) {  // best-ranked first
+        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kLtWorkspace)
+            continue;
+        p->algo = res[i].algo;
+        p->ws_bytes = res[i].workspaceSize;
+        return true;
+    }
+    return false;
 }
 
 // Column-major D[M x N] = op(A) op(B) (+ bias[M] per row), all of dtype dt,
@@ -523,8 +568,19 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
         if (rc != kSuccess) return rc;
     }
     if (need_bias && m && n) {
-        EFLA_LAUNCH("gemm_bwd_dbias", colsum_kernel, dim3((unsigned)((N + 63) / 64)), dim3(NTH),
-                    stream, (const bf16*)grad_c, (bf16*)grad_bias, M, N);
+        void* ws = nullptr;
+        if (N % 8 == 0 && aligned16(grad_c) &&
+            workspace_acquire((size_t)CS_RS * N * sizeof(float), stream, &ws) == kSuccess) {
+            EFLA_LAUNCH("gemm_bwd_dbias", colsum_part_kernel,
+                        dim3((unsigned)((N + 127) / 128), CS_RS), dim3(NTH), stream,
+                        (const bf16*)grad_c, (float*)ws, M, N);
+            EFLA_LAUNCH("gemm_bwd_dbias_final", colsum_final_kernel,
+                        dim3((unsigned)((N + NTH - 1) / NTH)), dim3(NTH), stream,
+                        (const float*)ws, (bf16*)grad_bias, N);
+        } else {
+            EFLA_LAUNCH("gemm_bwd_dbias", colsum_kernel, dim3((unsigned)((N + 63) / 64)),
+                        dim3(NTH), stream, (const bf16*)grad_c, (bf16*)grad_bias, M, N);
+        }
     }
     return (int)hipPeekAtLastError();
 }

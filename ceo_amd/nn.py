@@ -72,15 +72,23 @@ def gemm_forward(a: torch.Tensor, b: torch.Tensor, bias=None, out_dtype=None) ->
 
 
 def gemm_backward(dc: torch.Tensor, a: torch.Tensor, b: torch.Tensor, need_a=True, need_b=True,
-                  need_bias=False):
-    """(da, db, dbias) for c = a @ b + bias, all bf16."""
+                  need_bias=False, out_a=None, out_b=None, out_bias=None):
+    """(da, db, dbias) for c = a @ b + bias, all bf16; ``out_*`` (contiguous,
+    right shape) receive the results instead of new tensors."""
     m, k = a.shape
     n = b.shape[1]
     for t, nme in ((dc, "dc"), (a, "a"), (b, "b")):
         _require(t, nme, torch.bfloat16, a.device)
-    da = torch.empty_like(a) if need_a else None
-    dbm = torch.empty_like(b) if need_b else None
-    dbias = torch.empty(n, dtype=torch.bfloat16, device=a.device) if need_bias else None
+    for t, nme, shape in ((out_a, "out_a", (m, k)), (out_b, "out_b", (k, n)),
+                          (out_bias, "out_bias", (n,))):
+        if t is not None:
+            _require(t, nme, torch.bfloat16, a.device)
+            if tuple(t.shape) != shape:
+                raise ValueError(f"gemm_backward: {nme} must be {shape}")
+    da = (out_a if out_a is not None else torch.empty_like(a)) if need_a else None
+    dbm = (out_b if out_b is not None else torch.empty_like(b)) if need_b else None
+    dbias = (out_bias if out_bias is not None else
+             torch.empty(n, dtype=torch.bfloat16, device=a.device)) if need_bias else None
     rc = lib().gemm_backward_hip(_p(dc), _p(a), _p(b), _p(da), _p(dbm), _p(dbias), m, k, n,
                                  _stream(a))
     check(rc, "gemm_backward_hip")
