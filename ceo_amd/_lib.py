@@ -96,6 +96,9 @@ _SIGS = {
     "embedding_backward_hip": (i32, [vp, vp, vp, sz, sz, sz, vp]),
     "cross_entropy_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
     "cross_entropy_backward_hip": (i32, [vp, vp, vp, vp, sz, sz, f32, vp]),
+    # sequence packing (host)
+    "efla_pack_sequences": (i32, [vp, vp, sz, sz, vp, vp, vp, vp, ctypes.POINTER(sz),
+                                  ctypes.POINTER(sz)]),
     # runtime
     "efla_rt_device_count": (i32, [ctypes.POINTER(i32)]),
     "efla_rt_set_device": (i32, [i32]),

@@ -266,6 +266,23 @@ int cross_entropy_backward_hip(const void* grad_loss, const void* logits, const 
                                void* grad_logits, size_t batch_size, size_t vocab_size,
                                float label_smoothing, hipStream_t stream);
 
+/* ========================================================================
+ * Sequence packing (host, no GPU)
+ * ======================================================================== */
+
+/* Replaces packSequences (src/data/dataset.zig:421-465): the sequences are
+ * given concatenated in `tokens` with their `lengths`; each is packed in
+ * order if it fits in what is left of max_length and skipped otherwise.
+ * Outputs (each may be NULL): packed_tokens, positions (index within its
+ * sequence) and sequence_ids, max_length entries each; cu_seqlens int32, at
+ * most num_sequences_in + 1 entries, starting at 0 (the reference's
+ * cumulative_lengths are cu_seqlens[1..]).  Host memory; returns 0, 1 for a
+ * NULL count pointer or NULL inputs, 9 when max_length exceeds INT32_MAX. */
+int efla_pack_sequences(const uint32_t* tokens, const size_t* lengths, size_t num_sequences_in,
+                        size_t max_length, uint32_t* packed_tokens, size_t* positions,
+                        size_t* sequence_ids, int32_t* cu_seqlens, size_t* num_tokens_out,
+                        size_t* num_sequences_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -41,6 +41,9 @@ Contents and what pins each part (tests/test_oracle_*.py):
   (loss log V for every eps) and zero-sum gradient rows.
 * ``embedding_fwd`` / ``embedding_bwd`` -- layers.zig:658-686 and its
   adjoint; pinned by a dense one-hot matmul (E = onehot W, dW = onehot^T dY).
+* ``pack_sequences`` -- dataset.zig:421-465; pinned by the reference's own
+  test (dataset.zig:467-481: 9 tokens, 3 sequences) and by invariants (packed
+  tokens are the kept sequences in order, positions restart at 0).
 """
 from __future__ import annotations
 
@@ -499,6 +502,24 @@ def embedding_bwd(grad_output, indices, num_embeddings):
     dw = np.zeros((num_embeddings, g.shape[1]))
     np.add.at(dw, idx[ok], g[ok])
     return dw
+
+
+def pack_sequences(sequences, max_length):
+    """packSequences (dataset.zig:421-465), pure Python: in order, a sequence
+    is appended when it fits in what is left of max_length, else skipped.
+    Returns (tokens, positions, sequence_ids, cumulative_lengths)."""
+    toks, pos, sid, cum = [], [], [], []
+    cur = 0
+    for seq in sequences:
+        if cur + len(seq) > max_length:
+            continue
+        for p, t in enumerate(seq):
+            toks.append(int(t))
+            pos.append(p)
+            sid.append(len(cum))
+        cur += len(seq)
+        cum.append(cur)
+    return toks, pos, sid, cum
 
 
 def num_threads() -> int:

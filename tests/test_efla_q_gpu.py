@@ -166,3 +166,34 @@ def test_backward_reusing_forward_factors(oracle, dtype, K, V, states):
         else:
             # the generic fp32 path sums dL/db with LDS float atomics, whose order varies
             assert rel_l2(a, b.float().cpu().numpy()) <= 1e-6, n
+
+
+def test_packed_batch_runs_sequences_independently(oracle):
+    """efla_pack_sequences output drives the varlen entries: each packed
+    sequence's outputs and gradients equal a separate run on that sequence."""
+    from ceo_amd.data import pack_sequences
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd
+
+    announce("packed sequences -> varlen EFLA == per-sequence runs")
+    rng = np.random.default_rng(12)
+    H, K, V = 2, 64, 128
+    lens = [int(x) for x in rng.integers(1, 300, 12)]
+    ids = [np.arange(sum(lens[:i]), sum(lens[:i]) + n) for i, n in enumerate(lens)]
+    p = pack_sequences(ids, 1500)
+    assert 0 < p.num_sequences < len(lens)  # some sequences skipped
+    ntok = int(p.cu_seqlens[-1])
+    x = oracle.make_efla_inputs(5, sum(lens), H, K, V, bf16=True)
+    rows = p.tokens.astype(np.int64)  # packed token -> row of the unpacked inputs
+    g = {n: to_dev(a[rows], torch.bfloat16, (1, ntok, H, K) if n in "qk" else
+                   (1, ntok, H) if n == "beta" else (1, ntok, H, V)) for n, a in x.items()}
+    cu = p.cu_seqlens_device()
+    o, _ = chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], cu_seqlens=cu)
+    grads = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], cu_seqlens=cu)
+    for s in range(p.num_sequences):
+        a, b = int(p.cu_seqlens[s]), int(p.cu_seqlens[s + 1])
+        one = {n: t[:, a:b].contiguous() for n, t in g.items()}
+        o1, _ = chunk_efla_fwd(one["q"], one["k"], one["v"], one["beta"])
+        g1 = chunk_efla_bwd(one["q"], one["k"], one["v"], one["beta"], one["do"])
+        assert torch.equal(o[:, a:b], o1), s
+        for big, small in zip(grads[:4], g1[:4]):
+            assert torch.equal(big[:, a:b], small), s
