@@ -71,6 +71,8 @@ _SIGS = {
     "efla_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, sz, sz, f32, sz, vp]),
     "efla_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, f32, vp]),
     "efla_chunked_scan_hip": (i32, [ctypes.POINTER(vp), sz, sz, sz, vp]),
+    "efla_affine_state_scan_hip": (i32, [ctypes.POINTER(vp), ctypes.POINTER(vp), sz, sz, sz, sz,
+                                         vp]),
     # EFLA, query readout
     "efla_chunk_fwd_workspace_size": (sz, [sz, sz, sz, sz, sz, sz, i32]),
     "efla_chunk_bwd_workspace_size": (sz, [sz, sz, sz, sz, sz, sz, i32]),

@@ -144,6 +144,21 @@ int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, const void* 
                        size_t head_dim_v, size_t chunk_size, int dtype, void* workspace,
                        size_t workspace_bytes, unsigned flags, hipStream_t stream);
 
+/* No reference counterpart; the affine combine efla_chunked_scan_hip does not
+ * do (efla.cu:711-748 sums states; src/model/efla.zig:473-484 is empty).
+ * In place over consecutive segments of the same sequences:
+ *   states[i] = transitions[i] * states[i-1] + states[i],  i = 1 .. n-1,
+ * where states[i] (num_states, d_k, d_v) fp32 holds on entry the segment's
+ * final state from a zero start (B_i) and transitions[i] (num_states, d_k,
+ * d_k) fp32 its state transition A_i = prod_t (I - c_t k_t k_t^T) (the final
+ * state of efla_chunk_fwd_hip on the segment with S_0 = I and v = 0).  On
+ * return states[i] is the true state after segment i.  Host arrays of device
+ * pointers; transitions[0] is not read.  Zero sizes or NULL -> 1;
+ * d_k > 256 -> 9. */
+int efla_affine_state_scan_hip(const float* const* transitions, float* const* states,
+                               size_t num_chunks, size_t num_states, size_t head_dim_k,
+                               size_t head_dim_v, hipStream_t stream);
+
 /* ========================================================================
  * LayerNorm
  * ======================================================================== */

@@ -191,3 +191,16 @@ def test_embedding_and_cross_entropy_validation(L):
     assert L.cross_entropy_forward_hip(p, p, NULL, 4, 100, 0.0, NULL) == 1
     assert L.cross_entropy_backward_hip(NULL, p, p, p, 4, 100, 0.0, NULL) == 1
     assert L.cross_entropy_backward_hip(p, p, p, p, 4, 100, float("nan"), NULL) == 1
+
+
+def test_affine_state_scan_validation(L):
+    p = ctypes.c_void_p(16)
+    arr = (ctypes.c_void_p * 2)(p, p)
+    assert L.efla_affine_state_scan_hip(arr, arr, 0, 4, 64, 64, NULL) == 1
+    assert L.efla_affine_state_scan_hip(NULL, arr, 2, 4, 64, 64, NULL) == 1
+    assert L.efla_affine_state_scan_hip(arr, arr, 2, 4, 0, 64, NULL) == 1
+    assert L.efla_affine_state_scan_hip(arr, arr, 2, 4, 512, 64, NULL) == 9
+    holes = (ctypes.c_void_p * 2)(p, None)
+    assert L.efla_affine_state_scan_hip(arr, holes, 2, 4, 64, 64, NULL) == 1
+    assert L.efla_affine_state_scan_hip(holes, arr, 2, 4, 64, 64, NULL) == 1
+    assert L.efla_affine_state_scan_hip(arr, arr, 1, 4, 64, 64, NULL) == 0   # nothing to combine

@@ -194,3 +194,36 @@ def test_fp32_oracle_tracks_fp64(oracle):
     g32 = oracle.q_backward(d["q"], d["k"], d["v"], d["beta"], d["do"], T=T, dtype=np.float32)
     for a, b in zip(g32, g64):
         assert np.linalg.norm(a - b) / np.linalg.norm(b) < 1e-5
+
+
+def test_segments_compose_affinely(oracle):
+    """The state after two segments is A2 (A1 S0 + B1) + B2 with A the
+    product of (I - c k k^T) and B the final state from zero; A is also the
+    recurrence's final state from S0 = I with v = 0 (the transition the
+    affine state scan consumes)."""
+    rng = np.random.default_rng(21)
+    H, K, V, T1, T2 = 2, 6, 5, 9, 7
+    x = oracle.make_efla_inputs(31, T1 + T2, H, K, V, bf16=False)
+    q, k, v, b = x["q"], x["k"], x["v"], x["beta"]
+    S0 = rng.standard_normal((1, H, K, V))
+
+    def prod(kk, bb):
+        A = np.broadcast_to(np.eye(K), (H, K, K)).copy()
+        for t in range(kk.shape[0]):
+            kt = kk[t].astype(np.float64)
+            lam = (kt ** 2).sum(-1)
+            c = -np.expm1(-bb[t].astype(np.float64) * lam) / lam
+            M = np.eye(K) - c[:, None, None] * np.einsum("hi,hj->hij", kt, kt)
+            A = M @ A
+        return A
+
+    s1, s2 = slice(0, T1), slice(T1, T1 + T2)
+    A1, A2 = prod(k[s1], b[s1]), prod(k[s2], b[s2])
+    _, B1 = oracle.q_forward(q[s1], k[s1], v[s1], b[s1], T=T1)
+    _, B2 = oracle.q_forward(q[s2], k[s2], v[s2], b[s2], T=T2)
+    _, S_ref = oracle.q_forward(q, k, v, b, T=T1 + T2, S0=S0)
+    S_comp = A2 @ (A1 @ S0[0] + B1[0]) + B2[0]
+    assert np.abs(S_comp - S_ref[0]).max() < 1e-12
+    eye = np.broadcast_to(np.eye(K), (1, H, K, K)).copy()
+    _, A1_rec = oracle.q_forward(q[s1], k[s1], np.zeros((T1, H, K)), b[s1], T=T1, S0=eye)
+    assert np.abs(A1_rec[0] - A1).max() < 1e-12

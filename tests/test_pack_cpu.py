@@ -53,3 +53,14 @@ def test_empty_input_and_errors():
                                      ctypes.byref(n), ctypes.byref(n)) == 1
     assert lib().efla_pack_sequences(None, None, 0, 1 << 40, None, None, None, None,
                                      ctypes.byref(n), ctypes.byref(n)) == 9
+
+
+def test_chunked_scan_ranges_reference_test():
+    from ceo_amd.state import ChunkedScan
+
+    # efla.zig:497-505
+    s = ChunkedScan(10000, 1024)
+    assert s.chunk_size == 1024 and s.num_chunks == 10
+    assert s.get_chunk_range(5) == (5120, 6144)
+    # the reference clips to num_chunks * chunk_size (10240), not to 10000
+    assert s.get_chunk_range(9) == (9216, 10240)
