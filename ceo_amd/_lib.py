@@ -84,6 +84,8 @@ _SIGS = {
     "layernorm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, f32, vp]),
     "layernorm_forward_stats_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     "layernorm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
+    "rmsnorm_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
+    "rmsnorm_backward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     # GEMM
     "gemm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, sz, i32, i32, i32, vp]),
     "gemm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),

@@ -53,6 +53,41 @@ def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True)
     return dx, dw, db
 
 
+def rmsnorm_forward(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-5) -> torch.Tensor:
+    """y = x * rsqrt(mean(x^2) + eps) * weight over the last dim (bf16)."""
+    D = x.shape[-1]
+    _require(x, "x", torch.bfloat16)
+    _require(weight, "weight", torch.bfloat16, x.device)
+    y = torch.empty_like(x)
+    rc = lib().rmsnorm_forward_hip(_p(x), _p(weight), _p(y), x.numel(), D, float(eps),
+                                   _stream(x))
+    check(rc, "rmsnorm_forward_hip")
+    return y
+
+
+def rmsnorm_backward(dy, x, weight, eps: float = 1e-5, grad_weight=None,
+                     need_weight_grad: bool = True):
+    """(dx bf16, dweight fp32 or None).  dweight is added into ``grad_weight``
+    when given (fp32, (D,)), else into a new zero buffer."""
+    D = x.shape[-1]
+    for t, n in ((dy, "dy"), (x, "x"), (weight, "weight")):
+        _require(t, n, torch.bfloat16, x.device)
+    dx = torch.empty_like(x)
+    dw = None
+    if need_weight_grad:
+        if grad_weight is None:
+            dw = torch.zeros(D, dtype=torch.float32, device=x.device)
+        else:
+            _require(grad_weight, "grad_weight", torch.float32, x.device)
+            if grad_weight.numel() != D:
+                raise ValueError("grad_weight must hold normalized_shape values")
+            dw = grad_weight
+    rc = lib().rmsnorm_backward_hip(_p(dy), _p(x), _p(weight), _p(dx), _p(dw), x.numel(), D,
+                                    float(eps), _stream(x))
+    check(rc, "rmsnorm_backward_hip")
+    return dx, dw
+
+
 def gemm_forward(a: torch.Tensor, b: torch.Tensor, bias=None, out_dtype=None) -> torch.Tensor:
     """c = a @ b (+ bias), a (m,k), b (k,n) row-major; fp32 accumulation."""
     m, k = a.shape

@@ -183,6 +183,29 @@ int layernorm_backward_hip(const void* grad_output, const void* input, const voi
                            size_t normalized_shape, hipStream_t stream);
 
 /* ========================================================================
+ * RMSNorm
+ * ======================================================================== */
+
+/* Replaces rmsnorm_forward_cuda (kernels.h:125-133, layernorm.cu:15-48,
+ * 307-329): rows = numel / normalized_shape; y = x * rsqrt(mean(x^2) + eps)
+ * * w.  bf16 in/out, fp32 statistics.  normalized_shape == 0 or a NULL
+ * pointer -> 1; no whole row -> 0 with nothing launched. */
+int rmsnorm_forward_hip(const void* input, const void* weight, void* output, size_t numel,
+                        size_t normalized_shape, float eps, hipStream_t stream);
+
+/* Replaces rmsnorm_backward_cuda (kernels.h:138-148, layernorm.cu:51-127,
+ * 331-357) with the exact gradient, rs = rsqrt(mean(x^2) + eps), g = dy * w:
+ *   grad_input = rs g - x rs^3 mean(g x)    (bf16)
+ *   grad_weight += sum over rows of dy x rs (fp32, may be NULL).
+ * The reference scales the second term by rs instead of rs^3 and adds fp32
+ * values through a float pointer into a bf16 buffer; both are corrected here
+ * and grad_weight is an fp32 accumulator.  grad_weight with normalized_shape
+ * > 16384 -> 9.  Uses the cached workspace for per-block partials. */
+int rmsnorm_backward_hip(const void* grad_output, const void* input, const void* weight,
+                         void* grad_input, float* grad_weight, size_t numel,
+                         size_t normalized_shape, float eps, hipStream_t stream);
+
+/* ========================================================================
  * GEMM (row-major)
  * ======================================================================== */
 

@@ -30,6 +30,10 @@ Contents and what pins each part (tests/test_oracle_*.py):
 * ``layernorm_fwd`` / ``layernorm_bwd`` -- layernorm.cu:133-183 and the
   textbook gradient.  Pinned by the per-row mean 0 / variance 1 invariant and
   torch fp64 autograd.
+* ``rmsnorm_fwd`` / ``rmsnorm_bwd`` -- layernorm.cu:15-127 with the exact
+  gradient (the reference's dx drops a factor rs^2).  Pinned by the per-row
+  mean(y^2) = 1 invariant (w = 1, eps = 0), torch's rms_norm and fp64
+  autograd, and central differences that reject the reference's form.
 * ``gelu_fwd`` / ``gelu_bwd`` -- layernorm.cu:189-250, tanh and erf forms.
   Pinned by torch's own GELU (both forms) and its autograd, and special values.
 * ``adamw_step`` / ``adamw_step_bf16`` -- optim.cu:147-178, 657-709 with fp32
@@ -414,6 +418,31 @@ def layernorm_bwd(dy, x, w, mean, rstd):
                            _p(rstd, c_f32p), _p(dx, c_f32p), _p(dw, c_f64p), _p(db, c_f64p),
                            rows, D)
     return dx, dw, db
+
+
+def rmsnorm_fwd(x, w, eps=1e-5):
+    """y = x rs w with rs = 1 / sqrt(mean(x^2) + eps) per row, fp64
+    (layernorm.cu:15-48).  Returns (y, rs)."""
+    x = np.asarray(x, dtype=np.float64)
+    rs = 1.0 / np.sqrt((x * x).mean(axis=-1) + eps)
+    return x * rs[:, None] * np.asarray(w, dtype=np.float64), rs
+
+
+def rmsnorm_bwd(dy, x, w, eps=1e-5, reference_form=False):
+    """(dx, dw) of y = x rs w in fp64.  The exact gradient is
+    dx = rs g - x rs^3 mean(g x) with g = dy w, dw = sum_rows dy x rs.
+    ``reference_form`` gives the reference's dx instead (layernorm.cu:108-116:
+    the second term scaled by rs rather than rs^3), which a finite-difference
+    check rejects; the HIP kernels implement the exact gradient."""
+    dy, x, w = (np.asarray(a, dtype=np.float64) for a in (dy, x, w))
+    D = x.shape[-1]
+    rs = 1.0 / np.sqrt((x * x).mean(axis=-1) + eps)
+    g = dy * w
+    sgx = (g * x).sum(axis=-1)
+    scale = rs if reference_form else rs ** 3
+    dx = rs[:, None] * g - x * (scale * sgx / D)[:, None]
+    dw = (dy * x * rs[:, None]).sum(axis=0)
+    return dx, dw
 
 
 def gelu_fwd(x, approximate=True):

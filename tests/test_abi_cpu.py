@@ -145,6 +145,17 @@ def test_layernorm_validation(L):
     assert L.layernorm_forward_stats_hip(p, p, NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1
 
 
+def test_rmsnorm_validation(L):
+    p = ctypes.c_void_p(16)
+    assert L.rmsnorm_forward_hip(p, p, p, 1024, 0, 1e-6, NULL) == 1
+    assert L.rmsnorm_forward_hip(p, p, p, 1000, 1024, 1e-6, NULL) == 0
+    assert L.rmsnorm_forward_hip(NULL, p, p, 2048, 1024, 1e-6, NULL) == 1
+    assert L.rmsnorm_backward_hip(p, p, p, p, NULL, 1024, 0, 1e-6, NULL) == 1
+    assert L.rmsnorm_backward_hip(p, p, p, p, NULL, 0, 64, 1e-6, NULL) == 0
+    assert L.rmsnorm_backward_hip(p, NULL, p, p, NULL, 128, 64, 1e-6, NULL) == 1
+    assert L.rmsnorm_backward_hip(p, p, p, p, p, 32768, 32768, 1e-6, NULL) == 9
+
+
 def test_gelu_validation(L):
     p = ctypes.c_void_p(16)
     # numel == 0: the reference launches an empty grid -> InvalidConfiguration

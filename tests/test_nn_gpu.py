@@ -58,6 +58,86 @@ def test_layernorm_backward(oracle, rows, D):
     assert errs[0] <= 1e-2 and errs[1] <= 1e-4 and errs[2] <= 1e-5
 
 
+@pytest.mark.parametrize("rows,D", [(64, 1024), (37, 96), (16, 4096), (9, 1000), (5, 512),
+                                    (3, 8192)])
+def test_rmsnorm_forward(oracle, rows, D):
+    from ceo_amd.nn import rmsnorm_forward
+
+    announce(f"rmsnorm_forward rows={rows} D={D}")
+    rng = np.random.default_rng(rows * 7 + D)
+    x = _bf(rng.standard_normal((rows, D)) * 1.5 + 0.3)
+    w = _bf(1 + 0.1 * rng.standard_normal(D))
+    y = rmsnorm_forward(x.cuda(), w.cuda(), 1e-6)
+    torch.cuda.synchronize()
+    ry, _ = oracle.rmsnorm_fwd(x.double().numpy(), w.double().numpy(), 1e-6)
+    e = rel_l2(y, ry)
+    print(f"  rel-L2 y={e:.2e}", flush=True)
+    assert e <= 1e-2
+    # invariant: with w = 1 every row has mean square 1 (up to bf16 rounding)
+    y1 = rmsnorm_forward(x.cuda(), torch.ones(D, dtype=torch.bfloat16, device="cuda"), 0.0)
+    ms = (y1.float() ** 2).mean(1).cpu().numpy()
+    assert np.abs(ms - 1).max() < 1e-2
+
+
+@pytest.mark.parametrize("rows,D", [(64, 1024), (50, 96), (5000, 1024), (33, 1536), (300, 2048),
+                                    (17, 4096), (6, 16384), (4, 20000)])
+def test_rmsnorm_backward(oracle, rows, D):
+    from ceo_amd.nn import rmsnorm_backward
+
+    announce(f"rmsnorm_backward rows={rows} D={D}")
+    rng = np.random.default_rng(11 + D)
+    x = _bf(rng.standard_normal((rows, D)) * 1.3)
+    w = _bf(1 + 0.1 * rng.standard_normal(D))
+    dy = _bf(rng.standard_normal((rows, D)))
+    need_w = D <= 16384
+    dx, dw = rmsnorm_backward(dy.cuda(), x.cuda(), w.cuda(), 1e-6, need_weight_grad=need_w)
+    torch.cuda.synchronize()
+    rdx, rdw = oracle.rmsnorm_bwd(dy.double().numpy(), x.double().numpy(), w.double().numpy(),
+                                  1e-6)
+    e_dx = rel_l2(dx, rdx)
+    e_dw = rel_l2(dw, rdw) if need_w else 0.0
+    print(f"  rel-L2 dx={e_dx:.2e} dw={e_dw:.2e}", flush=True)
+    assert e_dx <= 1e-2 and e_dw <= 1e-4
+
+
+def test_rmsnorm_backward_accumulates_and_misaligned(oracle):
+    """grad_weight is added into (two calls give twice the sum); inputs that
+    are not 16-byte aligned take the looping kernels with the same results."""
+    from ceo_amd.nn import rmsnorm_backward, rmsnorm_forward
+
+    announce("rmsnorm_backward accumulate + misaligned rows=40 D=1024")
+    rows, D = 40, 1024
+    rng = np.random.default_rng(21)
+    x = _bf(rng.standard_normal((rows, D)))
+    w = _bf(1 + 0.1 * rng.standard_normal(D))
+    dy = _bf(rng.standard_normal((rows, D)))
+    xd, wd, dyd = x.cuda(), w.cuda(), dy.cuda()
+    acc = torch.zeros(D, dtype=torch.float32, device="cuda")
+    dx1, _ = rmsnorm_backward(dyd, xd, wd, 1e-6, grad_weight=acc)
+    dx2, _ = rmsnorm_backward(dyd, xd, wd, 1e-6, grad_weight=acc)
+    torch.cuda.synchronize()
+    _, rdw = oracle.rmsnorm_bwd(dy.double().numpy(), x.double().numpy(), w.double().numpy(), 1e-6)
+    assert rel_l2(acc, 2 * rdw) <= 1e-4
+    assert torch.equal(dx1, dx2)
+
+    def shifted(t):  # same values at an address 2 bytes past a 16-byte boundary
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device="cuda")
+        v = buf[1:].view(t.shape)
+        v.copy_(t)
+        return v
+
+    xs, ws, dys = shifted(xd), shifted(wd), shifted(dyd)
+    assert xs.data_ptr() % 16 != 0
+    y_al = rmsnorm_forward(xd, wd, 1e-6)
+    y_mis = rmsnorm_forward(xs, ws, 1e-6)
+    dxs, dws = rmsnorm_backward(dys, xs, ws, 1e-6)
+    dxa, dwa = rmsnorm_backward(dyd, xd, wd, 1e-6)
+    torch.cuda.synchronize()
+    assert rel_l2(y_mis, y_al.float().cpu().numpy()) <= 1e-2
+    assert rel_l2(dxs, dxa.float().cpu().numpy()) <= 1e-2
+    assert rel_l2(dws, dwa.cpu().numpy()) <= 1e-5
+
+
 @pytest.fixture(params=[0, 1], ids=["hipblaslt", "native"])
 def gemm_backend(request):
     """Runs a GEMM test on the hipBLASLt path and on the library's own MFMA

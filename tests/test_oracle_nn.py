@@ -152,3 +152,54 @@ def test_embedding_is_a_one_hot_product(oracle):
     bad = idx.copy()
     bad[3] = V
     assert not oracle.embedding_fwd(bad, w)[3].any()
+
+
+def test_rmsnorm_forward_invariant_and_torch(oracle):
+    """RMSNorm (layernorm.cu:15-48): rows of x rs have mean square 1 when
+    eps = 0, and the fp64 form equals torch's rms_norm."""
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((6, 80)) * 2 + 0.5).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(80)).astype(np.float32)
+    y1, rs = oracle.rmsnorm_fwd(x, np.ones(80), eps=0.0)
+    assert np.abs((y1 ** 2).mean(1) - 1).max() < 1e-12
+    assert np.allclose(rs, 1 / np.sqrt((x.astype(np.float64) ** 2).mean(1)), rtol=1e-14)
+    y, _ = oracle.rmsnorm_fwd(x, w, eps=1e-5)
+    ref = torch.nn.functional.rms_norm(torch.tensor(x, dtype=torch.float64), (80,),
+                                       torch.tensor(w, dtype=torch.float64), 1e-5)
+    assert np.abs(y - ref.numpy()).max() < 1e-12
+
+
+def test_rmsnorm_backward_autograd_and_reference_form(oracle):
+    """The exact gradient matches torch fp64 autograd and central differences;
+    the reference's dx (rs in place of rs^3 in the second term) fails them."""
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((4, 32)) * 1.7).astype(np.float64)
+    w = 1 + 0.2 * rng.standard_normal(32)
+    dy = rng.standard_normal((4, 32))
+    eps = 1e-5
+    dx, dw = oracle.rmsnorm_bwd(dy, x, w, eps)
+    xt = torch.tensor(x, requires_grad=True)
+    wt = torch.tensor(w, requires_grad=True)
+    yt = torch.nn.functional.rms_norm(xt, (32,), wt, eps)
+    (yt * torch.tensor(dy)).sum().backward()
+    assert np.abs(dx - xt.grad.numpy()).max() < 1e-10
+    assert np.abs(dw - wt.grad.numpy()).max() < 1e-10
+    # central differences of <dy, y(x)> at a few coordinates
+    f = lambda xx: float((dy * oracle.rmsnorm_fwd(xx, w, eps)[0]).sum())
+    h = 1e-6
+    for r, c in ((0, 0), (1, 7), (3, 31)):
+        e = np.zeros_like(x)
+        e[r, c] = h
+        fd = (f(x + e) - f(x - e)) / (2 * h)
+        assert abs(dx[r, c] - fd) < 1e-6
+    dx_ref_form, _ = oracle.rmsnorm_bwd(dy, x, w, eps, reference_form=True)
+    assert np.abs(dx_ref_form - xt.grad.numpy()).max() > 1e-2
+
+
+def test_rmsnorm_reference_known_answer(oracle):
+    """nn_kernels.zig:250-264: rows [1, 2, 3, 4], w = 1, eps = 1e-6 give a
+    mean square of 1 within 1%; the closed form is x / sqrt(7.5 + eps)."""
+    x = np.array([[1.0, 2.0, 3.0, 4.0], [1.0, 2.0, 3.0, 4.0]])
+    y, rs = oracle.rmsnorm_fwd(x, np.ones(4), eps=1e-6)
+    assert abs((y[0] ** 2).mean() - 1.0) < 0.01
+    assert np.allclose(y, x / np.sqrt(7.5 + 1e-6), rtol=1e-15)
