@@ -86,6 +86,10 @@ _SIGS = {
     "layernorm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
     "rmsnorm_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
     "rmsnorm_backward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, f32, vp]),
+    "shortconv_forward_hip": (i32, [vp, vp, vp, sz, sz, sz, sz, vp]),
+    "shortconv_backward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, sz, sz, vp]),
+    "prism_forward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, f32, vp]),
+    "prism_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz, vp]),
     # GEMM
     "gemm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, sz, i32, i32, i32, vp]),
     "gemm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),

@@ -206,6 +206,56 @@ int rmsnorm_backward_hip(const void* grad_output, const void* input, const void*
                          size_t normalized_shape, float eps, hipStream_t stream);
 
 /* ========================================================================
+ * ShortConv and PRISM (the consumer of the EFLA output in the reference's
+ * TransformerBlock, src/model/model.zig:169-176)
+ * ======================================================================== */
+
+/* Replaces shortconv_forward_cuda (kernels.h:107-116, declared only), with the
+ * semantics of ShortConv.forwardCpu (src/model/prism.zig:448-473): a causal
+ * depthwise convolution over (batch, seq_len, hidden_dim) bf16 with weight
+ * (hidden_dim, window_size) bf16,
+ *   y[b,t,c] = bf16(sum_{w < W, t-w >= 0} x[b,t-w,c] * weight[c,w]),
+ * products rounded to fp32 and added in increasing w, bit-identical to that
+ * loop.  No element -> 0; a NULL pointer -> 1. */
+int shortconv_forward_hip(const void* input, const void* weight, void* output,
+                          size_t batch_size, size_t seq_len, size_t hidden_dim,
+                          size_t window_size, hipStream_t stream);
+
+/* Replaces shortConvBackwardCuda (src/kernels/prism_kernels.zig:50-60,
+ * declared only): grad_input (bf16, may be NULL) and grad_weight (fp32
+ * (hidden_dim, window_size), added into, may be NULL). */
+int shortconv_backward_hip(const void* grad_output, const void* input, const void* weight,
+                           void* grad_input, float* grad_weight, size_t batch_size,
+                           size_t seq_len, size_t hidden_dim, size_t window_size,
+                           hipStream_t stream);
+
+/* Replaces prism_forward_cuda (kernels.h:86-102, declared only), with the
+ * semantics of PrismLayer.prismForwardCpu (src/model/prism.zig:251-323): for
+ * every row and channel d < head_dim, r = v - u and for each of the
+ * num_iterations steps l: delta = GELU_tanh(w_p[l][d] * r),
+ * o = bf16(o + 0.5 delta), r -= delta; channels >= head_dim are 0.  w_p is a
+ * host array of num_iterations device pointers (bf16, at least head_dim
+ * values each).  As in that path, prev_state, w_beta, w_k and alpha are not
+ * read; new_state (head_dim x head_dim bf16) is zero-filled when non-NULL.
+ * head_dim == 0 or > hidden_dim, or a NULL pointer -> 1; more than 16
+ * iterations -> 9. */
+int prism_forward_hip(const void* u, const void* v, const void* prev_state, void* new_state,
+                      void* output, const void** w_beta, const void** w_k, const void** w_p,
+                      size_t batch_size, size_t seq_len, size_t hidden_dim, size_t head_dim,
+                      size_t num_iterations, float alpha, hipStream_t stream);
+
+/* No usable reference counterpart (prismBackwardCuda, prism_kernels.zig:24-37,
+ * takes no weights; PrismLayer.backward, prism.zig:326-356, returns zeros):
+ * the gradient of prism_forward_hip with the bf16 rounding of o passed
+ * straight through.  grad_u, grad_v bf16 (full rows; 0 beyond head_dim);
+ * grad_w_p a host array of num_iterations fp32 device pointers, each added
+ * into over its first head_dim values (may be NULL). */
+int prism_backward_hip(const void* grad_output, const void* u, const void* v, const void** w_p,
+                       void* grad_u, void* grad_v, float** grad_w_p, size_t batch_size,
+                       size_t seq_len, size_t hidden_dim, size_t head_dim,
+                       size_t num_iterations, hipStream_t stream);
+
+/* ========================================================================
  * GEMM (row-major)
  * ======================================================================== */
 

@@ -34,6 +34,14 @@ Contents and what pins each part (tests/test_oracle_*.py):
   gradient (the reference's dx drops a factor rs^2).  Pinned by the per-row
   mean(y^2) = 1 invariant (w = 1, eps = 0), torch's rms_norm and fp64
   autograd, and central differences that reject the reference's form.
+* ``shortconv_fwd`` / ``shortconv_bwd`` -- prism.zig:448-473 in its own fp32
+  order (bit-exact before the bf16 rounding) and the adjoint.  Pinned by
+  torch's grouped conv1d (fp64) and its autograd, the impulse response (a unit
+  input at t = 0 reads out the weights) and window 1 (y = x w exactly).
+* ``prism_fwd`` / ``prism_bwd`` -- prism.zig:251-323 and its gradient.
+  Pinned by a one-iteration closed form, a hand-unrolled two-iteration
+  evaluation, torch fp64 autograd of an independent restatement and central
+  differences.
 * ``gelu_fwd`` / ``gelu_bwd`` -- layernorm.cu:189-250, tanh and erf forms.
   Pinned by torch's own GELU (both forms) and its autograd, and special values.
 * ``adamw_step`` / ``adamw_step_bf16`` -- optim.cu:147-178, 657-709 with fp32
@@ -443,6 +451,103 @@ def rmsnorm_bwd(dy, x, w, eps=1e-5, reference_form=False):
     dx = rs[:, None] * g - x * (scale * sgx / D)[:, None]
     dw = (dy * x * rs[:, None]).sum(axis=0)
     return dx, dw
+
+
+def shortconv_fwd(x, weight):
+    """ShortConv.forwardCpu (src/model/prism.zig:448-473) in its own arithmetic:
+    for x (B, T, C) and weight (C, W) holding bf16 values, every output is the
+    fp32 sum over w = 0..W-1 (t - w >= 0), in increasing w, of the fp32-rounded
+    products x[b,t-w,c] * weight[c,w], starting from +0.  numpy float32
+    multiplies and adds round each operation (no fused multiply-add), so this is
+    the reference's value before its bf16 rounding.  Returns fp32 (B, T, C)."""
+    x = np.asarray(x, dtype=np.float32)
+    wt = np.asarray(weight, dtype=np.float32)
+    B, T, C = x.shape
+    s = np.zeros((B, T, C), dtype=np.float32)
+    for w in range(wt.shape[1]):
+        if w >= T:
+            break
+        p = x[:, :T - w, :] * wt[None, None, :, w]
+        s[:, w:, :] = s[:, w:, :] + p
+    return s
+
+
+def shortconv_bwd(dy, x, weight):
+    """(dx, dweight) of y = ShortConv(x) in fp64: dx[t] = sum_w dy[t+w] w[c,w],
+    dweight[c,w] = sum_{b,t>=w} dy[b,t,c] x[b,t-w,c]."""
+    dy, x, wt = (np.asarray(a, dtype=np.float64) for a in (dy, x, weight))
+    B, T, C = x.shape
+    dx = np.zeros_like(x)
+    dw = np.zeros_like(wt)
+    for w in range(min(wt.shape[1], T)):
+        dx[:, :T - w, :] += dy[:, w:, :] * wt[None, None, :, w]
+        dw[:, w] = (dy[:, w:, :] * x[:, :T - w, :]).sum(axis=(0, 1))
+    return dx, dw
+
+
+def _gelu_tanh64(x):
+    """0.5 x (1 + tanh u) written x / (1 + e^(-2u)): the same value without the
+    cancellation of 1 + tanh u for x << 0."""
+    u = np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)
+    with np.errstate(over="ignore"):  # e^(-2u) = inf gives the limit -0
+        return x / (1.0 + np.exp(-2.0 * u))
+
+
+def _gelu_tanh64_grad(x):
+    """s + 2 x s (1 - s) u' with s = 1 / (1 + e^(-2u)) = 0.5 (1 + tanh u)."""
+    u = np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)
+    with np.errstate(over="ignore"):
+        s = 1.0 / (1.0 + np.exp(-2.0 * u))
+    return s + 2.0 * x * s * (1.0 - s) * np.sqrt(2.0 / np.pi) * (1.0 + 3 * 0.044715 * x ** 2)
+
+
+def prism_fwd(u, v, w_p, head_dim, round_output=True):
+    """PrismLayer.prismForwardCpu (prism.zig:251-323): per row and channel
+    d < head_dim, r = v - u; for each l: delta = GELU_tanh(p_l[d] r) with p_l
+    the first head_dim values of w_p[l], o = o + 0.5 delta (rounded to fp32 and
+    then bf16 after every step when ``round_output``), r -= delta.  Channels
+    >= head_dim are 0.  fp64 math; returns float32 (B, T, C)."""
+    u = np.asarray(u, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    out = np.zeros(u.shape, dtype=np.float64)
+    r = v[..., :head_dim] - u[..., :head_dim]
+    o = np.zeros_like(r)
+    for wp in w_p:
+        p = np.asarray(wp, dtype=np.float64).reshape(-1)[:head_dim]
+        d = _gelu_tanh64(p * r)
+        o = o + 0.5 * d
+        if round_output:
+            o = round_bf16(o.astype(np.float32)).astype(np.float64)
+        r = r - d
+    out[..., :head_dim] = o
+    return out.astype(np.float32)
+
+
+def prism_bwd(grad_output, u, v, w_p, head_dim):
+    """(grad_u, grad_v, [grad p_l]) of prism_fwd without the bf16 rounding of o
+    (fp64): the reverse of r_{l+1} = r_l - GELU(p_l r_l), o = 0.5 sum_l
+    GELU(p_l r_l)."""
+    g = np.asarray(grad_output, dtype=np.float64)[..., :head_dim]
+    u = np.asarray(u, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    ps = [np.asarray(wp, dtype=np.float64).reshape(-1)[:head_dim] for wp in w_p]
+    rs, xs = [], []
+    r = v[..., :head_dim] - u[..., :head_dim]
+    for p in ps:
+        rs.append(r)
+        xs.append(p * r)
+        r = r - _gelu_tanh64(xs[-1])
+    a = np.zeros_like(r)
+    dps = [None] * len(ps)
+    for l in range(len(ps) - 1, -1, -1):
+        gx = (0.5 * g - a) * _gelu_tanh64_grad(xs[l])
+        dps[l] = (gx * rs[l]).reshape(-1, head_dim).sum(axis=0)
+        a = a + gx * ps[l]
+    gu = np.zeros(u.shape)
+    gv = np.zeros(u.shape)
+    gv[..., :head_dim] = a
+    gu[..., :head_dim] = -a
+    return gu, gv, dps
 
 
 def gelu_fwd(x, approximate=True):

@@ -156,6 +156,39 @@ def test_rmsnorm_validation(L):
     assert L.rmsnorm_backward_hip(p, p, p, p, p, 32768, 32768, 1e-6, NULL) == 9
 
 
+def test_shortconv_and_prism_validation(L):
+    p = ctypes.c_void_p(16)
+    # ShortConv: nothing to do -> 0; NULL -> 1; window beyond the limits -> 9
+    assert L.shortconv_forward_hip(p, p, p, 0, 8, 8, 4, NULL) == 0
+    assert L.shortconv_forward_hip(NULL, p, p, 1, 8, 8, 4, NULL) == 1
+    assert L.shortconv_forward_hip(p, NULL, p, 1, 8, 8, 4, NULL) == 1
+    assert L.shortconv_forward_hip(p, p, p, 1, 8, 8, 1 << 21, NULL) == 9
+    assert L.shortconv_backward_hip(NULL, p, p, p, NULL, 1, 8, 8, 4, NULL) == 1
+    assert L.shortconv_backward_hip(p, NULL, p, p, p, 1, 8, 8, 4, NULL) == 1
+    assert L.shortconv_backward_hip(p, p, p, p, NULL, 0, 8, 8, 4, NULL) == 0
+    # PRISM: head_dim 0 or above hidden_dim -> 1; > 16 iterations -> 9
+    wp = (ctypes.c_void_p * 17)(*([16] * 17))
+    assert L.prism_forward_hip(p, p, NULL, NULL, p, NULL, NULL, wp, 1, 4, 64, 0, 3, 0.99,
+                               NULL) == 1
+    assert L.prism_forward_hip(p, p, NULL, NULL, p, NULL, NULL, wp, 1, 4, 64, 65, 3, 0.99,
+                               NULL) == 1
+    assert L.prism_forward_hip(p, p, NULL, NULL, p, NULL, NULL, wp, 1, 4, 64, 64, 17, 0.99,
+                               NULL) == 9
+    assert L.prism_forward_hip(p, p, NULL, NULL, p, NULL, NULL, NULL, 1, 4, 64, 64, 3, 0.99,
+                               NULL) == 1
+    assert L.prism_forward_hip(NULL, p, NULL, NULL, p, NULL, NULL, wp, 1, 4, 64, 64, 3, 0.99,
+                               NULL) == 1
+    wnull = (ctypes.c_void_p * 3)(16, None, 16)
+    assert L.prism_forward_hip(p, p, NULL, NULL, p, NULL, NULL, wnull, 1, 4, 64, 64, 3, 0.99,
+                               NULL) == 1
+    assert L.prism_forward_hip(p, p, NULL, NULL, p, NULL, NULL, wp, 0, 4, 64, 64, 3, 0.99,
+                               NULL) == 0
+    assert L.prism_backward_hip(p, p, p, wp, p, p, NULL, 1, 4, 64, 64, 17, NULL) == 9
+    assert L.prism_backward_hip(p, p, p, wp, NULL, p, NULL, 1, 4, 64, 64, 3, NULL) == 1
+    gnull = (ctypes.c_void_p * 3)(16, None, 16)
+    assert L.prism_backward_hip(p, p, p, wp, p, p, gnull, 1, 4, 64, 64, 3, NULL) == 1
+
+
 def test_gelu_validation(L):
     p = ctypes.c_void_p(16)
     # numel == 0: the reference launches an empty grid -> InvalidConfiguration
