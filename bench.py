@@ -225,12 +225,13 @@ CFG4 = {"tokens": 16384, "d_model": 1024, "mlp": 4096, "params": 368_000_000}
 def aux_bench(steps: int, warmup: int) -> int:
     """Times the kernels around EFLA at config-4 shapes: the GEMMs of one layer
     and the LM head against the bf16 MFMA roof (their FLOPs over the average
-    hipEvent duration), LayerNorm / GELU / AdamW against the HBM roof
-    (algorithmic bytes per launch: what each must read and write once).
+    hipEvent duration), LayerNorm / GELU / AdamW and the reference model's
+    RMSNorm / ShortConv / PRISM against the HBM roof (algorithmic bytes per
+    launch: what each must read and write once).
     Prints one JSON line."""
     import torch
 
-    from ceo_amd import nn, runtime
+    from ceo_amd import nn, prism, runtime
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(4)
@@ -247,6 +248,14 @@ def aux_bench(steps: int, warmup: int) -> int:
     gp = bf(P, scale=0.01)
     pcopy = torch.empty(P, dtype=torch.bfloat16, device=dev)
     y, mean, rstd = nn.layernorm_forward(x, w, b, save_stats=True)
+    # the reference model's RMSNorm, ShortConv (window 64, configs/train.yaml)
+    # and 3-iteration PRISM refinement on the same activations, as (8, 2048, 1024)
+    rms_dw = torch.zeros(D, device=dev)
+    x3, dy3 = x.view(8, N // 8, D), dy.view(8, N // 8, D)
+    conv_w = bf(D, 64, scale=0.125)
+    conv_dw = torch.zeros(D, 64, device=dev)
+    w_p = [bf(D, 64, scale=0.04) for _ in range(3)]
+    gw_p = [torch.zeros(D * 64, device=dev) for _ in range(3)]
     cases = {
         # name: (callable, algorithmic bytes per launch, what)
         "layernorm_fwd": (lambda: nn.layernorm_forward(x, w, b, save_stats=True),
@@ -258,6 +267,19 @@ def aux_bench(steps: int, warmup: int) -> int:
         "adamw_master": (lambda: nn.adamw_step_master(p32, gp, m32, v32, 3e-4, 0.9, 0.999,
                                                       1e-8, 0.1, 1, param_bf16=pcopy),
                          P * 28, "p, m, v fp32 in+out, g bf16 in, bf16 copy out"),
+        "rmsnorm_fwd": (lambda: nn.rmsnorm_forward(x, w, 1e-6), N * D * 4,
+                        "x in, y out (bf16)"),
+        "rmsnorm_bwd": (lambda: nn.rmsnorm_backward(dy, x, w, 1e-6, grad_weight=rms_dw),
+                        N * D * 6, "dy, x in, dx out (bf16)"),
+        "shortconv_fwd_w64": (lambda: prism.shortconv_forward(x3, conv_w), N * D * 4,
+                              "x in, y out (bf16); 64 taps per output"),
+        "shortconv_bwd_w64": (lambda: prism.shortconv_backward(dy3, x3, conv_w,
+                                                               grad_weight=conv_dw),
+                              N * D * 6, "dy, x in, dx out (bf16), dW partials"),
+        "prism_fwd_l3": (lambda: prism.prism_forward(x3, dy3, w_p, 64), N * 64 * 4 + N * D * 2,
+                         "u, v in over head_dim 64, output rows out (bf16)"),
+        "prism_bwd_l3": (lambda: prism.prism_backward(dy3, x3, dy3, w_p, 64, gw_p),
+                         N * 64 * 6 + N * D * 4, "g, u, v in over head_dim 64, du, dv rows out"),
     }
     # GEMMs of one config-4 layer and the LM head (MFMA-bound: FLOPs, not bytes)
     wq, wu, wd, wh = bf(D, 3 * D, scale=0.03), bf(D, F, scale=0.03), bf(F, D, scale=0.02), \

@@ -5,9 +5,11 @@
 // is declared only; the executed semantics are ShortConv.forwardCpu,
 // src/model/prism.zig:448-473):
 //   y[b,t,c] = bf16( sum over w = 0..W-1 with t-w >= 0 of x[b,t-w,c] * weight[c,w] )
-// with every product rounded to fp32 and the terms added in increasing w, as
-// the reference loop does (no fused multiply-add), so the output is
-// bit-identical to it.
+// with the terms added in fp32 in increasing w, as the reference loop does, so
+// the output is bit-identical to it.  The product of two bf16 values has at
+// most 16 significant bits and is exact in fp32 (unless it falls below fp32's
+// normal range), so a fused multiply-add rounds exactly as the reference's
+// separate multiply and add.
 // ShortConv backward (shortConvBackwardCuda, src/kernels/prism_kernels.zig:
 // 50-60, declared only, no body anywhere):
 //   grad_input[b,t,c] = sum over w with t+w < T of dy[b,t+w,c] weight[c,w]  (bf16)
@@ -36,8 +38,11 @@
 // weights for 256 multiply-adds.  Windows longer than 80 take direct kernels
 // that read through the caches.  The weight gradient splits the token tiles
 // over workgroups; each writes a partial, which a second pass sums in a fixed
-// order into grad_weight.  PRISM runs one lane per channel over blocks of 32
-// rows.
+// order into grad_weight.  PRISM runs one lane per active channel and one
+// wave per row phase over blocks of 64 rows; columns past head_dim are cleared
+// by a separate 16-byte store pass.  The w_p gradient is summed per workgroup
+// in LDS and added with one float atomic per workgroup and value, so the order
+// of those additions varies between runs.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -46,6 +51,7 @@
 #include "common.hpp"
 #include "gelu.hpp"
 #include "internal.hpp"
+#include "reduce.hpp"
 
 namespace efla {
 namespace prism {
@@ -60,65 +66,158 @@ constexpr int JB = 16;   // outputs (or lags) per lane and lag block
 constexpr int kMaxTiledW = 80;  // keeps every tile within 64 KiB of LDS
 constexpr int kMaxLagBlocks = kMaxTiledW / JB;
 constexpr int kMaxIter = 16;
-constexpr int RB = 32;  // PRISM rows per workgroup
+constexpr int PRB = 64;  // PRISM rows per workgroup (16 per wave)
 constexpr long kMaxBlocks = 16384;
 
 struct WPtrs {
     const bf16* p[kMaxIter];
 };
+struct GPtrs {
+    float* p[kMaxIter];
+};
 
 __device__ __forceinline__ int padded_window(int W) { return (W + JB - 1) & ~(JB - 1); }
 
-// dst[r][c] = src[b, t_lo + r, c0 + c] as fp32, 0 outside [0, T) x [0, C)
+constexpr int kStageIt = (TT + kMaxTiledW - 1 + 31) / 32;  // 16-byte row chunks per thread
+constexpr int kStageEl = ((TT + kMaxTiledW - 1) * CT + NTH - 1) / NTH;  // scalar elements
+
+// dst[r][c] = src[b, t_lo + r, c0 + c] as fp32 for r < nrows, 0 outside
+// [0, T) x [0, C).  Every load is issued before the first LDS write.  VEC:
+// 16-byte loads of 8 channels (C % 8 == 0 and src 16-byte aligned).
+template <bool VEC>
 __device__ __forceinline__ void stage_rows(float* dst, const bf16* __restrict__ src, long b,
                                            long t_lo, int nrows, int T, int C, int c0) {
-    for (int i = threadIdx.x; i < nrows * CT; i += NTH) {
-        const int r = i / CT, c = i % CT;
-        const long t = t_lo + r;
-        float val = 0.f;
-        if (t >= 0 && t < T && c0 + c < C) val = (float)src[(b * T + t) * C + c0 + c];
-        dst[r * CT + c] = val;
+    if constexpr (VEC) {
+        const int q = threadIdx.x & 7, ro = threadIdx.x >> 3;
+        const bool cok = c0 + q * 8 < C;
+        bf16x8 v[kStageIt];
+#pragma unroll
+        for (int it = 0; it < kStageIt; ++it) {
+            const int r = ro + 32 * it;
+            const long t = t_lo + r;
+            if (r < nrows && t >= 0 && t < T && cok) {
+                v[it] = *reinterpret_cast<const bf16x8*>(src + (b * T + t) * C + c0 + q * 8);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) v[it][i] = (bf16)0.f;
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < kStageIt; ++it) {
+            const int r = ro + 32 * it;
+            if (r < nrows) {
+                floatx4 lo, hi;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    lo[i] = (float)v[it][i];
+                    hi[i] = (float)v[it][4 + i];
+                }
+                *reinterpret_cast<floatx4*>(&dst[r * CT + q * 8]) = lo;
+                *reinterpret_cast<floatx4*>(&dst[r * CT + q * 8 + 4]) = hi;
+            }
+        }
+    } else {
+        float v[kStageEl];
+#pragma unroll
+        for (int k = 0; k < kStageEl; ++k) {
+            const int i = threadIdx.x + k * NTH;
+            const int r = i / CT, c = i % CT;
+            const long t = t_lo + r;
+            v[k] = (r < nrows && t >= 0 && t < T && c0 + c < C)
+                       ? (float)src[(b * T + t) * C + c0 + c] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < kStageEl; ++k) {
+            const int i = threadIdx.x + k * NTH;
+            if (i < nrows * CT) dst[i] = v[k];
+        }
     }
 }
 
-// ws[w][c] (row stride CT + 1) = weight[c0 + c][w], 0 for w >= W or c >= C
+// ws[w][c] (row stride CT + 1) = weight[c0 + c][w], 0 for w >= W or c >= C.
+// The tile's weights are one contiguous run of 64 W values (rows c0..c0+63).
 __device__ __forceinline__ void stage_weights(float* ws, const bf16* __restrict__ wt, int W, int Wp,
                                               int C, int c0) {
-    for (int i = threadIdx.x; i < CT * Wp; i += NTH) {
-        const int c = i / Wp, w = i % Wp;
-        ws[w * (CT + 1) + c] = (w < W && c0 + c < C) ? (float)wt[(long)(c0 + c) * W + w] : 0.f;
+    const bf16* base = wt + (long)c0 * W;
+    const int nvalid = min(CT, C - c0) * W;
+    const bool vec = ((uintptr_t)wt & 15) == 0;
+    constexpr int kIt = (CT * kMaxTiledW / 8 + NTH - 1) / NTH;
+    bf16x8 v[kIt];
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int e = 8 * (threadIdx.x + it * NTH);
+        if (vec && e + 8 <= nvalid) {
+            v[it] = *reinterpret_cast<const bf16x8*>(base + e);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[it][i] = e + i < nvalid ? base[e + i] : (bf16)0.f;
+        }
+    }
+#pragma unroll
+    for (int it = 0; it < kIt; ++it) {
+        const int e = 8 * (threadIdx.x + it * NTH);
+        if (e < CT * W) {
+            int c = e / W, w = e - c * W;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                ws[w * (CT + 1) + c] = (float)v[it][i];
+                if (++w == W) {
+                    w = 0;
+                    ++c;
+                }
+            }
+        }
+    }
+    for (int i = threadIdx.x; i < (Wp - W) * CT; i += NTH) {
+        const int w = W + i / CT, c = i % CT;
+        ws[w * (CT + 1) + c] = 0.f;
     }
 }
 
 // y = ShortConv(x) for one 64 x 64 tile; grid (token tiles, channel tiles, B)
-template <bool EDGE>
-__device__ __forceinline__ void conv_fwd_lane(float (&acc)[JB], const float* xs, const float* ws,
-                                              int W, int Wp, int g, int c, int tj0) {
-#pragma clang fp contract(off)
-    for (int w0 = 0; w0 < Wp; w0 += JB) {
-        // xr[m] = x[tj0 + m - (JB-1) - w0]
-        const int rbase = g * JB - (JB - 1) - w0 + (Wp - 1);
-        float xr[2 * JB - 1], wv[JB];
+// One block of 16 lags starting at w0.  EDGE: some x index t - w may be
+// negative (skip those terms, as the reference loop does); TAIL: lags at or
+// beyond W exist in this block (skip them).
+template <bool EDGE, bool TAIL>
+__device__ __forceinline__ void conv_fwd_block(float (&acc)[JB], const float* xs, const float* ws,
+                                               int W, int Wp, int g, int c, int tj0, int w0) {
+    // xr[m] = x[tj0 + m - (JB-1) - w0]
+    const int rbase = g * JB - (JB - 1) - w0 + (Wp - 1);
+    float xr[2 * JB - 1], wv[JB];
 #pragma unroll
-        for (int m = 0; m < 2 * JB - 1; ++m) xr[m] = xs[(rbase + m) * CT + c];
+    for (int m = 0; m < 2 * JB - 1; ++m) xr[m] = xs[(rbase + m) * CT + c];
 #pragma unroll
-        for (int k = 0; k < JB; ++k) wv[k] = ws[(w0 + k) * (CT + 1) + c];
+    for (int k = 0; k < JB; ++k) wv[k] = ws[(w0 + k) * (CT + 1) + c];
 #pragma unroll
-        for (int k = 0; k < JB; ++k) {
-            if (w0 + k < W) {
+    for (int k = 0; k < JB; ++k) {
+        if (!TAIL || w0 + k < W) {
 #pragma unroll
-                for (int j = 0; j < JB; ++j) {
-                    const float p = xr[j - k + JB - 1] * wv[k];
-                    if (EDGE)
-                        acc[j] = (tj0 + j - w0 - k >= 0) ? acc[j] + p : acc[j];
-                    else
-                        acc[j] = acc[j] + p;
-                }
+            for (int j = 0; j < JB; ++j) {
+                const float s = fmaf(xr[j - k + JB - 1], wv[k], acc[j]);
+                acc[j] = (!EDGE || tj0 + j - w0 - k >= 0) ? s : acc[j];
             }
         }
     }
 }
 
+__device__ __forceinline__ void conv_fwd_lane(float (&acc)[JB], const float* xs, const float* ws,
+                                              int W, int Wp, int g, int c, int tj0) {
+    const int wfull = W & ~(JB - 1);
+    for (int w0 = 0; w0 < wfull; w0 += JB) {
+        if (tj0 - w0 - (JB - 1) >= 0)
+            conv_fwd_block<false, false>(acc, xs, ws, W, Wp, g, c, tj0, w0);
+        else
+            conv_fwd_block<true, false>(acc, xs, ws, W, Wp, g, c, tj0, w0);
+    }
+    if (wfull < W) {
+        if (tj0 - wfull - (JB - 1) >= 0)
+            conv_fwd_block<false, true>(acc, xs, ws, W, Wp, g, c, tj0, wfull);
+        else
+            conv_fwd_block<true, true>(acc, xs, ws, W, Wp, g, c, tj0, wfull);
+    }
+}
+
+template <bool VEC>
 __global__ void __launch_bounds__(NTH) conv_fwd_kernel(const bf16* __restrict__ x,
                                                        const bf16* __restrict__ wt,
                                                        bf16* __restrict__ y, int T, int C, int W) {
@@ -129,7 +228,7 @@ __global__ void __launch_bounds__(NTH) conv_fwd_kernel(const bf16* __restrict__ 
     float* ws = smem + nrows * CT;   // [Wp][CT + 1]
     const long b = blockIdx.z;
     const int t0 = blockIdx.x * TT, c0 = blockIdx.y * CT;
-    stage_rows(xs, x, b, (long)t0 - (Wp - 1), nrows, T, C, c0);
+    stage_rows<VEC>(xs, x, b, (long)t0 - (Wp - 1), nrows, T, C, c0);
     stage_weights(ws, wt, W, Wp, C, c0);
     __syncthreads();
     const int c = lane_id(), g = __builtin_amdgcn_readfirstlane(wave_id());
@@ -137,10 +236,7 @@ __global__ void __launch_bounds__(NTH) conv_fwd_kernel(const bf16* __restrict__ 
     float acc[JB];
 #pragma unroll
     for (int j = 0; j < JB; ++j) acc[j] = 0.f;
-    if (tj0 < W - 1)
-        conv_fwd_lane<true>(acc, xs, ws, W, Wp, g, c, tj0);
-    else
-        conv_fwd_lane<false>(acc, xs, ws, W, Wp, g, c, tj0);
+    conv_fwd_lane(acc, xs, ws, W, Wp, g, c, tj0);
     if (c0 + c < C) {
 #pragma unroll
         for (int j = 0; j < JB; ++j)
@@ -153,19 +249,19 @@ __global__ void __launch_bounds__(NTH) conv_fwd_direct_kernel(const bf16* __rest
                                                               const bf16* __restrict__ wt,
                                                               bf16* __restrict__ y, long n, int T,
                                                               int C, int W) {
-#pragma clang fp contract(off)
     for (long i = (long)blockIdx.x * NTH + threadIdx.x; i < n; i += (long)gridDim.x * NTH) {
         const int c = (int)(i % C);
         const long bt = i / C;
         const int t = (int)(bt % T);
         const int wmax = min(W - 1, t);
         float s = 0.f;
-        for (int w = 0; w <= wmax; ++w) s = s + (float)x[(bt - w) * C + c] * (float)wt[(long)c * W + w];
+        for (int w = 0; w <= wmax; ++w) s = fmaf((float)x[(bt - w) * C + c], (float)wt[(long)c * W + w], s);
         y[i] = (bf16)s;
     }
 }
 
 // grad_input for one tile: dx[t] = sum_w dy[t + w] weight[w]
+template <bool VEC>
 __global__ void __launch_bounds__(NTH) conv_dx_kernel(const bf16* __restrict__ dy,
                                                       const bf16* __restrict__ wt,
                                                       bf16* __restrict__ dx, int T, int C, int W) {
@@ -176,7 +272,7 @@ __global__ void __launch_bounds__(NTH) conv_dx_kernel(const bf16* __restrict__ d
     float* ws = smem + nrows * CT;  // [Wp][CT + 1]
     const long b = blockIdx.z;
     const int t0 = blockIdx.x * TT, c0 = blockIdx.y * CT;
-    stage_rows(ds, dy, b, t0, nrows, T, C, c0);
+    stage_rows<VEC>(ds, dy, b, t0, nrows, T, C, c0);
     stage_weights(ws, wt, W, Wp, C, c0);
     __syncthreads();
     const int c = lane_id(), g = __builtin_amdgcn_readfirstlane(wave_id());
@@ -220,6 +316,7 @@ __global__ void __launch_bounds__(NTH) conv_dx_direct_kernel(const bf16* __restr
 // part[split][c][w] = sum over this split's token tiles of dy[t] x[t - w].
 // Wave g takes tokens 16g..16g+15 of every tile for all lags; the four waves'
 // sums are added in LDS in wave order at the end.
+template <bool VEC>
 __global__ void __launch_bounds__(NTH) conv_dw_kernel(const bf16* __restrict__ dy,
                                                       const bf16* __restrict__ x,
                                                       float* __restrict__ part, int B, int T,
@@ -242,8 +339,8 @@ __global__ void __launch_bounds__(NTH) conv_dw_kernel(const bf16* __restrict__ d
         const long b = tile / tiles_t;
         const int t0 = (int)(tile % tiles_t) * TT;
         __syncthreads();
-        stage_rows(xs, x, b, (long)t0 - (Wp - 1), nrx, T, C, c0);
-        stage_rows(ds, dy, b, t0, TT, T, C, c0);
+        stage_rows<VEC>(xs, x, b, (long)t0 - (Wp - 1), nrx, T, C, c0);
+        stage_rows<VEC>(ds, dy, b, t0, TT, T, C, c0);
         __syncthreads();
         float dr[JB];
 #pragma unroll
@@ -308,35 +405,26 @@ __global__ void __launch_bounds__(NTH) conv_dw_direct_kernel(const bf16* __restr
     part[(long)blockIdx.y * cw + i] = s;
 }
 
-// out[i] += sum_s part[s][i], s in order
-__global__ void __launch_bounds__(NTH) sum_parts_kernel(const float* __restrict__ part, int nsplit,
-                                                        long n, long stride,
-                                                        float* __restrict__ out) {
-    for (long i = (long)blockIdx.x * NTH + threadIdx.x; i < n; i += (long)gridDim.x * NTH) {
-        float s = 0.f;
-        for (int k = 0; k < nsplit; ++k) s += part[(long)k * stride + i];
-        out[i] += s;
-    }
-}
-
 // ---------------------------------------------------------------------------
 // PRISM
 // ---------------------------------------------------------------------------
+// Lane = channel c = 64 blockIdx.y + lane (active when c < HD); wave g takes
+// rows r0 + g, r0 + g + 4, ... of the block's PRB rows.
 __global__ void __launch_bounds__(NTH) prism_fwd_kernel(const bf16* __restrict__ u,
                                                         const bf16* __restrict__ v, WPtrs wp,
                                                         bf16* __restrict__ out, long rows, int C,
                                                         int HD, int L) {
-    const int c = blockIdx.y * NTH + threadIdx.x;
-    if (c >= C) return;
-    const long r0 = (long)blockIdx.x * RB, r1 = min(rows, r0 + RB);
-    if (c >= HD) {
-        for (long r = r0; r < r1; ++r) out[r * C + c] = (bf16)0.f;
-        return;
-    }
+    const int c = blockIdx.y * kWave + lane_id();
+    if (c >= HD) return;
+    const int g = wave_id();
+    const long r0 = (long)blockIdx.x * PRB;
     float p[kMaxIter];
 #pragma unroll
     for (int l = 0; l < kMaxIter; ++l) p[l] = l < L ? (float)wp.p[l][c] : 0.f;
-    for (long r = r0; r < r1; ++r) {
+#pragma unroll 4
+    for (int i = 0; i < PRB / 4; ++i) {
+        const long r = r0 + g + 4 * i;
+        if (r >= rows) break;
         float res = (float)v[r * C + c] - (float)u[r * C + c];
         float o = 0.f;
 #pragma unroll
@@ -351,56 +439,99 @@ __global__ void __launch_bounds__(NTH) prism_fwd_kernel(const bf16* __restrict__
     }
 }
 
-// part[blk][l][c] (c < HD) = this block's sum over rows of gx_l r_l
+// grad_w_p[l][c] += this block's sum of gx_l r_l (one atomic add per block,
+// so the order of the additions varies from run to run)
 __global__ void __launch_bounds__(NTH) prism_bwd_kernel(const bf16* __restrict__ go,
                                                         const bf16* __restrict__ u,
                                                         const bf16* __restrict__ v, WPtrs wp,
                                                         bf16* __restrict__ gu,
-                                                        bf16* __restrict__ gv,
-                                                        float* __restrict__ part, long rows,
-                                                        int C, int HD, int L) {
-    const int c = blockIdx.y * NTH + threadIdx.x;
-    if (c >= C) return;
-    const long r0 = (long)blockIdx.x * RB, r1 = min(rows, r0 + RB);
-    if (c >= HD) {
-        for (long r = r0; r < r1; ++r) {
-            gu[r * C + c] = (bf16)0.f;
-            gv[r * C + c] = (bf16)0.f;
-        }
-        return;
-    }
+                                                        bf16* __restrict__ gv, GPtrs gw,
+                                                        long rows, int C, int HD, int L) {
+    __shared__ float red[NTH / kWave][kMaxIter][kWave];
+    const int lane = lane_id(), g = wave_id();
+    const int c = blockIdx.y * kWave + lane;
+    const bool active = c < HD;
+    const long r0 = (long)blockIdx.x * PRB;
     float p[kMaxIter], dp[kMaxIter];
 #pragma unroll
     for (int l = 0; l < kMaxIter; ++l) {
-        p[l] = l < L ? (float)wp.p[l][c] : 0.f;
+        p[l] = (active && l < L) ? (float)wp.p[l][c] : 0.f;
         dp[l] = 0.f;
     }
-    for (long r = r0; r < r1; ++r) {
-        float res[kMaxIter], xl[kMaxIter];
-        float rr = (float)v[r * C + c] - (float)u[r * C + c];
+    if (active) {
+#pragma unroll 2
+        for (int i = 0; i < PRB / 4; ++i) {
+            const long r = r0 + g + 4 * i;
+            if (r >= rows) break;
+            float res[kMaxIter], xl[kMaxIter];
+            float rr = (float)v[r * C + c] - (float)u[r * C + c];
+            const float gr = (float)go[r * C + c];
+#pragma unroll
+            for (int l = 0; l < kMaxIter; ++l) {
+                res[l] = rr;
+                xl[l] = p[l] * rr;
+                if (l < L) rr -= gelu_f<true>(xl[l]);
+            }
+            float a = 0.f;
+#pragma unroll
+            for (int l = kMaxIter - 1; l >= 0; --l) {
+                if (l < L) {
+                    const float gx = (0.5f * gr - a) * gelu_df<true>(xl[l]);
+                    dp[l] = fmaf(gx, res[l], dp[l]);
+                    a = fmaf(gx, p[l], a);
+                }
+            }
+            gv[r * C + c] = (bf16)a;
+            gu[r * C + c] = (bf16)(-a);
+        }
+    }
+    if (!gw.p[0]) return;
+#pragma unroll
+    for (int l = 0; l < kMaxIter; ++l)
+        if (l < L) red[g][l][lane] = dp[l];
+    __syncthreads();
+    if (g == 0 && active) {
 #pragma unroll
         for (int l = 0; l < kMaxIter; ++l) {
-            res[l] = rr;
-            xl[l] = p[l] * rr;
-            if (l < L) rr -= gelu_f<true>(xl[l]);
-        }
-        const float g = (float)go[r * C + c];
-        float a = 0.f;
-#pragma unroll
-        for (int l = kMaxIter - 1; l >= 0; --l) {
             if (l < L) {
-                const float gx = (0.5f * g - a) * gelu_df<true>(xl[l]);
-                dp[l] = fmaf(gx, res[l], dp[l]);
-                a = fmaf(gx, p[l], a);
+                float t = 0.f;
+#pragma unroll
+                for (int k = 0; k < NTH / kWave; ++k) t += red[k][l][lane];
+                atomicAdd(&gw.p[l][c], t);
             }
         }
-        gv[r * C + c] = (bf16)a;
-        gu[r * C + c] = (bf16)(-a);
     }
-    if (part) {
+}
+
+// a[r, HD..C) = 0 and b[r, HD..C) = 0 (b may be NULL) for every row, with
+// 16-byte stores when VEC (C and HD multiples of 8, 16-byte aligned rows);
+// the first workgroup also clears extra[0..extra_n).
+template <bool VEC>
+__global__ void __launch_bounds__(NTH) zero_cols_kernel(bf16* __restrict__ a, bf16* __restrict__ b,
+                                                        long rows, int C, int HD,
+                                                        bf16* __restrict__ extra, long extra_n) {
+    if (blockIdx.x == 0)
+        for (long i = threadIdx.x; i < extra_n; i += NTH) extra[i] = (bf16)0.f;
+    const long gtid = (long)blockIdx.x * NTH + threadIdx.x, gstride = (long)gridDim.x * NTH;
+    if (VEC) {
+        const int per = (C - HD) / 8;
+        bf16x8 z;
 #pragma unroll
-        for (int l = 0; l < kMaxIter; ++l)
-            if (l < L) part[((long)blockIdx.x * L + l) * HD + c] = dp[l];
+        for (int i = 0; i < 8; ++i) z[i] = (bf16)0.f;
+        for (long i = gtid; i < rows * per; i += gstride) {
+            const long r = i / per;
+            const long off = r * C + HD + 8 * (i - r * per);
+            *reinterpret_cast<bf16x8*>(a + off) = z;
+            if (b) *reinterpret_cast<bf16x8*>(b + off) = z;
+        }
+    } else {
+        const int per = C - HD;
+        for (long i = gtid; i < rows * per; i += gstride) {
+            const long r = i / per;
+            const long off = r * C + HD + (i - r * per);
+            a[off] = (bf16)0.f;
+            if (b) b[off] = (bf16)0.f;
+        }
     }
 }
 
@@ -411,6 +542,8 @@ inline size_t conv_lds_bytes(int W, bool dw) {
     const size_t wts = dw ? 0 : (size_t)Wp * (CT + 1) * sizeof(float);
     return a + wts;
 }
+
+inline bool vec_ok(const void* p, int C) { return ((uintptr_t)p & 15) == 0 && C % 8 == 0; }
 
 inline unsigned grid_1d(long n) {
     long g = (n + NTH - 1) / NTH;
@@ -449,8 +582,12 @@ extern "C" int shortconv_forward_hip(const void* input, const void* weight, void
         const dim3 grid((unsigned)((T + prism::TT - 1) / prism::TT),
                         (unsigned)((C + prism::CT - 1) / prism::CT), (unsigned)batch_size);
         ::efla::ProfScope ps("shortconv_fwd", stream);
-        hipLaunchKernelGGL(prism::conv_fwd_kernel, grid, dim3(prism::NTH),
-                           prism::conv_lds_bytes(W, false), stream, x, wt, y, T, C, W);
+        if (prism::vec_ok(x, C))
+            hipLaunchKernelGGL(prism::conv_fwd_kernel<true>, grid, dim3(prism::NTH),
+                               prism::conv_lds_bytes(W, false), stream, x, wt, y, T, C, W);
+        else
+            hipLaunchKernelGGL(prism::conv_fwd_kernel<false>, grid, dim3(prism::NTH),
+                               prism::conv_lds_bytes(W, false), stream, x, wt, y, T, C, W);
     } else {
         EFLA_LAUNCH("shortconv_fwd_direct", prism::conv_fwd_direct_kernel,
                     dim3(prism::grid_1d((long)n)), dim3(prism::NTH), stream, x, wt, y, (long)n, T,
@@ -483,8 +620,12 @@ extern "C" int shortconv_backward_hip(const void* grad_output, const void* input
         if (tiled) {
             const dim3 grid((unsigned)ttiles, (unsigned)ctiles, (unsigned)B);
             ::efla::ProfScope ps("shortconv_dx", stream);
-            hipLaunchKernelGGL(prism::conv_dx_kernel, grid, dim3(prism::NTH),
-                               prism::conv_lds_bytes(W, false), stream, dy, wt, dx, T, C, W);
+            if (prism::vec_ok(dy, C))
+                hipLaunchKernelGGL(prism::conv_dx_kernel<true>, grid, dim3(prism::NTH),
+                                   prism::conv_lds_bytes(W, false), stream, dy, wt, dx, T, C, W);
+            else
+                hipLaunchKernelGGL(prism::conv_dx_kernel<false>, grid, dim3(prism::NTH),
+                                   prism::conv_lds_bytes(W, false), stream, dy, wt, dx, T, C, W);
         } else {
             EFLA_LAUNCH("shortconv_dx_direct", prism::conv_dx_direct_kernel,
                         dim3(prism::grid_1d((long)n)), dim3(prism::NTH), stream, dy, wt, dx,
@@ -507,18 +648,23 @@ extern "C" int shortconv_backward_hip(const void* grad_output, const void* input
         float* part = (float*)ws;
         if (tiled) {
             ::efla::ProfScope ps("shortconv_dw", stream);
-            hipLaunchKernelGGL(prism::conv_dw_kernel, dim3((unsigned)ctiles, (unsigned)nsplit),
-                               dim3(prism::NTH), prism::conv_lds_bytes(W, true), stream, dy, x,
-                               part, B, T, C, W, ttiles);
+            const dim3 grid((unsigned)ctiles, (unsigned)nsplit);
+            if (prism::vec_ok(dy, C) && prism::vec_ok(x, C))
+                hipLaunchKernelGGL(prism::conv_dw_kernel<true>, grid, dim3(prism::NTH),
+                                   prism::conv_lds_bytes(W, true), stream, dy, x, part, B, T, C,
+                                   W, ttiles);
+            else
+                hipLaunchKernelGGL(prism::conv_dw_kernel<false>, grid, dim3(prism::NTH),
+                                   prism::conv_lds_bytes(W, true), stream, dy, x, part, B, T, C,
+                                   W, ttiles);
         } else {
             EFLA_LAUNCH("shortconv_dw_direct", prism::conv_dw_direct_kernel,
                         dim3((unsigned)((cw + prism::NTH - 1) / prism::NTH), (unsigned)nsplit),
                         dim3(prism::NTH), stream, dy, x, part, B, T, C, W);
         }
         EFLA_CHECK(hipPeekAtLastError());
-        EFLA_LAUNCH("shortconv_dw_sum", prism::sum_parts_kernel, dim3(prism::grid_1d(cw)),
-                    dim3(prism::NTH), stream, (const float*)part, (int)nsplit, cw, cw,
-                    grad_weight);
+        EFLA_LAUNCH("shortconv_dw_sum", partial_colsum_add_kernel, partial_colsum_grid(cw),
+                    dim3(256), stream, (const float*)part, (int)nsplit, cw, grad_weight);
     }
     return (int)hipPeekAtLastError();
 }
@@ -531,12 +677,40 @@ int prism_check(size_t B, size_t T, size_t hidden, size_t head_dim, size_t L,
     if (L > (size_t)prism::kMaxIter || B * T * hidden > ((size_t)1 << 40) ||
         hidden > 0x7FFFFFFFull)
         return kInvalidConfiguration;
+    if ((B * T + prism::PRB - 1) / prism::PRB > 0x7FFFFFFFull) return kInvalidConfiguration;
     if (L > 0 && !w_p) return kInvalidValue;
     for (size_t l = 0; l < (size_t)prism::kMaxIter; ++l) {
         wp->p[l] = l < L ? (const bf16*)w_p[l] : nullptr;
         if (l < L && !wp->p[l]) return kInvalidValue;
     }
     return kSuccess;
+}
+
+}  // namespace
+
+namespace {
+
+// zero the columns [head_dim, hidden_dim) of a and b (b may be NULL) and the
+// extra_n values at extra
+int zero_tail(bf16* a, bf16* b, long rows, size_t hidden, size_t head_dim, bf16* extra,
+              long extra_n, hipStream_t stream) {
+    const long n = rows * (long)(hidden - head_dim);
+    if (n == 0 && extra_n == 0) return kSuccess;
+    const bool vec = hidden % 8 == 0 && head_dim % 8 == 0 && ((uintptr_t)a & 15) == 0 &&
+                     ((uintptr_t)b & 15) == 0;
+    const dim3 grid(prism::grid_1d(vec ? n / 8 : n));
+    if (vec)
+        EFLA_LAUNCH("prism_zero_cols", prism::zero_cols_kernel<true>, grid, dim3(prism::NTH),
+                    stream, a, b, rows, (int)hidden, (int)head_dim, extra, extra_n);
+    else
+        EFLA_LAUNCH("prism_zero_cols", prism::zero_cols_kernel<false>, grid, dim3(prism::NTH),
+                    stream, a, b, rows, (int)hidden, (int)head_dim, extra, extra_n);
+    return (int)hipPeekAtLastError();
+}
+
+dim3 prism_grid(long rows, size_t head_dim) {
+    return dim3((unsigned)((rows + prism::PRB - 1) / prism::PRB),
+                (unsigned)((head_dim + kWave - 1) / kWave));
 }
 
 }  // namespace
@@ -555,18 +729,17 @@ extern "C" int prism_forward_hip(const void* u, const void* v, const void* prev_
     if (rc != kSuccess) return rc;
     const long rows = (long)(batch_size * seq_len);
     if (rows > 0 && (!u || !v || !output)) return kInvalidValue;
-    if (new_state) {
-        rc = fill_zero(new_state, head_dim * head_dim * sizeof(bf16), stream);
-        if (rc != kSuccess) return rc;
+    if (rows == 0) {
+        return new_state ? fill_zero(new_state, head_dim * head_dim * sizeof(bf16), stream)
+                         : kSuccess;
     }
-    if (rows == 0) return kSuccess;
-    const dim3 grid((unsigned)((rows + prism::RB - 1) / prism::RB),
-                    (unsigned)((hidden_dim + prism::NTH - 1) / prism::NTH));
-    if (grid.x > 0x7FFFFFFFu) return kInvalidConfiguration;
+    const dim3 grid = prism_grid(rows, head_dim);
     EFLA_LAUNCH("prism_fwd", prism::prism_fwd_kernel, grid, dim3(prism::NTH), stream,
                 (const bf16*)u, (const bf16*)v, wp, (bf16*)output, rows, (int)hidden_dim,
                 (int)head_dim, (int)num_iterations);
-    return (int)hipPeekAtLastError();
+    EFLA_CHECK(hipPeekAtLastError());
+    return zero_tail((bf16*)output, nullptr, rows, hidden_dim, head_dim, (bf16*)new_state,
+                     new_state ? (long)(head_dim * head_dim) : 0, stream);
 }
 
 extern "C" int prism_backward_hip(const void* grad_output, const void* u, const void* v,
@@ -581,32 +754,15 @@ extern "C" int prism_backward_hip(const void* grad_output, const void* u, const 
     if (rows == 0) return kSuccess;
     if (!grad_output || !u || !v || !grad_u || !grad_v) return kInvalidValue;
     const int L = (int)num_iterations;
-    if (grad_w_p)
-        for (int l = 0; l < L; ++l)
-            if (!grad_w_p[l]) return kInvalidValue;
-    const dim3 grid((unsigned)((rows + prism::RB - 1) / prism::RB),
-                    (unsigned)((hidden_dim + prism::NTH - 1) / prism::NTH));
-    if (grid.x > 0x7FFFFFFFu) return kInvalidConfiguration;
-    float* part = nullptr;
-    const bool want_w = grad_w_p && L > 0;
-    if (want_w) {
-        void* ws = nullptr;
-        rc = workspace_acquire((size_t)grid.x * L * head_dim * sizeof(float), stream, &ws);
-        if (rc != kSuccess) return rc;
-        part = (float*)ws;
+    prism::GPtrs gw;
+    for (int l = 0; l < prism::kMaxIter; ++l) {
+        gw.p[l] = (grad_w_p && l < L) ? grad_w_p[l] : nullptr;
+        if (grad_w_p && l < L && !gw.p[l]) return kInvalidValue;
     }
+    const dim3 grid = prism_grid(rows, head_dim);
     EFLA_LAUNCH("prism_bwd", prism::prism_bwd_kernel, grid, dim3(prism::NTH), stream,
                 (const bf16*)grad_output, (const bf16*)u, (const bf16*)v, wp, (bf16*)grad_u,
-                (bf16*)grad_v, part, rows, (int)hidden_dim, (int)head_dim, L);
+                (bf16*)grad_v, gw, rows, (int)hidden_dim, (int)head_dim, L);
     EFLA_CHECK(hipPeekAtLastError());
-    if (want_w) {
-        for (int l = 0; l < L; ++l) {
-            EFLA_LAUNCH("prism_bwd_sum", prism::sum_parts_kernel,
-                        dim3(prism::grid_1d((long)head_dim)), dim3(prism::NTH), stream,
-                        (const float*)(part + (size_t)l * head_dim), (int)grid.x, (long)head_dim,
-                        (long)L * head_dim, grad_w_p[l]);
-            EFLA_CHECK(hipPeekAtLastError());
-        }
-    }
-    return kSuccess;
+    return zero_tail((bf16*)grad_u, (bf16*)grad_v, rows, hidden_dim, head_dim, nullptr, 0, stream);
 }

@@ -23,6 +23,7 @@
 #include "../../include/efla_hip.h"
 #include "common.hpp"
 #include "internal.hpp"
+#include "reduce.hpp"
 
 namespace efla {
 namespace rms {
@@ -179,29 +180,6 @@ __global__ void __launch_bounds__(NTH) bwd_loop_kernel(const bf16* __restrict__ 
     for (int i = threadIdx.x; i < D; i += NTH) part[(long)blockIdx.x * D + i] = acc[i];
 }
 
-// gw[c] += sum_b part[b][c], 16 row groups per 64-column block, fixed order
-__global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ part, int nblk,
-                                                     int D, float* __restrict__ gw) {
-    __shared__ float s_acc[16][64 + 1];
-    const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
-    const int c0 = blockIdx.x * 64 + 4 * q;
-    float s[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int b = rg; b < nblk; b += 16)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (c0 + i < D) s[i] += part[(long)b * D + c0 + i];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) s_acc[rg][4 * q + i] = s[i];
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const int c = blockIdx.x * 64 + threadIdx.x;
-        float t = 0.f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) t += s_acc[k][threadIdx.x];
-        if (c < D) gw[c] += t;
-    }
-}
-
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 }  // namespace rms
@@ -282,8 +260,9 @@ extern "C" int rmsnorm_backward_hip(const void* grad_output, const void* input,
     }
     EFLA_CHECK(hipPeekAtLastError());
     if (grad_weight) {
-        EFLA_LAUNCH("rmsnorm_bwd_reduce", rms::reduce_kernel, dim3((unsigned)((D + 63) / 64)),
-                    dim3(rms::NTH), stream, (const float*)part, (int)nblk, (int)D, grad_weight);
+        EFLA_LAUNCH("rmsnorm_bwd_reduce", partial_colsum_add_kernel,
+                    partial_colsum_grid((long)D), dim3(256), stream, (const float*)part,
+                    (int)nblk, (long)D, grad_weight);
     }
     return (int)hipPeekAtLastError();
 }

@@ -215,8 +215,9 @@ int rmsnorm_backward_hip(const void* grad_output, const void* input, const void*
  * depthwise convolution over (batch, seq_len, hidden_dim) bf16 with weight
  * (hidden_dim, window_size) bf16,
  *   y[b,t,c] = bf16(sum_{w < W, t-w >= 0} x[b,t-w,c] * weight[c,w]),
- * products rounded to fp32 and added in increasing w, bit-identical to that
- * loop.  No element -> 0; a NULL pointer -> 1. */
+ * the fp32 terms added in increasing w, bit-identical to that loop (a bf16
+ * product is exact in fp32 unless it falls below fp32's normal range).  No
+ * element -> 0; a NULL pointer -> 1. */
 int shortconv_forward_hip(const void* input, const void* weight, void* output,
                           size_t batch_size, size_t seq_len, size_t hidden_dim,
                           size_t window_size, hipStream_t stream);
@@ -249,7 +250,8 @@ int prism_forward_hip(const void* u, const void* v, const void* prev_state, void
  * the gradient of prism_forward_hip with the bf16 rounding of o passed
  * straight through.  grad_u, grad_v bf16 (full rows; 0 beyond head_dim);
  * grad_w_p a host array of num_iterations fp32 device pointers, each added
- * into over its first head_dim values (may be NULL). */
+ * into over its first head_dim values with float atomics (the summation order
+ * varies between runs; may be NULL). */
 int prism_backward_hip(const void* grad_output, const void* u, const void* v, const void** w_p,
                        void* grad_u, void* grad_v, float** grad_w_p, size_t batch_size,
                        size_t seq_len, size_t hidden_dim, size_t head_dim,
