@@ -169,16 +169,44 @@ def cpu_baseline(cfg: dict, seed: int, budget_s: float) -> dict:
               file=sys.stderr, flush=True)
         if elapsed >= budget_s:
             break
+    cores = oracle.num_threads()
+    # one thread on a slice of the heads of the first sequence (the recurrence
+    # is independent per head), scaled to whole-sequence tokens per second
+    x = inputs[0]
+    heads = 0
+    t1 = 0.0
+    oracle.set_num_threads(1)
+    try:
+        while heads < H and t1 < min(5.0, budget_s / 3):
+            hs = slice(heads, heads + 1)
+            part = {n: np.ascontiguousarray(a[:, hs]) for n, a in x.items()}
+            t0 = time.perf_counter()
+            oracle.q_forward(part["q"], part["k"], part["v"], part["beta"], T=T,
+                             dtype=np.float32)
+            if cfg["bwd"]:
+                oracle.q_backward(part["q"], part["k"], part["v"], part["beta"], part["do"],
+                                  T=T, dtype=np.float32)
+            t1 += time.perf_counter() - t0
+            heads += 1
+    finally:
+        oracle.set_num_threads(cores)
     return {
         "value": done * T / elapsed,
         "unit": "tokens/s",
-        "cores": oracle.num_threads(),
+        "cores": cores,
         "kind": "port",
         "sample": f"{done} sequences (cycling the workload's {n_seq}) of T={T}, H={H}, "
                   f"d_k={K}, d_v={V} "
                   f"({'fwd+bwd' if cfg['bwd'] else 'fwd'}, fp32 math on "
                   f"{'bf16-rounded ' if cfg['dtype'] == 'bf16' else ''}inputs), "
                   f"{elapsed:.2f} s",
+        "single_thread": {
+            "value": T * heads / H / t1,
+            "unit": "tokens/s",
+            "cores": 1,
+            "sample": f"{heads} of the {H} heads of one T={T} sequence, one thread, "
+                      f"{t1:.2f} s, scaled by heads / {H}",
+        },
     }
 
 

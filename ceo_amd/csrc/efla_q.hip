@@ -806,8 +806,8 @@ struct Problem {
 
 // Workspace layouts.  The forward's layout is a prefix of the backward's:
 // sequence offsets, the per-chunk WY data (bf16 T and fp32 b on the bf16 path;
-// W, U and per-token b on the generic path), then the chunk states h (and, on
-// the generic path, Vn).  A backward call given the forward's workspace finds
+// W, U and per-token b on the generic path), then the chunk states h and, on
+// the bf16 path, the chunks' P = tril(Q K^T) (on the generic path, Vn).  A backward call given the forward's workspace finds
 // the forward's factors, and its saved states, in place.
 template <typename T>
 struct FwdWs {
@@ -817,6 +817,7 @@ struct FwdWs {
     float* bc;    // bf16 path
     float* bco;   // generic path
     T* h;         // generic path; bf16 path when the states are saved
+    bf16* Pc;     // bf16 path when the states are saved
     T* Vn;        // generic path
 };
 
@@ -828,6 +829,7 @@ struct BwdWs {
     float* bc;
     float* bco;  // generic path
     T* h;        // chunk start states
+    bf16* Pc;    // bf16 path: tril(Q K^T) per chunk, as the forward saved it
     T* Vn;       // generic path
     T* dh;       // chunk end-state gradients
     T *dvloc, *dVn, *dW;  // generic path
@@ -837,7 +839,7 @@ struct BwdWs {
 // Takes the common prefix; returns with `c` at the end of h (and Vn).
 template <typename T>
 static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** coff, T** W,
-                         T** U, bf16** Tc, float** bc, float** bco, T** h, T** Vn,
+                         T** U, bf16** Tc, float** bc, float** bco, T** h, bf16** Pc, T** Vn,
                          bool with_h) {
     *cu_s = c.take<int32_t>(p.N + 1);
     *coff = c.take<int32_t>(p.N + 1);
@@ -845,10 +847,14 @@ static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** c
     *Tc = nullptr;
     *bc = *bco = nullptr;
     *h = *Vn = nullptr;
+    *Pc = nullptr;
     if (__is_same(T, bf16)) {
         *Tc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
         *bc = c.take<float>((size_t)p.slots * p.H * 64);
-        if (with_h) *h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
+        if (with_h) {
+            *h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
+            *Pc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
+        }
     } else {
         *W = c.take<T>((size_t)p.ntok * p.H * p.K);
         *U = c.take<T>((size_t)p.ntok * p.H * p.V);
@@ -864,8 +870,8 @@ template <typename T>
 static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out, bool with_states) {
     Carve c(base);
     FwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Vn,
-                    with_states);
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Pc,
+                    &w.Vn, with_states);
     if (out) *out = w;
     return c.off + 256;
 }
@@ -874,8 +880,8 @@ template <typename T>
 static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
     Carve c(base);
     BwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Vn,
-                    true);
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Pc,
+                    &w.Vn, true);
     w.dh = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
     if (!__is_same(T, bf16)) {
         w.dvloc = c.take<T>((size_t)p.ntok * p.H * p.V);
@@ -922,7 +928,7 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
                     dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
                     dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, v, w.Tc, w.bc, si,
-                    H, S0, ST, o, w.h);
+                    H, S0, ST, o, w.h, w.Pc);
         return (int)hipPeekAtLastError();
     }
     EFLA_LAUNCH("efla_q_fwd_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH), st,
@@ -955,12 +961,22 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
             EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
                         dim3(fast::NT), st, k, v, (const bf16*)w.Tc, (const float*)w.bc, si, H,
                         S0, w.h);
-        EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V>), scan_grid,
-                    dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc, si, H,
-                    dST, dS0, w.dh);
-        EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V>), dim3(H, p.slots),
-                    dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc, w.h, w.dh, si,
-                    H, dq, dk, dv, dbeta);
+        // the forward that saved the states also saved each chunk's P
+        if (reuse_states) {
+            EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, true>), scan_grid,
+                        dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        (const bf16*)w.Pc, si, H, dST, dS0, w.dh);
+            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true>), dim3(H, p.slots),
+                        dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc,
+                        (const bf16*)w.Pc, w.h, w.dh, si, H, dq, dk, dv, dbeta);
+        } else {
+            EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, false>), scan_grid,
+                        dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        (const bf16*)nullptr, si, H, dST, dS0, w.dh);
+            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false>), dim3(H, p.slots),
+                        dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc,
+                        (const bf16*)nullptr, w.h, w.dh, si, H, dq, dk, dv, dbeta);
+        }
         return (int)hipPeekAtLastError();
     } else if (!reuse) {
         EFLA_LAUNCH("efla_q_bwd_re_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H),

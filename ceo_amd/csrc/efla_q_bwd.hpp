@@ -133,32 +133,36 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
 // ---------------------------------------------------------------------------
 // reverse scan: chunk end-state gradients
 // ---------------------------------------------------------------------------
-template <int K>
+// PS: the forward saved each chunk's P = tril(Q K^T); it is staged with the
+// other chunk inputs instead of being recomputed.
+template <int K, bool PS>
 struct ScanDhBuf {
     bf16 Q[64 * ldb<K>()];
     bf16 Kr[64 * ldb<K>()];
     bf16 Vs[64 * LD64];  // dO[:, slice]
     bf16 T[64 * LD64];
+    bf16 P[PS ? 64 * LD64 : 8];  // the forward's P [t][t'] (PS)
     float b[64];
 };
 
-template <int K>
+template <int K, bool PS>
 struct ScanDhSmem {
-    ScanDhBuf<K> buf[2];  // chunk n in buf[n & 1]
-    bf16 P[64 * LD64];    // tril(Q K^T) [t][t']
+    ScanDhBuf<K, PS> buf[2];     // chunk n in buf[n & 1]
+    bf16 P[PS ? 8 : 64 * LD64];  // P [t][t'] computed here (not PS)
 };
 
-template <int K, int V>
+template <int K, int V, bool PS>
 __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
                                                      const bf16* __restrict__ k,
                                                      const bf16* __restrict__ dO,
                                                      const bf16* __restrict__ Tc,
-                                                     const float* __restrict__ bc, SeqInfo si,
+                                                     const float* __restrict__ bc,
+                                                     const bf16* __restrict__ Pc, SeqInfo si,
                                                      int H, const float* __restrict__ dST,
                                                      float* __restrict__ dS0,
                                                      bf16* __restrict__ dhist) {
     constexpr int LDK = ldb<K>(), NVS = V / VS;
-    __shared__ __attribute__((aligned(16))) ScanDhSmem<K> sm;
+    __shared__ __attribute__((aligned(16))) ScanDhSmem<K, PS> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
     int bh, vsl;
     scan_map(blockIdx.x, si.N * H, NVS, bh, vsl);
@@ -178,32 +182,43 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
 #pragma unroll
             for (int i = 0; i < 4; ++i) dS[fb][i] = dST[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
     }
-    for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;
+    if constexpr (!PS)
+        for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;
     ChunkRegs<K, true, true> pre;
+    mf::TileRegs<64, 64, NT> rp;  // PS: the chunk's P
     auto prefetch = [&](int n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
-        pre.load(q, k, dO, Tc, bc, bos, len, H, h, V, v0, (long)(slot0 + n) * H + h);
+        const long cid = (long)(slot0 + n) * H + h;
+        pre.load(q, k, dO, Tc, bc, bos, len, H, h, V, v0, cid);
+        if constexpr (PS) rp.load(Pc + cid * 64 * 64, 64, 64);
+    };
+    auto stage = [&](ScanDhBuf<K, PS>& bf) {
+        pre.stage(bf);
+        if constexpr (PS) rp.store_rows(bf.P, LD64);
     };
     if (nch > 0) {
         prefetch(nch - 1);
-        pre.stage(sm.buf[(nch - 1) & 1]);
+        stage(sm.buf[(nch - 1) & 1]);
         if (nch > 1) prefetch(nch - 2);
     }
     for (int n = nch - 1; n >= 0; --n) {
-        const ScanDhBuf<K>& cb = sm.buf[n & 1];
+        const ScanDhBuf<K, PS>& cb = sm.buf[n & 1];
+        const bf16* Pm = PS ? cb.P : sm.P;
         __syncthreads();  // chunk n staged; everyone is done with chunk n + 1
-        for (int nt = w; nt < 10; nt += 4) {
-            int I, J;
-            lower_tile(nt, I, J);
-            floatx4 acc = zero4();
+        if constexpr (!PS) {
+            for (int nt = w; nt < 10; nt += 4) {
+                int I, J;
+                lower_tile(nt, I, J);
+                floatx4 acc = zero4();
 #pragma unroll
-            for (int k0 = 0; k0 < K; k0 += 32)
-                acc = mma(frag_nat(cb.Kr, LDK, 16 * J, k0), frag_nat(cb.Q, LDK, 16 * I, k0), acc);
-            const int tq = 16 * I + r, tk = 16 * J + 4 * g;
-            *reinterpret_cast<bf16x4*>(sm.P + tq * LD64 + tk) =
-                bf16x4{(bf16)(tk + 0 <= tq ? acc[0] : 0.f), (bf16)(tk + 1 <= tq ? acc[1] : 0.f),
-                       (bf16)(tk + 2 <= tq ? acc[2] : 0.f), (bf16)(tk + 3 <= tq ? acc[3] : 0.f)};
+                for (int k0 = 0; k0 < K; k0 += 32)
+                    acc = mma(frag_nat(cb.Kr, LDK, 16 * J, k0), frag_nat(cb.Q, LDK, 16 * I, k0), acc);
+                const int tq = 16 * I + r, tk = 16 * J + 4 * g;
+                *reinterpret_cast<bf16x4*>(sm.P + tq * LD64 + tk) =
+                    bf16x4{(bf16)(tk + 0 <= tq ? acc[0] : 0.f), (bf16)(tk + 1 <= tq ? acc[1] : 0.f),
+                           (bf16)(tk + 2 <= tq ? acc[2] : 0.f), (bf16)(tk + 3 <= tq ? acc[3] : 0.f)};
+            }
         }
         bf16x8 sb[K / 32];
 #pragma unroll
@@ -222,15 +237,15 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
             dvn[tb] = acc;
         }
         if (n > 0) {
-            pre.stage(sm.buf[(n - 1) & 1]);
+            stage(sm.buf[(n - 1) & 1]);
             if (n > 1) prefetch(n - 2);
         }
-        __syncthreads();  // P complete
+        if constexpr (!PS) __syncthreads();  // P complete
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
             const int c0 = 32 * (tb >> 1) + 4 * (tb & 1);
-            if (tb < 2) dvn[tb] = mma(frag_tr(sm.P, LD64, 0, c0, 8), do0, dvn[tb]);
-            dvn[tb] = mma(frag_tr(sm.P, LD64, 32, c0, 8), do1, dvn[tb]);
+            if (tb < 2) dvn[tb] = mma(frag_tr(Pm, LD64, 0, c0, 8), do0, dvn[tb]);
+            dvn[tb] = mma(frag_tr(Pm, LD64, 32, c0, 8), do1, dvn[tb]);
         }
         // Z = D T^T dVn (k = t'' >= t)
         const bf16x8 dv0 = frag_from_c(dvn[0], dvn[1]), dv1 = frag_from_c(dvn[2], dvn[3]);
@@ -303,11 +318,11 @@ constexpr int NT8 = 512;  // grad_kernel: 8 waves
 // every transposed tile it computes); hf = wave >> 2 picks half of the value
 // tiles (slice phase), of the key tiles (dq / dk) and of the 16-token blocks
 // of the 64 x 64 chunk matrices.
-template <int K, int V>
+template <int K, int V, bool PS>
 __global__ void __launch_bounds__(NT8) grad_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ beta, const bf16* __restrict__ dO, const bf16* __restrict__ Tws,
-    const bf16* __restrict__ hist, const bf16* __restrict__ dhist, SeqInfo si, int H,
+    const bf16* __restrict__ Pws, const bf16* __restrict__ hist, const bf16* __restrict__ dhist, SeqInfo si, int H,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
     bf16* __restrict__ dbeta) {
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 32;  // NF key tiles per half
@@ -332,44 +347,52 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         rh.load(hist + chb + (long)vv * K, K, 64);
         rdh.load(dhist + chb + (long)vv * K, K, 64);
     };
+    // beta of token threadIdx.x, loaded with the other chunk inputs
+    const float bet = (threadIdx.x < 64 && (int)threadIdx.x < len)
+                          ? (float)beta[(bos + threadIdx.x) * H + h] : 0.f;
     // ---- chunk setup: q, k, T, b, P ----
     {
         mf::TileRegs<64, K, NT8> rq, rk;
-        mf::TileRegs<64, 64, NT8> rt;
+        mf::TileRegs<64, 64, NT8> rt, rp;
         rq.load(q + (bos * H + h) * K, (long)H * K, len);
         rk.load(k + (bos * H + h) * K, (long)H * K, len);
         rt.load(Tws + ((long)slot * H + h) * 64 * 64, 64, 64);
+        if constexpr (PS) rp.load(Pws + ((long)slot * H + h) * 64 * 64, 64, 64);
         prefetch(0);
         rq.store_rows(sm.Qs, LDK);
         rk.store_rows(sm.Ks, LDK);
         rt.store_rows(sm.Tb, LD64);
+        if constexpr (PS) rp.store_rows(sm.Ps, LD64);
 #pragma unroll
         for (int j = 0; j < rk.TPT; ++j) {
             const float s = rk.row_sumsq(j);
             if (rk.fg() == 0) sm.lam[rk.t0() + j] = s;
         }
-        for (int i = threadIdx.x; i < 64 * LD64; i += NT8) sm.Ps[i] = (bf16)0.f;
+        if constexpr (!PS)
+            for (int i = threadIdx.x; i < 64 * LD64; i += NT8) sm.Ps[i] = (bf16)0.f;
     }
     __syncthreads();
     if (threadIdx.x < 64) {
         const int tt = threadIdx.x;
         float c = 0.f, dcl = 0.f, dcb = 0.f;
-        if (tt < len) efla_coeff(sm.lam[tt], (float)beta[(bos + tt) * H + h], c, dcl, dcb);
+        if (tt < len) efla_coeff(sm.lam[tt], bet, c, dcl, dcb);
         sm.b[tt] = c;
         sm.dcl[tt] = dcl;
         sm.dcb[tt] = dcb;
     }
-    for (int n = w8; n < 10; n += 8) {
-        int I, J;
-        lower_tile(n, I, J);
-        floatx4 accp = zero4();
+    if constexpr (!PS) {
+        for (int n = w8; n < 10; n += 8) {
+            int I, J;
+            lower_tile(n, I, J);
+            floatx4 accp = zero4();
 #pragma unroll
-        for (int k0 = 0; k0 < K; k0 += 32)
-            accp = mma(frag_nat(sm.Ks, LDK, 16 * J, k0), frag_nat(sm.Qs, LDK, 16 * I, k0), accp);
-        const int tq = 16 * I + r, tk = 16 * J + 4 * g;
-        *reinterpret_cast<bf16x4*>(sm.Ps + tq * LD64 + tk) =
-            bf16x4{(bf16)(tk + 0 <= tq ? accp[0] : 0.f), (bf16)(tk + 1 <= tq ? accp[1] : 0.f),
-                   (bf16)(tk + 2 <= tq ? accp[2] : 0.f), (bf16)(tk + 3 <= tq ? accp[3] : 0.f)};
+            for (int k0 = 0; k0 < K; k0 += 32)
+                accp = mma(frag_nat(sm.Ks, LDK, 16 * J, k0), frag_nat(sm.Qs, LDK, 16 * I, k0), accp);
+            const int tq = 16 * I + r, tk = 16 * J + 4 * g;
+            *reinterpret_cast<bf16x4*>(sm.Ps + tq * LD64 + tk) =
+                bf16x4{(bf16)(tk + 0 <= tq ? accp[0] : 0.f), (bf16)(tk + 1 <= tq ? accp[1] : 0.f),
+                       (bf16)(tk + 2 <= tq ? accp[2] : 0.f), (bf16)(tk + 3 <= tq ? accp[3] : 0.f)};
+        }
     }
     // B operand (line t, k = t') of T
     const bf16x8 tfr0 = frag_nat(sm.Tb, LD64, 16 * tb, 0), tfr1 = frag_nat(sm.Tb, LD64, 16 * tb, 32);

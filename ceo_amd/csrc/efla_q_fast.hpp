@@ -97,6 +97,9 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
     if (!locate_chunk(si, slot, bos, len)) return;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
     const long cid = (long)slot * H + h;
+    // beta of token threadIdx.x, loaded with k so its latency is not paid twice
+    const float bet = (threadIdx.x < 64 && (int)threadIdx.x < len)
+                          ? (float)beta[(bos + threadIdx.x) * H + h] : 0.f;
     {
         mf::TileRegs<64, K, NT> kt;
         kt.load(k + (bos * H + h) * K, (long)H * K, len);
@@ -111,7 +114,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
     if (threadIdx.x < 64) {
         const int t = threadIdx.x;
         float c = 0.f, dcl, dcb;
-        if (t < len) efla_coeff(sm.lam[t], (float)beta[(bos + t) * H + h], c, dcl, dcb);
+        if (t < len) efla_coeff(sm.lam[t], bet, c, dcl, dcb);
         sm.b[t] = c;
         bout[cid * 64 + t] = c;
     }
@@ -277,7 +280,8 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
                                                     int H, const float* __restrict__ S0,
                                                     float* __restrict__ ST,
                                                     bf16* __restrict__ o,
-                                                    bf16* __restrict__ hist) {
+                                                    bf16* __restrict__ hist,
+                                                    bf16* __restrict__ pout) {
     constexpr int LDK = ldb<K>(), LDP = ldb<64>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanSmem<K> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
@@ -343,6 +347,14 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
             if (n + 2 < nch) prefetch(n + 2);
         }
         __syncthreads();  // P complete
+        if (pout && vsl == 0) {
+            // hand P to the backward: [t][t'] bf16, zero above the diagonal
+            const int tr = threadIdx.x >> 2, c0 = 16 * (threadIdx.x & 3);
+            bf16* dst = pout + ((long)(slot0 + n) * H + h) * 64 * 64 + tr * 64 + c0;
+            *reinterpret_cast<bf16x8*>(dst) = *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + c0);
+            *reinterpret_cast<bf16x8*>(dst + 8) =
+                *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + c0 + 8);
+        }
         const bf16x8 vb0 = frag_from_c(vn[0], vn[1]), vb1 = frag_from_c(vn[2], vn[3]);
         // o^T = S^T Q^T + Vn^T P^T: tile tb holds (value 16w + 4g + i, token 16tb + r)
         bf16* orow = o + (bos * H + h) * V + v0 + 16 * w + 4 * g;

@@ -123,9 +123,10 @@ def chunk_efla_fwd(q, k, v, beta, initial_state=None, output_final_state=False,
                    cu_seqlens=None, workspace=None, save_states=False):
     """Returns (o, final_state or None).
 
-    With ``save_states`` the chunk start states are also written into
-    ``workspace`` (which must then be a backward-sized one, ``new_workspace``),
-    for a backward call with ``reuse_states``."""
+    With ``save_states`` the chunk start states (and, for bf16, each chunk's
+    P = tril(Q K^T)) are also written into ``workspace`` (which must then be a
+    backward-sized one, ``new_workspace``), for a backward call with
+    ``reuse_states``."""
     if save_states and workspace is None:
         raise ValueError("save_states needs a caller workspace")
     B, T, H, K, V, N, dt = _q_shapes(q, k, v, beta, cu_seqlens)
@@ -157,7 +158,7 @@ def chunk_efla_bwd(q, k, v, beta, do, initial_state=None, dht=None, cu_seqlens=N
     the same inputs used (untouched since): the per-chunk WY factors are taken
     from it instead of being recomputed.  ``reuse_states`` (with
     ``reuse_forward``, after a forward with ``save_states``) takes the chunk
-    states from it too."""
+    states and P from it too."""
     if (reuse_forward or reuse_states) and workspace is None:
         raise ValueError("reuse_forward / reuse_states need the forward's workspace")
     if reuse_states and not reuse_forward:

@@ -98,9 +98,10 @@ size_t efla_chunk_fwd_workspace_size(size_t batch_size, size_t seq_len, size_t n
                                      int dtype);
 
 /* flags of efla_chunk_fwd_hip */
-/* Also write each chunk's start state into the caller-owned `workspace`, where
- * a backward call with EFLA_BWD_REUSE_STATES reads it instead of recomputing
- * the state scan.  Requires a non-NULL workspace of at least
+/* Also write each chunk's start state (bf16) and, on the bf16 path, its
+ * P = tril(Q K^T) (bf16) into the caller-owned `workspace`, where a backward
+ * call with EFLA_BWD_REUSE_STATES reads them instead of recomputing the state
+ * scan and the P tiles.  Requires a non-NULL workspace of at least
  * efla_chunk_bwd_workspace_size() bytes (the one the backward will get). */
 #define EFLA_FWD_SAVE_STATES 1u
 
@@ -126,9 +127,9 @@ size_t efla_chunk_bwd_workspace_size(size_t batch_size, size_t seq_len, size_t n
  * the forward. */
 #define EFLA_BWD_REUSE_FORWARD 1u
 /* With EFLA_BWD_REUSE_FORWARD only: the forward also ran with
- * EFLA_FWD_SAVE_STATES on this workspace, so the chunk states are read from it
- * too and the backward runs no forward recompute at all (bf16; the fp32 path
- * accepts the flag and recomputes the states). */
+ * EFLA_FWD_SAVE_STATES on this workspace, so the chunk states and P are read
+ * from it too and the backward runs no forward recompute at all (bf16; the
+ * fp32 path accepts the flag and recomputes the states). */
 #define EFLA_BWD_REUSE_STATES 2u
 
 /* Gradients of sum(output * grad_output) + sum(final_state * grad_final_state);
