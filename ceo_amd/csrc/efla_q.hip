@@ -968,14 +968,16 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
                         (const bf16*)w.Pc, si, H, dST, dS0, w.dh);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true>), dim3(H, p.slots),
                         dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc,
-                        (const bf16*)w.Pc, w.h, w.dh, si, H, dq, dk, dv, dbeta);
+                        (const float*)w.bc, (const bf16*)w.Pc, w.h, w.dh, si, H, dq, dk, dv,
+                        dbeta);
         } else {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, false>), scan_grid,
                         dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)nullptr, si, H, dST, dS0, w.dh);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false>), dim3(H, p.slots),
                         dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc,
-                        (const bf16*)nullptr, w.h, w.dh, si, H, dq, dk, dv, dbeta);
+                        (const float*)w.bc, (const bf16*)nullptr, w.h, w.dh, si, H, dq, dk, dv,
+                        dbeta);
         }
         return (int)hipPeekAtLastError();
     } else if (!reuse) {

@@ -322,7 +322,7 @@ template <int K, int V, bool PS>
 __global__ void __launch_bounds__(NT8) grad_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ beta, const bf16* __restrict__ dO, const bf16* __restrict__ Tws,
-    const bf16* __restrict__ Pws, const bf16* __restrict__ hist, const bf16* __restrict__ dhist, SeqInfo si, int H,
+    const float* __restrict__ bws, const bf16* __restrict__ Pws, const bf16* __restrict__ hist, const bf16* __restrict__ dhist, SeqInfo si, int H,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
     bf16* __restrict__ dbeta) {
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 32;  // NF key tiles per half
@@ -348,8 +348,12 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         rdh.load(dhist + chb + (long)vv * K, K, 64);
     };
     // beta of token threadIdx.x, loaded with the other chunk inputs
-    const float bet = (threadIdx.x < 64 && (int)threadIdx.x < len)
-                          ? (float)beta[(bos + threadIdx.x) * H + h] : 0.f;
+    // beta and the prep's b of token threadIdx.x, loaded with the other chunk
+    // inputs (b is taken as the forward used it; lambda here only feeds the
+    // derivatives of c)
+    const bool bthr = threadIdx.x < 64 && (int)threadIdx.x < len;
+    const float bet = bthr ? (float)beta[(bos + threadIdx.x) * H + h] : 0.f;
+    const float bpre = bthr ? bws[((long)slot * H + h) * 64 + threadIdx.x] : 0.f;
     // ---- chunk setup: q, k, T, b, P ----
     {
         mf::TileRegs<64, K, NT8> rq, rk;
@@ -376,7 +380,7 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         const int tt = threadIdx.x;
         float c = 0.f, dcl = 0.f, dcb = 0.f;
         if (tt < len) efla_coeff(sm.lam[tt], bet, c, dcl, dcb);
-        sm.b[tt] = c;
+        sm.b[tt] = tt < len ? bpre : 0.f;
         sm.dcl[tt] = dcl;
         sm.dcb[tt] = dcb;
     }

@@ -34,8 +34,7 @@ using mf::mma;
 using mf::mma_f32;
 using mf::zero4;
 
-constexpr int NT = 256;      // 4 waves
-constexpr int LDF = 64 + 8;  // 64 x 64 fp32 matrices
+constexpr int NT = 256;  // 4 waves
 
 // lower-triangular 16x16 tile (I >= J) number -> (I, J)
 __device__ __forceinline__ void lower_tile(int n, int& I, int& J) {
@@ -73,13 +72,28 @@ __device__ __forceinline__ void store_state_frag(bf16* __restrict__ hist, const 
 // ---------------------------------------------------------------------------
 // prep
 // ---------------------------------------------------------------------------
+// G = K K^T and T = (I + strict_lower(D G))^{-1} are kept as their ten lower
+// 16x16 tiles, packed, fp32 (row stride 17 for G, 20 for T), T in the space k
+// occupies until G is formed: 29 KB of LDS, so five workgroups fit on a CU
+// (the kernel is a chain of short dependent phases and runs as fast as it has
+// workgroups in flight).
+constexpr int PT_LD = 17;  // G tiles
+constexpr int PT_SZ = 16 * PT_LD;
+constexpr int PTT_LD = 20;  // T tiles: 16-byte aligned rows for the bf16 write-out
+constexpr int PTT_SZ = 16 * PTT_LD;
+
+// packed offset of lower tile (I, J), I >= J, for tiles of `sz` floats
+__device__ __forceinline__ int ptile(int I, int J, int sz = PT_SZ) {
+    return (I * (I + 1) / 2 + J) * sz;
+}
+
 template <int K>
 struct PrepSmem {
     union {
         bf16 Kr[64 * ldb<K>()];  // k, until K K^T is formed
-        float T[64 * LDF];       // (I + A)^{-1}
+        float T[10 * PTT_SZ];    // lower tiles of (I + A)^{-1}
     } u;
-    float G[64 * LDF];  // K K^T (lower tiles)
+    float G[10 * PT_SZ];  // lower tiles of K K^T
     float lam[64];
     float b[64];
 };
@@ -126,24 +140,26 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
 #pragma unroll
         for (int k0 = 0; k0 < K; k0 += 32)
             acc = mma(frag_nat(sm.u.Kr, LDK, 16 * I, k0), frag_nat(sm.u.Kr, LDK, 16 * J, k0), acc);
+        float* Gt = sm.G + ptile(I, J);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm.G[(16 * I + 4 * g + i) * LDF + 16 * J + r] = acc[i];
+        for (int i = 0; i < 4; ++i) Gt[(4 * g + i) * PT_LD + r] = acc[i];
     }
     __syncthreads();  // k is dead from here; T takes its place
-    float* T = sm.u.T;
     // diagonal 16x16 blocks of T by forward substitution (lane = column)
     if (l < 16) {
         const int base = 16 * w;
+        const float* Gd = sm.G + ptile(w, w);
         float x[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             float s = 0.f;
 #pragma unroll
-            for (int j = 0; j < i; ++j) s += sm.G[(base + i) * LDF + base + j] * x[j];
+            for (int j = 0; j < i; ++j) s += Gd[i * PT_LD + j] * x[j];
             x[i] = (i == l ? 1.f : 0.f) - sm.b[base + i] * s;
         }
+        float* Td = sm.u.T + ptile(w, w, PTT_SZ);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) T[(base + i) * LDF + base + l] = x[i];
+        for (int i = 0; i < 16; ++i) Td[i * PTT_LD + l] = x[i];
     }
     __syncthreads();
     // off-diagonal blocks by distance d: T_IJ = -T_II sum_{m=J}^{I-1} A_Im T_mJ
@@ -152,26 +168,45 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
             const int I = w + d, J = w;
             const float bi = sm.b[16 * I + r];
             floatx4 y = zero4();
-            for (int m = 16 * J; m < 16 * I; m += 4)
-                y = mma_f32(bi * sm.G[(16 * I + r) * LDF + m + g], T[(m + g) * LDF + 16 * J + r], y);
+            for (int m = 16 * J; m < 16 * I; m += 4) {
+                const int mb = m >> 4, mo = (m & 15) + g;
+                y = mma_f32(bi * sm.G[ptile(I, mb) + r * PT_LD + mo],
+                            sm.u.T[ptile(mb, J, PTT_SZ) + mo * PTT_LD + r], y);
+            }
+            const float* Tii = sm.u.T + ptile(I, I, PTT_SZ) + r * PTT_LD + 4 * g;
             floatx4 t = zero4();
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t = mma_f32(T[(16 * I + r) * LDF + 16 * I + 4 * g + i], y[i], t);
+            for (int i = 0; i < 4; ++i) t = mma_f32(Tii[i], y[i], t);
+            float* Tij = sm.u.T + ptile(I, J, PTT_SZ);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) T[(16 * I + 4 * g + i) * LDF + 16 * J + r] = -t[i];
+            for (int i = 0; i < 4; ++i) Tij[(4 * g + i) * PTT_LD + r] = -t[i];
         }
         __syncthreads();
     }
-    // bf16 T [t][t'], zero above the diagonal
+    // bf16 T [t][t'], zero above the diagonal: thread -> row tr, column tile J
     {
-        const int tr = threadIdx.x >> 2, c0 = 16 * (threadIdx.x & 3);
+        const int tr = threadIdx.x >> 2, J = threadIdx.x & 3, I = tr >> 4, i = tr & 15;
         bf16x8 lo, hi;
+        if (J <= I) {
+            const floatx4* src =
+                reinterpret_cast<const floatx4*>(sm.u.T + ptile(I, J, PTT_SZ) + i * PTT_LD);
+            float v[16];
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            lo[c] = (bf16)(c0 + c <= tr ? T[tr * LDF + c0 + c] : 0.f);
-            hi[c] = (bf16)(c0 + 8 + c <= tr ? T[tr * LDF + c0 + 8 + c] : 0.f);
+            for (int q4 = 0; q4 < 4; ++q4) {
+                const floatx4 f = src[q4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[4 * q4 + e] = f[e];
+            }
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                lo[c] = (bf16)(J < I || c <= i ? v[c] : 0.f);
+                hi[c] = (bf16)(J < I || 8 + c <= i ? v[8 + c] : 0.f);
+            }
+        } else {
+#pragma unroll
+            for (int c = 0; c < 8; ++c) lo[c] = hi[c] = (bf16)0.f;
         }
-        bf16* dst = Tout + cid * 64 * 64 + tr * 64 + c0;
+        bf16* dst = Tout + cid * 64 * 64 + tr * 64 + 16 * J;
         *reinterpret_cast<bf16x8*>(dst) = lo;
         *reinterpret_cast<bf16x8*>(dst + 8) = hi;
     }
