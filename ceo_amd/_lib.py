@@ -84,6 +84,7 @@ _SIGS = {
     "layernorm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, f32, vp]),
     "layernorm_forward_stats_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     "layernorm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
+    "layernorm_backward_residual_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
     "rmsnorm_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
     "rmsnorm_backward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     "shortconv_forward_hip": (i32, [vp, vp, vp, sz, sz, sz, sz, vp]),
@@ -94,6 +95,8 @@ _SIGS = {
     "gemm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, sz, i32, i32, i32, vp]),
     "gemm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),
     # GELU, AdamW
+    "gemm_ex_hip": (i32, [i32, i32, sz, sz, sz, f32, vp, sz, vp, sz, vp, f32, vp, sz, vp, sz,
+                          i32, vp]),
     "gelu_forward_hip": (i32, [vp, vp, sz, ctypes.c_bool, vp]),
     "gelu_backward_hip": (i32, [vp, vp, vp, sz, ctypes.c_bool, vp]),
     "adamw_step_hip": (i32, [vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, sz, vp]),

@@ -341,12 +341,12 @@ struct LtDevice {
     bool broken = false;  // creation failed: always use the native kernel
 };
 
-// (opA, opB, M, N, K, lda, ldb, ldd, dtype, has_bias)
-typedef std::tuple<int, int, long, long, long, long, long, long, int, int> LtKey;
+// (opA, opB, M, N, K, lda, ldb, ldd, dtype, has_bias, ldc or 0 without C)
+typedef std::tuple<int, int, long, long, long, long, long, long, int, int, long> LtKey;
 
 struct LtPlan {
     hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, d = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr, d = nullptr;
     hipblasLtMatmulAlgo_t algo;
     size_t ws_bytes = 0;
     bool ok = false;  // false: hipBLASLt offers no algorithm for this problem
@@ -390,6 +390,7 @@ static bool lt_plan(LtDevice* d, const LtKey& k, LtPlan* p) {
     const long lda = std::get<5>(k), ldb = std::get<6>(k), ldd = std::get<7>(k);
     const hipDataType t = lt_type(std::get<8>(k));
     const bool bias = std::get<9>(k) != 0;
+    const long ldc = std::get<10>(k);
     if (hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) !=
         HIPBLAS_STATUS_SUCCESS)
         return false;
@@ -410,6 +411,10 @@ static bool lt_plan(LtDevice* d, const LtKey& k, LtPlan* p) {
         hipblasLtMatrixLayoutCreate(&p->b, t, br, bc, ldb) != HIPBLAS_STATUS_SUCCESS ||
         hipblasLtMatrixLayoutCreate(&p->d, t, M, N, ldd) != HIPBLAS_STATUS_SUCCESS)
         return false;
+    p->c = p->d;
+    if (ldc != 0 && ldc != ldd &&
+        hipblasLtMatrixLayoutCreate(&p->c, t, M, N, ldc) != HIPBLAS_STATUS_SUCCESS)
+        return false;
     hipblasLtMatmulPreference_t pref;
     if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
     uint64_t wsb = kLtWorkspace;
@@ -418,7 +423,7 @@ static bool lt_plan(LtDevice* d, const LtKey& k, LtPlan* p) {
     hipblasLtMatmulHeuristicResult_t res[8];
     int n = 0;
     const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(d->handle, p->desc, p->a, p->b,
-                                                               p->d, p->d, pref, 8, res, &n);
+                                                               p->c, p->d, pref, 8, res, &n);
     hipblasLtMatmulPreferenceDestroy(pref);
     if (st != HIPBLAS_STATUS_SUCCESS) return false;
     for (int i = 0; i < n; ++i) {  // best-ranked first
@@ -431,19 +436,26 @@ static bool lt_plan(LtDevice* d, const LtKey& k, LtPlan* p) {
     return false;
 }
 
-// Column-major D[M x N] = op(A) op(B) (+ bias[M] per row), all of dtype dt,
-// fp32 accumulation.  Returns kSuccess, a launch error, or -1 when hipBLASLt
-// cannot take the problem (the caller then runs the native kernel).
+// Column-major D[M x N] = alpha op(A) op(B) (+ bias[M] per row) (+ beta C),
+// all of dtype dt, fp32 accumulation; C (leading dimension ldc) is read only
+// when beta != 0 and may be D itself.  Returns kSuccess, a launch error, or -1
+// when hipBLASLt cannot take the problem (the caller then runs the native
+// kernel, or reports it).
 static int lt_matmul(hipblasOperation_t ta, hipblasOperation_t tb, long M, long N, long K,
                      const void* A, long lda, const void* B, long ldb, void* D, long ldd,
-                     const void* bias, int dt, hipStream_t stream) {
+                     const void* bias, int dt, hipStream_t stream, float alpha = 1.f,
+                     float beta = 0.f, const void* C = nullptr, long ldc = 0) {
     std::lock_guard<std::mutex> lk(g_lt_mu);
     if (g_backend != 0) return -1;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return -1;
     LtDevice* d = lt_device(dev);
     if (!d) return -1;
-    const LtKey key(ta, tb, M, N, K, lda, ldb, ldd, dt, bias ? 1 : 0);
+    if (beta == 0.f) {
+        C = nullptr;
+        ldc = 0;
+    }
+    const LtKey key(ta, tb, M, N, K, lda, ldb, ldd, dt, bias ? 1 : 0, C ? ldc : 0);
     auto it = g_lt_plans.find({dev, key});
     if (it == g_lt_plans.end()) {
         LtPlan p;
@@ -455,10 +467,10 @@ static int lt_matmul(hipblasOperation_t ta, hipblasOperation_t tb, long M, long 
     if (bias)
         hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias,
                                         sizeof(bias));
-    const float one = 1.f, zero = 0.f;
     ::efla::ProfScope ps("gemm_hipblaslt", stream);
-    const hipblasStatus_t st = hipblasLtMatmul(d->handle, p.desc, &one, A, p.a, B, p.b, &zero, D,
-                                               p.d, D, p.d, &p.algo, d->ws, p.ws_bytes, stream);
+    const hipblasStatus_t st =
+        hipblasLtMatmul(d->handle, p.desc, &alpha, A, p.a, B, p.b, &beta, C ? C : D, p.c, D, p.d,
+                        &p.algo, d->ws, p.ws_bytes, stream);
     if (st != HIPBLAS_STATUS_SUCCESS) return kInvalidValue;
     return (int)hipPeekAtLastError();
 }
@@ -583,4 +595,29 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
         }
     }
     return (int)hipPeekAtLastError();
+}
+
+extern "C" int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t k, float alpha,
+                           const void* a, size_t lda, const void* b, size_t ldb,
+                           const void* bias, float beta, const void* c, size_t ldc, void* d,
+                           size_t ldd, int dtype, hipStream_t stream) {
+    if ((trans_a != 0 && trans_a != 1) || (trans_b != 0 && trans_b != 1) || !dsize(dtype))
+        return kInvalidValue;
+    if (m == 0 || n == 0) return kSuccess;
+    if (!d || (k > 0 && (!a || !b)) || (beta != 0.f && !c)) return kInvalidValue;
+    const size_t lim = (size_t)1 << 40;
+    if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim || ldd > lim)
+        return kInvalidValue;
+    // row strides: op(A) is m x k (A stored m x k, or k x m when transposed), etc.
+    if (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n) || ldd < n ||
+        (beta != 0.f && ldc < n))
+        return kInvalidValue;
+    if (k == 0) return kNotSupported;
+    // row-major D = op(A) op(B) as column-major D^T = op(B)^T op(A)^T: a row-major
+    // matrix is its own transpose read column-major with the same leading dimension
+    const int rc = lt_matmul(trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N,
+                             trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N, (long)n, (long)m, (long)k, b,
+                             (long)ldb, a, (long)lda, d, (long)ldd, bias, dtype, stream, alpha,
+                             beta, c, (long)ldc);
+    return rc < 0 ? kNotSupported : rc;
 }

@@ -15,6 +15,7 @@ constexpr int kSuccess = hipSuccess;
 constexpr int kInvalidValue = hipErrorInvalidValue;
 constexpr int kOutOfMemory = hipErrorOutOfMemory;
 constexpr int kInvalidConfiguration = hipErrorInvalidConfiguration;
+constexpr int kNotSupported = hipErrorNotSupported;
 
 // dtype codes shared with hipDataType (library_types.h): HIP_R_32F = 0,
 // HIP_R_16F = 2, HIP_R_16BF = 14 -- numerically the reference's cudaDataType codes.

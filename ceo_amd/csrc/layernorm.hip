@@ -129,6 +129,7 @@ __global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
                                                   const bf16* __restrict__ w,
                                                   const float* __restrict__ mean,
                                                   const float* __restrict__ rstd,
+                                                  const bf16* __restrict__ res,
                                                   bf16* __restrict__ dx,
                                                   float* __restrict__ part, long rows, int D,
                                                   int want_params) {
@@ -156,7 +157,8 @@ __global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
             const float xh = ((float)xr[c] - mu) * rs;
             const float gy = (float)gr[c];
             const float g = gy * (float)w[c];
-            dxr[c] = (bf16)(rs * (g - sg - xh * sgx));
+            const float add = res ? (float)res[row * D + c] : 0.f;
+            dxr[c] = (bf16)(rs * (g - sg - xh * sgx) + add);
             if (want_params) {
                 atomicAdd(&acc[c], gy * xh);
                 atomicAdd(&acc[D + c], gy);
@@ -177,6 +179,7 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
                                                       const bf16* __restrict__ w,
                                                       const float* __restrict__ mean,
                                                       const float* __restrict__ rstd,
+                                                      const bf16* __restrict__ res,
                                                       bf16* __restrict__ dx,
                                                       float* __restrict__ part, long rows,
                                                       int want_params) {
@@ -195,22 +198,24 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
     }
     const long waves = (long)gridDim.x * (NTH / kWave);
     long row = (long)blockIdx.x * (NTH / kWave) + wv;
-    // the next row's x, dy are loaded while this one computes
-    bf16x8 xn[NV], gn[NV];
+    // the next row's x, dy (and the residual gradient) are loaded while this one computes
+    bf16x8 xn[NV], gn[NV], rn[NV] = {};
     auto fetch = [&](long r) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             xn[j] = *reinterpret_cast<const bf16x8*>(x + r * D + (j * 64 + lane) * 8);
             gn[j] = *reinterpret_cast<const bf16x8*>(dy + r * D + (j * 64 + lane) * 8);
+            if (res) rn[j] = *reinterpret_cast<const bf16x8*>(res + r * D + (j * 64 + lane) * 8);
         }
     };
     if (row < rows) fetch(row);
     for (; row < rows; row += waves) {
-        bf16x8 xv[NV], gv[NV];
+        bf16x8 xv[NV], gv[NV], rv[NV];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             xv[j] = xn[j];
             gv[j] = gn[j];
+            rv[j] = rn[j];
         }
         if (row + waves < rows) fetch(row + waves);
         const float mu = mean[row], rs = rstd[row];
@@ -232,7 +237,8 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
             for (int i = 0; i < 8; ++i) {
                 const float xh = ((float)xv[j][i] - mu) * rs;
                 const float gy = (float)gv[j][i];
-                o[i] = (bf16)(rs * (gy * wf[j][i] - sg - xh * sgx));
+                const float add = res ? (float)rv[j][i] : 0.f;
+                o[i] = (bf16)(rs * (gy * wf[j][i] - sg - xh * sgx) + add);
                 dwa[j][i] += gy * xh;
                 dba[j][i] += gy;
             }
@@ -354,11 +360,10 @@ extern "C" int layernorm_forward_stats_hip(const void* input, const void* weight
                        stream);
 }
 
-extern "C" int layernorm_backward_hip(const void* grad_output, const void* input,
-                                      const void* weight, const float* mean, const float* rstd,
-                                      void* grad_input, float* grad_weight, float* grad_bias,
-                                      size_t numel, size_t normalized_shape,
-                                      hipStream_t stream) {
+static int ln_backward(const void* grad_output, const void* input, const void* weight,
+                       const float* mean, const float* rstd, const void* residual,
+                       void* grad_input, float* grad_weight, float* grad_bias, size_t numel,
+                       size_t normalized_shape, hipStream_t stream) {
     const size_t D = normalized_shape;
     if (D == 0) return kInvalidValue;
     const size_t rows = numel / D;
@@ -371,7 +376,7 @@ extern "C" int layernorm_backward_hip(const void* grad_output, const void* input
     if (!grad_output || !input || !weight || !mean || !rstd || !grad_input) return kInvalidValue;
     if ((params && D > 8192) || rows > ((size_t)1 << 40)) return kInvalidConfiguration;
     const bool aligned = ((uintptr_t)grad_output | (uintptr_t)input | (uintptr_t)weight |
-                          (uintptr_t)grad_input) % 16 == 0;
+                          (uintptr_t)grad_input | (uintptr_t)residual) % 16 == 0;
     const int nv = (aligned && D % 512 == 0 && D <= 2048) ? (int)(D / 512) : 0;
     // two workgroups per CU; each wave then takes several rows, which keeps the
     // per-workgroup dw/db partials (and their reduction) small
@@ -385,21 +390,22 @@ extern "C" int layernorm_backward_hip(const void* grad_output, const void* input
         part = (float*)ws;
     }
     const bf16 *g = (const bf16*)grad_output, *x = (const bf16*)input, *w = (const bf16*)weight;
+    const bf16* res = (const bf16*)residual;
     bf16* dx = (bf16*)grad_input;
     const dim3 grid((unsigned)nblk), block(ln::NTH);
     switch (nv) {
 #define LN_BWD_CASE(n)                                                                        \
     case n:                                                                                   \
         EFLA_LAUNCH("layernorm_bwd", ln::bwd_reg_kernel<n>, grid, block, stream, g, x, w, mean, \
-                    rstd, dx, part, (long)rows, params ? 1 : 0);                              \
+                    rstd, res, dx, part, (long)rows, params ? 1 : 0);                         \
         break;
         LN_BWD_CASE(1) LN_BWD_CASE(2) LN_BWD_CASE(3) LN_BWD_CASE(4)
 #undef LN_BWD_CASE
         default: {
             const size_t smem = params ? 2 * D * sizeof(float) : 0;
             ::efla::ProfScope ps("layernorm_bwd_loop", stream);
-            hipLaunchKernelGGL(ln::bwd_kernel, grid, block, smem, stream, g, x, w, mean, rstd, dx,
-                               part, (long)rows, (int)D, params ? 1 : 0);
+            hipLaunchKernelGGL(ln::bwd_kernel, grid, block, smem, stream, g, x, w, mean, rstd, res,
+                               dx, part, (long)rows, (int)D, params ? 1 : 0);
         }
     }
     EFLA_CHECK(hipPeekAtLastError());
@@ -409,4 +415,24 @@ extern "C" int layernorm_backward_hip(const void* grad_output, const void* input
                     (const float*)part, (int)nblk, (int)D, grad_weight, grad_bias);
     }
     return (int)hipPeekAtLastError();
+}
+
+extern "C" int layernorm_backward_hip(const void* grad_output, const void* input,
+                                      const void* weight, const float* mean, const float* rstd,
+                                      void* grad_input, float* grad_weight, float* grad_bias,
+                                      size_t numel, size_t normalized_shape,
+                                      hipStream_t stream) {
+    return ln_backward(grad_output, input, weight, mean, rstd, nullptr, grad_input, grad_weight,
+                       grad_bias, numel, normalized_shape, stream);
+}
+
+extern "C" int layernorm_backward_residual_hip(const void* grad_output, const void* input,
+                                               const void* weight, const float* mean,
+                                               const float* rstd, const void* residual,
+                                               void* grad_input, float* grad_weight,
+                                               float* grad_bias, size_t numel,
+                                               size_t normalized_shape, hipStream_t stream) {
+    if (!residual && numel / (normalized_shape ? normalized_shape : 1) > 0) return kInvalidValue;
+    return ln_backward(grad_output, input, weight, mean, rstd, residual, grad_input, grad_weight,
+                       grad_bias, numel, normalized_shape, stream);
 }

@@ -144,12 +144,14 @@ class EflaLM:
             beta = torch.sigmoid(p[:, 3 * HD:].float()).to(torch.bfloat16).view(B, T, H)
             o, _ = efla.chunk_efla_fwd(q, k, v, beta, workspace=ws[i], save_states=True)
             o2 = o.view(N, HD)
-            x1 = x + nn.gemm_forward(o2, self.w(L + "w_o"))
+            # x1 = x + o w_o with the residual added by the product's epilogue
+            x1 = nn.gemm_ex(o2, self.w(L + "w_o"), torch.empty_like(x), c=x, beta=1.0)
             a2, m2, r2 = nn.layernorm_forward(x1, self.w(L + "ln2.w"), self.w(L + "ln2.b"),
                                               cfg.ln_eps, save_stats=True)
             u = nn.gemm_forward(a2, self.w(L + "w_up"), self.w(L + "b_up"))
             gl = nn.gelu_forward(u)
-            x2 = x1 + nn.gemm_forward(gl, self.w(L + "w_down"), self.w(L + "b_down"))
+            x2 = nn.gemm_ex(gl, self.w(L + "w_down"), torch.empty_like(x),
+                            bias=self.w(L + "b_down"), c=x1, beta=1.0)
             saved["layers"].append(dict(x=x, a=a, m1=m1, r1=r1, q=q, k=k, v=v, beta=beta,
                                         o=o2, x1=x1, a2=a2, m2=m2, r2=r2, u=u, g=gl))
             x = x2
@@ -189,11 +191,11 @@ class EflaLM:
             du = nn.gelu_backward(dg, s["u"])
             da2, _, _ = nn.gemm_backward(du, s["a2"], self.w(L + "w_up"), need_bias=True,
                                          out_b=self.gr(L + "w_up"), out_bias=self.gr(L + "b_up"))
+            # dx1 = LN2's input gradient + the residual's dx, in one pass
             dx1, dw, db = nn.layernorm_backward(da2, s["x1"], self.w(L + "ln2.w"), s["m2"],
-                                                s["r2"])
+                                                s["r2"], residual=dx)
             self.gr(L + "ln2.w").copy_(dw)
             self.gr(L + "ln2.b").copy_(db)
-            dx1 += dx
             # x1 = x + o w_o, o = EFLA(q, k, v, beta)
             do, _, _ = nn.gemm_backward(dx1, s["o"], self.w(L + "w_o"), out_b=self.gr(L + "w_o"))
             dq, dk, dv, dbeta, _ = efla.chunk_efla_bwd(
@@ -203,10 +205,11 @@ class EflaLM:
             dpb = (dbeta.float() * bf * (1.0 - bf)).to(torch.bfloat16)
             dp = torch.cat([dq.view(N, HD), dk.view(N, HD), dv.view(N, HD), dpb.view(N, H)], 1)
             da, _, _ = nn.gemm_backward(dp, s["a"], self.w(L + "w_in"), out_b=self.gr(L + "w_in"))
-            dxa, dw, db = nn.layernorm_backward(da, s["x"], self.w(L + "ln1.w"), s["m1"], s["r1"])
+            # dx = dx1 + LN1's input gradient
+            dx, dw, db = nn.layernorm_backward(da, s["x"], self.w(L + "ln1.w"), s["m1"], s["r1"],
+                                               residual=dx1)
             self.gr(L + "ln1.w").copy_(dw)
             self.gr(L + "ln1.b").copy_(db)
-            dx = dx1 + dxa
             saved["layers"][i] = None
         self.embed_grad.zero_()
         nn.embedding_backward(dx, saved["tokens"].reshape(-1), self.embed_grad)

@@ -37,8 +37,10 @@ def layernorm_forward(x: torch.Tensor, weight: torch.Tensor, bias=None, eps: flo
     return y
 
 
-def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True):
-    """(dx bf16, dweight fp32 or None, dbias fp32 or None)."""
+def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True,
+                       residual=None):
+    """(dx bf16, dweight fp32 or None, dbias fp32 or None); with ``residual``
+    (bf16, x's shape) dx is LayerNorm's input gradient plus it."""
     D = x.shape[-1]
     for t, n in ((dy, "dy"), (x, "x"), (weight, "weight")):
         _require(t, n, torch.bfloat16, x.device)
@@ -47,9 +49,18 @@ def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True)
     dx = torch.empty_like(x)
     dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
     db = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
-    rc = lib().layernorm_backward_hip(_p(dy), _p(x), _p(weight), _p(mean), _p(rstd), _p(dx),
-                                      _p(dw), _p(db), x.numel(), D, _stream(x))
-    check(rc, "layernorm_backward_hip")
+    if residual is None:
+        rc = lib().layernorm_backward_hip(_p(dy), _p(x), _p(weight), _p(mean), _p(rstd), _p(dx),
+                                          _p(dw), _p(db), x.numel(), D, _stream(x))
+        check(rc, "layernorm_backward_hip")
+    else:
+        _require(residual, "residual", torch.bfloat16, x.device)
+        if residual.shape != x.shape:
+            raise ValueError("residual must have x's shape")
+        rc = lib().layernorm_backward_residual_hip(_p(dy), _p(x), _p(weight), _p(mean),
+                                                   _p(rstd), _p(residual), _p(dx), _p(dw),
+                                                   _p(db), x.numel(), D, _stream(x))
+        check(rc, "layernorm_backward_residual_hip")
     return dx, dw, db
 
 
@@ -104,6 +115,44 @@ def gemm_forward(a: torch.Tensor, b: torch.Tensor, bias=None, out_dtype=None) ->
                                 DTYPE_CODES[b.dtype], DTYPE_CODES[out_dtype], _stream(a))
     check(rc, "gemm_forward_hip")
     return c
+
+
+def _row_stride(t: torch.Tensor, name: str) -> int:
+    """Row stride of a 2-D tensor whose rows are contiguous (a column block of
+    a larger row-major matrix is fine)."""
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be 2-D with contiguous rows")
+    return t.stride(0)
+
+
+def gemm_ex(a, b, out, bias=None, c=None, alpha: float = 1.0, beta: float = 0.0,
+            trans_a: bool = False, trans_b: bool = False) -> torch.Tensor:
+    """out = alpha op(a) op(b) (+ bias) + beta c, row-major 2-D operands whose
+    rows are contiguous (views of column blocks allowed); ``c`` may be ``out``
+    itself.  Writes into ``out`` and returns it."""
+    m, n = out.shape
+    k = a.shape[0] if trans_a else a.shape[1]
+    if (a.shape[1] if trans_a else a.shape[0]) != m:
+        raise ValueError("gemm_ex: op(a) rows differ from out rows")
+    if (b.shape[1] if trans_b else b.shape[0]) != k or \
+            (b.shape[0] if trans_b else b.shape[1]) != n:
+        raise ValueError("gemm_ex: op(b) must be k x n")
+    for t, nme in ((a, "a"), (b, "b"), (out, "out")):
+        if not t.is_cuda or t.dtype != out.dtype:
+            raise ValueError(f"{nme} must be a device tensor of out's dtype")
+    if bias is not None:
+        _require(bias, "bias", out.dtype, out.device)
+    ldc = 0
+    if beta != 0.0:
+        if c is None or c.shape != out.shape or c.dtype != out.dtype:
+            raise ValueError("gemm_ex: beta != 0 needs c of out's shape and dtype")
+        ldc = _row_stride(c, "c")
+    rc = lib().gemm_ex_hip(int(trans_a), int(trans_b), m, n, k, float(alpha), _p(a),
+                           _row_stride(a, "a"), _p(b), _row_stride(b, "b"), _p(bias),
+                           float(beta), _p(c) if beta != 0.0 else None, ldc, _p(out),
+                           _row_stride(out, "out"), DTYPE_CODES[out.dtype], _stream(out))
+    check(rc, "gemm_ex_hip")
+    return out
 
 
 def gemm_backward(dc: torch.Tensor, a: torch.Tensor, b: torch.Tensor, need_a=True, need_b=True,

@@ -183,6 +183,16 @@ int layernorm_backward_hip(const void* grad_output, const void* input, const voi
                            float* grad_weight, float* grad_bias, size_t numel,
                            size_t normalized_shape, hipStream_t stream);
 
+/* No reference counterpart: layernorm_backward_hip with grad_input =
+ * LayerNorm's input gradient + residual (bf16, same shape), the add a
+ * pre-LN residual block does after each LayerNorm backward, fused into the
+ * row pass.  residual NULL (with rows to do) -> 1. */
+int layernorm_backward_residual_hip(const void* grad_output, const void* input,
+                                    const void* weight, const float* mean, const float* rstd,
+                                    const void* residual, void* grad_input, float* grad_weight,
+                                    float* grad_bias, size_t numel, size_t normalized_shape,
+                                    hipStream_t stream);
+
 /* ========================================================================
  * RMSNorm
  * ======================================================================== */
@@ -276,6 +286,21 @@ int gemm_forward_hip(const void* a, const void* b, const void* bias, void* c, si
 int gemm_backward_hip(const void* grad_c, const void* a, const void* b, void* grad_a,
                       void* grad_b, void* grad_bias, size_t m, size_t k, size_t n,
                       hipStream_t stream);
+
+/* No reference counterpart as an entry point (gemm.cu:182-234 keeps its
+ * strided helper gemm_row_major_ex internal): the strided, accumulating
+ * product the training step's projections use,
+ *   D[m x n] = alpha op(A) op(B) (+ bias[n]) + beta C,
+ * row-major with row strides lda, ldb, ldc, ldd; op(A) is A (stored m x k) or,
+ * with trans_a, A^T (A stored k x m); op(B) likewise (k x n or, transposed,
+ * n x k).  One dtype for every operand, fp32 accumulation.  C is read only
+ * when beta != 0 and may be D.  hipBLASLt only: a problem it does not take,
+ * or k == 0, -> 801 (not supported); m or n == 0 -> 0; bad strides or
+ * pointers -> 1. */
+int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t k, float alpha,
+                const void* a, size_t lda, const void* b, size_t ldb, const void* bias,
+                float beta, const void* c, size_t ldc, void* d, size_t ldd, int dtype,
+                hipStream_t stream);
 
 /* ========================================================================
  * GELU and AdamW (the config-4 training step around EFLA)

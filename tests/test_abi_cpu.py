@@ -189,6 +189,20 @@ def test_shortconv_and_prism_validation(L):
     assert L.prism_backward_hip(p, p, p, wp, p, p, gnull, 1, 4, 64, 64, 3, NULL) == 1
 
 
+def test_gemm_ex_and_residual_validation(L):
+    p = ctypes.c_void_p(16)
+    bf = 14
+    # m or n == 0 -> 0; bad transpose flag, short strides, NULL -> 1; k == 0 -> 801
+    assert L.gemm_ex_hip(0, 0, 0, 8, 8, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 0
+    assert L.gemm_ex_hip(2, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 1
+    assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 4, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 1
+    assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 4, bf, NULL) == 1
+    assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 1.0, NULL, 8, p, 8, bf, NULL) == 1
+    assert L.gemm_ex_hip(0, 0, 8, 8, 0, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 801
+    assert L.layernorm_backward_residual_hip(p, p, p, p, p, NULL, p, NULL, NULL, 2048, 1024,
+                                             NULL) == 1
+
+
 def test_gelu_validation(L):
     p = ctypes.c_void_p(16)
     # numel == 0: the reference launches an empty grid -> InvalidConfiguration

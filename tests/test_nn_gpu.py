@@ -138,6 +138,67 @@ def test_rmsnorm_backward_accumulates_and_misaligned(oracle):
     assert rel_l2(dws, dwa.cpu().numpy()) <= 1e-5
 
 
+@pytest.mark.parametrize("trans_a,trans_b", [(False, False), (True, False), (False, True),
+                                             (True, True)])
+def test_gemm_ex_strided_accumulating(trans_a, trans_b):
+    """gemm_ex on column-block views with bias and beta accumulation, against
+    an fp32 torch product of the same bf16 values."""
+    from ceo_amd.nn import gemm_ex
+
+    announce(f"gemm_ex trans_a={trans_a} trans_b={trans_b}")
+    g = torch.Generator().manual_seed(3 + 2 * trans_a + trans_b)
+    m, n, k = 192, 160, 96
+    # operands as column blocks of wider matrices
+    a_full = torch.randn(k if trans_a else m, (m if trans_a else k) + 40, generator=g)
+    b_full = torch.randn(n if trans_b else k, (k if trans_b else n) + 24, generator=g)
+    a = a_full.to(torch.bfloat16).cuda()[:, 8:8 + (m if trans_a else k)]
+    b = b_full.to(torch.bfloat16).cuda()[:, 16:16 + (k if trans_b else n)]
+    bias = (0.1 * torch.randn(n, generator=g)).to(torch.bfloat16).cuda()
+    c = torch.randn(m, n, generator=g).to(torch.bfloat16).cuda()
+    out_full = torch.zeros(m, n + 32, dtype=torch.bfloat16, device="cuda")
+    out = out_full[:, 32:]
+    gemm_ex(a, b, out, bias=bias, c=c, alpha=0.5, beta=2.0, trans_a=trans_a, trans_b=trans_b)
+    torch.cuda.synchronize()
+    af, bf = a.float(), b.float()
+    ref = 0.5 * ((af.T if trans_a else af) @ (bf.T if trans_b else bf)) + bias.float() + 2.0 * c.float()
+    e = rel_l2(out, ref.cpu().numpy())
+    print(f"  rel-L2 {e:.2e}", flush=True)
+    assert e <= 1e-2
+    assert not out_full[:, :32].float().abs().sum().item()  # nothing written outside the view
+    # in-place accumulation: out += a b
+    before = out.float().clone()
+    gemm_ex(a, b, out, c=out, beta=1.0, trans_a=trans_a, trans_b=trans_b)
+    torch.cuda.synchronize()
+    ref2 = before + (af.T if trans_a else af) @ (bf.T if trans_b else bf)
+    assert rel_l2(out, ref2.cpu().numpy()) <= 1e-2
+
+
+def test_layernorm_backward_residual(oracle):
+    """layernorm_backward with a residual: the input gradient plus it."""
+    from ceo_amd.nn import layernorm_backward, layernorm_forward
+
+    rows, D = 300, 1024
+    announce(f"layernorm_backward residual rows={rows} D={D}")
+    rng = np.random.default_rng(17)
+    x = _bf(rng.standard_normal((rows, D)))
+    w = _bf(1 + 0.1 * rng.standard_normal(D))
+    dy = _bf(rng.standard_normal((rows, D)))
+    res = _bf(rng.standard_normal((rows, D)))
+    for D2, sl in ((D, slice(None)), (96, slice(0, 96))):
+        xs, ws, dys, rs = (x[:, sl].contiguous(), w[sl].contiguous(), dy[:, sl].contiguous(),
+                           res[:, sl].contiguous())
+        _, mean, rstd = layernorm_forward(xs.cuda(), ws.cuda(), None, 1e-5, save_stats=True)
+        dx, dw, db = layernorm_backward(dys.cuda(), xs.cuda(), ws.cuda(), mean, rstd,
+                                        residual=rs.cuda())
+        torch.cuda.synchronize()
+        _, rm, rr = oracle.layernorm_fwd(xs.float().numpy(), ws.float().numpy(), None, 1e-5)
+        rdx, rdw, _ = oracle.layernorm_bwd(dys.float().numpy(), xs.float().numpy(),
+                                           ws.float().numpy(), rm, rr)
+        e = rel_l2(dx, rdx + rs.float().numpy())
+        print(f"  D={D2} rel-L2 dx+res {e:.2e}", flush=True)
+        assert e <= 1e-2 and rel_l2(dw, rdw) <= 1e-4
+
+
 @pytest.fixture(params=[0, 1], ids=["hipblaslt", "native"])
 def gemm_backend(request):
     """Runs a GEMM test on the hipBLASLt path and on the library's own MFMA
