@@ -815,6 +815,7 @@ struct FwdWs {
     T *W, *U;     // generic path
     bf16* Tc;     // bf16 path
     float* bc;    // bf16 path
+    float* dcc;   // bf16 path: dc/dlambda, dc/dbeta per token
     float* bco;   // generic path
     T* h;         // generic path; bf16 path when the states are saved
     bf16* Pc;     // bf16 path when the states are saved
@@ -827,6 +828,7 @@ struct BwdWs {
     T *W, *U;
     bf16* Tc;
     float* bc;
+    float* dcc;  // bf16 path: dc/dlambda, dc/dbeta per token, as the forward's prep wrote them
     float* bco;  // generic path
     T* h;        // chunk start states
     bf16* Pc;    // bf16 path: tril(Q K^T) per chunk, as the forward saved it
@@ -839,18 +841,19 @@ struct BwdWs {
 // Takes the common prefix; returns with `c` at the end of h (and Vn).
 template <typename T>
 static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** coff, T** W,
-                         T** U, bf16** Tc, float** bc, float** bco, T** h, bf16** Pc, T** Vn,
-                         bool with_h) {
+                         T** U, bf16** Tc, float** bc, float** dcc, float** bco, T** h,
+                         bf16** Pc, T** Vn, bool with_h) {
     *cu_s = c.take<int32_t>(p.N + 1);
     *coff = c.take<int32_t>(p.N + 1);
     *W = *U = nullptr;
     *Tc = nullptr;
-    *bc = *bco = nullptr;
+    *bc = *dcc = *bco = nullptr;
     *h = *Vn = nullptr;
     *Pc = nullptr;
     if (__is_same(T, bf16)) {
         *Tc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
         *bc = c.take<float>((size_t)p.slots * p.H * 64);
+        *dcc = c.take<float>((size_t)p.slots * p.H * 128);
         if (with_h) {
             *h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
             *Pc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
@@ -870,7 +873,7 @@ template <typename T>
 static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out, bool with_states) {
     Carve c(base);
     FwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Pc,
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.dcc, &w.bco, &w.h, &w.Pc,
                     &w.Vn, with_states);
     if (out) *out = w;
     return c.off + 256;
@@ -880,7 +883,7 @@ template <typename T>
 static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
     Carve c(base);
     BwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.bco, &w.h, &w.Pc,
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.dcc, &w.bco, &w.h, &w.Pc,
                     &w.Vn, true);
     w.dh = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
     if (!__is_same(T, bf16)) {
@@ -925,7 +928,7 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const int H = p.H;
     if constexpr (__is_same(T, bf16)) {
         EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
-                    dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc);
+                    dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc, w.dcc);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
                     dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, v, w.Tc, w.bc, si,
                     H, S0, ST, o, w.h, w.Pc);
@@ -956,27 +959,32 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
         const dim3 scan_grid(p.N * H * (V / fast::VS));
         if (!reuse)
             EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
-                        dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc);
+                        dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc, w.dcc);
         if (!reuse_states)
             EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
                         dim3(fast::NT), st, k, v, (const bf16*)w.Tc, (const float*)w.bc, si, H,
                         S0, w.h);
+        // persistent gradient kernel: one workgroup per CU (its LDS allows no
+        // more), each looping over (chunk, head) items
+        const int nitems = H * p.slots;
+        const int ncu = device_cu_count();
+        const dim3 grad_grid((unsigned)(ncu > 0 && ncu < nitems ? ncu : nitems));
         // the forward that saved the states also saved each chunk's P
         if (reuse_states) {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, true>), scan_grid,
                         dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)w.Pc, si, H, dST, dS0, w.dh);
-            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true>), dim3(H, p.slots),
-                        dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc,
-                        (const float*)w.bc, (const bf16*)w.Pc, w.h, w.dh, si, H, dq, dk, dv,
+            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true>), grad_grid,
+                        dim3(fast::NT8), st, q, k, v, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        (const float*)w.dcc, (const bf16*)w.Pc, w.h, w.dh, si, H, nitems, dq, dk, dv,
                         dbeta);
         } else {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, false>), scan_grid,
                         dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)nullptr, si, H, dST, dS0, w.dh);
-            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false>), dim3(H, p.slots),
-                        dim3(fast::NT8), st, q, k, v, beta, dO, (const bf16*)w.Tc,
-                        (const float*)w.bc, (const bf16*)nullptr, w.h, w.dh, si, H, dq, dk, dv,
+            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false>), grad_grid,
+                        dim3(fast::NT8), st, q, k, v, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        (const float*)w.dcc, (const bf16*)nullptr, w.h, w.dh, si, H, nitems, dq, dk, dv,
                         dbeta);
         }
         return (int)hipPeekAtLastError();

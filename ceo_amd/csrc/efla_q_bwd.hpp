@@ -24,7 +24,7 @@
 //   dS through the chunks backwards (dVn = P^T dO + K dS, Z = D T^T dVn,
 //   dS <- dS + Q^T dO - K^T Z); writes each chunk's end-state gradient to
 //   `dhist` in the same layout, and dS_0.
-// grad_kernel     (grid: chunk slots x H)
+// grad_kernel     (persistent, one workgroup per CU over the chunk x H items)
 //   everything above for one chunk from q, k, v, beta, dO, h, dh, looping over
 //   64-wide value slices; writes dq, dk, dv, dbeta.
 #pragma once
@@ -291,14 +291,18 @@ struct GradSmem {
     bf16 Ks[64 * ldb<K>()];
     bf16 Ps[64 * LD64];  // P[t][t'] (t' <= t)
     bf16 Tb[64 * LD64];  // bf16(T)[t][t'] (t' <= t), from the WY prep
-    float lam[64], b[64], dcl[64], dcb[64];
+    // b, dc/dlambda, dc/dbeta per token for items of even / odd position in
+    // this workgroup's sequence (the next item's arrive during the closing)
+    float coef[2][3][64];
     float dbh[2][64];    // per-half partial dL/db
+    // one 64-wide value slice's inputs; during an item's closing products the
+    // next item's first slice is copied in here
+    bf16 V[64 * LD64];   // v[:, slice]; each wave's (rows, value tiles) later hold D Y
+    bf16 dO[64 * LD64];  // dO[:, slice]
+    bf16 h[64 * ldb<K>()];   // h[v][f] for the slice's v
+    bf16 dh[64 * ldb<K>()];  // dh[v][f]
     union {
         struct {  // one 64-wide value slice
-            bf16 V[64 * LD64];   // v[:, slice]; each wave's (rows, value tiles) later hold D Y
-            bf16 dO[64 * LD64];  // dO[:, slice]
-            bf16 h[64 * ldb<K>()];   // h[v][f] for the slice's v
-            bf16 dh[64 * ldb<K>()];  // dh[v][f]
             bf16 DR[64 * LD64];  // D R [t][v]
             bf16 Vn[64 * LD64];  // Vn [t][v]
             bf16 dVn[64 * LD64]; // dVn [t][v]
@@ -318,71 +322,107 @@ constexpr int NT8 = 512;  // grad_kernel: 8 waves
 // every transposed tile it computes); hf = wave >> 2 picks half of the value
 // tiles (slice phase), of the key tiles (dq / dk) and of the 16-token blocks
 // of the 64 x 64 chunk matrices.
+//
+// Persistent: workgroup b (one per CU) takes the (chunk, head) items b,
+// b + gridDim.x, ... in heads-fastest order (the heads of one chunk are
+// neighbouring row pieces of the same token rows).  An item's inputs are
+// copied straight into LDS (global_load_lds) while the previous item runs its
+// closing products: its first value slice (v, dO, h, dh), P and the per-token
+// coefficients as soon as the slice buffers are free, q once the closing no
+// longer reads Q, T once it no longer reads T, and k after the last product
+// that reads K.  Nothing of the next item passes through registers, so the
+// copies never make a wave wait.
 template <int K, int V, bool PS>
 __global__ void __launch_bounds__(NT8) grad_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
-    const bf16* __restrict__ beta, const bf16* __restrict__ dO, const bf16* __restrict__ Tws,
-    const float* __restrict__ bws, const bf16* __restrict__ Pws, const bf16* __restrict__ hist, const bf16* __restrict__ dhist, SeqInfo si, int H,
+    const bf16* __restrict__ dO, const bf16* __restrict__ Tws, const float* __restrict__ bws,
+    const float* __restrict__ dcws, const bf16* __restrict__ Pws, const bf16* __restrict__ hist,
+    const bf16* __restrict__ dhist, SeqInfo si, int H, int nitems,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
     bf16* __restrict__ dbeta) {
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 32;  // NF key tiles per half
     __shared__ __attribute__((aligned(16))) GradSmem<K> sm;
-    const int h = blockIdx.x, slot = blockIdx.y;  // heads fastest: one chunk's rows stay together
-    long bos;
-    int len;
-    if (!locate_chunk(si, slot, bos, len)) return;
     const int w8 = mf::wave(), tb = w8 & 3, hf = w8 >> 2;
-    const int l = mf::lane(), g = l >> 4, r = l & 15;
-    const int t = 16 * tb + r;  // this lane's token (column of the transposed tiles)
-    const long chb = ((long)slot * H + h) * V * K;  // this chunk's h / dh block
     const int nks = tb >= 2 ? 1 : 0;  // first k-step (of 32) that reaches t'' >= t
     const int f0 = hf * NF;            // first key tile of this half
+
+    struct Item {
+        int h, slot, len;
+        long bos;
+    };
+    auto locate = [&](int it, Item& I) -> bool {
+        if (it >= nitems) return false;
+        I.h = it % H;
+        I.slot = it / H;
+        return locate_chunk(si, I.slot, I.bos, I.len);
+    };
+    // copies into LDS (l: lane); each is issued by all waves
+    auto copy_slice0 = [&](const Item& I, int par, int l) {
+        const long cid = (long)I.slot * H + I.h, chb = cid * V * K;
+        mf::dma_tile<64, VS, LD64, 8>(sm.V, v + (I.bos * H + I.h) * V, (long)H * V, I.len, 0, l);
+        mf::dma_tile<64, VS, LD64, 8>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
+        mf::dma_tile<64, K, LDK, 8>(sm.h, hist + chb, K, 64, 4, l);
+        mf::dma_tile<64, K, LDK, 8>(sm.dh, dhist + chb, K, 64, 6, l);
+        if constexpr (PS)
+            mf::dma_tile<64, 64, LD64, 8>(sm.Ps, Pws + cid * 64 * 64, 64, 64, 2, l);
+        // b (16 chunks of 16 bytes) and dc/dlambda, dc/dbeta (32 chunks)
+        if (w8 == 7 && l < 16) mf::dma16(bws + cid * 64, 16u * l, sm.coef[par][0]);
+        if (w8 == 6 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
+    };
+    auto copy_q = [&](const Item& I, int l) {
+        mf::dma_tile<64, K, LDK, 8>(sm.Qs, q + (I.bos * H + I.h) * K, (long)H * K, I.len, 3, l);
+    };
+    auto copy_t = [&](const Item& I, int l) {
+        mf::dma_tile<64, 64, LD64, 8>(sm.Tb, Tws + ((long)I.slot * H + I.h) * 64 * 64, 64, 64, 5,
+                                      l);
+    };
+    auto copy_k = [&](const Item& I, int l) {
+        mf::dma_tile<64, K, LDK, 8>(sm.Ks, k + (I.bos * H + I.h) * K, (long)H * K, I.len, 1, l);
+    };
+
+    int it = blockIdx.x, par = 0;
+    Item cur;
+    if (!locate(it, cur)) return;  // uniform over the workgroup
+    if constexpr (!PS)  // P's tiles above the diagonal are never written
+        for (int i = threadIdx.x; i < 64 * LD64; i += NT8) sm.Ps[i] = (bf16)0.f;
+    copy_slice0(cur, par, mf::lane());
+    copy_q(cur, mf::lane());
+    copy_t(cur, mf::lane());
+    copy_k(cur, mf::lane());
+    for (;;) {
+    // lane-dependent values are derived per item (see mf::tid_in)
+    const int tid = mf::tid_in(it);
+    const int l = tid & 63, g = l >> 4, r = l & 15;
+    const int t = 16 * tb + r;  // this lane's token (column of the transposed tiles)
+    const int h = cur.h, slot = cur.slot, len = cur.len;
+    const long bos = cur.bos;
+    const long chb = ((long)slot * H + h) * V * K;  // this chunk's h / dh block
+    const float* cf = sm.coef[par][0];  // b, dc/dlambda, dc/dbeta at cf[0, 64, 128 + t]
 
     mf::TileRegs<64, VS, NT8> rv, rd;
     mf::TileRegs<64, K, NT8> rh, rdh;
     auto prefetch = [&](int s) {
         const int vv = s * VS;
-        rv.load(v + (bos * H + h) * V + vv, (long)H * V, len);
-        rd.load(dO + (bos * H + h) * V + vv, (long)H * V, len);
-        rh.load(hist + chb + (long)vv * K, K, 64);
-        rdh.load(dhist + chb + (long)vv * K, K, 64);
+        rv.load(v + (bos * H + h) * V + vv, (long)H * V, len, tid);
+        rd.load(dO + (bos * H + h) * V + vv, (long)H * V, len, tid);
+        rh.load(hist + chb + (long)vv * K, K, 64, tid);
+        rdh.load(dhist + chb + (long)vv * K, K, 64, tid);
     };
-    // beta of token threadIdx.x, loaded with the other chunk inputs
-    // beta and the prep's b of token threadIdx.x, loaded with the other chunk
-    // inputs (b is taken as the forward used it; lambda here only feeds the
-    // derivatives of c)
-    const bool bthr = threadIdx.x < 64 && (int)threadIdx.x < len;
-    const float bet = bthr ? (float)beta[(bos + threadIdx.x) * H + h] : 0.f;
-    const float bpre = bthr ? bws[((long)slot * H + h) * 64 + threadIdx.x] : 0.f;
-    // ---- chunk setup: q, k, T, b, P ----
-    {
-        mf::TileRegs<64, K, NT8> rq, rk;
-        mf::TileRegs<64, 64, NT8> rt, rp;
-        rq.load(q + (bos * H + h) * K, (long)H * K, len);
-        rk.load(k + (bos * H + h) * K, (long)H * K, len);
-        rt.load(Tws + ((long)slot * H + h) * 64 * 64, 64, 64);
-        if constexpr (PS) rp.load(Pws + ((long)slot * H + h) * 64 * 64, 64, 64);
-        prefetch(0);
-        rq.store_rows(sm.Qs, LDK);
-        rk.store_rows(sm.Ks, LDK);
-        rt.store_rows(sm.Tb, LD64);
-        if constexpr (PS) rp.store_rows(sm.Ps, LD64);
-#pragma unroll
-        for (int j = 0; j < rk.TPT; ++j) {
-            const float s = rk.row_sumsq(j);
-            if (rk.fg() == 0) sm.lam[rk.t0() + j] = s;
+    // ---- item setup: every input of the item's first slice is in flight
+    mf::dma_wait();
+    __syncthreads();  // every wave's copies have landed
+    if (len < 64) {  // a sequence's last chunk: token rows past its end read as zero
+        for (int i = tid; i < (64 - len) * (K / 8); i += NT8) {
+            const int o = (len + i / (K / 8)) * LDK + 8 * (i % (K / 8));
+            *reinterpret_cast<bf16x8*>(sm.Qs + o) = bf16x8{};
+            *reinterpret_cast<bf16x8*>(sm.Ks + o) = bf16x8{};
         }
-        if constexpr (!PS)
-            for (int i = threadIdx.x; i < 64 * LD64; i += NT8) sm.Ps[i] = (bf16)0.f;
-    }
-    __syncthreads();
-    if (threadIdx.x < 64) {
-        const int tt = threadIdx.x;
-        float c = 0.f, dcl = 0.f, dcb = 0.f;
-        if (tt < len) efla_coeff(sm.lam[tt], bet, c, dcl, dcb);
-        sm.b[tt] = tt < len ? bpre : 0.f;
-        sm.dcl[tt] = dcl;
-        sm.dcb[tt] = dcb;
+        for (int i = tid; i < (64 - len) * (VS / 8); i += NT8) {
+            const int o = (len + i / (VS / 8)) * LD64 + 8 * (i % (VS / 8));
+            *reinterpret_cast<bf16x8*>(sm.V + o) = bf16x8{};
+            *reinterpret_cast<bf16x8*>(sm.dO + o) = bf16x8{};
+        }
+        __syncthreads();
     }
     if constexpr (!PS) {
         for (int n = w8; n < 10; n += 8) {
@@ -391,17 +431,17 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
             floatx4 accp = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)
-                accp = mma(frag_nat(sm.Ks, LDK, 16 * J, k0), frag_nat(sm.Qs, LDK, 16 * I, k0), accp);
+                accp = mma(frag_nat(l, sm.Ks, LDK, 16 * J, k0), frag_nat(l, sm.Qs, LDK, 16 * I, k0), accp);
             const int tq = 16 * I + r, tk = 16 * J + 4 * g;
             *reinterpret_cast<bf16x4*>(sm.Ps + tq * LD64 + tk) =
                 bf16x4{(bf16)(tk + 0 <= tq ? accp[0] : 0.f), (bf16)(tk + 1 <= tq ? accp[1] : 0.f),
                        (bf16)(tk + 2 <= tq ? accp[2] : 0.f), (bf16)(tk + 3 <= tq ? accp[3] : 0.f)};
         }
+        __syncthreads();
     }
     // B operand (line t, k = t') of T
-    const bf16x8 tfr0 = frag_nat(sm.Tb, LD64, 16 * tb, 0), tfr1 = frag_nat(sm.Tb, LD64, 16 * tb, 32);
-    __syncthreads();
-    const float bt = sm.b[t];
+    const bf16x8 tfr0 = frag_nat(l, sm.Tb, LD64, 16 * tb, 0), tfr1 = frag_nat(l, sm.Tb, LD64, 16 * tb, 32);
+    const float bt = cf[t];
 
     // ---- value slices ----
     floatx4 dqa[NF], dka[NF], dma[2], dta[2];
@@ -412,12 +452,14 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     float dbp = 0.f;
     for (int s = 0; s < NS; ++s) {
         const int vv = s * VS;
-        if (s > 0) __syncthreads();
-        rv.store_rows(sm.u.s.V, LD64);
-        rd.store_rows(sm.u.s.dO, LD64);
-        rh.store_rows(sm.u.s.h, LDK);
-        rdh.store_rows(sm.u.s.dh, LDK);
-        __syncthreads();
+        if (s > 0) {  // slice 0 was copied in with the item's other inputs
+            __syncthreads();
+            rv.store_rows(sm.V, LD64);
+            rd.store_rows(sm.dO, LD64);
+            rh.store_rows(sm.h, LDK);
+            rdh.store_rows(sm.dh, LDK);
+            __syncthreads();
+        }
         if (s + 1 < NS) prefetch(s + 1);
         // R^T = V^T - h K^T and dVn^T = dO^T P + dh K^T for value tiles 2hf, 2hf+1:
         // tile (value 16vb + 4g + i, token t)
@@ -425,16 +467,16 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int vb = 2 * hf + e;
-            floatx4 ra = load4(sm.u.s.V + t * LD64 + 16 * vb + 4 * g);
+            floatx4 ra = load4(sm.V + t * LD64 + 16 * vb + 4 * g);
             floatx4 da = zero4();
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb) {
-                const bf16x8 kt = frag_nat(sm.Ks, LDK, 16 * tb, 32 * kb);
-                ra = mma(frag_nat(sm.u.s.h, LDK, 16 * vb, 32 * kb), mf::neg(kt), ra);
-                da = mma(frag_nat(sm.u.s.dh, LDK, 16 * vb, 32 * kb), kt, da);
+                const bf16x8 kt = frag_nat(l, sm.Ks, LDK, 16 * tb, 32 * kb);
+                ra = mma(frag_nat(l, sm.h, LDK, 16 * vb, 32 * kb), mf::neg(kt), ra);
+                da = mma(frag_nat(l, sm.dh, LDK, 16 * vb, 32 * kb), kt, da);
             }
-            if (nks == 0) da = mma(frag_tr(sm.u.s.dO, LD64, 0, 16 * vb), frag_tr(sm.Ps, LD64, 0, 16 * tb), da);
-            da = mma(frag_tr(sm.u.s.dO, LD64, 32, 16 * vb), frag_tr(sm.Ps, LD64, 32, 16 * tb), da);
+            if (nks == 0) da = mma(frag_tr(l, sm.dO, LD64, 0, 16 * vb), frag_tr(l, sm.Ps, LD64, 0, 16 * tb), da);
+            da = mma(frag_tr(l, sm.dO, LD64, 32, 16 * vb), frag_tr(l, sm.Ps, LD64, 32, 16 * tb), da);
             rT[e] = ra;
             store4s(sm.u.s.DR + t * LD64 + 16 * vb + 4 * g, ra, bt);
             store4(sm.u.s.dVn + t * LD64 + 16 * vb + 4 * g, da);
@@ -445,40 +487,40 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int vb = 2 * hf + e;
-            floatx4 vn = mma(frag_tr(sm.u.s.DR, LD64, 0, 16 * vb), tfr0, zero4());
-            if (tb >= 2) vn = mma(frag_tr(sm.u.s.DR, LD64, 32, 16 * vb), tfr1, vn);
+            floatx4 vn = mma(frag_tr(l, sm.u.s.DR, LD64, 0, 16 * vb), tfr0, zero4());
+            if (tb >= 2) vn = mma(frag_tr(l, sm.u.s.DR, LD64, 32, 16 * vb), tfr1, vn);
             store4(sm.u.s.Vn + t * LD64 + 16 * vb + 4 * g, vn);
             floatx4 y = zero4();
             if (nks == 0)
-                y = mma(frag_tr(sm.u.s.dVn, LD64, 0, 16 * vb), frag_tr(sm.Tb, LD64, 0, 16 * tb), y);
-            y = mma(frag_tr(sm.u.s.dVn, LD64, 32, 16 * vb), frag_tr(sm.Tb, LD64, 32, 16 * tb), y);
+                y = mma(frag_tr(l, sm.u.s.dVn, LD64, 0, 16 * vb), frag_tr(l, sm.Tb, LD64, 0, 16 * tb), y);
+            y = mma(frag_tr(l, sm.u.s.dVn, LD64, 32, 16 * vb), frag_tr(l, sm.Tb, LD64, 32, 16 * tb), y);
 #pragma unroll
             for (int i = 0; i < 4; ++i) dbp += y[i] * rT[e][i];
             if (t < len) store4s(vrow + 16 * vb, y, bt);
-            store4s(sm.u.s.V + t * LD64 + 16 * vb + 4 * g, y, bt);
+            store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
         __syncthreads();
         // dq^T += h^T dO^T; dk^T += dh^T Vn^T - h^T (D Y)^T  (key tiles f0 .. f0+NF-1)
         // dT^T[t'][t] += sum_v D R[t'] dVn[t]; Dm^T[t'][t] += sum_v Vn[t'] dO[t]
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            const bf16x8 dob = frag_nat(sm.u.s.dO, LD64, 16 * tb, 32 * ks);
-            const bf16x8 dyb = mf::neg(frag_nat(sm.u.s.V, LD64, 16 * tb, 32 * ks));
-            const bf16x8 vnb = frag_nat(sm.u.s.Vn, LD64, 16 * tb, 32 * ks);
+            const bf16x8 dob = frag_nat(l, sm.dO, LD64, 16 * tb, 32 * ks);
+            const bf16x8 dyb = mf::neg(frag_nat(l, sm.V, LD64, 16 * tb, 32 * ks));
+            const bf16x8 vnb = frag_nat(l, sm.u.s.Vn, LD64, 16 * tb, 32 * ks);
 #pragma unroll
             for (int fb = 0; fb < NF; ++fb) {
-                const bf16x8 ha = frag_tr(sm.u.s.h, LDK, 32 * ks, 16 * (f0 + fb));
+                const bf16x8 ha = frag_tr(l, sm.h, LDK, 32 * ks, 16 * (f0 + fb));
                 dqa[fb] = mma(ha, dob, dqa[fb]);
                 dka[fb] = mma(ha, dyb, dka[fb]);
-                dka[fb] = mma(frag_tr(sm.u.s.dh, LDK, 32 * ks, 16 * (f0 + fb)), vnb, dka[fb]);
+                dka[fb] = mma(frag_tr(l, sm.dh, LDK, 32 * ks, 16 * (f0 + fb)), vnb, dka[fb]);
             }
             if (jlive) {
-                const bf16x8 dvb = frag_nat(sm.u.s.dVn, LD64, 16 * tb, 32 * ks);
+                const bf16x8 dvb = frag_nat(l, sm.u.s.dVn, LD64, 16 * tb, 32 * ks);
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     const int J = 2 * hf + e;
-                    dta[e] = mma(frag_row(sm.u.s.DR, LD64, pim(J, r), 32 * ks), dvb, dta[e]);
-                    dma[e] = mma(frag_row(sm.u.s.Vn, LD64, pim(J, r), 32 * ks), dob, dma[e]);
+                    dta[e] = mma(frag_row(l, sm.u.s.DR, LD64, pim(J, r), 32 * ks), dvb, dta[e]);
+                    dma[e] = mma(frag_row(l, sm.u.s.Vn, LD64, pim(J, r), 32 * ks), dob, dma[e]);
                 }
             }
         }
@@ -488,6 +530,11 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     dbp += __shfl_xor(dbp, 32);
     if (g == 0) sm.dbh[hf][t] = dbp;
     __syncthreads();  // slice buffers are free
+    // the next item: its first slice and P into the free slice buffers, its
+    // k, beta, b into registers (the closing products touch neither)
+    Item nxt;
+    const bool more = locate(it + (int)gridDim.x, nxt);
+    if (more) copy_slice0(nxt, par ^ 1, l);
 
     // ---- closing products ----
     // Dm[t][t'] keeps t' <= t, dT[t][t'] keeps t' < t; share both [t][t']
@@ -506,31 +553,32 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     __syncthreads();
     // X^T[t''][t] = sum_t' T[t''][t'] dT[t][t'] for t'' blocks 2hf, 2hf+1
     {
-        const bf16x8 d0 = frag_nat(sm.u.e.dT, LD64, 16 * tb, 0), d1 = frag_nat(sm.u.e.dT, LD64, 16 * tb, 32);
+        const bf16x8 d0 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 0), d1 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 32);
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int J = 2 * hf + e;
-            floatx4 x = mma(frag_nat(sm.Tb, LD64, 16 * J, 0), d0, zero4());
-            x = mma(frag_nat(sm.Tb, LD64, 16 * J, 32), d1, x);
+            floatx4 x = mma(frag_nat(l, sm.Tb, LD64, 16 * J, 0), d0, zero4());
+            x = mma(frag_nat(l, sm.Tb, LD64, 16 * J, 32), d1, x);
             store4(sm.u.e.X + t * LD64 + 16 * J + 4 * g, x);
         }
     }
     // dq^T += K^T Dm^T (k = t' <= t);  dk^T += Q^T Dm (token t' = t, k = t >= t')
     {
-        const bf16x8 m0 = frag_nat(sm.u.e.Dm, LD64, 16 * tb, 0), m1 = frag_nat(sm.u.e.Dm, LD64, 16 * tb, 32);
-        const bf16x8 c1 = frag_tr(sm.u.e.Dm, LD64, 32, 16 * tb);
+        const bf16x8 m0 = frag_nat(l, sm.u.e.Dm, LD64, 16 * tb, 0), m1 = frag_nat(l, sm.u.e.Dm, LD64, 16 * tb, 32);
+        const bf16x8 c1 = frag_tr(l, sm.u.e.Dm, LD64, 32, 16 * tb);
         bf16x8 c0 = c1;
-        if (nks == 0) c0 = frag_tr(sm.u.e.Dm, LD64, 0, 16 * tb);
+        if (nks == 0) c0 = frag_tr(l, sm.u.e.Dm, LD64, 0, 16 * tb);
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
-            dqa[fb] = mma(frag_tr(sm.Ks, LDK, 0, fc), m0, dqa[fb]);
-            if (tb >= 2) dqa[fb] = mma(frag_tr(sm.Ks, LDK, 32, fc), m1, dqa[fb]);
-            if (nks == 0) dka[fb] = mma(frag_tr(sm.Qs, LDK, 0, fc), c0, dka[fb]);
-            dka[fb] = mma(frag_tr(sm.Qs, LDK, 32, fc), c1, dka[fb]);
+            dqa[fb] = mma(frag_tr(l, sm.Ks, LDK, 0, fc), m0, dqa[fb]);
+            if (tb >= 2) dqa[fb] = mma(frag_tr(l, sm.Ks, LDK, 32, fc), m1, dqa[fb]);
+            if (nks == 0) dka[fb] = mma(frag_tr(l, sm.Qs, LDK, 0, fc), c0, dka[fb]);
+            dka[fb] = mma(frag_tr(l, sm.Qs, LDK, 32, fc), c1, dka[fb]);
         }
     }
     __syncthreads();
+    if (more) copy_q(nxt, l);  // Q is not read again in this item
     // M^T[j][i] = sum_t X[t][j] T[t][i] (i = t owned here, j in blocks 2hf, 2hf+1, j < i);
     // dA = -M, G recomputed: db += sum_j dA G; dG = b_i dA -> shared [i][j]
     float dbg = 0.f;
@@ -541,12 +589,12 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         if (jlive) {
             const int c0 = 32 * (J >> 1) + 4 * (J & 1);
             floatx4 m = zero4();
-            if (nks == 0) m = mma(frag_tr(sm.u.e.X, LD64, 0, c0, 8), frag_tr(sm.Tb, LD64, 0, 16 * tb), m);
-            m = mma(frag_tr(sm.u.e.X, LD64, 32, c0, 8), frag_tr(sm.Tb, LD64, 32, 16 * tb), m);
+            if (nks == 0) m = mma(frag_tr(l, sm.u.e.X, LD64, 0, c0, 8), frag_tr(l, sm.Tb, LD64, 0, 16 * tb), m);
+            m = mma(frag_tr(l, sm.u.e.X, LD64, 32, c0, 8), frag_tr(l, sm.Tb, LD64, 32, 16 * tb), m);
             floatx4 gg = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)
-                gg = mma(frag_row(sm.Ks, LDK, pim(J, r), k0), frag_nat(sm.Ks, LDK, 16 * tb, k0), gg);
+                gg = mma(frag_row(l, sm.Ks, LDK, pim(J, r), k0), frag_nat(l, sm.Ks, LDK, 16 * tb, k0), gg);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int j = pim(J, 4 * g + i);
@@ -560,42 +608,53 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     dbg += __shfl_xor(dbg, 16);
     dbg += __shfl_xor(dbg, 32);
     __syncthreads();
+    if (more) copy_t(nxt, l);  // nor T
     if (g == 0) sm.dbh[hf][t] += dbg;
     // dk^T += K^T dG^T (k = j < i = t) + K^T dG (token j = t, k = i > j)
     {
-        const bf16x8 a0 = frag_nat(sm.u.e.dG, LD64, 16 * tb, 0), a1 = frag_nat(sm.u.e.dG, LD64, 16 * tb, 32);
-        const bf16x8 b1 = frag_tr(sm.u.e.dG, LD64, 32, 16 * tb);
+        const bf16x8 a0 = frag_nat(l, sm.u.e.dG, LD64, 16 * tb, 0), a1 = frag_nat(l, sm.u.e.dG, LD64, 16 * tb, 32);
+        const bf16x8 b1 = frag_tr(l, sm.u.e.dG, LD64, 32, 16 * tb);
         bf16x8 b0 = b1;
-        if (nks == 0) b0 = frag_tr(sm.u.e.dG, LD64, 0, 16 * tb);
+        if (nks == 0) b0 = frag_tr(l, sm.u.e.dG, LD64, 0, 16 * tb);
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
-            const bf16x8 k0 = frag_tr(sm.Ks, LDK, 0, fc), k1 = frag_tr(sm.Ks, LDK, 32, fc);
+            const bf16x8 k0 = frag_tr(l, sm.Ks, LDK, 0, fc), k1 = frag_tr(l, sm.Ks, LDK, 32, fc);
             dka[fb] = mma(k0, a0, dka[fb]);
             if (tb >= 2) dka[fb] = mma(k1, a1, dka[fb]);
             if (nks == 0) dka[fb] = mma(k0, b0, dka[fb]);
             dka[fb] = mma(k1, b1, dka[fb]);
         }
     }
+    // k of this lane's token and key tiles for the last term, then K is free
+    bf16x4 kfin[NF];
+#pragma unroll
+    for (int fb = 0; fb < NF; ++fb)
+        kfin[fb] = *reinterpret_cast<const bf16x4*>(sm.Ks + t * LDK + 16 * (f0 + fb) + 4 * g);
     __syncthreads();
+    if (more) copy_k(nxt, l);
     const float dbt = sm.dbh[0][t] + sm.dbh[1][t];  // dL/db for token t
     // dk += 2 db c'(lambda) k; write dq, dk (this half's key tiles), dbeta
     if (t < len) {
-        const float s2 = 2.f * dbt * sm.dcl[t];
+        const float s2 = 2.f * dbt * cf[64 + t];
         bf16* qrow = dq + ((bos + t) * H + h) * K + 4 * g;
         bf16* krow = dk + ((bos + t) * H + h) * K + 4 * g;
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
             store4(qrow + fc, dqa[fb]);
-            const floatx4 kk = load4(sm.Ks + t * LDK + fc + 4 * g);
             floatx4 a = dka[fb];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] += s2 * kk[i];
+            for (int i = 0; i < 4; ++i) a[i] += s2 * (float)kfin[fb][i];
             store4(krow + fc, a);
         }
-        if (hf == 0 && g == 0) dbeta[(bos + t) * H + h] = (bf16)(dbt * sm.dcb[t]);
+        if (hf == 0 && g == 0) dbeta[(bos + t) * H + h] = (bf16)(dbt * cf[128 + t]);
     }
+    if (!more) break;
+    it += (int)gridDim.x;
+    par ^= 1;
+    cur = nxt;
+    }  // items
 }
 
 }  // namespace fast

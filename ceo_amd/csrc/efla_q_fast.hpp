@@ -102,7 +102,8 @@ template <int K>
 __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
                                                   const bf16* __restrict__ beta, SeqInfo si,
                                                   int H, bf16* __restrict__ Tout,
-                                                  float* __restrict__ bout) {
+                                                  float* __restrict__ bout,
+                                                  float* __restrict__ dcout) {
     constexpr int LDK = ldb<K>();
     __shared__ __attribute__((aligned(16))) PrepSmem<K> sm;
     const int h = blockIdx.x, slot = blockIdx.y;  // heads fastest: one chunk's rows stay together
@@ -127,10 +128,15 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
     __syncthreads();
     if (threadIdx.x < 64) {
         const int t = threadIdx.x;
-        float c = 0.f, dcl, dcb;
+        float c = 0.f, dcl = 0.f, dcb = 0.f;
         if (t < len) efla_coeff(sm.lam[t], bet, c, dcl, dcb);
         sm.b[t] = c;
         bout[cid * 64 + t] = c;
+        // dc/dlambda and dc/dbeta for the backward: [chunk][head][2][64]
+        if (dcout) {
+            dcout[cid * 128 + t] = dcl;
+            dcout[cid * 128 + 64 + t] = dcb;
+        }
     }
     // G = K K^T, lower tiles
     for (int n = w; n < 10; n += 4) {

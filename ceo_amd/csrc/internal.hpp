@@ -81,4 +81,7 @@ int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr);
 // stream capture).
 int fill_zero(void* ptr, size_t bytes, hipStream_t stream);
 
+// Compute units of the current device (cached per device); 0 if the query fails.
+int device_cu_count();
+
 }  // namespace efla

@@ -28,6 +28,15 @@ typedef __attribute__((__vector_size__(16))) int int4v;
 typedef __attribute__((__vector_size__(8))) int int2v;
 
 __device__ __forceinline__ int lane() { return threadIdx.x & 63; }
+// threadIdx.x as a value that depends on `epoch` (an empty asm ties them): in a
+// loop, lane-dependent address arithmetic derived from it is recomputed each
+// iteration instead of being hoisted out of the loop and held live across it.
+// The asm has no side effects, so repeated uses within an iteration still merge.
+__device__ __forceinline__ int tid_in(int epoch) {
+    int x = (int)threadIdx.x;
+    asm("" : "+v"(x) : "s"(epoch));
+    return x;
+}
 // wave index as a scalar (wave-uniform branches and addresses stay in SGPRs)
 __device__ __forceinline__ int wave() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
@@ -44,9 +53,11 @@ __device__ __forceinline__ floatx4 mma_f32(float a, float b, floatx4 c) {
 
 // Operand fragment from a [line][k] bf16 array (line = A row or B column),
 // natural k order, lines line0 .. line0+15, k range k0 .. k0+31.
-__device__ __forceinline__ bf16x8 frag_nat(const bf16* base, int ld, int line0, int k0) {
-    const int l = lane();
+__device__ __forceinline__ bf16x8 frag_nat(int l, const bf16* base, int ld, int line0, int k0) {
     return *reinterpret_cast<const bf16x8*>(base + (line0 + (l & 15)) * ld + k0 + 8 * (l >> 4));
+}
+__device__ __forceinline__ bf16x8 frag_nat(const bf16* base, int ld, int line0, int k0) {
+    return frag_nat(lane(), base, ld, line0, k0);
 }
 
 // Same, c-order.
@@ -114,23 +125,33 @@ __device__ __forceinline__ bf16x4 ds_tr16(const bf16* p) {
 
 // Lane (g, j) gets rows k0 + 8g + i (i = 0..3) of column
 // c0 + (j >> 2) * cs + (j & 3) of a row-major tile with row stride ld.
-__device__ __forceinline__ bf16x4 tr_rows4(const bf16* base, int ld, int k0, int c0, int cs) {
-    const int l = lane(), g = l >> 4, a = (l & 15) >> 2, b = l & 3;
+__device__ __forceinline__ bf16x4 tr_rows4(int l, const bf16* base, int ld, int k0, int c0, int cs) {
+    const int g = l >> 4, a = (l & 15) >> 2, b = l & 3;
     return ds_tr16(base + (k0 + 8 * g + a) * ld + c0 + b * cs);
+}
+__device__ __forceinline__ bf16x4 tr_rows4(const bf16* base, int ld, int k0, int c0, int cs) {
+    return tr_rows4(lane(), base, ld, k0, c0, cs);
 }
 
 // Operand fragment whose k runs along the ROWS of a row-major [k][line] tile:
 // lane (g, j) gets line c0 + (j >> 2) * cs + (j & 3), k = k0 + 8g + s
 // (natural order).  cs = 4 gives lines c0 .. c0+15 in order.
-__device__ __forceinline__ bf16x8 frag_tr(const bf16* base, int ld, int k0, int c0, int cs = 4) {
-    const bf16x4 lo = tr_rows4(base, ld, k0, c0, cs);
-    const bf16x4 hi = tr_rows4(base, ld, k0 + 4, c0, cs);
+__device__ __forceinline__ bf16x8 frag_tr(int l, const bf16* base, int ld, int k0, int c0,
+                                         int cs = 4) {
+    const bf16x4 lo = tr_rows4(l, base, ld, k0, c0, cs);
+    const bf16x4 hi = tr_rows4(l, base, ld, k0 + 4, c0, cs);
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+__device__ __forceinline__ bf16x8 frag_tr(const bf16* base, int ld, int k0, int c0, int cs = 4) {
+    return frag_tr(lane(), base, ld, k0, c0, cs);
 }
 
 // frag_nat with an explicit row for this lane (row permutations).
+__device__ __forceinline__ bf16x8 frag_row(int l, const bf16* base, int ld, int row, int k0) {
+    return *reinterpret_cast<const bf16x8*>(base + row * ld + k0 + 8 * (l >> 4));
+}
 __device__ __forceinline__ bf16x8 frag_row(const bf16* base, int ld, int row, int k0) {
-    return *reinterpret_cast<const bf16x8*>(base + row * ld + k0 + 8 * (lane() >> 4));
+    return frag_row(lane(), base, ld, row, k0);
 }
 
 // Natural-order fragment from two C tiles: lanes of group g hold rows 4g..4g+3
@@ -151,9 +172,10 @@ struct TileRegs {
     static_assert(TPT >= 1 && ROWS * FG == TPT * NT, "tile does not split evenly");
     bf16x8 x[TPT];
     int valid;
+    int tid;  // this thread's index in the workgroup (set by load)
 
-    __device__ __forceinline__ int fg() const { return threadIdx.x % FG; }
-    __device__ __forceinline__ int t0() const { return (threadIdx.x / FG) * TPT; }
+    __device__ __forceinline__ int fg() const { return tid % FG; }
+    __device__ __forceinline__ int t0() const { return (tid / FG) * TPT; }
 
     // valid >= 1.  Rows past `valid` re-read the last valid row, so every load
     // is issued unconditionally and stays in bounds; they are zeroed by
@@ -163,7 +185,9 @@ struct TileRegs {
     // `src` is uniform across the workgroup and ROWS * ld * 2 < 2^32 (the
     // host validates H * max(d_k, d_v) < 2^24), so each row is a 32-bit byte
     // offset from a scalar base (global_load ... v_off, s_base).
-    __device__ __forceinline__ void load(const bf16* __restrict__ src, long ld, int nvalid) {
+    __device__ __forceinline__ void load(const bf16* __restrict__ src, long ld, int nvalid,
+                                         int thread = (int)threadIdx.x) {
+        tid = thread;
         const int f = fg(), t = t0();
         valid = nvalid;
         const char* base = reinterpret_cast<const char*>(src);
@@ -233,6 +257,44 @@ __device__ __forceinline__ void store_tile(bf16* __restrict__ dst, long ld, cons
         if (t < valid)
             *reinterpret_cast<int4v*>(dst + (long)t * ld + 8 * f) =
                 *reinterpret_cast<const int4v*>(src + t * lds + 8 * f);
+    }
+}
+
+// --- direct global -> LDS copies ---------------------------------------------
+// global_load_lds_dwordx4: lane i of the wave writes 16 bytes at LDS address
+// m0 + 16 i, without staging through VGPRs.  It is issued from inline asm so
+// the compiler does not make later, unrelated LDS reads wait for it (the
+// builtin form makes every following ds_read wait for vmcnt(0)); the caller
+// runs dma_wait() and a workgroup barrier before anyone reads the destination,
+// and keeps the destination unread and unwritten while the copy is in flight.
+__device__ __forceinline__ void dma16(const void* base, unsigned off, const void* lds) {
+    const unsigned m0 =
+        (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(m0) : "memory");
+}
+// this wave's vector memory operations (loads, stores and LDS copies) done
+__device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
+
+// ROWS x D bf16 tile from global rows of stride ld (elements) into LDS rows of
+// stride LDR > D: one wave instruction fills 64 consecutive 16-byte LDS
+// chunks, so a row's pad chunks are copied too (they re-read the row's first
+// 16 bytes and are never read back).  The NW waves of the workgroup take the
+// instructions in turn, starting with wave `rot % NW`; l is the lane.  Rows past `nvalid`
+// re-read the last valid row, so every access stays inside the source rows;
+// the caller zeroes those rows where they matter.  `src` is uniform and
+// ROWS * ld * 2 < 2^32 (as for TileRegs), so offsets are 32-bit.
+template <int ROWS, int D, int LDR, int NW>
+__device__ __forceinline__ void dma_tile(bf16* lds, const bf16* src, long ld, int nvalid, int rot,
+                                         int l) {
+    constexpr int CPR = LDR / 8, NI = ROWS * CPR / 64;
+    static_assert(LDR % 8 == 0 && LDR > D && D % 8 == 0 && (ROWS * CPR) % 64 == 0,
+                  "tile does not split into 64-chunk instructions");
+    const int w = wave();
+    for (int i = (w + NW - rot % NW) % NW; i < NI; i += NW) {
+        const int c = 64 * i + l, row = c / CPR, col = c - row * CPR;
+        const int rr = min(row, nvalid - 1);
+        const unsigned off = (unsigned)(rr * (int)ld + (col < D / 8 ? 8 * col : 0)) * 2u;
+        dma16(src, off, lds + 512 * i);
     }
 }
 

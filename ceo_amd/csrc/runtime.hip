@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <string.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
@@ -306,6 +307,20 @@ int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr) {
     }
     *ptr = w.ptr;
     return kSuccess;
+}
+
+int device_cu_count() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+    if (dev < 64) {
+        const int c = cached[dev].load(std::memory_order_relaxed);
+        if (c > 0) return c;
+    }
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    if (n > 0 && dev < 64) cached[dev].store(n, std::memory_order_relaxed);
+    return n;
 }
 }  // namespace efla
 

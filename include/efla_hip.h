@@ -121,7 +121,8 @@ size_t efla_chunk_bwd_workspace_size(size_t batch_size, size_t seq_len, size_t n
 /* The caller-owned `workspace` is the one the forward call on these exact
  * inputs (same q, k, v, beta, cu_seqlens, shapes) used, and nothing has
  * written to it since: the backward takes the forward's per-chunk WY factors
- * (W, U, T) from it instead of recomputing them.  The chunk states are
+ * (W, U, T) and per-token coefficients (b, dc/dlambda, dc/dbeta) from it
+ * instead of recomputing them.  The chunk states are
  * recomputed unless EFLA_BWD_REUSE_STATES is also set.  Requires a non-NULL
  * workspace of at least efla_chunk_bwd_workspace_size() bytes, also passed to
  * the forward. */
