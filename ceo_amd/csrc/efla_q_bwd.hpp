@@ -410,6 +410,10 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     };
     // ---- item setup: every input of the item's first slice is in flight
     mf::dma_wait();
+    // the next item, looked up here where nothing is in flight (the varlen
+    // lookup reads cu_seqlens offsets and waits for its loads)
+    Item nxt;
+    const bool more = locate(it + (int)gridDim.x, nxt);
     __syncthreads();  // every wave's copies have landed
     if (len < 64) {  // a sequence's last chunk: token rows past its end read as zero
         for (int i = tid; i < (64 - len) * (K / 8); i += NT8) {
@@ -532,8 +536,6 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     __syncthreads();  // slice buffers are free
     // the next item: its first slice and P into the free slice buffers, its
     // k, beta, b into registers (the closing products touch neither)
-    Item nxt;
-    const bool more = locate(it + (int)gridDim.x, nxt);
     if (more) copy_slice0(nxt, par ^ 1, l);
 
     // ---- closing products ----
