@@ -313,6 +313,10 @@ struct GradSmem {
             bf16 X[64 * LD64];   // dT T^T [t][t'']
             bf16 dG[64 * LD64];  // dG [i][j] (j < i)
         } e;
+        struct {  // the item's dq, dk rows on their way out
+            bf16 dq[64 * ldb<K>()];
+            bf16 dk[64 * ldb<K>()];
+        } o;
     } u;
 };
 
@@ -636,21 +640,31 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     __syncthreads();
     if (more) copy_k(nxt, l);
     const float dbt = sm.dbh[0][t] + sm.dbh[1][t];  // dL/db for token t
-    // dk += 2 db c'(lambda) k; write dq, dk (this half's key tiles), dbeta
-    if (t < len) {
+    // dk += 2 db c'(lambda) k; dq, dk (this half's key tiles) into LDS (the
+    // closing buffers are free), then written out as whole 16-byte row pieces
+    {
         const float s2 = 2.f * dbt * cf[64 + t];
-        bf16* qrow = dq + ((bos + t) * H + h) * K + 4 * g;
-        bf16* krow = dk + ((bos + t) * H + h) * K + 4 * g;
+        bf16* qs = sm.u.o.dq;  // [t][f], row stride LDK
+        bf16* ks = sm.u.o.dk;
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
-            store4(qrow + fc, dqa[fb]);
+            store4(qs + t * LDK + fc + 4 * g, dqa[fb]);
             floatx4 a = dka[fb];
 #pragma unroll
             for (int i = 0; i < 4; ++i) a[i] += s2 * (float)kfin[fb][i];
-            store4(krow + fc, a);
+            store4(ks + t * LDK + fc + 4 * g, a);
         }
-        if (hf == 0 && g == 0) dbeta[(bos + t) * H + h] = (bf16)(dbt * cf[128 + t]);
+        if (t < len && hf == 0 && g == 0) dbeta[(bos + t) * H + h] = (bf16)(dbt * cf[128 + t]);
+        __syncthreads();
+        for (int i = tid; i < 64 * (K / 8); i += NT8) {
+            const int tt = i / (K / 8), f = 8 * (i % (K / 8));
+            if (tt < len) {
+                const long o = ((bos + tt) * H + h) * K + f;
+                *reinterpret_cast<bf16x8*>(dq + o) = *reinterpret_cast<const bf16x8*>(qs + tt * LDK + f);
+                *reinterpret_cast<bf16x8*>(dk + o) = *reinterpret_cast<const bf16x8*>(ks + tt * LDK + f);
+            }
+        }
     }
     if (!more) break;
     it += (int)gridDim.x;
