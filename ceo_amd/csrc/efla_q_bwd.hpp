@@ -490,8 +490,7 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
             store4(sm.u.s.dVn + t * LD64 + 16 * vb + 4 * g, da);
         }
         __syncthreads();
-        // Vn^T = (D R)^T T^T; Y^T = dVn^T T; dv = D Y; db += sum_v Y R; D Y -> V
-        bf16* vrow = dv + ((bos + t) * H + h) * V + vv + 4 * g;
+        // Vn^T = (D R)^T T^T; Y^T = dVn^T T; db += sum_v Y R; D Y -> V (and dv)
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int vb = 2 * hf + e;
@@ -504,10 +503,16 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
             y = mma(frag_tr(l, sm.u.s.dVn, LD64, 32, 16 * vb), frag_tr(l, sm.Tb, LD64, 32, 16 * tb), y);
 #pragma unroll
             for (int i = 0; i < 4; ++i) dbp += y[i] * rT[e][i];
-            if (t < len) store4s(vrow + 16 * vb, y, bt);
             store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
         __syncthreads();
+        {  // dv = D Y of this slice from its bf16 copy in V, as whole 16-byte row pieces
+            static_assert(NT8 == 64 * (VS / 8), "one piece per thread");
+            const int tt = tid / (VS / 8), f = 8 * (tid % (VS / 8));
+            if (tt < len)
+                *reinterpret_cast<bf16x8*>(dv + ((bos + tt) * H + h) * V + vv + f) =
+                    *reinterpret_cast<const bf16x8*>(sm.V + tt * LD64 + f);
+        }
         // dq^T += h^T dO^T; dk^T += dh^T Vn^T - h^T (D Y)^T  (key tiles f0 .. f0+NF-1)
         // dT^T[t'][t] += sum_v D R[t'] dVn[t]; Dm^T[t'][t] += sum_v Vn[t'] dO[t]
 #pragma unroll
