@@ -543,9 +543,6 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     dbp += __shfl_xor(dbp, 32);
     if (g == 0) sm.dbh[hf][t] = dbp;
     __syncthreads();  // slice buffers are free
-    // the next item: its first slice and P into the free slice buffers, its
-    // k, beta, b into registers (the closing products touch neither)
-    if (more) copy_slice0(nxt, par ^ 1, l);
 
     // ---- closing products ----
     // Dm[t][t'] keeps t' <= t, dT[t][t'] keeps t' < t; share both [t][t']
@@ -562,6 +559,9 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         store4(sm.u.e.dT + t * LD64 + pim(J, 4 * g), dta[e]);
     }
     __syncthreads();
+    // the next item's first slice, P and coefficients into the free slice
+    // buffers (the closing products touch neither)
+    if (more) copy_slice0(nxt, par ^ 1, l);
     // X^T[t''][t] = sum_t' T[t''][t'] dT[t][t'] for t'' blocks 2hf, 2hf+1
     {
         const bf16x8 d0 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 0), d1 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 32);
