@@ -18,6 +18,7 @@
 // carries dW, dU through T and b (including the dc/dlambda term of
 // efla.cu:384-451 and dbeta = dc * exp(-beta lambda)).
 #include <hip/hip_runtime.h>
+#include <stdlib.h>
 
 #include "../../include/efla_hip.h"
 #include "common.hpp"
@@ -965,9 +966,15 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
                         dim3(fast::NT), st, k, v, (const bf16*)w.Tc, (const float*)w.bc, si, H,
                         S0, w.h);
         // persistent gradient kernel: one workgroup per CU (its LDS allows no
-        // more), each looping over (chunk, head) items
+        // more), each looping over (chunk, head) items.  EFLA_GRAD_WORKGROUPS
+        // caps the grid (tests use it to run many items per workgroup at
+        // small sizes; the results do not depend on the grid)
         const int nitems = H * p.slots;
-        const int ncu = device_cu_count();
+        int ncu = device_cu_count();
+        if (const char* cap = getenv("EFLA_GRAD_WORKGROUPS")) {
+            const int c = atoi(cap);
+            if (c > 0 && (ncu <= 0 || c < ncu)) ncu = c;
+        }
         const dim3 grad_grid((unsigned)(ncu > 0 && ncu < nitems ? ncu : nitems));
         // the forward that saved the states also saved each chunk's P
         if (reuse_states) {

@@ -197,3 +197,57 @@ def test_packed_batch_runs_sequences_independently(oracle):
         assert torch.equal(o[:, a:b], o1), s
         for big, small in zip(grads[:4], g1[:4]):
             assert torch.equal(big[:, a:b], small), s
+
+
+# The gradient kernel is persistent: min(#CUs, items) workgroups each loop over
+# (chunk, head) items, copying the next item's inputs into LDS while the
+# current one finishes.  At test sizes every workgroup would get one item, so
+# EFLA_GRAD_WORKGROUPS caps the grid and makes each workgroup run many items,
+# including partial chunks and sequence boundaries in the middle of its loop.
+def _grads(g, cu_t, s0_t, dst_t, reuse):
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd, new_workspace
+
+    if reuse:
+        ws = new_workspace(g["q"], g["v"], cu_t)
+        chunk_efla_fwd(g["q"], g["k"], g["v"], g["beta"], s0_t, cu_seqlens=cu_t, workspace=ws,
+                       save_states=True)
+        out = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], s0_t, dst_t,
+                             cu_seqlens=cu_t, workspace=ws, reuse_forward=True,
+                             reuse_states=True)
+    else:
+        out = chunk_efla_bwd(g["q"], g["k"], g["v"], g["beta"], g["do"], s0_t, dst_t,
+                             cu_seqlens=cu_t)
+    torch.cuda.synchronize()
+    return [t.clone() for t in out]
+
+
+@pytest.mark.parametrize("reuse", [False, True], ids=["recompute", "reuse-states"])
+@pytest.mark.parametrize("K,V", [(128, 128), (64, 256), (64, 64)])
+def test_grad_kernel_grid_cap_bit_exact(oracle, monkeypatch, K, V, reuse):
+    announce(f"grad kernel grid cap K={K} V={V} reuse={reuse}")
+    lens = [130, 64, 1, 0, 257, 63, 65, 200, 9, 128]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    ntok, H = int(cu[-1]), 3
+    x = oracle.make_efla_inputs(57 + K + V, ntok, H, K, V, bf16=True)
+    g = {n: to_dev(a, torch.bfloat16, (1, ntok, H, K) if n in "qk" else
+                   (1, ntok, H) if n == "beta" else (1, ntok, H, V)) for n, a in x.items()}
+    cu_t = torch.tensor(cu, dtype=torch.int32, device="cuda:0")
+    rng = np.random.default_rng(3)
+    s0_t = torch.from_numpy((rng.standard_normal((len(lens), H, K, V)) * 0.3)
+                            .astype(np.float32)).cuda()
+    dst_t = torch.from_numpy(rng.standard_normal((len(lens), H, K, V)).astype(np.float32)).cuda()
+    monkeypatch.delenv("EFLA_GRAD_WORKGROUPS", raising=False)
+    ref = _grads(g, cu_t, s0_t, dst_t, reuse)
+    for cap in ("1", "3", "7"):
+        monkeypatch.setenv("EFLA_GRAD_WORKGROUPS", cap)
+        got = _grads(g, cu_t, s0_t, dst_t, reuse)
+        for a, b, n in zip(got, ref, ("dq", "dk", "dv", "dbeta", "dS0")):
+            assert torch.equal(a, b), (cap, n)
+
+
+def test_grad_kernel_many_items_per_workgroup_vs_oracle(oracle, monkeypatch):
+    # the varlen case above, with 3 workgroups looping over all the items
+    monkeypatch.setenv("EFLA_GRAD_WORKGROUPS", "3")
+    lens = [1, 63, 64, 65, 130, 7, 0, 200]
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    _case(oracle, 43, 1, int(cu[-1]), 2, 128, 256, torch.bfloat16, s0=True, dst=True, cu=cu)
