@@ -36,6 +36,7 @@ namespace fast {
 
 using mf::frag_row;
 using mf::frag_tr;
+using mf::frag_trc;
 using mf::tr_rows4;
 
 constexpr int LD64 = ldb<64>();
@@ -224,7 +225,8 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(dS[2 * kb], dS[2 * kb + 1]);
         store_state_frag<K>(dhist + ((long)(slot0 + n) * H + h) * V * K, sb, vcol);
-        const bf16x8 do0 = frag_tr(cb.Vs, LD64, 0, 16 * w), do1 = frag_tr(cb.Vs, LD64, 32, 16 * w);
+        // dO^T in c-order over the tokens; its partners (P, Q) are read the same way
+        const bf16x8 do0 = mf::frag_trc(cb.Vs, LD64, 0, 16 * w), do1 = mf::frag_trc(cb.Vs, LD64, 32, 16 * w);
         // K dS part of dVn (P^T dO is added once P is complete); tile tb row
         // 4g + i is token pim(tb, 4g + i)
         floatx4 dvn[4];
@@ -244,8 +246,8 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
             const int c0 = 32 * (tb >> 1) + 4 * (tb & 1);
-            if (tb < 2) dvn[tb] = mma(frag_tr(Pm, LD64, 0, c0, 8), do0, dvn[tb]);
-            dvn[tb] = mma(frag_tr(Pm, LD64, 32, c0, 8), do1, dvn[tb]);
+            if (tb < 2) dvn[tb] = mma(mf::frag_trc(Pm, LD64, 0, c0, 8), do0, dvn[tb]);
+            dvn[tb] = mma(mf::frag_trc(Pm, LD64, 32, c0, 8), do1, dvn[tb]);
         }
         // Z = D T^T dVn (k = t'' >= t)
         const bf16x8 dv0 = frag_from_c(dvn[0], dvn[1]), dv1 = frag_from_c(dvn[2], dvn[3]);
@@ -267,8 +269,8 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         for (int fb = 0; fb < K / 16; ++fb) {
             const int c0 = 32 * (fb >> 1) + 4 * (fb & 1);
             floatx4 acc = dS[fb];
-            acc = mma(frag_tr(cb.Q, LDK, 0, c0, 8), do0, acc);
-            acc = mma(frag_tr(cb.Q, LDK, 32, c0, 8), do1, acc);
+            acc = mma(mf::frag_trc(cb.Q, LDK, 0, c0, 8), do0, acc);
+            acc = mma(mf::frag_trc(cb.Q, LDK, 32, c0, 8), do1, acc);
             acc = mma(frag_tr(cb.Kr, LDK, 0, c0, 8), nz0, acc);
             acc = mma(frag_tr(cb.Kr, LDK, 32, c0, 8), nz1, acc);
             dS[fb] = acc;
@@ -483,8 +485,9 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
                 ra = mma(frag_nat(l, sm.h, LDK, 16 * vb, 32 * kb), mf::neg(kt), ra);
                 da = mma(frag_nat(l, sm.dh, LDK, 16 * vb, 32 * kb), kt, da);
             }
-            if (nks == 0) da = mma(frag_tr(l, sm.dO, LD64, 0, 16 * vb), frag_tr(l, sm.Ps, LD64, 0, 16 * tb), da);
-            da = mma(frag_tr(l, sm.dO, LD64, 32, 16 * vb), frag_tr(l, sm.Ps, LD64, 32, 16 * tb), da);
+            // (both operands transposed: c-order rows, see mf::frag_trc)
+            if (nks == 0) da = mma(frag_trc(l, sm.dO, LD64, 0, 16 * vb), frag_trc(l, sm.Ps, LD64, 0, 16 * tb), da);
+            da = mma(frag_trc(l, sm.dO, LD64, 32, 16 * vb), frag_trc(l, sm.Ps, LD64, 32, 16 * tb), da);
             rT[e] = ra;
             store4s(sm.u.s.DR + t * LD64 + 16 * vb + 4 * g, ra, bt);
             store4(sm.u.s.dVn + t * LD64 + 16 * vb + 4 * g, da);
@@ -499,8 +502,8 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
             store4(sm.u.s.Vn + t * LD64 + 16 * vb + 4 * g, vn);
             floatx4 y = zero4();
             if (nks == 0)
-                y = mma(frag_tr(l, sm.u.s.dVn, LD64, 0, 16 * vb), frag_tr(l, sm.Tb, LD64, 0, 16 * tb), y);
-            y = mma(frag_tr(l, sm.u.s.dVn, LD64, 32, 16 * vb), frag_tr(l, sm.Tb, LD64, 32, 16 * tb), y);
+                y = mma(frag_trc(l, sm.u.s.dVn, LD64, 0, 16 * vb), frag_trc(l, sm.Tb, LD64, 0, 16 * tb), y);
+            y = mma(frag_trc(l, sm.u.s.dVn, LD64, 32, 16 * vb), frag_trc(l, sm.Tb, LD64, 32, 16 * tb), y);
 #pragma unroll
             for (int i = 0; i < 4; ++i) dbp += y[i] * rT[e][i];
             store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
@@ -576,16 +579,16 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     // dq^T += K^T Dm^T (k = t' <= t);  dk^T += Q^T Dm (token t' = t, k = t >= t')
     {
         const bf16x8 m0 = frag_nat(l, sm.u.e.Dm, LD64, 16 * tb, 0), m1 = frag_nat(l, sm.u.e.Dm, LD64, 16 * tb, 32);
-        const bf16x8 c1 = frag_tr(l, sm.u.e.Dm, LD64, 32, 16 * tb);
+        const bf16x8 c1 = frag_trc(l, sm.u.e.Dm, LD64, 32, 16 * tb);
         bf16x8 c0 = c1;
-        if (nks == 0) c0 = frag_tr(l, sm.u.e.Dm, LD64, 0, 16 * tb);
+        if (nks == 0) c0 = frag_trc(l, sm.u.e.Dm, LD64, 0, 16 * tb);
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
             dqa[fb] = mma(frag_tr(l, sm.Ks, LDK, 0, fc), m0, dqa[fb]);
             if (tb >= 2) dqa[fb] = mma(frag_tr(l, sm.Ks, LDK, 32, fc), m1, dqa[fb]);
-            if (nks == 0) dka[fb] = mma(frag_tr(l, sm.Qs, LDK, 0, fc), c0, dka[fb]);
-            dka[fb] = mma(frag_tr(l, sm.Qs, LDK, 32, fc), c1, dka[fb]);
+            if (nks == 0) dka[fb] = mma(frag_trc(l, sm.Qs, LDK, 0, fc), c0, dka[fb]);
+            dka[fb] = mma(frag_trc(l, sm.Qs, LDK, 32, fc), c1, dka[fb]);
         }
     }
     __syncthreads();
@@ -600,8 +603,8 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         if (jlive) {
             const int c0 = 32 * (J >> 1) + 4 * (J & 1);
             floatx4 m = zero4();
-            if (nks == 0) m = mma(frag_tr(l, sm.u.e.X, LD64, 0, c0, 8), frag_tr(l, sm.Tb, LD64, 0, 16 * tb), m);
-            m = mma(frag_tr(l, sm.u.e.X, LD64, 32, c0, 8), frag_tr(l, sm.Tb, LD64, 32, 16 * tb), m);
+            if (nks == 0) m = mma(frag_trc(l, sm.u.e.X, LD64, 0, c0, 8), frag_trc(l, sm.Tb, LD64, 0, 16 * tb), m);
+            m = mma(frag_trc(l, sm.u.e.X, LD64, 32, c0, 8), frag_trc(l, sm.Tb, LD64, 32, 16 * tb), m);
             floatx4 gg = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)

@@ -146,6 +146,24 @@ __device__ __forceinline__ bf16x8 frag_tr(const bf16* base, int ld, int k0, int 
     return frag_tr(lane(), base, ld, k0, c0, cs);
 }
 
+// frag_tr with the k rows in c-order: lane (g, j) gets k = k0 + 4g + i in
+// slots 0-3 and k0 + 16 + 4g + i in slots 4-7 (as frag_cc / frag_from_c).  It
+// pairs only with another c-order operand of the same k range, typically a
+// second frag_trc.  Measured on gfx950 with SQ_LDS_BANK_CONFLICT: its two
+// transposing reads take 2 LDS cycles each, against 4 for frag_tr, whose rows
+// r and r + 8 fall in the same banks for every row stride that keeps 16-byte
+// alignment.
+__device__ __forceinline__ bf16x8 frag_trc(int l, const bf16* base, int ld, int k0, int c0,
+                                          int cs = 4) {
+    const int g = l >> 4, a = (l & 15) >> 2, b = l & 3;
+    const bf16x4 lo = ds_tr16(base + (k0 + 4 * g + a) * ld + c0 + b * cs);
+    const bf16x4 hi = ds_tr16(base + (k0 + 16 + 4 * g + a) * ld + c0 + b * cs);
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+__device__ __forceinline__ bf16x8 frag_trc(const bf16* base, int ld, int k0, int c0, int cs = 4) {
+    return frag_trc(lane(), base, ld, k0, c0, cs);
+}
+
 // frag_nat with an explicit row for this lane (row permutations).
 __device__ __forceinline__ bf16x8 frag_row(int l, const bf16* base, int ld, int row, int k0) {
     return *reinterpret_cast<const bf16x8*>(base + row * ld + k0 + 8 * (l >> 4));
