@@ -803,6 +803,7 @@ struct Problem {
     bool varlen;
     long slots;     // chunk slots launched for per-chunk kernels
     int nt;         // chunks per sequence (fixed-length case)
+    TokLd ld;       // token strides of q, k, v, dq, dk, dv (bf16 path)
 };
 
 // Workspace layouts.  The forward's layout is a prefix of the backward's:
@@ -929,10 +930,10 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
     const int H = p.H;
     if constexpr (__is_same(T, bf16)) {
         EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
-                    dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc, w.dcc);
+                    dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc, w.dcc, p.ld.k);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
                     dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, v, w.Tc, w.bc, si,
-                    H, S0, ST, o, w.h, w.Pc);
+                    H, S0, ST, o, w.h, w.Pc, p.ld);
         return (int)hipPeekAtLastError();
     }
     EFLA_LAUNCH("efla_q_fwd_prep", (fwd_prep_kernel<T, K, V>), dim3(p.slots, H), dim3(NTH), st,
@@ -960,11 +961,11 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
         const dim3 scan_grid(p.N * H * (V / fast::VS));
         if (!reuse)
             EFLA_LAUNCH("efla_q_bwd_re_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
-                        dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc, w.dcc);
+                        dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc, w.dcc, p.ld.k);
         if (!reuse_states)
             EFLA_LAUNCH("efla_q_bwd_re_state", (fast::scan_h_kernel<K, V>), scan_grid,
                         dim3(fast::NT), st, k, v, (const bf16*)w.Tc, (const float*)w.bc, si, H,
-                        S0, w.h);
+                        S0, w.h, p.ld);
         // persistent gradient kernel: one workgroup per CU (its LDS allows no
         // more), each looping over (chunk, head) items.  EFLA_GRAD_WORKGROUPS
         // caps the grid (tests use it to run many items per workgroup at
@@ -980,19 +981,19 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
         if (reuse_states) {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, true>), scan_grid,
                         dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
-                        (const bf16*)w.Pc, si, H, dST, dS0, w.dh);
+                        (const bf16*)w.Pc, si, H, dST, dS0, w.dh, p.ld);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true>), grad_grid,
                         dim3(fast::NT8), st, q, k, v, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const float*)w.dcc, (const bf16*)w.Pc, w.h, w.dh, si, H, nitems, dq, dk, dv,
-                        dbeta);
+                        dbeta, p.ld);
         } else {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, false>), scan_grid,
                         dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
-                        (const bf16*)nullptr, si, H, dST, dS0, w.dh);
+                        (const bf16*)nullptr, si, H, dST, dS0, w.dh, p.ld);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false>), grad_grid,
                         dim3(fast::NT8), st, q, k, v, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const float*)w.dcc, (const bf16*)nullptr, w.h, w.dh, si, H, nitems, dq, dk, dv,
-                        dbeta);
+                        dbeta, p.ld);
         }
         return (int)hipPeekAtLastError();
     } else if (!reuse) {
@@ -1068,6 +1069,8 @@ static int make_problem(const void* q, const void* k, const void* v, const void*
     p->T = p->varlen ? 0 : (long)seq_len;
     p->nt = p->varlen ? 0 : (int)((seq_len + BT - 1) / BT);
     p->slots = p->varlen ? (long)(ntok / BT + num_seqs) : (long)num_seqs * p->nt;
+    p->ld = TokLd{(long)(H * K), (long)(H * K), (long)(H * V), (long)(H * K), (long)(H * K),
+                  (long)(H * V)};
     if ((size_t)p->N * H > (size_t)INT32_MAX || (size_t)p->slots > (size_t)INT32_MAX)
         return kInvalidConfiguration;
     if (seq_len == 0) {
@@ -1129,18 +1132,47 @@ extern "C" size_t efla_chunk_bwd_workspace_size(size_t batch_size, size_t seq_le
                                : carve_bwd<float>(p, nullptr, nullptr);
 }
 
-extern "C" int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, const void* beta,
-                                  const float* initial_state, void* output, float* final_state,
-                                  const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
-                                  size_t num_seqs, size_t num_heads, size_t head_dim_k,
-                                  size_t head_dim_v, size_t chunk_size, int dtype,
-                                  void* workspace, size_t workspace_bytes, unsigned flags,
-                                  hipStream_t stream) {
+// Token strides of the strided entry points (NULL: packed), in the order
+// q, k, v[, dq, dk, dv].  A stride other than the packed one (H*K or H*V
+// elements) is at least that, a multiple of 8 elements (whole 16-byte row
+// pieces) and below 2^24 (the kernels' 32-bit offsets within a 64-token
+// chunk); its pointer must then be 16-byte aligned.  Only the bf16 kernels
+// take non-packed strides.
+static int apply_strides(Problem* p, const int64_t* ts, int n, int dtype,
+                         const void* const* ptrs) {
+    if (ts == nullptr) return kSuccess;
+    long ld[6] = {p->ld.q, p->ld.k, p->ld.v, p->ld.dq, p->ld.dk, p->ld.dv};
+    bool custom = false;
+    for (int i = 0; i < n; ++i) {
+        const int64_t s = ts[i];
+        if (s == ld[i]) continue;
+        if (s < ld[i] || s % 8 != 0 || s >= ((int64_t)1 << 24)) return kInvalidValue;
+        if (ptrs[i] != nullptr && ((uintptr_t)ptrs[i] & 15) != 0) return kInvalidValue;
+        if ((uint64_t)p->ntok * (uint64_t)s > ((uint64_t)1 << 46)) return kInvalidConfiguration;
+        ld[i] = (long)s;
+        custom = true;
+    }
+    if (custom && dtype != kDtypeBF16) return kNotSupported;
+    p->ld = TokLd{ld[0], ld[1], ld[2], ld[3], ld[4], ld[5]};
+    return kSuccess;
+}
+
+static int chunk_fwd(const void* q, const void* k, const void* v, const void* beta,
+                     const float* initial_state, void* output, float* final_state,
+                     const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                     size_t num_seqs, size_t num_heads, size_t head_dim_k, size_t head_dim_v,
+                     size_t chunk_size, int dtype, void* workspace, size_t workspace_bytes,
+                     unsigned flags, const int64_t* token_strides, hipStream_t stream) {
     Problem p;
     bool empty;
     int rc = make_problem(q, k, v, beta, cu_seqlens, batch_size, seq_len, num_seqs, num_heads,
                           head_dim_k, head_dim_v, chunk_size, dtype, &p, &empty);
     if (rc != kSuccess) return rc;
+    {
+        const void* ptrs[3] = {q, k, v};
+        rc = apply_strides(&p, token_strides, 3, dtype, ptrs);
+        if (rc != kSuccess) return rc;
+    }
     if ((flags & ~(unsigned)EFLA_FWD_SAVE_STATES) != 0) return kInvalidValue;
     const bool save = (flags & EFLA_FWD_SAVE_STATES) != 0;
     if (save && workspace == nullptr) return kInvalidValue;
@@ -1174,20 +1206,24 @@ extern "C" int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, c
     return kInvalidValue;
 }
 
-extern "C" int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, const void* beta,
-                                  const float* initial_state, const void* grad_output,
-                                  const float* grad_final_state, void* grad_q, void* grad_k,
-                                  void* grad_v, void* grad_beta, float* grad_initial_state,
-                                  const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
-                                  size_t num_seqs, size_t num_heads, size_t head_dim_k,
-                                  size_t head_dim_v, size_t chunk_size, int dtype,
-                                  void* workspace, size_t workspace_bytes, unsigned flags,
-                                  hipStream_t stream) {
+static int chunk_bwd(const void* q, const void* k, const void* v, const void* beta,
+                     const float* initial_state, const void* grad_output,
+                     const float* grad_final_state, void* grad_q, void* grad_k, void* grad_v,
+                     void* grad_beta, float* grad_initial_state, const int32_t* cu_seqlens,
+                     size_t batch_size, size_t seq_len, size_t num_seqs, size_t num_heads,
+                     size_t head_dim_k, size_t head_dim_v, size_t chunk_size, int dtype,
+                     void* workspace, size_t workspace_bytes, unsigned flags,
+                     const int64_t* token_strides, hipStream_t stream) {
     Problem p;
     bool empty;
     int rc = make_problem(q, k, v, beta, cu_seqlens, batch_size, seq_len, num_seqs, num_heads,
                           head_dim_k, head_dim_v, chunk_size, dtype, &p, &empty);
     if (rc != kSuccess) return rc;
+    {
+        const void* ptrs[6] = {q, k, v, grad_q, grad_k, grad_v};
+        rc = apply_strides(&p, token_strides, 6, dtype, ptrs);
+        if (rc != kSuccess) return rc;
+    }
     if ((flags & ~(unsigned)(EFLA_BWD_REUSE_FORWARD | EFLA_BWD_REUSE_STATES)) != 0)
         return kInvalidValue;
     const bool reuse = (flags & EFLA_BWD_REUSE_FORWARD) != 0;
@@ -1227,4 +1263,55 @@ extern "C" int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, c
                                       reuse, reuse_states, stream);
     }
     return kInvalidValue;
+}
+
+extern "C" int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, const void* beta,
+                                  const float* initial_state, void* output, float* final_state,
+                                  const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                                  size_t num_seqs, size_t num_heads, size_t head_dim_k,
+                                  size_t head_dim_v, size_t chunk_size, int dtype,
+                                  void* workspace, size_t workspace_bytes, unsigned flags,
+                                  hipStream_t stream) {
+    return chunk_fwd(q, k, v, beta, initial_state, output, final_state, cu_seqlens, batch_size,
+                     seq_len, num_seqs, num_heads, head_dim_k, head_dim_v, chunk_size, dtype,
+                     workspace, workspace_bytes, flags, nullptr, stream);
+}
+
+extern "C" int efla_chunk_fwd_strided_hip(
+    const void* q, const void* k, const void* v, const void* beta, const float* initial_state,
+    void* output, float* final_state, const int32_t* cu_seqlens, size_t batch_size,
+    size_t seq_len, size_t num_seqs, size_t num_heads, size_t head_dim_k, size_t head_dim_v,
+    size_t chunk_size, int dtype, void* workspace, size_t workspace_bytes, unsigned flags,
+    const int64_t* token_strides, hipStream_t stream) {
+    return chunk_fwd(q, k, v, beta, initial_state, output, final_state, cu_seqlens, batch_size,
+                     seq_len, num_seqs, num_heads, head_dim_k, head_dim_v, chunk_size, dtype,
+                     workspace, workspace_bytes, flags, token_strides, stream);
+}
+
+extern "C" int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, const void* beta,
+                                  const float* initial_state, const void* grad_output,
+                                  const float* grad_final_state, void* grad_q, void* grad_k,
+                                  void* grad_v, void* grad_beta, float* grad_initial_state,
+                                  const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                                  size_t num_seqs, size_t num_heads, size_t head_dim_k,
+                                  size_t head_dim_v, size_t chunk_size, int dtype,
+                                  void* workspace, size_t workspace_bytes, unsigned flags,
+                                  hipStream_t stream) {
+    return chunk_bwd(q, k, v, beta, initial_state, grad_output, grad_final_state, grad_q, grad_k,
+                     grad_v, grad_beta, grad_initial_state, cu_seqlens, batch_size, seq_len,
+                     num_seqs, num_heads, head_dim_k, head_dim_v, chunk_size, dtype, workspace,
+                     workspace_bytes, flags, nullptr, stream);
+}
+
+extern "C" int efla_chunk_bwd_strided_hip(
+    const void* q, const void* k, const void* v, const void* beta, const float* initial_state,
+    const void* grad_output, const float* grad_final_state, void* grad_q, void* grad_k,
+    void* grad_v, void* grad_beta, float* grad_initial_state, const int32_t* cu_seqlens,
+    size_t batch_size, size_t seq_len, size_t num_seqs, size_t num_heads, size_t head_dim_k,
+    size_t head_dim_v, size_t chunk_size, int dtype, void* workspace, size_t workspace_bytes,
+    unsigned flags, const int64_t* token_strides, hipStream_t stream) {
+    return chunk_bwd(q, k, v, beta, initial_state, grad_output, grad_final_state, grad_q, grad_k,
+                     grad_v, grad_beta, grad_initial_state, cu_seqlens, batch_size, seq_len,
+                     num_seqs, num_heads, head_dim_k, head_dim_v, chunk_size, dtype, workspace,
+                     workspace_bytes, flags, token_strides, stream);
 }

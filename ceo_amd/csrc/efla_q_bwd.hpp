@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
                                                     const bf16* __restrict__ Tc,
                                                     const float* __restrict__ bc, SeqInfo si,
                                                     int H, const float* __restrict__ S0,
-                                                    bf16* __restrict__ hist) {
+                                                    bf16* __restrict__ hist, TokLd ld) {
     constexpr int LDK = ldb<K>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanHSmem<K> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
@@ -101,7 +101,8 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
     auto prefetch = [&](int n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
-        pre.load(nullptr, k, v, Tc, bc, bos, len, H, h, V, v0, (long)(slot0 + n) * H + h);
+        pre.load(nullptr, k, v, Tc, bc, bos, len, h, V, v0, (long)(slot0 + n) * H + h, 0, ld.k,
+                 ld.v);
     };
     if (nch > 0) {
         prefetch(0);
@@ -161,7 +162,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
                                                      const bf16* __restrict__ Pc, SeqInfo si,
                                                      int H, const float* __restrict__ dST,
                                                      float* __restrict__ dS0,
-                                                     bf16* __restrict__ dhist) {
+                                                     bf16* __restrict__ dhist, TokLd ld) {
     constexpr int LDK = ldb<K>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanDhSmem<K, PS> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
@@ -191,7 +192,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
         const long cid = (long)(slot0 + n) * H + h;
-        pre.load(q, k, dO, Tc, bc, bos, len, H, h, V, v0, cid);
+        pre.load(q, k, dO, Tc, bc, bos, len, h, V, v0, cid, ld.q, ld.k, (long)H * V);
         if constexpr (PS) rp.load(Pc + cid * 64 * 64, 64, 64);
     };
     auto stage = [&](ScanDhBuf<K, PS>& bf) {
@@ -345,7 +346,7 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     const float* __restrict__ dcws, const bf16* __restrict__ Pws, const bf16* __restrict__ hist,
     const bf16* __restrict__ dhist, SeqInfo si, int H, int nitems,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
-    bf16* __restrict__ dbeta) {
+    bf16* __restrict__ dbeta, TokLd ld) {
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 32;  // NF key tiles per half
     __shared__ __attribute__((aligned(16))) GradSmem<K> sm;
     const int w8 = mf::wave(), tb = w8 & 3, hf = w8 >> 2;
@@ -365,7 +366,7 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     // copies into LDS (l: lane); each is issued by all waves
     auto copy_slice0 = [&](const Item& I, int par, int l) {
         const long cid = (long)I.slot * H + I.h, chb = cid * V * K;
-        mf::dma_tile<64, VS, LD64, 8>(sm.V, v + (I.bos * H + I.h) * V, (long)H * V, I.len, 0, l);
+        mf::dma_tile<64, VS, LD64, 8>(sm.V, v + I.bos * ld.v + (long)I.h * V, ld.v, I.len, 0, l);
         mf::dma_tile<64, VS, LD64, 8>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
         mf::dma_tile<64, K, LDK, 8>(sm.h, hist + chb, K, 64, 4, l);
         mf::dma_tile<64, K, LDK, 8>(sm.dh, dhist + chb, K, 64, 6, l);
@@ -376,14 +377,14 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         if (w8 == 6 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
     };
     auto copy_q = [&](const Item& I, int l) {
-        mf::dma_tile<64, K, LDK, 8>(sm.Qs, q + (I.bos * H + I.h) * K, (long)H * K, I.len, 3, l);
+        mf::dma_tile<64, K, LDK, 8>(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
     };
     auto copy_t = [&](const Item& I, int l) {
         mf::dma_tile<64, 64, LD64, 8>(sm.Tb, Tws + ((long)I.slot * H + I.h) * 64 * 64, 64, 64, 5,
                                       l);
     };
     auto copy_k = [&](const Item& I, int l) {
-        mf::dma_tile<64, K, LDK, 8>(sm.Ks, k + (I.bos * H + I.h) * K, (long)H * K, I.len, 1, l);
+        mf::dma_tile<64, K, LDK, 8>(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);
     };
 
     int it = blockIdx.x, par = 0;
@@ -409,7 +410,7 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     mf::TileRegs<64, K, NT8> rh, rdh;
     auto prefetch = [&](int s) {
         const int vv = s * VS;
-        rv.load(v + (bos * H + h) * V + vv, (long)H * V, len, tid);
+        rv.load(v + bos * ld.v + (long)h * V + vv, ld.v, len, tid);
         rd.load(dO + (bos * H + h) * V + vv, (long)H * V, len, tid);
         rh.load(hist + chb + (long)vv * K, K, 64, tid);
         rdh.load(dhist + chb + (long)vv * K, K, 64, tid);
@@ -513,7 +514,7 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
             static_assert(NT8 == 64 * (VS / 8), "one piece per thread");
             const int tt = tid / (VS / 8), f = 8 * (tid % (VS / 8));
             if (tt < len)
-                *reinterpret_cast<bf16x8*>(dv + ((bos + tt) * H + h) * V + vv + f) =
+                *reinterpret_cast<bf16x8*>(dv + (bos + tt) * ld.dv + (long)h * V + vv + f) =
                     *reinterpret_cast<const bf16x8*>(sm.V + tt * LD64 + f);
         }
         // dq^T += h^T dO^T; dk^T += dh^T Vn^T - h^T (D Y)^T  (key tiles f0 .. f0+NF-1)
@@ -668,9 +669,11 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         for (int i = tid; i < 64 * (K / 8); i += NT8) {
             const int tt = i / (K / 8), f = 8 * (i % (K / 8));
             if (tt < len) {
-                const long o = ((bos + tt) * H + h) * K + f;
-                *reinterpret_cast<bf16x8*>(dq + o) = *reinterpret_cast<const bf16x8*>(qs + tt * LDK + f);
-                *reinterpret_cast<bf16x8*>(dk + o) = *reinterpret_cast<const bf16x8*>(ks + tt * LDK + f);
+                const long o = (long)h * K + f;
+                *reinterpret_cast<bf16x8*>(dq + (bos + tt) * ld.dq + o) =
+                    *reinterpret_cast<const bf16x8*>(qs + tt * LDK + f);
+                *reinterpret_cast<bf16x8*>(dk + (bos + tt) * ld.dk + o) =
+                    *reinterpret_cast<const bf16x8*>(ks + tt * LDK + f);
             }
         }
     }

@@ -103,7 +103,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
                                                   const bf16* __restrict__ beta, SeqInfo si,
                                                   int H, bf16* __restrict__ Tout,
                                                   float* __restrict__ bout,
-                                                  float* __restrict__ dcout) {
+                                                  float* __restrict__ dcout, long ldk) {
     constexpr int LDK = ldb<K>();
     __shared__ __attribute__((aligned(16))) PrepSmem<K> sm;
     const int h = blockIdx.x, slot = blockIdx.y;  // heads fastest: one chunk's rows stay together
@@ -117,7 +117,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
                           ? (float)beta[(bos + threadIdx.x) * H + h] : 0.f;
     {
         mf::TileRegs<64, K, NT> kt;
-        kt.load(k + (bos * H + h) * K, (long)H * K, len);
+        kt.load(k + bos * ldk + (long)h * K, ldk, len);
         kt.store_rows(sm.u.Kr, LDK);
 #pragma unroll
         for (int j = 0; j < kt.TPT; ++j) {
@@ -261,10 +261,11 @@ struct ChunkRegs {
     float b;                      // thread < 64: b of token threadIdx.x
     __device__ __forceinline__ void load(const bf16* q, const bf16* k, const bf16* vsl,
                                          const bf16* Tc, const float* bc, long bos, int len,
-                                         int H, int h, int V, int v0, long cid) {
-        if (WITH_Q) rq.load(q + (bos * H + h) * K, (long)H * K, len);
-        rk.load(k + (bos * H + h) * K, (long)H * K, len);
-        rv.load(vsl + (bos * H + h) * V + v0, (long)H * V, len);
+                                         int h, int V, int v0, long cid, long lq, long lk,
+                                         long lv) {
+        if (WITH_Q) rq.load(q + bos * lq + (long)h * K, lq, len);
+        rk.load(k + bos * lk + (long)h * K, lk, len);
+        rv.load(vsl + bos * lv + (long)h * V + v0, lv, len);
         rt.load(Tc + cid * 64 * 64, 64, 64);
         if (threadIdx.x < 64) b = bc[cid * 64 + threadIdx.x];
     }
@@ -322,7 +323,7 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
                                                     float* __restrict__ ST,
                                                     bf16* __restrict__ o,
                                                     bf16* __restrict__ hist,
-                                                    bf16* __restrict__ pout) {
+                                                    bf16* __restrict__ pout, TokLd ld) {
     constexpr int LDK = ldb<K>(), LDP = ldb<64>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanSmem<K> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
@@ -350,7 +351,8 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
     auto prefetch = [&](int n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
-        pre.load(q, k, v, Tc, bc, bos, len, H, h, V, v0, (long)(slot0 + n) * H + h);
+        pre.load(q, k, v, Tc, bc, bos, len, h, V, v0, (long)(slot0 + n) * H + h, ld.q, ld.k,
+                 ld.v);
     };
     if (nch > 0) {
         prefetch(0);

@@ -32,6 +32,14 @@ __device__ __forceinline__ void seq_bounds(const SeqInfo& s, int seq, long& bos,
     }
 }
 
+// Elements between consecutive tokens of the head-sliced q, k, v inputs and
+// dq, dk, dv outputs of the bf16 kernels: H*K, H*K, H*V for packed
+// (tokens, H, D) arrays, more when each is a column slice of a wider row
+// (a fused projection).  grad_output, output and beta stay packed.
+struct TokLd {
+    long q, k, v, dq, dk, dv;
+};
+
 // Chunk slot -> first token and length; false for slots past the last chunk.
 __device__ __forceinline__ bool locate_chunk(const SeqInfo& s, int slot, long& bos, int& len) {
     if (s.cu == nullptr) {

@@ -34,12 +34,12 @@ def _stream(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def _require(t, name, dtype=None, device=None):
+def _require(t, name, dtype=None, device=None, contiguous=True):
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a tensor")
     if not t.is_cuda:
         raise ValueError(f"{name} must be a device tensor")
-    if not t.is_contiguous():
+    if contiguous and not t.is_contiguous():
         raise ValueError(f"{name} must be contiguous")
     if dtype is not None and t.dtype != dtype:
         raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
@@ -94,14 +94,31 @@ def efla_chunked_scan(chunk_states, num_heads: int, head_dim: int) -> None:
 # ---------------------------------------------------------------------------
 # chunked query readout
 # ---------------------------------------------------------------------------
+def token_stride(t: torch.Tensor, name: str = "tensor") -> int:
+    """Elements from one token's row to the next of a (B, T, H, D) tensor whose
+    heads are packed within each token row and whose batches follow each other
+    (a contiguous tensor, or a column slice of a wider per-token row such as a
+    fused projection, viewed as (B, T, H, D))."""
+    B, T, H, D = t.shape
+    if t.is_contiguous():
+        return H * D
+    s = t.stride()
+    ts = s[1] if T > 1 else (s[0] if B > 1 else H * D)
+    if s[3] != 1 or (H > 1 and s[2] != D) or (B > 1 and s[0] != T * ts):
+        raise ValueError(f"{name} must be contiguous or a token-strided view "
+                         "(heads packed within each token row)")
+    return ts
+
+
 def _q_shapes(q, k, v, beta, cu_seqlens):
     if q.dim() != 4 or k.shape != q.shape or v.dim() != 4 or v.shape[:3] != q.shape[:3]:
         raise ValueError("q, k must be (B,T,H,K) and v (B,T,H,V)")
     if beta.shape != q.shape[:3]:
         raise ValueError("beta must be (B,T,H)")
     dt = q.dtype
-    for t, n in ((q, "q"), (k, "k"), (v, "v"), (beta, "beta")):
-        _require(t, n, dt, q.device)
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _require(t, n, dt, q.device, contiguous=False)
+    _require(beta, "beta", dt, q.device)
     if dt not in (torch.bfloat16, torch.float32):
         raise ValueError(f"unsupported dtype {dt}")
     B, T, H, K = q.shape
@@ -138,11 +155,17 @@ def chunk_efla_fwd(q, k, v, beta, initial_state=None, output_final_state=False,
     st = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) \
         if output_final_state else None
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    rc = lib().efla_chunk_fwd_hip(_p(q), _p(k), _p(v), _p(beta), _p(initial_state), _p(o),
-                                  _p(st), _p(cu_seqlens), B, T, N if cu_seqlens is not None
-                                  else 0, H, K, V, 64, dt, _p(workspace), ws_bytes,
-                                  SAVE_STATES if save_states else 0, _stream(q))
-    check(rc, "efla_chunk_fwd_hip")
+    args = (_p(q), _p(k), _p(v), _p(beta), _p(initial_state), _p(o), _p(st), _p(cu_seqlens),
+            B, T, N if cu_seqlens is not None else 0, H, K, V, 64, dt, _p(workspace), ws_bytes,
+            SAVE_STATES if save_states else 0)
+    strides = [token_stride(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v"))]
+    if strides == [H * K, H * K, H * V]:
+        rc = lib().efla_chunk_fwd_hip(*args, _stream(q))
+        check(rc, "efla_chunk_fwd_hip")
+    else:
+        arr = (ctypes.c_int64 * 3)(*strides)
+        rc = lib().efla_chunk_fwd_strided_hip(*args, arr, _stream(q))
+        check(rc, "efla_chunk_fwd_strided_hip")
     return o, st
 
 
@@ -151,8 +174,12 @@ REUSE_STATES = 2  # EFLA_BWD_REUSE_STATES
 
 
 def chunk_efla_bwd(q, k, v, beta, do, initial_state=None, dht=None, cu_seqlens=None,
-                   workspace=None, reuse_forward=False, reuse_states=False):
+                   workspace=None, reuse_forward=False, reuse_states=False, grads_out=None):
     """Returns (dq, dk, dv, dbeta, dh0 or None).
+
+    ``grads_out`` = (dq, dk, dv): tensors shaped like q, k, v to write the
+    gradients into, which may be token-strided views (column slices of one
+    fused gradient row); by default new contiguous tensors.
 
     With ``reuse_forward`` the ``workspace`` must be the one the forward call on
     the same inputs used (untouched since): the per-chunk WY factors are taken
@@ -172,20 +199,33 @@ def chunk_efla_bwd(q, k, v, beta, do, initial_state=None, dht=None, cu_seqlens=N
             _require(t, n, torch.float32, q.device)
             if t.shape != (N, H, K, V):
                 raise ValueError(f"{n} must be (N,H,K,V) fp32")
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
+    if grads_out is None:
+        dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
+        dk = torch.empty(k.shape, dtype=q.dtype, device=q.device)
+        dv = torch.empty(v.shape, dtype=q.dtype, device=q.device)
+    else:
+        dq, dk, dv = grads_out
+        for t, ref, n in ((dq, q, "dq"), (dk, k, "dk"), (dv, v, "dv")):
+            _require(t, n, q.dtype, q.device, contiguous=False)
+            if t.shape != ref.shape:
+                raise ValueError(f"{n} must be shaped like {n[1:]}")
     db = torch.empty_like(beta)
     dh0 = torch.empty(N, H, K, V, dtype=torch.float32, device=q.device) \
         if initial_state is not None else None
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    rc = lib().efla_chunk_bwd_hip(_p(q), _p(k), _p(v), _p(beta), _p(initial_state), _p(do),
-                                  _p(dht), _p(dq), _p(dk), _p(dv), _p(db), _p(dh0),
-                                  _p(cu_seqlens), B, T, N if cu_seqlens is not None else 0, H,
-                                  K, V, 64, dt, _p(workspace), ws_bytes,
-                                  (REUSE_FORWARD if reuse_forward else 0)
-                                  | (REUSE_STATES if reuse_states else 0), _stream(q))
-    check(rc, "efla_chunk_bwd_hip")
+    args = (_p(q), _p(k), _p(v), _p(beta), _p(initial_state), _p(do), _p(dht), _p(dq), _p(dk),
+            _p(dv), _p(db), _p(dh0), _p(cu_seqlens), B, T,
+            N if cu_seqlens is not None else 0, H, K, V, 64, dt, _p(workspace), ws_bytes,
+            (REUSE_FORWARD if reuse_forward else 0) | (REUSE_STATES if reuse_states else 0))
+    strides = [token_stride(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v"), (dq, "dq"),
+                                                (dk, "dk"), (dv, "dv"))]
+    if strides == [H * K, H * K, H * V, H * K, H * K, H * V]:
+        rc = lib().efla_chunk_bwd_hip(*args, _stream(q))
+        check(rc, "efla_chunk_bwd_hip")
+    else:
+        arr = (ctypes.c_int64 * 6)(*strides)
+        rc = lib().efla_chunk_bwd_strided_hip(*args, arr, _stream(q))
+        check(rc, "efla_chunk_bwd_strided_hip")
     return dq, dk, dv, db, dh0
 
 

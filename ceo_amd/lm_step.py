@@ -62,6 +62,9 @@ class EflaLM:
         D, H, dh, F, V = cfg.d_model, cfg.n_heads, cfg.head_dim, cfg.mlp, cfg.vocab
         HD = H * dh
         self.proj = 3 * HD + H  # fused q, k, v, beta projection width
+        # the EFLA kernels read q, k, v and write their gradients in place in
+        # the fused rows when a row is whole 16-byte pieces
+        self.fused_io = self.proj % 8 == 0
         specs = [("embed", (V, D), "normal", math.sqrt(1.0 / D))]
         for i in range(cfg.n_layers):
             specs += [
@@ -112,6 +115,11 @@ class EflaLM:
     def gr(self, name):
         return self._view(self.grads, name)
 
+    def _io(self, cols: torch.Tensor) -> torch.Tensor:
+        """A column slice of a fused row as the EFLA kernels take it: itself
+        when the rows are whole 16-byte pieces, else a packed copy."""
+        return cols if self.fused_io else cols.contiguous()
+
     def _workspaces(self, B, T):
         """One backward-sized EFLA workspace per layer (T, b and chunk states
         handed from each layer's forward to its backward)."""
@@ -138,9 +146,9 @@ class EflaLM:
             a, m1, r1 = nn.layernorm_forward(x, self.w(L + "ln1.w"), self.w(L + "ln1.b"),
                                              cfg.ln_eps, save_stats=True)
             p = nn.gemm_forward(a, self.w(L + "w_in"))
-            q = p[:, 0:HD].contiguous().view(B, T, H, dh)
-            k = p[:, HD:2 * HD].contiguous().view(B, T, H, dh)
-            v = p[:, 2 * HD:3 * HD].contiguous().view(B, T, H, dh)
+            # q, k, v are read in place from the fused projection's rows
+            # (copied out when the row width is not whole 16-byte pieces)
+            q, k, v = (self._io(p[:, j * HD:(j + 1) * HD]).view(B, T, H, dh) for j in range(3))
             beta = torch.sigmoid(p[:, 3 * HD:].float()).to(torch.bfloat16).view(B, T, H)
             o, _ = efla.chunk_efla_fwd(q, k, v, beta, workspace=ws[i], save_states=True)
             o2 = o.view(N, HD)
@@ -198,12 +206,18 @@ class EflaLM:
             self.gr(L + "ln2.b").copy_(db)
             # x1 = x + o w_o, o = EFLA(q, k, v, beta)
             do, _, _ = nn.gemm_backward(dx1, s["o"], self.w(L + "w_o"), out_b=self.gr(L + "w_o"))
-            dq, dk, dv, dbeta, _ = efla.chunk_efla_bwd(
+            # dq, dk, dv are written in place into the fused projection's gradient
+            dp = torch.empty(N, 3 * HD + H, dtype=torch.bfloat16, device=self.device)
+            views = tuple(self._io(dp[:, j * HD:(j + 1) * HD]).view(B, T, H, dh)
+                          for j in range(3))
+            _, _, _, dbeta, _ = efla.chunk_efla_bwd(
                 s["q"], s["k"], s["v"], s["beta"], do.view(B, T, H, dh), workspace=ws[i],
-                reuse_forward=True, reuse_states=True)
+                reuse_forward=True, reuse_states=True, grads_out=views)
+            if not self.fused_io:
+                for j in range(3):
+                    dp[:, j * HD:(j + 1) * HD] = views[j].view(N, HD)
             bf = s["beta"].float()
-            dpb = (dbeta.float() * bf * (1.0 - bf)).to(torch.bfloat16)
-            dp = torch.cat([dq.view(N, HD), dk.view(N, HD), dv.view(N, HD), dpb.view(N, H)], 1)
+            dp[:, 3 * HD:] = (dbeta.float() * bf * (1.0 - bf)).view(N, H)
             da, _, _ = nn.gemm_backward(dp, s["a"], self.w(L + "w_in"), out_b=self.gr(L + "w_in"))
             # dx = dx1 + LN1's input gradient
             dx, dw, db = nn.layernorm_backward(da, s["x"], self.w(L + "ln1.w"), s["m1"], s["r1"],

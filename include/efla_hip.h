@@ -146,6 +146,38 @@ int efla_chunk_bwd_hip(const void* q, const void* k, const void* v, const void* 
                        size_t head_dim_v, size_t chunk_size, int dtype, void* workspace,
                        size_t workspace_bytes, unsigned flags, hipStream_t stream);
 
+/*
+ * No reference counterpart (the reference slices its projections into
+ * separate buffers).  efla_chunk_fwd_hip / efla_chunk_bwd_hip with explicit
+ * token strides, so q, k, v (and grad_q, grad_k, grad_v) can be column slices
+ * of one fused projection row, [q | k | v | beta-logit] per token, read and
+ * written in place without copies.  token_strides[i] is the number of
+ * elements from one token's row to the next's: q, k, v for the forward;
+ * q, k, v, grad_q, grad_k, grad_v for the backward; NULL means packed
+ * (H*d_k, H*d_k, H*d_v, ...).  Within a row, heads stay packed (head h at
+ * h*d).  output, grad_output and beta stay packed.  A non-packed stride must
+ * be at least the packed one, a multiple of 8 elements and below 2^24, with
+ * its pointer 16-byte aligned (else 1); non-packed strides with the fp32
+ * path return 801.  Everything else is as in the packed entry points.
+ */
+int efla_chunk_fwd_strided_hip(const void* q, const void* k, const void* v, const void* beta,
+                               const float* initial_state, void* output, float* final_state,
+                               const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                               size_t num_seqs, size_t num_heads, size_t head_dim_k,
+                               size_t head_dim_v, size_t chunk_size, int dtype,
+                               void* workspace, size_t workspace_bytes, unsigned flags,
+                               const int64_t* token_strides, hipStream_t stream);
+
+int efla_chunk_bwd_strided_hip(const void* q, const void* k, const void* v, const void* beta,
+                               const float* initial_state, const void* grad_output,
+                               const float* grad_final_state, void* grad_q, void* grad_k,
+                               void* grad_v, void* grad_beta, float* grad_initial_state,
+                               const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                               size_t num_seqs, size_t num_heads, size_t head_dim_k,
+                               size_t head_dim_v, size_t chunk_size, int dtype,
+                               void* workspace, size_t workspace_bytes, unsigned flags,
+                               const int64_t* token_strides, hipStream_t stream);
+
 /* No reference counterpart; the affine combine efla_chunked_scan_hip does not
  * do (efla.cu:711-748 sums states; src/model/efla.zig:473-484 is empty).
  * In place over consecutive segments of the same sequences:

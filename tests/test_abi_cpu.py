@@ -111,6 +111,46 @@ def test_chunk_fwd_flags(L):
     assert _fwd(L, flags=1, T=0) == 1   # flags are checked before the empty case
 
 
+def _fwd_strided(L, strides, q=16, B=2, T=128, dt=14):
+    vp = ctypes.c_void_p
+    arr = None if strides is None else (ctypes.c_int64 * 3)(*strides)
+    return L.efla_chunk_fwd_strided_hip(vp(q), vp(16), vp(16), vp(16), None, vp(16), None, None,
+                                        B, T, 0, 2, 64, 64, 64, dt, None, 0, 0, arr, None)
+
+
+def test_chunk_fwd_strided_validation(L):
+    # H = 2, d = 64: the packed token stride is 128 elements
+    assert _fwd_strided(L, [120, 128, 128]) == 1           # below the packed row
+    assert _fwd_strided(L, [132, 128, 128]) == 1           # not whole 16-byte pieces
+    assert _fwd_strided(L, [1 << 24, 128, 128]) == 1       # beyond 32-bit chunk offsets
+    assert _fwd_strided(L, [136, 128, 128], q=24) == 1     # pointer not 16-byte aligned
+    assert _fwd_strided(L, [128, 128, 128], q=24, T=0) == 0  # packed: no alignment rule
+    assert _fwd_strided(L, [136, 128, 128], dt=0) == 801   # fp32 path: packed only
+    assert _fwd_strided(L, [128, 128, 128], dt=0, T=0) == 0
+    assert _fwd_strided(L, [136, 256, 1000], T=0) == 0     # valid, nothing to do
+    assert _fwd_strided(L, None, T=0) == 0                 # NULL: packed
+    # the whole strided extent beyond 2^46 elements
+    assert _fwd_strided(L, [1 << 17, 128, 128], B=1 << 22, T=256) == 9
+
+
+def _bwd_strided(L, strides, dq=16, dt=14, T=128):
+    vp = ctypes.c_void_p
+    p = vp(16)
+    arr = (ctypes.c_int64 * 6)(*strides)
+    return L.efla_chunk_bwd_strided_hip(p, p, p, p, None, p, None, vp(dq), p, p, p, None, None,
+                                        2, T, 0, 2, 64, 64, 64, dt, None, 0, 0, arr, None)
+
+
+def test_chunk_bwd_strided_validation(L):
+    packed = [128] * 6
+    assert _bwd_strided(L, packed, T=0) == 0
+    assert _bwd_strided(L, [128, 128, 128, 120, 128, 128]) == 1   # gradient rows overlap
+    assert _bwd_strided(L, [128, 128, 128, 128, 128, 140]) == 1
+    assert _bwd_strided(L, [128, 128, 128, 392, 392, 392], dq=40) == 1
+    assert _bwd_strided(L, [392] * 6, dt=0) == 801
+    assert _bwd_strided(L, [392] * 6, T=0) == 0
+
+
 def test_workspace_sizes(L):
     f = L.efla_chunk_fwd_workspace_size
     b = L.efla_chunk_bwd_workspace_size

@@ -251,3 +251,80 @@ def test_grad_kernel_many_items_per_workgroup_vs_oracle(oracle, monkeypatch):
     lens = [1, 63, 64, 65, 130, 7, 0, 200]
     cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     _case(oracle, 43, 1, int(cu[-1]), 2, 128, 256, torch.bfloat16, s0=True, dst=True, cu=cu)
+
+
+# Token-strided I/O: q, k, v read as column slices of one fused row per token
+# and dq, dk, dv written into the slices of a fused gradient row, as a model
+# with a fused q/k/v/beta projection holds them.  The pad columns hold NaN, so
+# a read outside the slices would show in the outputs, and a write outside
+# them in the pad; the results must equal the packed call's bit for bit.
+def _fused(parts, pad, fill):
+    N = parts[0].shape[0] * parts[0].shape[1]
+    widths = [p.shape[2] * p.shape[3] for p in parts]
+    buf = torch.full((N, sum(widths) + pad), fill, dtype=torch.bfloat16, device="cuda:0")
+    views, c = [], 0
+    for p, w in zip(parts, widths):
+        buf[:, c:c + w] = p.reshape(N, w)
+        views.append(buf[:, c:c + w].view(p.shape))
+        c += w
+    return buf, views
+
+
+@pytest.mark.parametrize("reuse", [False, True], ids=["recompute", "reuse-states"])
+@pytest.mark.parametrize("layout", ["fixed", "varlen"])
+@pytest.mark.parametrize("K,V", [(64, 64), (128, 128), (64, 256)])
+def test_token_strided_io_bit_exact(oracle, K, V, layout, reuse):
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd, new_workspace, token_stride
+
+    announce(f"token-strided io K={K} V={V} {layout} reuse={reuse}")
+    H = 3
+    if layout == "fixed":
+        B, T, cu = 2, 200, None
+    else:
+        lens = [70, 1, 130, 0, 64, 99]
+        cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        B, T = 1, int(cu[-1])
+    N = B if cu is None else len(cu) - 1
+    x = oracle.make_efla_inputs(91 + K + V, B * T, H, K, V, bf16=True)
+    g = {n: to_dev(a, torch.bfloat16, (B, T, H, K) if n in "qk" else
+                   (B, T, H) if n == "beta" else (B, T, H, V)) for n, a in x.items()}
+    cu_t = None if cu is None else torch.tensor(cu, dtype=torch.int32, device="cuda:0")
+    rng = np.random.default_rng(5)
+    s0 = torch.from_numpy((rng.standard_normal((N, H, K, V)) * 0.3).astype(np.float32)).cuda()
+    dst = torch.from_numpy(rng.standard_normal((N, H, K, V)).astype(np.float32)).cuda()
+    nan = float("nan")
+    _, (q, k, v) = _fused([g["q"], g["k"], g["v"]], 24, nan)
+    assert token_stride(q) == H * (2 * K + V) + 24
+    gbuf, gviews = _fused([torch.empty_like(g["q"]), torch.empty_like(g["k"]),
+                           torch.empty_like(g["v"])], 24, nan)
+
+    def run(qq, kk, vv, grads_out):
+        ws = new_workspace(g["q"], g["v"], cu_t)
+        o, st = chunk_efla_fwd(qq, kk, vv, g["beta"], s0, True, cu_t, workspace=ws,
+                               save_states=reuse)
+        out = chunk_efla_bwd(qq, kk, vv, g["beta"], g["do"], s0, dst, cu_t, workspace=ws,
+                             reuse_forward=reuse, reuse_states=reuse, grads_out=grads_out)
+        torch.cuda.synchronize()
+        return [o.clone(), st.clone()] + [t.clone() for t in out]
+
+    ref = run(g["q"], g["k"], g["v"], None)
+    got = run(q, k, v, tuple(gviews))
+    for a, b, n in zip(got, ref, ("o", "S_T", "dq", "dk", "dv", "dbeta", "dS0")):
+        assert torch.equal(a, b), n
+    for a, b in zip(gviews, ref[2:5]):
+        assert torch.equal(a, b)
+    assert torch.isnan(gbuf[:, -24:]).all()  # nothing written outside the slices
+    assert all(torch.isfinite(t).all() for t in ref)
+
+
+def test_token_stride_rejects_other_layouts():
+    from ceo_amd.efla import token_stride
+
+    x = torch.zeros(2, 5, 3, 64, device="cuda:0", dtype=torch.bfloat16)
+    assert token_stride(x) == 192
+    assert token_stride(torch.zeros(2, 5, 400, device="cuda:0")[:, :, :192]
+                        .view(2, 5, 3, 64)) == 400
+    with pytest.raises(ValueError):
+        token_stride(x.transpose(1, 2))  # heads outside the token row
+    with pytest.raises(ValueError):
+        token_stride(torch.zeros(3, 5, 3, 64, device="cuda:0")[::2])  # a gap between batches

@@ -87,6 +87,32 @@ def test_step_gradients_match_autograd():
     print(f"  worst {worst:.2e}", flush=True)
 
 
+def test_fused_projection_io_matches_copied_io():
+    # 8 heads: the fused q/k/v/beta row (3 * 512 + 8 bf16) is whole 16-byte
+    # pieces, so the EFLA calls read q, k, v and write their gradients in place
+    # in it; with the copies they take packed tensors.  Same results, bit for bit.
+    from ceo_amd.lm_step import EflaLM, LMConfig, synthetic_batch
+
+    announce("lm step: fused-row EFLA io vs packed copies (8 heads)")
+    cfg = LMConfig(vocab=256, d_model=128, n_layers=2, n_heads=8, head_dim=64, mlp=512)
+    model = EflaLM(cfg, seed=5)
+    model.master.mul_(4.0)
+    model.weights.copy_(model.master)
+    tokens, targets = synthetic_batch(cfg, 2, 160, seed=6)
+    assert model.fused_io
+    res = []
+    for fused in (True, False):
+        model.fused_io = fused
+        loss, saved = model.forward(tokens, targets)
+        model.backward(saved)
+        torch.cuda.synchronize()
+        res.append((loss.clone(), model.grads.clone(), model.embed_grad.clone()))
+    assert torch.equal(res[0][0], res[1][0])
+    assert torch.equal(res[0][1], res[1][1])
+    assert torch.equal(res[0][2], res[1][2])
+    assert torch.isfinite(res[0][1].float()).all()
+
+
 def test_training_reduces_loss():
     from ceo_amd.lm_step import EflaLM, synthetic_batch
 
