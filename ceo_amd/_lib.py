@@ -104,6 +104,8 @@ _SIGS = {
                           i32, vp]),
     "gelu_forward_hip": (i32, [vp, vp, sz, ctypes.c_bool, vp]),
     "gelu_backward_hip": (i32, [vp, vp, vp, sz, ctypes.c_bool, vp]),
+    "sigmoid_gate_forward_hip": (i32, [vp, sz, vp, sz, sz, vp]),
+    "sigmoid_gate_backward_hip": (i32, [vp, vp, vp, sz, sz, sz, vp]),
     "adamw_step_hip": (i32, [vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, sz, vp]),
     "adamw_step_master_hip": (i32, [vp, vp, vp, vp, vp, sz, f32, f32, f32, f32, f32, sz, vp]),
     # embedding, cross-entropy

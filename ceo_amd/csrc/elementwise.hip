@@ -198,10 +198,75 @@ int adam_args(float lr, float beta1, float beta2, float eps, float weight_decay,
     return kSuccess;
 }
 
+// ---------------------------------------------------------------------------
+// Per-token beta gate of a fused projection row: the row ends in `cols` beta
+// logits at row stride `ld`; beta is packed (rows, cols).  fp32 math, bf16
+// rounding of each result, as torch's sigmoid(x.float()).to(bf16) forward and
+// (g.float() * b) * (1 - b) backward.
+// ---------------------------------------------------------------------------
+__global__ void __launch_bounds__(NTH) gate_fwd_kernel(const bf16* __restrict__ x, long ld,
+                                                       bf16* __restrict__ y, long n, int cols) {
+    for (long i = gid(); i < n; i += gstride()) {
+        const long r = i / cols;
+        const float v = (float)x[r * ld + (i - r * cols)];
+        y[i] = (bf16)(1.f / (1.f + expf(-v)));
+    }
+}
+
+__global__ void __launch_bounds__(NTH) gate_bwd_kernel(const bf16* __restrict__ g,
+                                                       const bf16* __restrict__ b,
+                                                       bf16* __restrict__ dx, long ld, long n,
+                                                       int cols) {
+    for (long i = gid(); i < n; i += gstride()) {
+        const long r = i / cols;
+        const float bb = (float)b[i];
+        dx[r * ld + (i - r * cols)] = (bf16)(((float)g[i] * bb) * (1.f - bb));
+    }
+}
+
 }  // namespace ew
 }  // namespace efla
 
 using namespace efla;
+
+static int gate_args(size_t ld, size_t rows, size_t cols, size_t* n) {
+    if (ld < cols || cols > (size_t)INT32_MAX) return kInvalidValue;
+    if (rows > ((size_t)1 << 40) || ld >= ((size_t)1 << 24)) return kInvalidConfiguration;
+    *n = rows * cols;
+    return kSuccess;
+}
+
+extern "C" int sigmoid_gate_forward_hip(const void* logits, size_t ld, void* beta, size_t rows,
+                                        size_t cols, hipStream_t stream) {
+    if (rows == 0 || cols == 0) return kSuccess;
+    if (!logits || !beta) return kInvalidValue;
+    size_t n;
+    const int rc = gate_args(ld, rows, cols, &n);
+    if (rc != kSuccess) return rc;
+    long n8;
+    dim3 grid;
+    ew::plan(n, false, &n8, &grid);
+    EFLA_LAUNCH("sigmoid_gate_fwd", ew::gate_fwd_kernel, grid, dim3(ew::NTH), stream,
+                (const bf16*)logits, (long)ld, (bf16*)beta, (long)n, (int)cols);
+    return (int)hipPeekAtLastError();
+}
+
+extern "C" int sigmoid_gate_backward_hip(const void* grad_beta, const void* beta,
+                                         void* grad_logits, size_t ld, size_t rows, size_t cols,
+                                         hipStream_t stream) {
+    if (rows == 0 || cols == 0) return kSuccess;
+    if (!grad_beta || !beta || !grad_logits) return kInvalidValue;
+    size_t n;
+    const int rc = gate_args(ld, rows, cols, &n);
+    if (rc != kSuccess) return rc;
+    long n8;
+    dim3 grid;
+    ew::plan(n, false, &n8, &grid);
+    EFLA_LAUNCH("sigmoid_gate_bwd", ew::gate_bwd_kernel, grid, dim3(ew::NTH), stream,
+                (const bf16*)grad_beta, (const bf16*)beta, (bf16*)grad_logits, (long)ld,
+                (long)n, (int)cols);
+    return (int)hipPeekAtLastError();
+}
 
 // gelu_forward_cuda (layernorm.cu:385-403) launches ceil(numel / 256) blocks
 // without checking numel: an empty grid, which the runtime rejects as an

@@ -14,9 +14,9 @@ the config and is left out.
 
 Kernels: embedding (lm.hip), LayerNorm (layernorm.hip), GEMMs (gemm.hip),
 chunked EFLA with the forward's T, b and chunk states handed to the backward
-(efla_q.hip), GELU and AdamW (elementwise.hip), cross-entropy (lm.hip).
-torch provides memory, the residual adds, the beta sigmoid and the
-slicing/packing of the fused q/k/v/beta projection.
+(efla_q.hip, reading q, k, v and writing their gradients in place in the
+fused q/k/v/beta projection rows), GELU, AdamW and the beta gate
+(elementwise.hip), cross-entropy (lm.hip).  torch provides memory and views.
 
 Parameters live in flat buffers: fp32 master weights, fp32 AdamW moments, a
 bf16 copy that the GEMMs read (each weight a contiguous view into it) and a
@@ -149,7 +149,7 @@ class EflaLM:
             # q, k, v are read in place from the fused projection's rows
             # (copied out when the row width is not whole 16-byte pieces)
             q, k, v = (self._io(p[:, j * HD:(j + 1) * HD]).view(B, T, H, dh) for j in range(3))
-            beta = torch.sigmoid(p[:, 3 * HD:].float()).to(torch.bfloat16).view(B, T, H)
+            beta = nn.sigmoid_gate_forward(p[:, 3 * HD:]).view(B, T, H)
             o, _ = efla.chunk_efla_fwd(q, k, v, beta, workspace=ws[i], save_states=True)
             o2 = o.view(N, HD)
             # x1 = x + o w_o with the residual added by the product's epilogue
@@ -216,8 +216,7 @@ class EflaLM:
             if not self.fused_io:
                 for j in range(3):
                     dp[:, j * HD:(j + 1) * HD] = views[j].view(N, HD)
-            bf = s["beta"].float()
-            dp[:, 3 * HD:] = (dbeta.float() * bf * (1.0 - bf)).view(N, H)
+            nn.sigmoid_gate_backward(dbeta.view(N, H), s["beta"].view(N, H), dp[:, 3 * HD:])
             da, _, _ = nn.gemm_backward(dp, s["a"], self.w(L + "w_in"), out_b=self.gr(L + "w_in"))
             # dx = dx1 + LN1's input gradient
             dx, dw, db = nn.layernorm_backward(da, s["x"], self.w(L + "ln1.w"), s["m1"], s["r1"],

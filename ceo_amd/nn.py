@@ -201,6 +201,35 @@ def gelu_backward(dy: torch.Tensor, x: torch.Tensor, approximate: bool = True) -
     return dx
 
 
+def sigmoid_gate_forward(logits: torch.Tensor) -> torch.Tensor:
+    """beta = bf16(sigmoid(float(logits))) of a (rows, cols) bf16 column block
+    (row stride free, e.g. the end of a fused projection row); beta is packed."""
+    if logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be (rows, cols) with unit column stride")
+    _require(logits, "logits", torch.bfloat16, contiguous=False)
+    rows, cols = logits.shape
+    beta = torch.empty(rows, cols, dtype=torch.bfloat16, device=logits.device)
+    rc = lib().sigmoid_gate_forward_hip(_p(logits), logits.stride(0), _p(beta), rows, cols,
+                                        _stream(logits))
+    check(rc, "sigmoid_gate_forward_hip")
+    return beta
+
+
+def sigmoid_gate_backward(dbeta: torch.Tensor, beta: torch.Tensor, out: torch.Tensor) -> None:
+    """out = bf16((float(dbeta) * b) * (1 - b)), b = float(beta), written into the
+    (rows, cols) block ``out`` (row stride free); dbeta, beta packed."""
+    _require(beta, "beta", torch.bfloat16)
+    _require(dbeta, "dbeta", torch.bfloat16, beta.device)
+    _require(out, "out", torch.bfloat16, beta.device, contiguous=False)
+    if beta.dim() != 2 or dbeta.shape != beta.shape or out.shape != beta.shape \
+            or out.stride(1) != 1:
+        raise ValueError("sigmoid_gate_backward: dbeta, beta, out must be (rows, cols)")
+    rows, cols = beta.shape
+    rc = lib().sigmoid_gate_backward_hip(_p(dbeta), _p(beta), _p(out), out.stride(0), rows,
+                                         cols, _stream(beta))
+    check(rc, "sigmoid_gate_backward_hip")
+
+
 def adamw_step(param, grad, exp_avg, exp_avg_sq, lr, beta1=0.9, beta2=0.999, eps=1e-8,
                weight_decay=0.0, step=1) -> None:
     """In-place AdamW step with bf16 parameters and state (the reference's layout)."""

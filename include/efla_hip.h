@@ -372,6 +372,20 @@ int adamw_step_master_hip(float* param, const void* grad, float* exp_avg, float*
                           void* param_bf16, size_t numel, float lr, float beta1, float beta2,
                           float eps, float weight_decay, size_t step, hipStream_t stream);
 
+/* No reference counterpart: the per-token beta gate of a model whose fused
+ * projection row ends in `cols` beta logits (the config-4 model, one logit
+ * per head).  beta[r*cols + c] = bf16(sigmoid(float(logits[r*ld + c]))) for
+ * r < rows, c < cols; fp32 math.  rows or cols == 0 -> 0; a NULL pointer or
+ * ld < cols -> 1; ld >= 2^24 or rows > 2^40 -> 9. */
+int sigmoid_gate_forward_hip(const void* logits, size_t ld, void* beta, size_t rows,
+                             size_t cols, hipStream_t stream);
+
+/* Its gradient: grad_logits[r*ld + c] = bf16((float(grad_beta[i]) * b) * (1 - b))
+ * with i = r*cols + c and b = float(beta[i]); grad_beta and beta packed
+ * (rows, cols).  Same return codes as sigmoid_gate_forward_hip. */
+int sigmoid_gate_backward_hip(const void* grad_beta, const void* beta, void* grad_logits,
+                              size_t ld, size_t rows, size_t cols, hipStream_t stream);
+
 /* ========================================================================
  * Token embedding and cross-entropy (the ends of the config-4 step)
  * ======================================================================== */

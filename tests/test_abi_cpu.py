@@ -151,6 +151,17 @@ def test_chunk_bwd_strided_validation(L):
     assert _bwd_strided(L, [392] * 6, T=0) == 0
 
 
+def test_sigmoid_gate_validation(L):
+    p = ctypes.c_void_p(16)
+    assert L.sigmoid_gate_forward_hip(p, 64, p, 0, 16, NULL) == 0      # nothing to do
+    assert L.sigmoid_gate_forward_hip(NULL, 64, p, 4, 16, NULL) == 1
+    assert L.sigmoid_gate_forward_hip(p, 8, p, 4, 16, NULL) == 1       # ld < cols
+    assert L.sigmoid_gate_forward_hip(p, 1 << 24, p, 4, 16, NULL) == 9
+    assert L.sigmoid_gate_backward_hip(p, p, p, 64, 4, 0, NULL) == 0
+    assert L.sigmoid_gate_backward_hip(p, NULL, p, 64, 4, 16, NULL) == 1
+    assert L.sigmoid_gate_backward_hip(p, p, p, 15, 4, 16, NULL) == 1
+
+
 def test_workspace_sizes(L):
     f = L.efla_chunk_fwd_workspace_size
     b = L.efla_chunk_bwd_workspace_size

@@ -293,3 +293,28 @@ def test_gemm_backward(m, k, n, gemm_backend):
     assert rel_l2(da, (dc.double() @ b.double().T).numpy()) <= 1e-2
     assert rel_l2(db, (a.double().T @ dc.double()).numpy()) <= 1e-2
     assert rel_l2(dbias, dc.double().sum(0).numpy()) <= 1e-2
+
+
+def test_sigmoid_gate_forward_backward_vs_torch():
+    # beta = sigmoid of the last H columns of a fused projection row, and its
+    # gradient written back into that block of the fused gradient row
+    from ceo_amd import nn
+
+    announce("sigmoid gate: fused-row block vs torch")
+    torch.manual_seed(7)
+    N, W, H = 3000, 3088, 16
+    p = (torch.randn(N, W, device="cuda:0") * 4).to(torch.bfloat16)
+    beta = nn.sigmoid_gate_forward(p[:, W - H:])
+    ref = torch.sigmoid(p[:, W - H:].float()).to(torch.bfloat16)
+    # fp32 sigmoid then bf16 rounding: at most one bf16 step apart from torch's
+    diff = (beta.float() - ref.float()).abs()
+    assert (diff <= ref.float().abs() * 2.0 ** -7).all()
+    print(f"  forward: {(diff > 0).sum().item()} of {N * H} differ by one bf16 step",
+          flush=True)
+    g = torch.randn(N, H, device="cuda:0").to(torch.bfloat16)
+    dp = torch.full((N, W), float("nan"), device="cuda:0", dtype=torch.bfloat16)
+    nn.sigmoid_gate_backward(g, beta, dp[:, W - H:])
+    bf = beta.float()
+    want = (g.float() * bf * (1.0 - bf)).to(torch.bfloat16)
+    assert torch.equal(dp[:, W - H:], want)
+    assert torch.isnan(dp[:, :W - H]).all()  # nothing written outside the block
