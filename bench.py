@@ -1,20 +1,30 @@
 """EFLA fwd+bwd throughput on one MI355X (the headline benchmark).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config cfg3|cfg2|cfg4|cfg5]
-                    [--no-cpu] [--cpu-budget SECONDS] [--aux]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--config cfg3|cfg1|cfg2|cfg4|cfg5] [--no-cpu] [--cpu-budget SECONDS]
+                    [--aux] [--no-recompute]
 
-A step is one chunked EFLA forward plus one backward (the backward recomputes
-the chunk states; nothing is carried over from the forward) over one batch of
-synthetic inputs already resident in HBM.  Default workload: configs[2] of the
-benchmark definition, B=4, T=8192, H=32, d_k=d_v=128, chunk 64, bf16 storage
-with fp32 accumulation.  W untimed steps, then K timed steps bracketed by
-torch.cuda.synchronize() and hipEvents on the launch stream.
+A step is one chunked EFLA forward plus one backward over one batch of
+synthetic inputs already resident in HBM.  As the library's autograd function
+runs it, the forward writes its per-chunk factors (T, b), chunk start states
+and P = tril(Q K^T) into a caller workspace and the backward reuses them, so
+the backward runs no forward recompute.  The design north_star names (the
+backward recomputes the chunk states instead of storing them) is timed in a
+second pass and reported as ``recompute``.  Default workload: configs[2] of
+the benchmark definition, B=4, T=8192, H=32, d_k=d_v=128, chunk 64, bf16
+storage with fp32 accumulation.
 
-Prints ONE JSON line with the metric, the per-kernel timing from the library's
-own launch events (recorded on the launch stream during the timed steps), the
-roofline of the dominant kernel and the step, and a CPU baseline: the scalar
-fp32 restatement of the same recurrence (oracle/, OpenMP over (sequence,
-head)) timed on a bounded sample of the same workload on this host.
+Timing: W untimed steps, then K timed steps between torch.cuda.synchronize()
+calls, with a hipEvent pair per step on the launch stream; ``ms_per_step`` is
+the median step (median of 50 timed steps after 10 warm-up
+steps, the defaults), ``mean_ms_per_step`` the mean.  The per-kernel split
+comes from a separate pass of K steps with the library's launch profiler
+(an event pair around each launch, which would inflate the timed steps).
+
+Prints ONE JSON line with the metric, the per-kernel split, the roofline of
+the dominant kernel and of the step, and a CPU baseline: the scalar fp32
+restatement of the same recurrence (oracle/, OpenMP over (sequence, head))
+timed on a bounded sample of the same workload on this host.
 """
 from __future__ import annotations
 
@@ -36,6 +46,7 @@ PEAK_HBM_GBS = 8000.0
 CONFIGS = {
     # name: (B, T, H, K, V, dtype, fwd+bwd?, varlen?)
     "cfg3": dict(B=4, T=8192, H=32, K=128, V=128, dtype="bf16", bwd=True, varlen=False),
+    "cfg1": dict(B=2, T=256, H=4, K=64, V=64, dtype="fp32", bwd=True, varlen=False),
     "cfg2": dict(B=8, T=2048, H=16, K=128, V=128, dtype="bf16", bwd=False, varlen=False),
     "cfg5": dict(B=1, T=65536, H=16, K=128, V=256, dtype="bf16", bwd=True, varlen=True),
 }
@@ -322,38 +333,66 @@ def aux_bench(steps: int, warmup: int) -> int:
         "gemm_up_bwd": (lambda: nn.gemm_backward(dcu, x, wu, need_bias=False), 4.0 * N * D * F),
     }
     out = {}
-    for name, (fn, flops) in gemms.items():
-        for _ in range(warmup):
+    stream = torch.cuda.current_stream(dev)
+
+    def run(fn, n_warm, n):
+        """Average ms per call over n back-to-back calls between one event pair
+        (no per-launch events), then the per-kernel split from a profiled pass."""
+        for _ in range(n_warm):
             fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        avg = e0.elapsed_time(e1) / n
         with runtime.Profiler() as prof:
-            for _ in range(steps):
+            for _ in range(n):
                 fn()
         res = prof.results()
-        avg_ms = sum(tot for _, tot in res.values()) / steps
+        return avg, {k: round(tot / cnt, 4) for k, (cnt, tot) in res.items()}
+
+    for name, (fn, flops) in gemms.items():
+        avg_ms, kms = run(fn, warmup, steps)
         tf = flops / (avg_ms * 1e-3) / 1e12
         out[name] = {"avg_ms": round(avg_ms, 4), "flops": flops, "TFLOP/s": round(tf, 1),
                      "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "kernels_ms": {k: round(tot / n, 4) for k, (n, tot) in res.items()}}
+                     "kernels_ms": kms}
         print(f"[bench] {name}: {avg_ms:.4f} ms, {tf:.0f} TFLOP/s", file=sys.stderr, flush=True)
     del xu, dcu
     for name, (fn, nbytes, what) in cases.items():
-        for _ in range(warmup):
-            fn()
-        torch.cuda.synchronize()
-        with runtime.Profiler() as prof:
-            for _ in range(steps):
-                fn()
-        res = prof.results()
         # the op's time: every kernel it launched (LayerNorm's backward has a
         # second, small reduction kernel), averaged over the timed calls
-        avg_ms = sum(tot for _, tot in res.values()) / steps
+        avg_ms, kms = run(fn, warmup, steps)
         gbs = nbytes / (avg_ms * 1e-3) / 1e9
         out[name] = {"avg_ms": round(avg_ms, 4), "bytes": nbytes, "bytes_are": what,
                      "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
-                     "kernels_ms": {k: round(tot / n, 4) for k, (n, tot) in res.items()}}
+                     "kernels_ms": kms}
         print(f"[bench] {name}: {avg_ms:.4f} ms, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
-    print(json.dumps({"aux": "config-4 kernels around EFLA", "shapes": CFG4, "steps": steps,
+    del cases, x, dy, h, dh, p32, m32, v32, gp, pcopy
+    # the reference ABI's entries (efla_forward_hip / efla_backward_hip, Mode R:
+    # scalar beta, key readout, bf16 state rounded per token) at cfg3's shape
+    from ceo_amd import efla
+
+    B, T, H, d = 4, 8192, 32, 128
+    kr = torch.randn(B, T, H, d, generator=g, device=dev)
+    kr = (kr / kr.norm(dim=-1, keepdim=True)).to(torch.bfloat16)
+    vr, dor = bf(B, T, H, d), bf(B, T, H, d)
+    s0 = torch.zeros(B * H, d, d, dtype=torch.bfloat16, device=dev)
+    state = s0.clone()
+    mode_r = {
+        "efla_forward_hip_cfg3": lambda: efla.efla_forward(kr, vr, state.copy_(s0), 0.5, 64),
+        "efla_backward_hip_cfg3": lambda: efla.efla_backward(dor, kr, vr, s0, 0.5),
+    }
+    for name, fn in mode_r.items():
+        avg_ms, kms = run(fn, 1, 3)
+        out[name] = {"avg_ms": round(avg_ms, 3), "tokens_per_s": round(B * T / (avg_ms * 1e-3), 1),
+                     "shape": f"B={B} T={T} H={H} d={d} bf16", "kernels_ms": kms}
+        print(f"[bench] {name}: {avg_ms:.3f} ms", file=sys.stderr, flush=True)
+    print(json.dumps({"aux": "config-4 kernels around EFLA, and the reference-ABI EFLA "
+                             "entries at cfg3's shape", "shapes": CFG4, "steps": steps,
                       "kernels": out}), flush=True)
     return 0
 
@@ -439,10 +478,12 @@ def lm_bench(steps: int, warmup: int, seed: int) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="cfg3", choices=sorted(CONFIGS) + ["cfg4"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-recompute", action="store_true",
+                    help="skip the pass timing the recompute variant")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (whole sequences, at least one)")
     ap.add_argument("--seed", type=int, default=0xEF1A0002)
@@ -486,7 +527,7 @@ def main() -> int:
           file=sys.stderr, flush=True)
 
     # one workspace for both calls, as the autograd function uses it: the
-    # forward leaves its per-chunk WY factors and chunk start states there and
+    # forward leaves its per-chunk factors, chunk start states and P there and
     # the backward reads them instead of recomputing them
     ws = efla.new_workspace(x["q"], x["v"], cu)
 
@@ -498,27 +539,55 @@ def main() -> int:
                                 workspace=ws, reuse_forward=True, reuse_states=True)
         return o
 
+    def step_recompute():
+        # north_star's design: nothing handed over, the backward rebuilds the
+        # chunk factors and states (into the library's cached workspace)
+        efla.chunk_efla_fwd(x["q"], x["k"], x["v"], x["beta"], cu_seqlens=cu)
+        efla.chunk_efla_bwd(x["q"], x["k"], x["v"], x["beta"], x["do"], cu_seqlens=cu)
+
+    stream = torch.cuda.current_stream(dev)
+
+    def timed(fn, n):
+        """Per-step milliseconds from a hipEvent pair per step on the launch
+        stream, and the total between the first and the last event."""
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+        torch.cuda.synchronize()
+        evs[0].record(stream)
+        for i in range(n):
+            fn()
+            evs[i + 1].record(stream)
+        torch.cuda.synchronize()
+        per = [evs[i].elapsed_time(evs[i + 1]) for i in range(n)]
+        return per, evs[0].elapsed_time(evs[n])
+
+    def median(xs):
+        ys = sorted(xs)
+        m = len(ys) // 2
+        return ys[m] if len(ys) % 2 else 0.5 * (ys[m - 1] + ys[m])
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     print(f"[bench] warmup done ({args.warmup} steps)", file=sys.stderr, flush=True)
-
-    stream = torch.cuda.current_stream(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
+    per_step, ms_total = timed(step, args.steps)
+    ms_step = median(per_step)
+    print(f"[bench] timed {args.steps} steps: median {ms_step:.4f} ms/step, "
+          f"mean {ms_total / args.steps:.4f}", file=sys.stderr, flush=True)
+    # the per-kernel split, from a second pass with the launch profiler
     prof = runtime.Profiler()
-    torch.cuda.synchronize()
     with prof:
-        ev0.record(stream)
-        for _ in range(args.steps):
-            step()
-        ev1.record(stream)
-    torch.cuda.synchronize()
-    ms_total = ev0.elapsed_time(ev1)
-    ms_step = ms_total / args.steps
+        _, prof_total = timed(step, args.steps)
     kern = prof.results()
-    print(f"[bench] timed {args.steps} steps: {ms_step:.3f} ms/step", file=sys.stderr,
+    print(f"[bench] profiled pass: {prof_total / args.steps:.4f} ms/step", file=sys.stderr,
           flush=True)
+    recompute = None
+    if cfg["bwd"] and not args.no_recompute:
+        for _ in range(args.warmup):
+            step_recompute()
+        per_re, _ = timed(step_recompute, args.steps)
+        recompute = median(per_re)
+        print(f"[bench] recompute variant: median {recompute:.4f} ms/step", file=sys.stderr,
+              flush=True)
 
     # FLOPs / bytes
     if cu is not None:
@@ -536,10 +605,12 @@ def main() -> int:
         fl = per_chunk.get(name, 0.0) * n_chunks * H
         kernels[name] = {
             "launches": launches, "avg_ms": round(avg_ms, 4),
-            "share": round(tot_ms / max(ms_total, 1e-9), 4),
+            "share": round(tot_ms / max(prof_total, 1e-9), 4),
             "tflops": round(fl / (avg_ms * 1e-3) / 1e12, 2) if fl else None,
         }
     dom = max(kern.items(), key=lambda kv: kv[1][1])[0] if kern else None
+    # the MFMA rate the path computes at: bf16 operands, or fp32 for cfg1
+    peak = PEAK_BF16_TFLOPS if cfg["dtype"] == "bf16" else PEAK_FP32_TFLOPS
     roof = None
     if dom is not None:
         launches, tot_ms = kern[dom]
@@ -548,8 +619,8 @@ def main() -> int:
         ach = fl / (avg_ms * 1e-3) / 1e12
         traffic = measured_traffic(args.config, dom)
         roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2),
-                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                "peak": peak, "unit": "TFLOP/s",
+                "frac": round(ach / peak, 4),
                 "traffic": traffic,
                 "avg_ms": round(avg_ms, 4),
                 "flops_per_launch": fl}
@@ -559,7 +630,15 @@ def main() -> int:
             roof["hbm"] = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
                            "frac": round(gbs / PEAK_HBM_GBS, 4)}
     step_tflops = step_flops / (ms_step * 1e-3) / 1e12
-    io = io_bytes(ntok, H, K, V, cfg["bwd"])
+    io = io_bytes(ntok, H, K, V, cfg["bwd"], esize=2 if cfg["dtype"] == "bf16" else 4)
+    if recompute is not None:
+        recompute = {
+            "what": "north_star's design: no workspace handed over, the backward "
+                    "recomputes the chunk factors and states",
+            "ms_per_step": round(recompute, 4),
+            "tokens_per_s": round(ntok / (recompute * 1e-3), 1),
+            "pct_mfma_peak": round(100 * step_flops / (recompute * 1e-3) / 1e12 / peak, 3),
+        }
 
     cpu = None
     if not args.no_cpu:
@@ -576,6 +655,8 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "mean_ms_per_step": round(ms_total / args.steps, 4),
+        "timing": "median of the timed steps (hipEvent pair per step on the launch stream)",
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -587,10 +668,13 @@ def main() -> int:
                                f"{cfg['dtype']}{' varlen' if cu is not None else ''}",
                    "tokens_per_step": ntok, "parallelism": "single GPU"},
         "pct_bf16_mfma_peak": round(100 * step_tflops / PEAK_BF16_TFLOPS, 3),
+        "pct_mfma_peak": round(100 * step_tflops / peak, 3),
+        "mfma_peak_tflops": peak,
         "step_tflops": round(step_tflops, 2),
         "step_flops": step_flops,
         "step_io_gbs": round(io / (ms_step * 1e-3) / 1e9, 1),
         "roofline": roof,
+        "recompute": recompute,
         "kernels": kernels,
         "cpu_baseline": cpu,
         "device": {"arch": info["arch"], "cus": info["compute_units"],

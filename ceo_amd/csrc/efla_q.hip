@@ -1188,8 +1188,9 @@ static int chunk_fwd(const void* q, const void* k, const void* v, const void* be
     const size_t need = dtype == kDtypeBF16 ? carve_fwd<bf16>(p, nullptr, nullptr, save)
                                             : carve_fwd<float>(p, nullptr, nullptr, save);
     void* ws = workspace;
+    WsLease lease;
     if (ws == nullptr) {
-        rc = workspace_acquire(need, stream, &ws);
+        rc = workspace_acquire(need, stream, &ws, lease);
         if (rc != kSuccess) return rc;
     } else if (workspace_bytes < need) {
         return kInvalidValue;
@@ -1242,8 +1243,9 @@ static int chunk_bwd(const void* q, const void* k, const void* v, const void* be
     const size_t need = dtype == kDtypeBF16 ? carve_bwd<bf16>(p, nullptr, nullptr)
                                             : carve_bwd<float>(p, nullptr, nullptr);
     void* ws = workspace;
+    WsLease lease;
     if (ws == nullptr) {
-        rc = workspace_acquire(need, stream, &ws);
+        rc = workspace_acquire(need, stream, &ws, lease);
         if (rc != kSuccess) return rc;
     } else if (workspace_bytes < need) {
         return kInvalidValue;

@@ -352,7 +352,8 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
     const size_t off_g = (off_hist + hist_elems * 2 + 255) & ~(size_t)255;
     const size_t need = off_g + g_elems * 4 + 256;
     void* ws = nullptr;
-    int rc = workspace_acquire(need, stream, &ws);
+    WsLease lease;
+    int rc = workspace_acquire(need, stream, &ws, lease);
     if (rc != kSuccess) return rc;
     bf16* ck = (bf16*)ws;
     bf16* hist = (bf16*)((char*)ws + off_hist);
@@ -387,7 +388,8 @@ extern "C" int efla_chunked_scan_hip(void** chunk_states, size_t num_chunks, siz
     size_t pbytes;
     if (!mul_ok(num_chunks, sizeof(void*), &pbytes)) return kInvalidConfiguration;
     void* ws = nullptr;
-    int rc = workspace_acquire(pbytes, stream, &ws);
+    WsLease lease;
+    int rc = workspace_acquire(pbytes, stream, &ws, lease);
     if (rc != kSuccess) return rc;
     // pageable source: the runtime stages it before returning, so the caller's
     // array may be released as soon as this call returns

@@ -2,8 +2,8 @@
 // (kernels/cuda/gemm.cu:182-234, 303-548).
 //
 // Matching bf16 / fp16 / fp32 operands go to hipBLASLt (a plain library GEMM,
-// as the reference's cuBLAS call is): one handle and one 128 MiB workspace per
-// device, created on first use and kept; the chosen algorithm and descriptors
+// as the reference's cuBLAS call is): one handle per device, created on first
+// use and kept, and the library's cached workspace of the calling stream; the chosen algorithm and descriptors
 // are cached per (shape, transposes, dtype, bias) so a steady-state call does
 // no heuristic query and no device allocation.  The row-major product
 // C = A B is issued as the column-major C^T = B^T A^T, the bias as the
@@ -337,7 +337,6 @@ constexpr int kMaxDev = 64;
 
 struct LtDevice {
     hipblasLtHandle_t handle = nullptr;
-    void* ws = nullptr;
     bool broken = false;  // creation failed: always use the native kernel
 };
 
@@ -369,13 +368,6 @@ static LtDevice* lt_device(int dev) {
     if (!d.handle) {
         if (hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) {
             d.handle = nullptr;
-            d.broken = true;
-            return nullptr;
-        }
-        if (hipMalloc(&d.ws, kLtWorkspace) != hipSuccess) {
-            hipblasLtDestroy(d.handle);
-            d.handle = nullptr;
-            d.ws = nullptr;
             d.broken = true;
             return nullptr;
         }
@@ -464,13 +456,20 @@ static int lt_matmul(hipblasOperation_t ta, hipblasOperation_t tb, long M, long 
     }
     LtPlan& p = it->second;
     if (!p.ok) return -1;
+    // the library workspace of this stream (slot 1), held while the product is queued
+    void* ws = nullptr;
+    WsLease lease;
+    if (p.ws_bytes) {
+        const int rc = workspace_acquire(p.ws_bytes, stream, &ws, lease, 1);
+        if (rc != kSuccess) return rc;
+    }
     if (bias)
         hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias,
                                         sizeof(bias));
     ::efla::ProfScope ps("gemm_hipblaslt", stream);
     const hipblasStatus_t st =
         hipblasLtMatmul(d->handle, p.desc, &alpha, A, p.a, B, p.b, &beta, C ? C : D, p.c, D, p.d,
-                        &p.algo, d->ws, p.ws_bytes, stream);
+                        &p.algo, ws, p.ws_bytes, stream);
     if (st != HIPBLAS_STATUS_SUCCESS) return kInvalidValue;
     return (int)hipPeekAtLastError();
 }
@@ -581,8 +580,10 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
     }
     if (need_bias && m && n) {
         void* ws = nullptr;
+        WsLease lease;
         if (N % 8 == 0 && aligned16(grad_c) &&
-            workspace_acquire((size_t)CS_RS * N * sizeof(float), stream, &ws) == kSuccess) {
+            workspace_acquire((size_t)CS_RS * N * sizeof(float), stream, &ws, lease) ==
+                kSuccess) {
             EFLA_LAUNCH("gemm_bwd_dbias", colsum_part_kernel,
                         dim3((unsigned)((N + 127) / 128), CS_RS), dim3(NTH), stream,
                         (const bf16*)grad_c, (float*)ws, M, N);

@@ -71,11 +71,30 @@ struct ProfScope {
     } while (0)
 
 // --- workspace ------------------------------------------------------------
-// Returns a device buffer of at least `bytes` owned by the library for the
-// current device.  Growing it synchronises `stream` first (the previous buffer
-// may still be in use by work queued on it) and then reallocates; steady-state
-// calls allocate nothing.
-int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr);
+// The library's cached scratch buffers, one per (device, stream, slot).  A
+// call that needs scratch takes a lease on the buffer of its own stream and
+// keeps it until its kernels are queued: the lease holds the buffer's lock, so
+// two host threads on one stream take turns, and callers on different streams
+// never share memory.  A buffer that has to grow is freed only after its
+// stream has drained (every earlier user of it queued its work on that
+// stream, under the same lock), then reallocated; steady-state calls allocate
+// nothing.  Slot 0 is general scratch, slot 1 the GEMM library's workspace.
+struct WsEntry;
+class WsLease {
+   public:
+    WsLease() = default;
+    WsLease(const WsLease&) = delete;
+    WsLease& operator=(const WsLease&) = delete;
+    ~WsLease() { release(); }
+    void release();
+    WsEntry* entry = nullptr;
+};
+
+// Returns in *ptr a buffer of at least `bytes` for `stream` on the current
+// device, valid while `lease` is held.  A lease covers one buffer; a caller
+// never takes a second lease on the same (stream, slot) while holding one.
+int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr, WsLease& lease,
+                      int slot = 0);
 
 // Zero-fill through a kernel (no hipMemsetAsync, so the call is safe inside
 // stream capture).

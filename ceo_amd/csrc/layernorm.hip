@@ -383,9 +383,10 @@ static int ln_backward(const void* grad_output, const void* input, const void* w
     size_t nblk = (rows + 3) / 4;
     if (nblk > 512) nblk = 512;
     float* part = nullptr;
+    WsLease lease;
     if (params) {
         void* ws = nullptr;
-        int rc = workspace_acquire(nblk * 2 * D * sizeof(float), stream, &ws);
+        int rc = workspace_acquire(nblk * 2 * D * sizeof(float), stream, &ws, lease);
         if (rc != kSuccess) return rc;
         part = (float*)ws;
     }

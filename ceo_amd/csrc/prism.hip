@@ -643,7 +643,8 @@ extern "C" int shortconv_backward_hip(const void* grad_output, const void* input
             nsplit = std::max(1L, std::min((long)B * T, 4096L / (long)prism::grid_1d(cw)));
         }
         void* ws = nullptr;
-        const int wrc = workspace_acquire((size_t)nsplit * cw * sizeof(float), stream, &ws);
+        WsLease lease;
+        const int wrc = workspace_acquire((size_t)nsplit * cw * sizeof(float), stream, &ws, lease);
         if (wrc != kSuccess) return wrc;
         float* part = (float*)ws;
         if (tiled) {

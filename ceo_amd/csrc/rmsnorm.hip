@@ -231,9 +231,10 @@ extern "C" int rmsnorm_backward_hip(const void* grad_output, const void* input,
     size_t nblk = (rows + rms::RPB - 1) / rms::RPB;
     if (nblk > 512) nblk = 512;
     float* part = nullptr;
+    WsLease lease;
     if (grad_weight) {
         void* ws = nullptr;
-        const int rc = workspace_acquire(nblk * D * sizeof(float), stream, &ws);
+        const int rc = workspace_acquire(nblk * D * sizeof(float), stream, &ws, lease);
         if (rc != kSuccess) return rc;
         part = (float*)ws;
     }

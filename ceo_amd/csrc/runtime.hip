@@ -5,8 +5,10 @@
 
 #include <atomic>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <vector>
 
 #include "../../include/efla_runtime.h"
@@ -111,8 +113,6 @@ void prof_end(void* token, hipStream_t stream) {
     const size_t idx = (size_t)(uintptr_t)token - 1;
     if (idx < s.pending.size()) (void)hipEventRecord(s.pending[idx].e1, stream);
 }
-
-int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr);
 
 }  // namespace efla
 
@@ -277,35 +277,53 @@ int efla_rt_event_elapsed_ms(float* ms, hipEvent_t start, hipEvent_t stop) {
 // workspace
 // ---------------------------------------------------------------------------
 namespace efla {
-namespace {
-struct Ws {
+
+struct WsEntry {
+    std::mutex mu;  // held by the lease for as long as a caller uses the buffer
     void* ptr = nullptr;
     size_t bytes = 0;
 };
-std::mutex g_ws_mu;
-std::map<int, Ws> g_ws;
+
+namespace {
+typedef std::tuple<int, hipStream_t, int> WsKey;  // (device, stream, slot)
+std::mutex g_ws_mu;                                // guards the map, not the entries
+std::map<WsKey, std::unique_ptr<WsEntry>> g_ws;
+
+WsEntry* ws_entry(int dev, hipStream_t stream, int slot) {
+    std::lock_guard<std::mutex> g(g_ws_mu);
+    std::unique_ptr<WsEntry>& e = g_ws[WsKey(dev, stream, slot)];
+    if (!e) e.reset(new WsEntry);
+    return e.get();  // entries are never erased, so the pointer stays valid
+}
 }  // namespace
 
-int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr) {
+void WsLease::release() {
+    if (entry) entry->mu.unlock();
+    entry = nullptr;
+}
+
+int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr, WsLease& lease, int slot) {
+    if (lease.entry) return kInvalidValue;  // one buffer per lease
     int dev = 0;
     EFLA_CHECK(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> g(g_ws_mu);
-    Ws& w = g_ws[dev];
-    if (w.bytes < bytes) {
-        if (w.ptr) {
+    WsEntry* e = ws_entry(dev, stream, slot);
+    e->mu.lock();
+    lease.entry = e;
+    if (e->bytes < bytes) {
+        if (e->ptr) {
+            // every earlier user of this buffer queued its work on `stream`
             EFLA_CHECK(hipStreamSynchronize(stream));
-            EFLA_CHECK(hipDeviceSynchronize());
-            EFLA_CHECK(hipFree(w.ptr));
-            w.ptr = nullptr;
-            w.bytes = 0;
+            EFLA_CHECK(hipFree(e->ptr));
+            e->ptr = nullptr;
+            e->bytes = 0;
         }
         // round up to 64 MiB steps so slowly growing problems do not realloc
         const size_t step = (size_t)64 << 20;
         const size_t want = (bytes + step - 1) / step * step;
-        EFLA_CHECK(hipMalloc(&w.ptr, want));
-        w.bytes = want;
+        EFLA_CHECK(hipMalloc(&e->ptr, want));
+        e->bytes = want;
     }
-    *ptr = w.ptr;
+    *ptr = e->ptr;
     return kSuccess;
 }
 
@@ -324,22 +342,45 @@ int device_cu_count() {
 }
 }  // namespace efla
 
+namespace efla {
+namespace {
+// the current device's entries; the map lock is not held
+// while an entry is locked (a lease holder may be waiting for the map lock)
+std::vector<WsEntry*> device_entries(int dev) {
+    std::vector<WsEntry*> out;
+    std::lock_guard<std::mutex> g(g_ws_mu);
+    for (auto& kv : g_ws)
+        if (std::get<0>(kv.first) == dev) out.push_back(kv.second.get());
+    return out;
+}
+}  // namespace
+}  // namespace efla
+
 extern "C" size_t efla_rt_workspace_bytes(void) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
-    std::lock_guard<std::mutex> g(efla::g_ws_mu);
-    auto it = efla::g_ws.find(dev);
-    return it == efla::g_ws.end() ? 0 : it->second.bytes;
+    size_t total = 0;
+    for (efla::WsEntry* e : efla::device_entries(dev)) {
+        std::lock_guard<std::mutex> ge(e->mu);
+        total += e->bytes;
+    }
+    return total;
 }
 
 extern "C" int efla_rt_workspace_release(void) {
     int dev = 0;
     EFLA_CHECK(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> g(efla::g_ws_mu);
-    auto it = efla::g_ws.find(dev);
-    if (it == efla::g_ws.end() || it->second.ptr == nullptr) return kSuccess;
-    EFLA_CHECK(hipDeviceSynchronize());
-    EFLA_CHECK(hipFree(it->second.ptr));
-    it->second = efla::Ws{};
+    for (efla::WsEntry* ep : efla::device_entries(dev)) {
+        efla::WsEntry& e = *ep;
+        std::lock_guard<std::mutex> ge(e.mu);  // waits for a caller still launching
+        if (e.ptr) {
+            // after the lock: work a caller queued while this call waited is
+            // done too (the stream itself may since have been destroyed)
+            EFLA_CHECK(hipDeviceSynchronize());
+            EFLA_CHECK(hipFree(e.ptr));
+        }
+        e.ptr = nullptr;
+        e.bytes = 0;
+    }
     return kSuccess;
 }

@@ -57,10 +57,15 @@ int efla_rt_event_record(hipEvent_t event, hipStream_t stream);
 int efla_rt_event_synchronize(hipEvent_t event);
 int efla_rt_event_elapsed_ms(float* ms, hipEvent_t start, hipEvent_t stop);
 
-/* --- library workspace --- */
-/* Bytes currently held by the cached workspace of the current device. */
+/* --- library workspace ---
+ * Entry points that need scratch and are given none use buffers the library
+ * caches per (device, stream): callers on different streams never share
+ * scratch, and calls on one stream from several host threads take turns
+ * while they queue their kernels.  A buffer grows (after its stream drains)
+ * only when a larger problem arrives. */
+/* Bytes currently held by the cached workspaces of the current device. */
 size_t efla_rt_workspace_bytes(void);
-/* Release the cached workspace of the current device (synchronises it). */
+/* Release the cached workspaces of the current device (synchronises it). */
 int efla_rt_workspace_release(void);
 
 /* GEMM backend of gemm_forward_hip / gemm_backward_hip for this process:

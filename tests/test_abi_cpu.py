@@ -313,3 +313,16 @@ def test_affine_state_scan_validation(L):
     assert L.efla_affine_state_scan_hip(arr, holes, 2, 4, 64, 64, NULL) == 1
     assert L.efla_affine_state_scan_hip(holes, arr, 2, 4, 64, 64, NULL) == 1
     assert L.efla_affine_state_scan_hip(arr, arr, 1, 4, 64, 64, NULL) == 0   # nothing to combine
+
+
+def test_runtime_validation(L):
+    """Argument checks of the device layer that run before any HIP call."""
+    p = ctypes.c_void_p(16)
+    f = ctypes.c_float(1.0)
+    assert L.efla_rt_fill(NULL, f, 0, 0, NULL) == 0  # nothing to fill
+    assert L.efla_rt_fill(NULL, f, 5, 14, NULL) == 1  # NULL with elements
+    for dt in (1, 3, 99, -1):  # only fp32 (0), fp16 (2), bf16 (14)
+        assert L.efla_rt_fill(p, f, 5, dt, NULL) == 1
+    assert L.efla_rt_set_gemm_backend(2) == 1
+    assert L.efla_rt_set_gemm_backend(-1) == 1
+    assert L.efla_rt_set_gemm_backend(0) == 0
