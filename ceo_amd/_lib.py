@@ -80,6 +80,8 @@ _SIGS = {
                                  i32, vp, sz, ctypes.c_uint, vp]),
     "efla_chunk_bwd_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz,
                                  sz, sz, sz, sz, sz, i32, vp, sz, ctypes.c_uint, vp]),
+    "efla_chunk_fwd_noalloc_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz,
+                                         sz, sz, i32, vp]),
     "efla_chunk_fwd_strided_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, sz, sz,
                                          sz, sz, i32, vp, sz, ctypes.c_uint, vp, vp]),
     "efla_chunk_bwd_strided_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp,

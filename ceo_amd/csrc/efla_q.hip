@@ -20,6 +20,8 @@
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "../../include/efla_hip.h"
 #include "common.hpp"
 #include "efla_coeff.hpp"
@@ -1277,6 +1279,66 @@ extern "C" int efla_chunk_fwd_hip(const void* q, const void* k, const void* v, c
     return chunk_fwd(q, k, v, beta, initial_state, output, final_state, cu_seqlens, batch_size,
                      seq_len, num_seqs, num_heads, head_dim_k, head_dim_v, chunk_size, dtype,
                      workspace, workspace_bytes, flags, nullptr, stream);
+}
+
+// ---------------------------------------------------------------------------
+// Forward without allocation: the per-chunk factors go to a fixed device array
+// ---------------------------------------------------------------------------
+// Each GPU the library runs on holds its own copy of `scratch` from the first
+// call there until the process ends.  Host code never passes the array's name
+// to a kernel (on the host it is only a stand-in for the symbol): the address
+// of the current device's copy comes from hipGetSymbolAddress, taken once per
+// device on the first call with that device current.
+static __device__ __align__(256) unsigned char scratch[EFLA_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDev = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDev];  // per device: its copy of `scratch`
+}  // namespace
+
+static int scratch_address(void** out) {
+    int dev = 0;
+    EFLA_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxScratchDev) return kInvalidValue;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* ptr = nullptr;
+        EFLA_CHECK(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        if (ptr == nullptr) return kInvalidValue;
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return kSuccess;
+}
+
+extern "C" int efla_chunk_fwd_noalloc_hip(const void* q, const void* k, const void* v,
+                                          const void* beta, const float* initial_state,
+                                          void* output, float* final_state,
+                                          const int32_t* cu_seqlens, size_t batch_size,
+                                          size_t seq_len, size_t num_seqs, size_t num_heads,
+                                          size_t head_dim_k, size_t head_dim_v,
+                                          size_t chunk_size, int dtype, hipStream_t stream) {
+    Problem p;
+    bool empty;
+    int rc = make_problem(q, k, v, beta, cu_seqlens, batch_size, seq_len, num_seqs, num_heads,
+                          head_dim_k, head_dim_v, chunk_size, dtype, &p, &empty);
+    if (rc != kSuccess) return rc;
+    if (!empty) {
+        // the forward's factors (T, b and the coefficients, or W, U, h, Vn on
+        // the fp32 path) must fit in the fixed array; nothing else is used
+        const size_t need = dtype == kDtypeBF16 ? carve_fwd<bf16>(p, nullptr, nullptr, false)
+                                                : carve_fwd<float>(p, nullptr, nullptr, false);
+        if (need > EFLA_NOALLOC_SCRATCH_BYTES) return kOutOfMemory;
+    }
+    void* scr = nullptr;
+    rc = scratch_address(&scr);
+    if (rc != kSuccess) return rc;
+    // every kernel writes what it reads back of the scratch before reading it,
+    // so nothing has to be cleared between calls
+    return chunk_fwd(q, k, v, beta, initial_state, output, final_state, cu_seqlens, batch_size,
+                     seq_len, num_seqs, num_heads, head_dim_k, head_dim_v, chunk_size, dtype,
+                     scr, EFLA_NOALLOC_SCRATCH_BYTES, 0u, nullptr, stream);
 }
 
 extern "C" int efla_chunk_fwd_strided_hip(

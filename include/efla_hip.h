@@ -178,6 +178,29 @@ int efla_chunk_bwd_strided_hip(const void* q, const void* k, const void* v, cons
                                void* workspace, size_t workspace_bytes, unsigned flags,
                                const int64_t* token_strides, hipStream_t stream);
 
+/*
+ * No reference counterpart.  For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc): efla_chunk_fwd_hip with no workspace argument and no flags,
+ * whose per-chunk factors go to a fixed device array of
+ * EFLA_NOALLOC_SCRATCH_BYTES that the library holds on each GPU it runs on
+ * until the process ends.  The call allocates nothing.  A problem whose
+ * forward workspace (efla_chunk_fwd_workspace_size) exceeds that size returns
+ * 2 (out of memory) before any work is queued; every other argument and
+ * return code is as in efla_chunk_fwd_hip, and the results are identical to
+ * its.  All calls on one GPU share the array: calls that overlap on one GPU
+ * (on different streams, or from different host threads) race and must be
+ * serialised by the caller.
+ */
+#define EFLA_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+int efla_chunk_fwd_noalloc_hip(const void* q, const void* k, const void* v, const void* beta,
+                               const float* initial_state, void* output, float* final_state,
+                               const int32_t* cu_seqlens, size_t batch_size, size_t seq_len,
+                               size_t num_seqs, size_t num_heads, size_t head_dim_k,
+                               size_t head_dim_v, size_t chunk_size, int dtype,
+                               hipStream_t stream);
+
 /* No reference counterpart; the affine combine efla_chunked_scan_hip does not
  * do (efla.cu:711-748 sums states; src/model/efla.zig:473-484 is empty).
  * In place over consecutive segments of the same sequences:

@@ -326,3 +326,17 @@ def test_runtime_validation(L):
     assert L.efla_rt_set_gemm_backend(2) == 1
     assert L.efla_rt_set_gemm_backend(-1) == 1
     assert L.efla_rt_set_gemm_backend(0) == 0
+
+
+def test_chunk_fwd_noalloc_validation(L):
+    """Argument checks and the scratch-size refusal come before any HIP call."""
+    p = ctypes.c_void_p(16)
+
+    def call(B=2, T=128, H=2, K=64, V=64, dt=14, q=p):
+        return L.efla_chunk_fwd_noalloc_hip(q, p, p, p, NULL, p, NULL, NULL, B, T, 0, H, K, V,
+                                            64, dt, NULL)
+    assert call(H=0) == 1
+    assert call(K=96) == 1  # no kernel for this head size
+    assert call(q=NULL) == 1
+    # forward workspace beyond EFLA_NOALLOC_SCRATCH_BYTES (64 MiB) -> 2
+    assert call(B=8, T=8192, H=32, K=128, V=128) == 2
