@@ -8,8 +8,10 @@
  * (0 success, 1 invalid value, 2 out of memory, 9 invalid configuration).
  * Pointers are caller-owned device pointers to contiguous row-major buffers;
  * calls are asynchronous on `stream`.  No entry point allocates per call: the
- * Mode Q entries take a caller workspace (or use one cached per device,
- * allocated once and grown only when a larger problem arrives).
+ * Mode Q entries take a caller workspace, or use scratch the library caches
+ * per (device, stream), allocated once and grown only when a larger problem
+ * arrives; callers on different streams never share it, and calls on one
+ * stream from several host threads take turns while they queue their work.
  *
  * Layouts:
  *   tokens      (B, T, H, D) row-major, i.e. token-major with heads interleaved
@@ -90,8 +92,8 @@ int efla_chunked_scan_hip(void** chunk_states, size_t num_chunks, size_t num_hea
  * final_state (num_seqs, H, d_k, d_v) fp32, either may be NULL.
  * Supported: chunk_size 64 (0 selects 64); (d_k, d_v) in
  * {64,128} x {64,128,256} for bf16, d_k = d_v = 64 for fp32.
- * Workspace: pass NULL to use the library's cached per-device buffer, or a
- * buffer of at least efla_chunk_*_workspace_size() bytes.
+ * Workspace: pass NULL to use the library's cached buffer for `stream`, or
+ * a buffer of at least efla_chunk_*_workspace_size() bytes.
  * ======================================================================== */
 size_t efla_chunk_fwd_workspace_size(size_t batch_size, size_t seq_len, size_t num_seqs,
                                      size_t num_heads, size_t head_dim_k, size_t head_dim_v,
