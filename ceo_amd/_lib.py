@@ -101,6 +101,8 @@ _SIGS = {
     # GEMM
     "gemm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, sz, i32, i32, i32, vp]),
     "gemm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),
+    "gemm_gelu_forward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, sz, vp]),
+    "gemm_gelu_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),
     # GELU, AdamW
     "gemm_ex_hip": (i32, [i32, i32, sz, sz, sz, f32, vp, sz, vp, sz, vp, f32, vp, sz, vp, sz,
                           i32, vp]),

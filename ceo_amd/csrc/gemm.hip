@@ -29,13 +29,16 @@
 #include <hip/hip_runtime.h>
 #include <hipblaslt/hipblaslt.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
+#include <type_traits>
 
 #include "../../include/efla_hip.h"
 #include "../../include/efla_runtime.h"
 #include "common.hpp"
+#include "gemm_fast.hpp"
 #include "internal.hpp"
 
 namespace efla {
@@ -119,16 +122,17 @@ struct TileLoader {
     }
 };
 
-// C[m, n] = sum_k opA(m, k) opB(k, n) (+ bias[n]); ldc is C's row stride.
+// C[m, n] = alpha sum_k opA(m, k) opB(k, n) (+ bias[n]) (+ beta R[m, n]);
+// ldc is C's row stride, ldr R's (R is read only when beta != 0 and may be C).
 //   opA(m, k) = AKM ? A[m*lda + k] : A[k*lda + m]
 //   opB(k, n) = BKM ? B[n*ldb + k] : B[k*ldb + n]
 template <typename TA, typename TB, typename TC, typename MT, bool AKM, bool BKM>
 __global__ void __launch_bounds__(NTH) gemm_kernel(const TA* __restrict__ A,
                                                    const TB* __restrict__ B,
-                                                   const TC* __restrict__ bias,
-                                                   TC* __restrict__ C, long M, long N, long K,
-                                                   long lda, long ldb, long ldc, int vec_a,
-                                                   int vec_b) {
+                                                   const TC* __restrict__ bias, TC* C, long M,
+                                                   long N, long K, long lda, long ldb, long ldc,
+                                                   int vec_a, int vec_b, float alpha,
+                                                   float beta, const TC* R, long ldr) {
     constexpr int LD = BK + lpad<MT>();
     __shared__ __attribute__((aligned(16))) MT As[BM * LD];
     __shared__ __attribute__((aligned(16))) MT Bs[BN * LD];
@@ -192,7 +196,11 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const TA* __restrict__ A,
             const float bb = bias ? to_f(bias[c]) : 0.f;
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                if (r + e < M) C[(r + e) * ldc + c] = from_f<TC>(acc[i][j][e] + bb);
+                if (r + e < M) {
+                    float v = alpha * acc[i][j][e] + bb;
+                    if (beta != 0.f) v += beta * to_f(R[(r + e) * ldr + c]);
+                    C[(r + e) * ldc + c] = from_f<TC>(v);
+                }
         }
 }
 
@@ -266,7 +274,8 @@ static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 template <typename TA, typename TB, typename TC, typename MT, bool AKM, bool BKM>
 static int launch(const void* a, const void* b, const void* bias, void* c, long M, long N,
-                  long K, long lda, long ldb, long ldc, const char* name, hipStream_t st) {
+                  long K, long lda, long ldb, long ldc, const char* name, hipStream_t st,
+                  float alpha = 1.f, float beta = 0.f, const void* r = nullptr, long ldr = 0) {
     const long tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
     if (tiles > 0x7FFFFFFFL) return kInvalidConfiguration;
     // 16-byte runs need an aligned base and a row stride that keeps them aligned
@@ -274,7 +283,7 @@ static int launch(const void* a, const void* b, const void* bias, void* c, long 
     const int vb = aligned16(b) && (ldb * (long)sizeof(TB)) % 16 == 0;
     EFLA_LAUNCH(name, (gemm_kernel<TA, TB, TC, MT, AKM, BKM>), dim3((unsigned)tiles), dim3(NTH),
                 st, (const TA*)a, (const TB*)b, (const TC*)bias, (TC*)c, M, N, K, lda, ldb, ldc,
-                va, vb);
+                va, vb, alpha, beta, (const TC*)r, ldr);
     return (int)hipPeekAtLastError();
 }
 
@@ -330,6 +339,117 @@ static int launch_bias_fill(void* c, const void* bias, long M, long N, hipStream
 }
 
 // ---------------------------------------------------------------------------
+// large-tile kernel (gemm_fast.hpp)
+// ---------------------------------------------------------------------------
+// An operand of the large-tile kernel: element (line, k) at p[line * ld + k]
+// (k-contiguous) or p[k * ld + line].
+struct FastOp {
+    const void* p;
+    long ld;
+    bool kc;
+};
+
+static bool aligned_to(const void* p, uintptr_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Whether the large-tile kernel takes the problem: whole 16-byte rows and
+// chunks along k (K % 8), along every line-contiguous operand's lines and
+// along the output's columns (N % 8); 16-byte aligned operands and outputs
+// (the epilogue moves 16-byte row pieces); 32-bit in-tile offsets
+// (256 * ld * 2 < 2^31).
+static bool fast_ok(long M, long N, long K, const FastOp& a, const FastOp& b, const void* d,
+                    long ldd, const void* bias, const void* c, long ldc, const void* aux,
+                    long ldaux) {
+    const long lim = (long)1 << 22;
+    if (M < 1 || N < 1 || K < 1 || M > INT32_MAX / 2 || N > INT32_MAX / 2) return false;
+    if (K % 8 || N % 8 || (!a.kc && M % 8)) return false;
+    for (long ld : {a.ld, b.ld, ldd})
+        if (ld % 8 || ld >= lim) return false;
+    if (!aligned_to(a.p, 16) || !aligned_to(b.p, 16) || !aligned_to(d, 16)) return false;
+    if (bias && !aligned_to(bias, 16)) return false;
+    if (c && (ldc % 8 || ldc >= lim || !aligned_to(c, 16))) return false;
+    if (aux && (ldaux % 8 || ldaux >= lim || !aligned_to(aux, 16))) return false;
+    return true;
+}
+
+template <typename T, int EPI, int NW>
+static void fast_kernel_launch_nw(const FastOp& a, const FastOp& b, const gf::Opnd& A,
+                                  const gf::Opnd& B, long M, long N, long K,
+                                  const gf::EpiArgs<T>& ea, int ksplit, long kper, long tiles,
+                                  const char* name, hipStream_t st) {
+    // persistent: at most one workgroup per CU (the LDS allows no more)
+    const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const long items = tiles * ksplit;
+    const dim3 grid((unsigned)(items < cus ? items : cus)), block(64 * NW);
+    if (a.kc && b.kc)
+        EFLA_LAUNCH(name, (gf::gemm_fast_kernel<T, true, true, EPI, NW>), grid, block, st, A, B,
+                    M, N, K, ea, ksplit, kper);
+    else if (a.kc)
+        EFLA_LAUNCH(name, (gf::gemm_fast_kernel<T, true, false, EPI, NW>), grid, block, st, A, B,
+                    M, N, K, ea, ksplit, kper);
+    else if (b.kc)
+        EFLA_LAUNCH(name, (gf::gemm_fast_kernel<T, false, true, EPI, NW>), grid, block, st, A, B,
+                    M, N, K, ea, ksplit, kper);
+    else
+        EFLA_LAUNCH(name, (gf::gemm_fast_kernel<T, false, false, EPI, NW>), grid, block, st, A,
+                    B, M, N, K, ea, ksplit, kper);
+}
+
+// 8 waves (two per SIMD) measured faster than 4 at every config-4 shape
+template <typename T, int EPI>
+static void fast_kernel_launch(const FastOp& a, const FastOp& b, const gf::Opnd& A,
+                               const gf::Opnd& B, long M, long N, long K,
+                               const gf::EpiArgs<T>& ea, int ksplit, long kper, long tiles,
+                               const char* name, hipStream_t st) {
+    fast_kernel_launch_nw<T, EPI, 8>(a, b, A, B, M, N, K, ea, ksplit, kper, tiles, name, st);
+}
+
+// Large-tile product.  Problems with fewer output tiles than the GPU has CUs
+// and a long contraction are split along k: fp32
+// partial tiles go to the stream's cached workspace and a second kernel adds
+// them in split order and runs the epilogue (plain epilogues only).
+template <typename T, int EPI>
+static int fast_launch(const FastOp& a, const FastOp& b, long M, long N, long K,
+                       const gf::EpiArgs<T>& ea, const char* name, hipStream_t st) {
+    const gf::Opnd A{(const char*)a.p, a.ld, (int)M}, B{(const char*)b.p, b.ld, (int)N};
+    const long tiles = ((M + gf::BM - 1) / gf::BM) * ((N + gf::BN - 1) / gf::BN);
+    if (tiles > 0x7FFFFFFFL / 64) return kInvalidConfiguration;
+    int ksplit = 1;
+    const long cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    if ((EPI == gf::EPI_PLAIN || EPI == gf::EPI_RESID) && tiles < cus) {
+        const long want = cus / tiles;       // splits that fill every CU once
+        const long most = K / (4 * gf::BK);  // at least 4 k-iterations each
+        ksplit = (int)std::max(1L, std::min({want, most, 32L}));
+    }
+    if (ksplit == 1) {
+        fast_kernel_launch<T, EPI>(a, b, A, B, M, N, K, ea, 1, K, tiles, name, st);
+        return (int)hipPeekAtLastError();
+    }
+    const long kper = ((K + ksplit - 1) / ksplit + gf::BK - 1) / gf::BK * gf::BK;
+    ksplit = (int)((K + kper - 1) / kper);
+    void* ws = nullptr;
+    WsLease lease;
+    EFLA_CHECK((hipError_t)workspace_acquire((size_t)ksplit * M * N * sizeof(float), st, &ws,
+                                             lease));
+    gf::EpiArgs<T> ep = ea;
+    ep.part = (float*)ws;
+    fast_kernel_launch<T, gf::EPI_PARTIAL>(a, b, A, B, M, N, K, ep, ksplit, kper, tiles, name,
+                                           st);
+    long g = (M * (N / 4) + 255) / 256;
+    if (g > 4096) g = 4096;
+    EFLA_LAUNCH("gemm_splitk_reduce", gf::gemm_splitk_reduce<T>, dim3((unsigned)g), dim3(256), st,
+                ep, M, N, ksplit);
+    return (int)hipPeekAtLastError();
+}
+
+template <typename T>
+static gf::EpiArgs<T> epi(void* d, long ldd, const void* bias = nullptr, float alpha = 1.f,
+                          float beta = 0.f, const void* c = nullptr, long ldc = 0,
+                          void* aux = nullptr, long ldaux = 0) {
+    return gf::EpiArgs<T>{(T*)d, ldd, (const T*)bias, (const T*)c, ldc, alpha, beta, (T*)aux,
+                          ldaux, nullptr};
+}
+
+// ---------------------------------------------------------------------------
 // hipBLASLt path
 // ---------------------------------------------------------------------------
 constexpr size_t kLtWorkspace = (size_t)128 << 20;
@@ -354,7 +474,10 @@ struct LtPlan {
 static std::mutex g_lt_mu;
 static LtDevice g_lt_dev[kMaxDev];
 static std::map<std::pair<int, LtKey>, LtPlan> g_lt_plans;
-static int g_backend = 0;  // 0: hipBLASLt where possible, 1: native kernel only
+// 0: the hand-written kernels (large-tile where it takes the problem, else the
+// generic one); 1: the generic hand-written kernel only; 2: hipBLASLt where it
+// takes the problem, else the hand-written kernels
+static int g_backend = 0;
 
 static hipDataType lt_type(int dt) {
     return dt == kDtypeF32 ? HIP_R_32F : dt == kDtypeF16 ? HIP_R_16F : HIP_R_16BF;
@@ -438,7 +561,7 @@ static int lt_matmul(hipblasOperation_t ta, hipblasOperation_t tb, long M, long 
                      const void* bias, int dt, hipStream_t stream, float alpha = 1.f,
                      float beta = 0.f, const void* C = nullptr, long ldc = 0) {
     std::lock_guard<std::mutex> lk(g_lt_mu);
-    if (g_backend != 0) return -1;
+    if (g_backend != 2) return -1;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return -1;
     LtDevice* d = lt_device(dev);
@@ -487,8 +610,13 @@ static int lt_forward(const void* a, const void* b, const void* bias, void* c, l
 using namespace efla;
 using namespace efla::gm;
 
+static int backend() {
+    std::lock_guard<std::mutex> lk(g_lt_mu);
+    return g_backend;
+}
+
 extern "C" int efla_rt_set_gemm_backend(int backend) {
-    if (backend != 0 && backend != 1) return kInvalidValue;
+    if (backend < 0 || backend > 2) return kInvalidValue;
     std::lock_guard<std::mutex> lk(g_lt_mu);
     g_backend = backend;
     return kSuccess;
@@ -514,6 +642,18 @@ extern "C" int gemm_forward_hip(const void* a, const void* b, const void* bias, 
     if (dtype_a == dtype_b && dtype_b == dtype_c) {
         const int rc = lt_forward(a, b, bias, c, (long)m, (long)k, (long)n, dtype_a, stream);
         if (rc >= 0) return rc;
+        // C[m, n] = A[m, k] B[k, n]: A k-contiguous, B line (n) contiguous
+        const FastOp fa{a, (long)k, true}, fb{b, (long)n, false};
+        if (dtype_a != kDtypeF32 && backend() != 1 &&
+            fast_ok((long)m, (long)n, (long)k, fa, fb, c, (long)n, bias, nullptr, 0, nullptr, 0)) {
+            if (dtype_a == kDtypeBF16)
+                return fast_launch<bf16, gf::EPI_PLAIN>(fa, fb, (long)m, (long)n, (long)k,
+                                                        epi<bf16>(c, (long)n, bias), "gemm_fwd",
+                                                        stream);
+            return fast_launch<f16, gf::EPI_PLAIN>(fa, fb, (long)m, (long)n, (long)k,
+                                                   epi<f16>(c, (long)n, bias), "gemm_fwd",
+                                                   stream);
+        }
     }
     switch (dtype_a) {
         case kDtypeF32:
@@ -563,6 +703,12 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
         // with B' = B as (n x k, ld n) and dC^T as (n x m, ld n)
         int rc = lt_matmul(HIPBLAS_OP_T, HIPBLAS_OP_N, K, M, N, b, N, grad_c, N, grad_a, K,
                            nullptr, kDtypeBF16, stream);
+        // dA = dC B^T: contraction over n, both operands n-contiguous
+        const FastOp fa{grad_c, N, true}, fb{b, N, true};
+        if (rc < 0 && backend() != 1 &&
+            fast_ok(M, K, N, fa, fb, grad_a, K, nullptr, nullptr, 0, nullptr, 0))
+            rc = fast_launch<bf16, gf::EPI_PLAIN>(fa, fb, M, K, N, epi<bf16>(grad_a, K),
+                                                  "gemm_bwd_da", stream);
         if (rc < 0)
             rc = launch<bf16, bf16, bf16, bf16, true, true>(grad_c, b, nullptr, grad_a, M, K, N,
                                                             N, N, K, "gemm_bwd_da", stream);
@@ -573,6 +719,12 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
         // with dC^T as (n x m, ld n) and A' = A as (k x m, ld k)
         int rc = lt_matmul(HIPBLAS_OP_N, HIPBLAS_OP_T, N, K, M, grad_c, N, a, K, grad_b, N,
                            nullptr, kDtypeBF16, stream);
+        // dB = A^T dC: contraction over m, A k- (line-) contiguous, dC n-contiguous
+        const FastOp fa{a, K, false}, fb{grad_c, N, false};
+        if (rc < 0 && backend() != 1 &&
+            fast_ok(K, N, M, fa, fb, grad_b, N, nullptr, nullptr, 0, nullptr, 0))
+            rc = fast_launch<bf16, gf::EPI_PLAIN>(fa, fb, K, N, M, epi<bf16>(grad_b, N),
+                                                  "gemm_bwd_db", stream);
         if (rc < 0)
             rc = launch<bf16, bf16, bf16, bf16, false, false>(a, grad_c, nullptr, grad_b, K, N, M,
                                                               K, N, N, "gemm_bwd_db", stream);
@@ -598,6 +750,23 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
     return (int)hipPeekAtLastError();
 }
 
+// gemm_ex on the generic kernel: any shape, strides and transposes.
+template <typename T>
+static int ex_generic(int ta, int tb, size_t m, size_t n, size_t k, float alpha, const void* a,
+                      size_t lda, const void* b, size_t ldb, const void* bias, float beta,
+                      const void* c, size_t ldc, void* d, size_t ldd, hipStream_t st) {
+    typedef typename std::conditional<__is_same(T, float), float, T>::type MT;
+    const long M = (long)m, N = (long)n, K = (long)k;
+#define EX_CASE(AK, BK)                                                                          \
+    return launch<T, T, T, MT, AK, BK>(a, b, bias, d, M, N, K, (long)lda, (long)ldb, (long)ldd, \
+                                       "gemm_ex", st, alpha, beta, c, (long)ldc)
+    if (!ta && !tb) EX_CASE(true, false);
+    if (!ta && tb) EX_CASE(true, true);
+    if (ta && !tb) EX_CASE(false, false);
+    EX_CASE(false, true);
+#undef EX_CASE
+}
+
 extern "C" int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t k, float alpha,
                            const void* a, size_t lda, const void* b, size_t ldb,
                            const void* bias, float beta, const void* c, size_t ldc, void* d,
@@ -613,12 +782,111 @@ extern "C" int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t 
     if (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n) || ldd < n ||
         (beta != 0.f && ldc < n))
         return kInvalidValue;
-    if (k == 0) return kNotSupported;
     // row-major D = op(A) op(B) as column-major D^T = op(B)^T op(A)^T: a row-major
     // matrix is its own transpose read column-major with the same leading dimension
-    const int rc = lt_matmul(trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N,
-                             trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N, (long)n, (long)m, (long)k, b,
-                             (long)ldb, a, (long)lda, d, (long)ldd, bias, dtype, stream, alpha,
-                             beta, c, (long)ldc);
-    return rc < 0 ? kNotSupported : rc;
+    int rc = k == 0 ? -1 : lt_matmul(trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N,
+                       trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N, (long)n, (long)m, (long)k, b,
+                       (long)ldb, a, (long)lda, d, (long)ldd, bias, dtype, stream, alpha, beta, c,
+                       (long)ldc);
+    if (rc >= 0) return rc;
+    // op(A) is A (k-contiguous) or A^T of a stored k x m (m-contiguous); op(B)
+    // is B of a stored k x n (n-contiguous) or B^T of a stored n x k
+    const FastOp fa{a, (long)lda, trans_a == 0}, fb{b, (long)ldb, trans_b != 0};
+    const void* cc = beta != 0.f ? c : nullptr;
+    if (dtype != kDtypeF32 && backend() != 1 &&
+        fast_ok((long)m, (long)n, (long)k, fa, fb, d, (long)ldd, bias, cc, (long)ldc, nullptr, 0)) {
+        if (cc) {
+            if (dtype == kDtypeBF16)
+                return fast_launch<bf16, gf::EPI_RESID>(
+                    fa, fb, (long)m, (long)n, (long)k,
+                    epi<bf16>(d, (long)ldd, bias, alpha, beta, cc, (long)ldc), "gemm_ex", stream);
+            return fast_launch<f16, gf::EPI_RESID>(
+                fa, fb, (long)m, (long)n, (long)k,
+                epi<f16>(d, (long)ldd, bias, alpha, beta, cc, (long)ldc), "gemm_ex", stream);
+        }
+        if (dtype == kDtypeBF16)
+            return fast_launch<bf16, gf::EPI_PLAIN>(fa, fb, (long)m, (long)n, (long)k,
+                                                    epi<bf16>(d, (long)ldd, bias, alpha),
+                                                    "gemm_ex", stream);
+        return fast_launch<f16, gf::EPI_PLAIN>(fa, fb, (long)m, (long)n, (long)k,
+                                               epi<f16>(d, (long)ldd, bias, alpha), "gemm_ex",
+                                               stream);
+    }
+    switch (dtype) {
+        case kDtypeBF16: return ex_generic<bf16>(trans_a, trans_b, m, n, k, alpha, a, lda, b, ldb,
+                                                 bias, beta, cc, ldc, d, ldd, stream);
+        case kDtypeF16: return ex_generic<f16>(trans_a, trans_b, m, n, k, alpha, a, lda, b, ldb,
+                                               bias, beta, cc, ldc, d, ldd, stream);
+        default: return ex_generic<float>(trans_a, trans_b, m, n, k, alpha, a, lda, b, ldb, bias,
+                                          beta, cc, ldc, d, ldd, stream);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// GEMMs with the MLP's GELU fused into the epilogue
+// ---------------------------------------------------------------------------
+extern "C" int gelu_forward_hip(const void* input, void* output, size_t numel, bool approximate,
+                                hipStream_t stream);
+extern "C" int gelu_backward_hip(const void* grad_output, const void* input, void* grad_input,
+                                 size_t numel, bool approximate, hipStream_t stream);
+
+extern "C" int gemm_gelu_forward_hip(const void* a, const void* b, const void* bias, void* pre,
+                                     void* out, size_t m, size_t k, size_t n,
+                                     hipStream_t stream) {
+    if (!a || !b || !pre || !out) return kInvalidValue;
+    size_t mn;
+    if (!mul_ok(m, n, &mn)) return kInvalidValue;
+    if (m == 0 || n == 0) return kSuccess;
+    if (m > ((size_t)1 << 40) || n > ((size_t)1 << 40) || k > ((size_t)1 << 40))
+        return kInvalidValue;
+    const FastOp fa{a, (long)k, true}, fb{b, (long)n, false};
+    if (k > 0 && backend() == 0 &&
+        fast_ok((long)m, (long)n, (long)k, fa, fb, out, (long)n, bias, nullptr, 0, pre,
+                (long)n))
+        return fast_launch<bf16, gf::EPI_GELU_AUX>(
+            fa, fb, (long)m, (long)n, (long)k,
+            epi<bf16>(out, (long)n, bias, 1.f, 0.f, nullptr, 0, pre, (long)n), "gemm_gelu_fwd",
+            stream);
+    // the product, then GELU over it (the same functions, so the same bits)
+    const int rc = gemm_forward_hip(a, b, bias, pre, m, k, n, kDtypeBF16, kDtypeBF16, kDtypeBF16,
+                                    stream);
+    if (rc != kSuccess) return rc;
+    return gelu_forward_hip(pre, out, mn, true, stream);
+}
+
+extern "C" int gemm_gelu_backward_hip(const void* grad_c, const void* a, const void* b,
+                                      const void* pre, void* grad_pre, void* grad_b,
+                                      void* grad_bias, size_t m, size_t k, size_t n,
+                                      hipStream_t stream) {
+    size_t mk;
+    if (!mul_ok(m, k, &mk)) return kInvalidValue;
+    if (grad_pre) {
+        if (m == 0 || k == 0) {
+            // nothing to contract or no rows: gemm_backward_hip's zero fill
+            int rc = gemm_backward_hip(grad_c, a, b, grad_pre, nullptr, nullptr, m, k, n, stream);
+            if (rc != kSuccess) return rc;
+        } else {
+            if (!grad_c || !b || !pre) return kInvalidValue;
+            // grad_pre = (grad_c b^T) * GELU'(pre): contraction over n, both n-contiguous
+            const FastOp fa{grad_c, (long)n, true}, fb{b, (long)n, true};
+            if (n > 0 && backend() == 0 &&
+                fast_ok((long)m, (long)k, (long)n, fa, fb, grad_pre, (long)k, nullptr, nullptr,
+                        0, pre, (long)k)) {
+                const int rc = fast_launch<bf16, gf::EPI_DGELU>(
+                    fa, fb, (long)m, (long)k, (long)n,
+                    epi<bf16>(grad_pre, (long)k, nullptr, 1.f, 0.f, nullptr, 0, (void*)pre,
+                              (long)k),
+                    "gemm_gelu_bwd_da", stream);
+                if (rc != kSuccess) return rc;
+            } else {
+                int rc = gemm_backward_hip(grad_c, a, b, grad_pre, nullptr, nullptr, m, k, n,
+                                           stream);
+                if (rc != kSuccess) return rc;
+                rc = gelu_backward_hip(grad_pre, pre, grad_pre, mk, true, stream);
+                if (rc != kSuccess) return rc;
+            }
+        }
+    }
+    if (!grad_b && !grad_bias) return kSuccess;
+    return gemm_backward_hip(grad_c, a, b, nullptr, grad_b, grad_bias, m, k, n, stream);
 }

@@ -12,11 +12,12 @@ per-token beta (Mode Q: q, k, v and beta projections, beta = sigmoid), and the
 PRISM mixer the reference inserts after EFLA (model.zig:172) is not part of
 the config and is left out.
 
-Kernels: embedding (lm.hip), LayerNorm (layernorm.hip), GEMMs (gemm.hip),
+Kernels: embedding (lm.hip), LayerNorm (layernorm.hip), GEMMs (gemm.hip, the
+MLP's GELU and its derivative fused into the products' epilogues),
 chunked EFLA with the forward's T, b and chunk states handed to the backward
 (efla_q.hip, reading q, k, v and writing their gradients in place in the
-fused q/k/v/beta projection rows), GELU, AdamW and the beta gate
-(elementwise.hip), cross-entropy (lm.hip).  torch provides memory and views.
+fused q/k/v/beta projection rows), AdamW and the beta gate (elementwise.hip),
+cross-entropy (lm.hip).  torch provides memory and views.
 
 Parameters live in flat buffers: fp32 master weights, fp32 AdamW moments, a
 bf16 copy that the GEMMs read (each weight a contiguous view into it) and a
@@ -156,8 +157,8 @@ class EflaLM:
             x1 = nn.gemm_ex(o2, self.w(L + "w_o"), torch.empty_like(x), c=x, beta=1.0)
             a2, m2, r2 = nn.layernorm_forward(x1, self.w(L + "ln2.w"), self.w(L + "ln2.b"),
                                               cfg.ln_eps, save_stats=True)
-            u = nn.gemm_forward(a2, self.w(L + "w_up"), self.w(L + "b_up"))
-            gl = nn.gelu_forward(u)
+            # u = a2 w_up + b_up and gl = GELU(u) from one product (GELU in its epilogue)
+            u, gl = nn.gemm_gelu_forward(a2, self.w(L + "w_up"), self.w(L + "b_up"))
             x2 = nn.gemm_ex(gl, self.w(L + "w_down"), torch.empty_like(x),
                             bias=self.w(L + "b_down"), c=x1, beta=1.0)
             saved["layers"].append(dict(x=x, a=a, m1=m1, r1=r1, q=q, k=k, v=v, beta=beta,
@@ -194,9 +195,10 @@ class EflaLM:
             L = f"l{i}."
             s = saved["layers"][i]
             # x2 = x1 + down(gelu(up(ln2(x1))))
-            dg, _, _ = nn.gemm_backward(dx, s["g"], self.w(L + "w_down"), need_bias=True,
-                                        out_b=self.gr(L + "w_down"), out_bias=self.gr(L + "b_down"))
-            du = nn.gelu_backward(dg, s["u"])
+            # du = (dx w_down^T) * GELU'(u) from one product (derivative in its epilogue)
+            du, _, _ = nn.gemm_gelu_backward(dx, s["g"], self.w(L + "w_down"), s["u"],
+                                             need_bias=True, out_b=self.gr(L + "w_down"),
+                                             out_bias=self.gr(L + "b_down"))
             da2, _, _ = nn.gemm_backward(du, s["a2"], self.w(L + "w_up"), need_bias=True,
                                          out_b=self.gr(L + "w_up"), out_bias=self.gr(L + "b_up"))
             # dx1 = LN2's input gradient + the residual's dx, in one pass

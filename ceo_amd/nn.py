@@ -179,6 +179,51 @@ def gemm_backward(dc: torch.Tensor, a: torch.Tensor, b: torch.Tensor, need_a=Tru
     return da, dbm, dbias
 
 
+def gemm_gelu_forward(a: torch.Tensor, b: torch.Tensor, bias=None):
+    """(pre, out) with pre = a @ b (+ bias) and out = GELU_tanh(pre), bf16, in
+    one product with the GELU in its epilogue."""
+    m, k = a.shape
+    k2, n = b.shape
+    if k2 != k:
+        raise ValueError("gemm_gelu_forward: inner dimensions differ")
+    _require(a, "a", torch.bfloat16)
+    _require(b, "b", torch.bfloat16, a.device)
+    if bias is not None:
+        _require(bias, "bias", torch.bfloat16, a.device)
+    pre = torch.empty(m, n, dtype=torch.bfloat16, device=a.device)
+    out = torch.empty_like(pre)
+    rc = lib().gemm_gelu_forward_hip(_p(a), _p(b), _p(bias), _p(pre), _p(out), m, k, n,
+                                     _stream(a))
+    check(rc, "gemm_gelu_forward_hip")
+    return pre, out
+
+
+def gemm_gelu_backward(dc, a, b, pre, need_pre=True, need_b=True, need_bias=False,
+                       out_b=None, out_bias=None):
+    """(dpre, db, dbias) for c = a @ b + bias with a = GELU_tanh(pre): dpre =
+    (dc @ b^T) * GELU'(pre) from one product with the derivative in its
+    epilogue; bf16."""
+    m, k = a.shape
+    n = b.shape[1]
+    for t, nme in ((dc, "dc"), (a, "a"), (b, "b"), (pre, "pre")):
+        _require(t, nme, torch.bfloat16, a.device)
+    if pre.shape != a.shape:
+        raise ValueError("gemm_gelu_backward: pre must have a's shape")
+    for t, nme, shape in ((out_b, "out_b", (k, n)), (out_bias, "out_bias", (n,))):
+        if t is not None:
+            _require(t, nme, torch.bfloat16, a.device)
+            if tuple(t.shape) != shape:
+                raise ValueError(f"gemm_gelu_backward: {nme} must be {shape}")
+    dpre = torch.empty_like(a) if need_pre else None
+    dbm = (out_b if out_b is not None else torch.empty_like(b)) if need_b else None
+    dbias = (out_bias if out_bias is not None else
+             torch.empty(n, dtype=torch.bfloat16, device=a.device)) if need_bias else None
+    rc = lib().gemm_gelu_backward_hip(_p(dc), _p(a), _p(b), _p(pre), _p(dpre), _p(dbm),
+                                      _p(dbias), m, k, n, _stream(a))
+    check(rc, "gemm_gelu_backward_hip")
+    return dpre, dbm, dbias
+
+
 def gelu_forward(x: torch.Tensor, approximate: bool = True) -> torch.Tensor:
     """GELU of a bf16 tensor (tanh form unless approximate=False)."""
     _require(x, "x", torch.bfloat16)

@@ -328,6 +328,12 @@ int prism_backward_hip(const void* grad_output, const void* u, const void* v, co
 
 /* ========================================================================
  * GEMM (row-major)
+ *
+ * Hand-written MFMA kernels: bf16 / fp16 problems whose k, output columns
+ * and strides are multiples of 8 elements (16-byte rows) run a 256 x 256 x 64
+ * tile kernel; everything else (fp32, mixed dtypes, other shapes) a generic
+ * 128 x 128 one.  efla_rt_set_gemm_backend selects hipBLASLt instead, for
+ * comparison.
  * ======================================================================== */
 
 /* Replaces gemm_forward_cuda (kernels.h:211-223, gemm.cu:303-398):
@@ -352,13 +358,30 @@ int gemm_backward_hip(const void* grad_c, const void* a, const void* b, void* gr
  * row-major with row strides lda, ldb, ldc, ldd; op(A) is A (stored m x k) or,
  * with trans_a, A^T (A stored k x m); op(B) likewise (k x n or, transposed,
  * n x k).  One dtype for every operand, fp32 accumulation.  C is read only
- * when beta != 0 and may be D.  hipBLASLt only: a problem it does not take,
- * or k == 0, -> 801 (not supported); m or n == 0 -> 0; bad strides or
- * pointers -> 1. */
+ * when beta != 0 and may be D; k == 0 gives D = bias + beta C.  m or n == 0
+ * -> 0; bad strides or pointers -> 1. */
 int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t k, float alpha,
                 const void* a, size_t lda, const void* b, size_t ldb, const void* bias,
                 float beta, const void* c, size_t ldc, void* d, size_t ldd, int dtype,
                 hipStream_t stream);
+
+/* No reference counterpart: the MLP's first product with the GELU fused into
+ * its epilogue (bf16, row-major, contiguous),
+ *   pre[m x n] = a[m x k] b[k x n] + bias[n]   (bias may be NULL)
+ *   out        = GELU_tanh(pre)                 (computed from bf16(pre))
+ * pre is written for the backward.  Same codes as gemm_forward_hip. */
+int gemm_gelu_forward_hip(const void* a, const void* b, const void* bias, void* pre, void* out,
+                          size_t m, size_t k, size_t n, hipStream_t stream);
+
+/* No reference counterpart: gemm_backward_hip for c = GELU_tanh(pre) b + bias
+ * with the GELU derivative fused into grad_a's epilogue,
+ *   grad_pre  = bf16(grad_c b^T) * GELU'(pre)   (m x k; NULL skips it)
+ *   grad_b    = a^T grad_c                      (k x n, a = GELU(pre); NULL skips it)
+ *   grad_bias = column sums of grad_c           (n; NULL skips it)
+ * bf16, row-major, contiguous.  Same codes as gemm_backward_hip. */
+int gemm_gelu_backward_hip(const void* grad_c, const void* a, const void* b, const void* pre,
+                           void* grad_pre, void* grad_b, void* grad_bias, size_t m, size_t k,
+                           size_t n, hipStream_t stream);
 
 /* ========================================================================
  * GELU and AdamW (the config-4 training step around EFLA)

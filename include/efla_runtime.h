@@ -68,9 +68,11 @@ size_t efla_rt_workspace_bytes(void);
 /* Release the cached workspaces of the current device (synchronises it). */
 int efla_rt_workspace_release(void);
 
-/* GEMM backend of gemm_forward_hip / gemm_backward_hip for this process:
- * 0 (default) hipBLASLt where it takes the problem, else the library's own
- * MFMA kernel; 1 the library's own kernel always.  Other values -> 1. */
+/* GEMM backend of the gemm_* entries for this process: 0 (default) the
+ * library's hand-written kernels (the large-tile kernel where it takes the
+ * problem, else the generic one); 1 the generic hand-written kernel only;
+ * 2 hipBLASLt where it takes the problem (for comparison), else the
+ * hand-written kernels.  Other values -> 1. */
 int efla_rt_set_gemm_backend(int backend);
 
 /* --- launch profiler ---

@@ -243,13 +243,12 @@ def test_shortconv_and_prism_validation(L):
 def test_gemm_ex_and_residual_validation(L):
     p = ctypes.c_void_p(16)
     bf = 14
-    # m or n == 0 -> 0; bad transpose flag, short strides, NULL -> 1; k == 0 -> 801
+    # m or n == 0 -> 0; bad transpose flag, short strides, NULL -> 1
     assert L.gemm_ex_hip(0, 0, 0, 8, 8, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 0
     assert L.gemm_ex_hip(2, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 1
     assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 4, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 1
     assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 4, bf, NULL) == 1
     assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 1.0, NULL, 8, p, 8, bf, NULL) == 1
-    assert L.gemm_ex_hip(0, 0, 8, 8, 0, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 801
     assert L.layernorm_backward_residual_hip(p, p, p, p, p, NULL, p, NULL, NULL, 2048, 1024,
                                              NULL) == 1
 
@@ -323,7 +322,7 @@ def test_runtime_validation(L):
     assert L.efla_rt_fill(NULL, f, 5, 14, NULL) == 1  # NULL with elements
     for dt in (1, 3, 99, -1):  # only fp32 (0), fp16 (2), bf16 (14)
         assert L.efla_rt_fill(p, f, 5, dt, NULL) == 1
-    assert L.efla_rt_set_gemm_backend(2) == 1
+    assert L.efla_rt_set_gemm_backend(3) == 1
     assert L.efla_rt_set_gemm_backend(-1) == 1
     assert L.efla_rt_set_gemm_backend(0) == 0
 

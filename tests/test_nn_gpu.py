@@ -199,10 +199,11 @@ def test_layernorm_backward_residual(oracle):
         assert e <= 1e-2 and rel_l2(dw, rdw) <= 1e-4
 
 
-@pytest.fixture(params=[0, 1], ids=["hipblaslt", "native"])
+@pytest.fixture(params=[0, 1, 2], ids=["mfma", "generic", "hipblaslt"])
 def gemm_backend(request):
-    """Runs a GEMM test on the hipBLASLt path and on the library's own MFMA
-    kernel (efla_rt_set_gemm_backend), restoring the default afterwards."""
+    """Runs a GEMM test on the library's kernels (the large-tile MFMA kernel
+    where it takes the shape), on its generic kernel only, and on hipBLASLt
+    (efla_rt_set_gemm_backend), restoring the default afterwards."""
     from ceo_amd._lib import lib
 
     assert lib().efla_rt_set_gemm_backend(request.param) == 0
@@ -210,7 +211,8 @@ def gemm_backend(request):
     assert lib().efla_rt_set_gemm_backend(0) == 0
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (1, 64, 8), (300, 1024, 260)])
+@pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (1, 64, 8), (300, 1024, 260),
+                                   (777, 3088, 520)])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 def test_gemm_forward(m, k, n, dt, gemm_backend):
     from ceo_amd.nn import gemm_forward
@@ -279,7 +281,8 @@ def test_gemm_k0_gives_bias():
     assert lib().gemm_forward_hip(None, P(buf), None, P(c), m, 0, n, 14, 14, 14, st) == 1
 
 
-@pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (513, 200, 129)])
+@pytest.mark.parametrize("m,k,n", [(256, 128, 384), (100, 70, 33), (513, 200, 129),
+                                   (4096, 1032, 264)])
 def test_gemm_backward(m, k, n, gemm_backend):
     from ceo_amd.nn import gemm_backward
 
@@ -318,3 +321,83 @@ def test_sigmoid_gate_forward_backward_vs_torch():
     want = (g.float() * bf * (1.0 - bf)).to(torch.bfloat16)
     assert torch.equal(dp[:, W - H:], want)
     assert torch.isnan(dp[:, :W - H]).all()  # nothing written outside the block
+
+
+# ---------------------------------------------------------------------------
+# the large-tile kernel (gemm_fast.hpp): transposes, residual, split-K, GELU
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("m,k,n", [(600, 1000, 328), (256, 64, 256), (40, 8, 8)])
+def test_gemm_ex_transposes_residual(m, k, n, ta, tb, gemm_backend):
+    """out = 0.5 op(a) op(b) + bias + out, for every transpose combination,
+    against torch fp32; shapes with k-tails (1000 = 15 x 64 + 40) and edge tiles."""
+    from ceo_amd import nn
+
+    announce(f"gemm_ex {m}x{k}x{n} ta={ta} tb={tb} backend={gemm_backend}")
+    g = torch.Generator(device="cuda").manual_seed(m + 3 * k + 7 * n + 2 * ta + tb)
+    a = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+    b = (0.1 * torch.randn(k, n, generator=g, device="cuda")).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g, device="cuda").to(torch.bfloat16)
+    out = torch.randn(m, n, generator=g, device="cuda").to(torch.bfloat16)
+    ref = 0.5 * (a.float() @ b.float()) + bias.float() + out.float()
+    A = a.t().contiguous() if ta else a
+    B = b.t().contiguous() if tb else b
+    nn.gemm_ex(A, B, out, bias=bias, c=out, alpha=0.5, beta=1.0, trans_a=bool(ta),
+               trans_b=bool(tb))
+    e = rel_l2(out, ref.cpu().numpy())
+    print(f"  rel-L2={e:.2e}", flush=True)
+    assert e <= 1e-2
+
+
+def test_gemm_split_k_deterministic():
+    """An output with few tiles and a long contraction (the weight gradient of
+    a config-4 projection) runs split along k with an ordered reduction: the
+    same inputs give the same bits, and the result matches fp64 (sampled)."""
+    from ceo_amd import nn
+
+    announce("gemm_backward dB 16384 x 1024 x 1024 (split-K), twice")
+    g = torch.Generator(device="cuda").manual_seed(11)
+    a = torch.randn(16384, 1024, generator=g, device="cuda").to(torch.bfloat16)
+    w = torch.randn(1024, 1024, generator=g, device="cuda").to(torch.bfloat16)
+    dc = torch.randn(16384, 1024, generator=g, device="cuda").to(torch.bfloat16)
+    _, db1, _ = nn.gemm_backward(dc, a, w, need_a=False)
+    _, db2, _ = nn.gemm_backward(dc, a, w, need_a=False)
+    torch.cuda.synchronize()
+    assert torch.equal(db1, db2)
+    cols = torch.arange(0, 1024, 37, device="cuda")
+    ref = a.double().t() @ dc.double()[:, cols]
+    e = rel_l2(db1[:, cols], ref.cpu().numpy())
+    print(f"  rel-L2={e:.2e}", flush=True)
+    assert e <= 1e-2
+
+
+@pytest.mark.parametrize("m,k,n", [(2048, 1024, 4096), (300, 200, 264), (130, 70, 33)])
+def test_gemm_gelu_fused(m, k, n):
+    """gemm_gelu_forward / gemm_gelu_backward: pre = a b + bias, out =
+    GELU_tanh(bf16(pre)); dpre = bf16(dc b2^T) GELU'(pre), db2 = out^T dc,
+    dbias = colsum(dc), against torch fp32 with the same bf16 roundings
+    (the last shape is not one the large-tile kernel takes: fallback path)."""
+    from ceo_amd import nn
+
+    announce(f"gemm_gelu fused {m}x{k}x{n}")
+    g = torch.Generator(device="cuda").manual_seed(m + k + n)
+    a = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+    w = (0.05 * torch.randn(k, n, generator=g, device="cuda")).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g, device="cuda").to(torch.bfloat16)
+    pre, out = nn.gemm_gelu_forward(a, w, bias)
+    pre_ref = (a.float() @ w.float() + bias.float()).to(torch.bfloat16)
+    out_ref = torch.nn.functional.gelu(pre_ref.float(), approximate="tanh")
+    e1, e2 = rel_l2(pre, pre_ref.float().cpu().numpy()), rel_l2(out, out_ref.cpu().numpy())
+    # the MLP's second product and its backward through the GELU
+    w2 = (0.05 * torch.randn(n, k, generator=g, device="cuda")).to(torch.bfloat16)
+    dc = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+    dpre, dw2, dbias = nn.gemm_gelu_backward(dc, out, w2, pre, need_bias=True)
+    x = pre.float().requires_grad_(True)
+    gl = torch.nn.functional.gelu(x, approximate="tanh")
+    (gl * (dc.float() @ w2.float().t()).to(torch.bfloat16).float()).sum().backward()
+    e3 = rel_l2(dpre, x.grad.cpu().numpy())
+    e4 = rel_l2(dw2, (out.float().t() @ dc.float()).cpu().numpy())
+    e5 = rel_l2(dbias, dc.float().sum(0).cpu().numpy())
+    print(f"  rel-L2 pre {e1:.2e} out {e2:.2e} dpre {e3:.2e} dw2 {e4:.2e} dbias {e5:.2e}",
+          flush=True)
+    assert max(e1, e2, e3, e4, e5) <= 1e-2
