@@ -13,7 +13,10 @@
 // holding 4 consecutive n of one output row m and writes 8-byte row pieces.
 // Per k-iteration each operand tile (256 lines x 64 k, 32 KB) is copied
 // straight from global memory into LDS (global_load_lds_dwordx4, 16 bytes per
-// lane, no VGPR staging) one iteration ahead, double-buffered.  Both LDS
+// lane, no VGPR staging) one iteration ahead, double-buffered; all of an
+// iteration's copies are issued at its start, and the MFMA operand fragments
+// are double-buffered in registers with the LDS reads of k step ks + 1
+// interleaved between the MFMAs of k step ks.  Both LDS
 // layouts are XOR-swizzled in 16-byte chunks so the fragment reads are free
 // of bank conflicts:
 //   KC tile [line][k]  (128 B rows):  chunk c of line L at c ^ ((L >> 1) & 7)
@@ -214,59 +217,60 @@ __device__ __forceinline__ void epilogue4(const EpiArgs<T>& ea, long m, long n, 
 }
 
 // --- epilogue staged through LDS ---------------------------------------------
-// The 256 x 256 output tile goes through the free 64 KB LDS buffer as fp32 in
-// four quarters of 64 rows.  The waves that own a quarter's rows write their
-// alpha acc there; then all waves read it back as 8-element row
-// pieces and finish the epilogue -- bias, residual, GELU and its derivative, with
-// the residual and pre-activation read, and the outputs written, as whole
-// 16-byte pieces coalesced along the rows (an MFMA result tile instead holds
-// 8-byte pieces of 32 rows per store instruction).  Layout [64][256] fp32
-// (1 KB rows), 16-byte chunk c of row r at c ^ (r & 15): conflict-free for
-// both the owners' writes (32 rows, one chunk) and the row-wise reads.
+// Each wave finishes its own 128 x (32 TNI) block of the output through a
+// private slice of the free LDS buffer (32 rows x 32 TNI columns of fp32,
+// 4 KB TNI), one 32-row m tile at a time: it writes alpha acc there in the
+// MFMA layout, reads it back as 8-element row pieces and finishes the
+// epilogue on them -- bias, residual, GELU and its derivative, with the
+// residual and pre-activation read, and the outputs written, as whole
+// 16-byte (32-byte for fp32 partials) pieces, eight or more lanes to a row
+// (an MFMA result tile instead holds 8-byte pieces of 32 rows per store
+// instruction).  No workgroup barrier is needed until the buffer is handed
+// back.  Slice layout [32][32 TNI] fp32, 16-byte chunk c of row r at
+// c ^ (r & 15): conflict-free for the MFMA-layout writes (32 rows, one chunk)
+// and the row-wise reads.
+template <int TNI>
 __device__ __forceinline__ unsigned ep_off(int row, int col) {  // col % 4 == 0
-    return (unsigned)(row * 1024 + (((col >> 2) ^ (row & 15)) << 4));
+    return (unsigned)(row * (128 * TNI) + (((col >> 2) ^ (row & 15)) << 4));
 }
 
-template <typename T, int EPI, int NW, int TNI>
-__device__ __forceinline__ void epilogue_tile(const EpiArgs<T>& ea, const floatx16 (&acc)[TNI][4],
-                                              int m0, int n0, long M, long N, int wm, int wn,
-                                              int w, int l, char* ep) {
-    constexpr int NTH = 64 * NW;
+template <typename T, int EPI, int TNI>
+__device__ __forceinline__ void epilogue_wave(const EpiArgs<T>& ea, const floatx16 (&acc)[TNI][4],
+                                              int split, long mw, long nw, long M, long N, int l,
+                                              char* wp) {
+    constexpr int WC = 32 * TNI;  // columns of the wave's block
     typedef __attribute__((__vector_size__(8 * sizeof(T)))) T t8;
-    const int tid = 64 * w + l;
 #pragma unroll
-    for (int Q = 0; Q < 4; ++Q) {
-        const long r0 = m0 + 64 * Q;
-        if (r0 >= M) break;  // no row of this quarter exists (uniform over the workgroup)
-        if ((wm >> 7) == (Q >> 1)) {  // owners: m tiles 2 (Q & 1) and 2 (Q & 1) + 1
+    for (int j = 0; j < 4; ++j) {
+        const long r0 = mw + 32 * j;
+        if (r0 >= M) break;  // uniform over the wave
 #pragma unroll
-            for (int i = 0; i < TNI; ++i) {
-                const int col0 = wn + 32 * i + 4 * (l >> 5);
+        for (int i = 0; i < TNI; ++i)
 #pragma unroll
-                for (int qd = 0; qd < 4; ++qd) {
-                    const int col = col0 + 8 * qd;
+            for (int qd = 0; qd < 4; ++qd) {
+                const int col = 32 * i + 8 * qd + 4 * (l >> 5);
+                mf::floatx4 v;
 #pragma unroll
-                    for (int jj = 0; jj < 2; ++jj) {
-                        const int j = 2 * (Q & 1) + jj;
-                        const int row = 32 * jj + (l & 31);
-                        mf::floatx4 v;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) v[e] = ea.alpha * acc[i][j][4 * qd + e];
-                        *reinterpret_cast<mf::floatx4*>(ep + ep_off(row, col)) = v;
-                    }
-                }
+                for (int e = 0; e < 4; ++e)
+                    v[e] = (EPI == EPI_PARTIAL ? 1.f : ea.alpha) * acc[i][j][4 * qd + e];
+                *reinterpret_cast<mf::floatx4*>(wp + ep_off<TNI>(l & 31, col)) = v;
             }
-        }
-        __syncthreads();
 #pragma unroll
-        for (int s = 0; s < 2048 / NTH; ++s) {
-            const int q = NTH * s + tid;
-            const int row = q >> 5, c = q & 31;  // 8-element piece c of the row
-            const long m = r0 + row, n = n0 + 8 * c;
-            if (m >= M || n >= N) continue;
-            const mf::floatx4 v0 = *reinterpret_cast<const mf::floatx4*>(ep + ep_off(row, 8 * c));
+        for (int s = 0; s < WC / 16; ++s) {
+            const int p = 64 * s + l;
+            const int row = p / (WC / 8), c8 = p % (WC / 8);  // 8-element piece c8 of the row
+            const long m = r0 + row, n = nw + 8 * c8;
+            const mf::floatx4 v0 =
+                *reinterpret_cast<const mf::floatx4*>(wp + ep_off<TNI>(row, 8 * c8));
             const mf::floatx4 v1 =
-                *reinterpret_cast<const mf::floatx4*>(ep + ep_off(row, 8 * c + 4));
+                *reinterpret_cast<const mf::floatx4*>(wp + ep_off<TNI>(row, 8 * c8 + 4));
+            if (m >= M || n >= N) continue;
+            if constexpr (EPI == EPI_PARTIAL) {
+                float* dst = ea.part + ((long)split * M + m) * N + n;
+                *reinterpret_cast<mf::floatx4*>(dst) = v0;
+                *reinterpret_cast<mf::floatx4*>(dst + 4) = v1;
+                continue;
+            }
             float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
             if (ea.bias) {
                 const t8 bb = *reinterpret_cast<const t8*>(ea.bias + n);
@@ -296,7 +300,6 @@ __device__ __forceinline__ void epilogue_tile(const EpiArgs<T>& ea, const floatx
             }
             *reinterpret_cast<t8*>(ea.d + m * ea.ldd + n) = y;
         }
-        __syncthreads();  // the buffer is rewritten by the next quarter / item
     }
 }
 
@@ -325,7 +328,6 @@ __global__ void __launch_bounds__(64 * NW) gemm_fast_kernel(Opnd A, Opnd B, long
                                                             long kper) {
     constexpr int NTH = 64 * NW;
     constexpr int TNI = 8 / NW * 2;  // 32-wide n tiles per wave: 4 (NW = 4) or 2 (NW = 8)
-    constexpr int CPW = 32 / NW;     // copy instructions per wave per operand tile
     // two buffers of [A tile | B tile]; the epilogue stages the output through
     // the one the next item's first k-block is not in
     __shared__ __attribute__((aligned(1024))) char smem[4 * TILE_BYTES];
@@ -401,58 +403,66 @@ __global__ void __launch_bounds__(64 * NW) gemm_fast_kernel(Opnd A, Opnd B, long
             }
             const char* at = As(buf);
             const char* bt = Bs(buf);
+            // fragments double-buffered in registers: k step ks + 1 is read
+            // while the MFMAs of k step ks run
+            bf16x8 fb[2][TNI], fa[2][4];
+#pragma unroll
+            for (int i = 0; i < TNI; ++i) fb[0][i] = frag<BKC>(bt, wn + 32 * i, 0, l);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) fa[0][j] = frag<AKC>(at, wm + 32 * j, 0, l);
+            // the next block's copies all go out now, a whole iteration ahead
+            // of the wait (the buffer they fill was last read in the previous
+            // iteration, which every wave has finished)
+            if (fetch && direct) {
+                copy_tile<AKC, NW>(A, src.m0, k0, As(buf ^ 1), w, l);
+                copy_tile<BKC, NW>(B, src.n0, k0, Bs(buf ^ 1), w, l);
+            }
 #pragma unroll
             for (int ks = 0; ks < BK / 16; ++ks) {
-                bf16x8 fb[TNI], fa[4];
+                const int c = ks & 1;
+                if (ks + 1 < BK / 16) {
 #pragma unroll
-                for (int i = 0; i < TNI; ++i) fb[i] = frag<BKC>(bt, wn + 32 * i, ks, l);
+                    for (int i = 0; i < TNI; ++i)
+                        fb[c ^ 1][i] = frag<BKC>(bt, wn + 32 * i, ks + 1, l);
 #pragma unroll
-                for (int j = 0; j < 4; ++j) fa[j] = frag<AKC>(at, wm + 32 * j, ks, l);
-                // a quarter of the next block's copies per k step, between the
-                // MFMAs (the buffer they fill was last read in the previous
-                // iteration, which every wave has finished)
-                if (fetch && direct) {
-                    copy_tile<AKC, NW>(A, src.m0, k0, As(buf ^ 1), w, l, ks * CPW / 4,
-                                       (ks + 1) * CPW / 4);
-                    copy_tile<BKC, NW>(B, src.n0, k0, Bs(buf ^ 1), w, l, ks * CPW / 4,
-                                       (ks + 1) * CPW / 4);
+                    for (int j = 0; j < 4; ++j)
+                        fa[c ^ 1][j] = frag<AKC>(at, wm + 32 * j, ks + 1, l);
                 }
 #pragma unroll
                 for (int i = 0; i < TNI; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = mma32<T>(fb[i], fa[j], acc[i][j]);
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = mma32<T>(fb[c][i], fa[c][j], acc[i][j]);
+                if (ks + 1 < BK / 16) {
+                    // one LDS read between consecutive MFMAs
+                    constexpr int NR = TNI * (BKC ? 1 : 2) + 4 * (AKC ? 1 : 2);
+                    constexpr int NM = 4 * TNI;
+                    constexpr int R = NR < NM ? NR : NM;
+#pragma unroll
+                    for (int r = 0; r < R; ++r) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                    }
+                    if constexpr (NM > R) __builtin_amdgcn_sched_group_barrier(0x008, NM - R, 0);
+                    if constexpr (NR > R) __builtin_amdgcn_sched_group_barrier(0x100, NR - R, 0);
+                }
             }
             mf::dma_wait();
             __syncthreads();
             buf ^= 1;
         }
         // lane l holds, for tile (i, j), output row m = m0 + wm + 32 j + (l & 31)
-        // and columns n = n0 + wn + 32 i + 8 q + 4 (l >> 5) + e in acc[i][j][4 q + e]
-        if constexpr (EPI == EPI_PARTIAL) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const long m = cur.m0 + wm + 32 * j + (l & 31);
-                if (m >= M) continue;
-#pragma unroll
-                for (int i = 0; i < TNI; ++i)
-#pragma unroll
-                    for (int qd = 0; qd < 4; ++qd) {
-                        const long n = cur.n0 + wn + 32 * i + 8 * qd + 4 * (l >> 5);
-                        if (n < N)
-                            *reinterpret_cast<mf::floatx4*>(
-                                ea.part + ((long)cur.split * M + m) * N + n) =
-                                mf::floatx4{acc[i][j][4 * qd], acc[i][j][4 * qd + 1],
-                                            acc[i][j][4 * qd + 2], acc[i][j][4 * qd + 3]};
-                    }
-            }
-        } else {
-            // the lane index re-derived per item (mf::tid_in): the epilogue's
-            // lane-dependent addresses are then not hoisted out of the item
-            // loop, where they would stay live across the main loop
+        // and columns n = n0 + wn + 32 i + 8 q + 4 (l >> 5) + e in acc[i][j][4 q + e].
+        // The lane index is re-derived per item (mf::tid_in): the epilogue's
+        // lane-dependent addresses are then not hoisted out of the item loop,
+        // where they would stay live across the main loop.
+        {
             const int le = mf::tid_in((int)it) & 63;
-            epilogue_tile<T, EPI, NW, TNI>(ea, acc, cur.m0, cur.n0, M, N, wm, wn, w, le,
-                                           smem + 2 * (buf ^ 1) * TILE_BYTES);
+            char* wp = smem + 2 * (buf ^ 1) * TILE_BYTES + (4096 * TNI) * w;
+            epilogue_wave<T, EPI, TNI>(ea, acc, cur.split, (long)cur.m0 + wm, (long)cur.n0 + wn,
+                                       M, N, le, wp);
         }
+        __syncthreads();  // the next item's first copies refill the buffer
         if (!more) break;
         it = nitn;
         cur = nxt;

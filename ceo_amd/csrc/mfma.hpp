@@ -285,10 +285,15 @@ __device__ __forceinline__ void store_tile(bf16* __restrict__ dst, long ld, cons
 // builtin form makes every following ds_read wait for vmcnt(0)); the caller
 // runs dma_wait() and a workgroup barrier before anyone reads the destination,
 // and keeps the destination unread and unwritten while the copy is in flight.
+// The compiler inserts no hazard wait states in front of inline asm, so the asm
+// starts with its own: gfx9 needs 5 after a VALU write of an SGPR the VMEM
+// instruction reads (the base, when it was made uniform by v_readfirstlane)
+// and 1 after the write of m0.
 __device__ __forceinline__ void dma16(const void* base, unsigned off, const void* lds) {
     const unsigned m0 =
         (unsigned)(uintptr_t)(__attribute__((address_space(3))) const void*)lds;
-    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(m0) : "memory");
+    asm volatile("s_nop 4\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(off), "s"(base), "{m0}"(m0)
+                 : "memory");
 }
 // this wave's vector memory operations (loads, stores and LDS copies) done
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
