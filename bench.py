@@ -335,41 +335,87 @@ def aux_bench(steps: int, warmup: int) -> int:
     out = {}
     stream = torch.cuda.current_stream(dev)
 
-    def run(fn, n_warm, n):
-        """Average ms per call over n back-to-back calls between one event pair
-        (no per-launch events), then the per-kernel split from a profiled pass."""
+    def run(fn, n_warm, n, graph=True):
+        """Average ms per call over n back-to-back calls between one event pair.
+        With ``graph`` the n calls are captured in one HIP graph on a side
+        stream (warmed first, so its cached workspace exists before capture)
+        and the graph is replayed between the events: the Python wrappers cost
+        several microseconds of host time per call, which would otherwise show
+        up as GPU idle time between the short HBM-bound kernels.  Then the
+        per-kernel split from an eager profiled pass."""
         for _ in range(n_warm):
             fn()
+        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(stream)
-        for _ in range(n):
-            fn()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        avg = e0.elapsed_time(e1) / n
+        avg, mode = None, "eager"
+        if graph:
+            try:
+                cs = torch.cuda.Stream()
+                cs.wait_stream(stream)
+                with torch.cuda.stream(cs):
+                    for _ in range(2):
+                        fn()
+                torch.cuda.synchronize()
+                gr = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(gr, stream=cs):
+                    for _ in range(n):
+                        fn()
+                gr.replay()
+                torch.cuda.synchronize()
+                e0.record(stream)
+                gr.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                avg, mode = e0.elapsed_time(e1) / n, "graph"
+                del gr
+            except Exception as exc:  # capture refused: time the eager calls
+                print(f"[bench] graph capture failed ({exc}); eager timing", file=sys.stderr,
+                      flush=True)
+                torch.cuda.synchronize()
+        if avg is None:
+            e0.record(stream)
+            for _ in range(n):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            avg = e0.elapsed_time(e1) / n
         with runtime.Profiler() as prof:
             for _ in range(n):
                 fn()
         res = prof.results()
-        return avg, {k: round(tot / cnt, 4) for k, (cnt, tot) in res.items()}
+        return avg, {k: round(tot / cnt, 4) for k, (cnt, tot) in res.items()}, mode
 
     for name, (fn, flops) in gemms.items():
-        avg_ms, kms = run(fn, warmup, steps)
+        avg_ms, kms, mode = run(fn, warmup, steps)
         tf = flops / (avg_ms * 1e-3) / 1e12
         out[name] = {"avg_ms": round(avg_ms, 4), "flops": flops, "TFLOP/s": round(tf, 1),
                      "frac_of_bf16_peak": round(tf / PEAK_BF16_TFLOPS, 4),
-                     "kernels_ms": kms}
+                     "timing": mode, "kernels_ms": kms}
         print(f"[bench] {name}: {avg_ms:.4f} ms, {tf:.0f} TFLOP/s", file=sys.stderr, flush=True)
     del xu, dcu
+    # the practical HBM ceiling for a read + write stream: a device copy of
+    # 1 GiB (too large for the 256 MB MALL to hold across calls)
+    csrc = torch.empty(1 << 28, dtype=torch.float32, device=dev).fill_(1.0)
+    cdst = torch.empty_like(csrc)
+    c_ms, _, c_mode = run(lambda: cdst.copy_(csrc), 2, 10)
+    copy_gbs = 2 * csrc.numel() * 4 / (c_ms * 1e-3) / 1e9
+    out["copy_1GiB_ceiling"] = {"avg_ms": round(c_ms, 4), "bytes": 2 * csrc.numel() * 4,
+                                "bytes_are": "1 GiB fp32 in, 1 GiB out (torch copy_)",
+                                "GB/s": round(copy_gbs, 1),
+                                "frac_of_hbm_peak": round(copy_gbs / PEAK_HBM_GBS, 4),
+                                "timing": c_mode}
+    print(f"[bench] copy_1GiB_ceiling: {c_ms:.4f} ms, {copy_gbs:.0f} GB/s", file=sys.stderr,
+          flush=True)
+    del csrc, cdst
     for name, (fn, nbytes, what) in cases.items():
         # the op's time: every kernel it launched (LayerNorm's backward has a
         # second, small reduction kernel), averaged over the timed calls
-        avg_ms, kms = run(fn, warmup, steps)
+        avg_ms, kms, mode = run(fn, warmup, steps)
         gbs = nbytes / (avg_ms * 1e-3) / 1e9
         out[name] = {"avg_ms": round(avg_ms, 4), "bytes": nbytes, "bytes_are": what,
                      "GB/s": round(gbs, 1), "frac_of_hbm_peak": round(gbs / PEAK_HBM_GBS, 4),
-                     "kernels_ms": kms}
+                     "frac_of_copy_ceiling": round(gbs / copy_gbs, 4) if copy_gbs else None,
+                     "timing": mode, "kernels_ms": kms}
         print(f"[bench] {name}: {avg_ms:.4f} ms, {gbs:.0f} GB/s", file=sys.stderr, flush=True)
     del cases, x, dy, h, dh, p32, m32, v32, gp, pcopy
     # the reference ABI's entries (efla_forward_hip / efla_backward_hip, Mode R:
@@ -387,7 +433,7 @@ def aux_bench(steps: int, warmup: int) -> int:
         "efla_backward_hip_cfg3": lambda: efla.efla_backward(dor, kr, vr, s0, 0.5),
     }
     for name, fn in mode_r.items():
-        avg_ms, kms = run(fn, 1, 3)
+        avg_ms, kms, _ = run(fn, 1, 3, graph=False)
         out[name] = {"avg_ms": round(avg_ms, 3), "tokens_per_s": round(B * T / (avg_ms * 1e-3), 1),
                      "shape": f"B={B} T={T} H={H} d={d} bf16", "kernels_ms": kms}
         print(f"[bench] {name}: {avg_ms:.3f} ms", file=sys.stderr, flush=True)

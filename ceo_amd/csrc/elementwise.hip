@@ -173,12 +173,12 @@ __global__ void __launch_bounds__(NTH) adamw_master_kernel(float* __restrict__ p
 inline bool aligned16(const void* q) { return q == nullptr || ((uintptr_t)q & 15) == 0; }
 
 // Vector count (0: scalar loop only) and grid for n elements.
-inline void plan(size_t n, bool vec, long* n8, dim3* grid) {
+inline void plan(size_t n, bool vec, long* n8, dim3* grid, long max_blocks = kMaxBlocks) {
     *n8 = vec ? (long)(n / 8) : 0;
     const long work = vec ? *n8 : (long)n;
     long blocks = (work + NTH - 1) / NTH;
     if (blocks < 1) blocks = 1;
-    if (blocks > kMaxBlocks) blocks = kMaxBlocks;
+    if (blocks > max_blocks) blocks = max_blocks;
     *grid = dim3((unsigned)blocks);
 }
 
@@ -340,7 +340,7 @@ extern "C" int adamw_step_master_hip(float* param, const void* grad, float* exp_
     ew::plan(numel,
              ew::aligned16(param) && ew::aligned16(grad) && ew::aligned16(exp_avg) &&
                  ew::aligned16(exp_avg_sq) && ew::aligned16(param_bf16),
-             &n8, &grid);
+             &n8, &grid, 4 * ew::kMaxBlocks);  // 2-3 % faster than 4096 on 368M values
     EFLA_LAUNCH("adamw_master", ew::adamw_master_kernel, grid, dim3(ew::NTH), stream, param,
                 (const bf16*)grad, exp_avg, exp_avg_sq, (bf16*)param_bf16, (long)numel, n8, a);
     return (int)hipPeekAtLastError();
