@@ -261,12 +261,14 @@ def measured_traffic(config: str, kernel: str):
 CFG4 = {"tokens": 16384, "d_model": 1024, "mlp": 4096, "params": 368_000_000}
 
 
-def aux_bench(steps: int, warmup: int) -> int:
+def aux_bench(steps: int, warmup: int, ops_only: int = 0) -> int:
     """Times the kernels around EFLA at config-4 shapes: the GEMMs of one layer
     and the LM head against the bf16 MFMA roof (their FLOPs over the average
     hipEvent duration), LayerNorm / GELU / AdamW and the reference model's
     RMSNorm / ShortConv / PRISM against the HBM roof (algorithmic bytes per
     launch: what each must read and write once).
+    With ``ops_only`` = N it instead runs each HBM-bound op N times, untimed
+    (the program that rocprofv3 FETCH_SIZE / WRITE_SIZE passes profile).
     Prints one JSON line."""
     import torch
 
@@ -320,6 +322,14 @@ def aux_bench(steps: int, warmup: int) -> int:
         "prism_bwd_l3": (lambda: prism.prism_backward(dy3, x3, dy3, w_p, 64, gw_p),
                          N * 64 * 6 + N * D * 4, "g, u, v in over head_dim 64, du, dv rows out"),
     }
+    if ops_only:
+        for name, (fn, nbytes, _) in cases.items():
+            for _ in range(ops_only):
+                fn()
+            torch.cuda.synchronize()
+        print(json.dumps({"aux_ops": {k: v[1] for k, v in cases.items()},
+                          "launches_each": ops_only}), flush=True)
+        return 0
     # GEMMs of one config-4 layer and the LM head (MFMA-bound: FLOPs, not bytes)
     wq, wu, wd, wh = bf(D, 3 * D, scale=0.03), bf(D, F, scale=0.03), bf(F, D, scale=0.02), \
         bf(D, 32000, scale=0.03)
@@ -537,12 +547,17 @@ def main() -> int:
                     help="only run a plain device-to-device copy of MIB MiB five times "
                          "(the known-size kernel that calibrates rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings) and exit")
+    ap.add_argument("--aux-ops", type=int, default=0, metavar="N",
+                    help="only run each --aux HBM-bound op N times, untimed, and exit "
+                         "(for rocprofv3 counter passes)")
     ap.add_argument("--aux", action="store_true",
                     help="only time the config-4 LayerNorm / GELU / AdamW kernels against "
                          "the HBM roof (one JSON line) and exit")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.aux_ops:
+        return aux_bench(0, 0, ops_only=args.aux_ops)
     if args.aux:
         return aux_bench(args.steps, args.warmup)
 
