@@ -242,7 +242,7 @@ def test_gemm_forward_mixed_dtypes():
 
 
 def test_gemm_bias_epilogue_at_layer_shape():
-    """hipBLASLt's bias epilogue on a config-4 projection shape, against torch."""
+    """The bias epilogue on a config-4 projection shape, against torch."""
     from ceo_amd.nn import gemm_forward
 
     announce("gemm_forward 2048x1024x3072 bf16 + bias")
@@ -399,5 +399,59 @@ def test_gemm_gelu_fused(m, k, n):
     e4 = rel_l2(dw2, (out.float().t() @ dc.float()).cpu().numpy())
     e5 = rel_l2(dbias, dc.float().sum(0).cpu().numpy())
     print(f"  rel-L2 pre {e1:.2e} out {e2:.2e} dpre {e3:.2e} dw2 {e4:.2e} dbias {e5:.2e}",
+          flush=True)
+    assert max(e1, e2, e3, e4, e5) <= 1e-2
+
+
+@pytest.mark.parametrize("name,m,k,n", [("qkv", 16384, 1024, 3088), ("out", 16384, 1024, 1024),
+                                        ("up", 16384, 1024, 4096), ("down", 16384, 4096, 1024)])
+def test_gemm_config4_products(name, m, k, n):
+    """Every product of a config-4 layer at its full size on the default
+    (hand-written) kernel: the forward with bias, the input gradient, the
+    weight gradient (split-K) and the bias gradient, against torch fp32."""
+    from ceo_amd import nn
+
+    announce(f"gemm config-4 {name} {m}x{k}x{n}: forward, dA, dB, dbias")
+    g = torch.Generator(device="cuda").manual_seed(k + n)
+    a = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
+    w = (0.03 * torch.randn(k, n, generator=g, device="cuda")).to(torch.bfloat16)
+    bias = torch.randn(n, generator=g, device="cuda").to(torch.bfloat16)
+    dc = torch.randn(m, n, generator=g, device="cuda").to(torch.bfloat16)
+    c = nn.gemm_forward(a, w, bias)
+    e0 = rel_l2(c, (a.float() @ w.float() + bias.float()).cpu().numpy())
+    da, dw, db = nn.gemm_backward(dc, a, w, need_bias=True)
+    e1 = rel_l2(da, (dc.float() @ w.float().t()).cpu().numpy())
+    e2 = rel_l2(dw, (a.float().t() @ dc.float()).cpu().numpy())
+    e3 = rel_l2(db, dc.float().sum(0).cpu().numpy())
+    print(f"  rel-L2 fwd {e0:.2e} dA {e1:.2e} dB {e2:.2e} dbias {e3:.2e}", flush=True)
+    assert max(e0, e1, e2, e3) <= 1e-2
+
+
+def test_gemm_gelu_config4_mlp():
+    """The config-4 MLP's fused products at full size: up-projection with bias
+    and GELU (pre-activation kept), and the down-projection's input gradient
+    through GELU', against torch fp32 with the same bf16 roundings."""
+    from ceo_amd import nn
+
+    m, d, f = 16384, 1024, 4096
+    announce(f"gemm_gelu config-4 MLP {m}x{d}x{f}")
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(m, d, generator=g, device="cuda").to(torch.bfloat16)
+    w_up = (0.03 * torch.randn(d, f, generator=g, device="cuda")).to(torch.bfloat16)
+    b_up = torch.randn(f, generator=g, device="cuda").to(torch.bfloat16)
+    w_down = (0.02 * torch.randn(f, d, generator=g, device="cuda")).to(torch.bfloat16)
+    pre, out = nn.gemm_gelu_forward(x, w_up, b_up)
+    pre_ref = (x.float() @ w_up.float() + b_up.float()).to(torch.bfloat16)
+    e1 = rel_l2(pre, pre_ref.float().cpu().numpy())
+    e2 = rel_l2(out, torch.nn.functional.gelu(pre_ref.float(), approximate="tanh").cpu().numpy())
+    dy = torch.randn(m, d, generator=g, device="cuda").to(torch.bfloat16)
+    dpre, dw, db = nn.gemm_gelu_backward(dy, out, w_down, pre, need_bias=True)
+    t = pre.float().requires_grad_(True)
+    gl = torch.nn.functional.gelu(t, approximate="tanh")
+    (gl * (dy.float() @ w_down.float().t()).to(torch.bfloat16).float()).sum().backward()
+    e3 = rel_l2(dpre, t.grad.cpu().numpy())
+    e4 = rel_l2(dw, (out.float().t() @ dy.float()).cpu().numpy())
+    e5 = rel_l2(db, dy.float().sum(0).cpu().numpy())
+    print(f"  rel-L2 pre {e1:.2e} out {e2:.2e} dpre {e3:.2e} dw {e4:.2e} dbias {e5:.2e}",
           flush=True)
     assert max(e1, e2, e3, e4, e5) <= 1e-2
