@@ -61,10 +61,22 @@ def _small():
     return LMConfig(vocab=256, d_model=128, n_layers=2, n_heads=2, head_dim=64, mlp=512)
 
 
-def test_step_gradients_match_autograd():
+@pytest.fixture(params=[0, 1, 2], ids=["mfma", "generic", "hipblaslt"])
+def gemm_backend(request):
+    """The step on the library's large-tile GEMM (default), on its generic
+    kernel only, and with hipBLASLt's products, restoring the default after."""
+    from ceo_amd._lib import lib
+
+    assert lib().efla_rt_set_gemm_backend(request.param) == 0
+    yield request.param
+    assert lib().efla_rt_set_gemm_backend(0) == 0
+
+
+def test_step_gradients_match_autograd(gemm_backend):
     from ceo_amd.lm_step import EflaLM, synthetic_batch
 
-    announce("lm step: gradients vs torch autograd (2 layers, d=128, T=128)")
+    announce(f"lm step: gradients vs torch autograd (2 layers, d=128, T=128), "
+             f"gemm backend {gemm_backend}")
     cfg = _small()
     model = EflaLM(cfg, seed=1)
     # larger weights than the default init so every path carries signal
