@@ -118,6 +118,7 @@ _SIGS = {
     "embedding_backward_hip": (i32, [vp, vp, vp, sz, sz, sz, vp]),
     "cross_entropy_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
     "cross_entropy_backward_hip": (i32, [vp, vp, vp, vp, sz, sz, f32, vp]),
+    "cross_entropy_forward_backward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     # sequence packing (host)
     "efla_pack_sequences": (i32, [vp, vp, sz, sz, vp, vp, vp, vp, ctypes.POINTER(sz),
                                   ctypes.POINTER(sz)]),

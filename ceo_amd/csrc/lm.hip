@@ -19,8 +19,9 @@
 // One workgroup per row; when the row fits (V <= 8192 * NV for the compiled
 // NV, V % 8 == 0, aligned rows) it is held in registers, so the forward reads
 // the logits once and the backward reads them once and writes the gradient
-// once.  Other rows take a looped two-pass path.  A target outside [0, V)
-// gives loss NaN and a zero gradient row.
+// once; cross_entropy_forward_backward_hip (no reference counterpart) does
+// both from one read, optionally in place.  Other rows take a looped two-pass
+// path.  A target outside [0, V) gives loss NaN and a zero gradient row.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -114,19 +115,25 @@ __device__ __forceinline__ void ms_push(float& m, float& s, float x) {
     }
 }
 
-// NV = 16-byte vectors per thread held in registers (0: looped path)
-template <int NV, bool BWD>
-__global__ void __launch_bounds__(CNT) ce_kernel(const bf16* __restrict__ logits,
+// NV = 16-byte vectors per thread held in registers (0: looped path).
+// MODE: CE_FWD loss only; CE_BWD gradient only; CE_BOTH both from one read of
+// the row (grad_loss NULL: 1 for every row; grad may be the logits themselves:
+// every element is read before any is written, by the thread that writes it).
+enum { CE_FWD = 0, CE_BWD = 1, CE_BOTH = 2 };
+template <int NV, int MODE>
+__global__ void __launch_bounds__(CNT) ce_kernel(const bf16* logits,
                                                  const int32_t* __restrict__ targets,
                                                  const float* __restrict__ grad_loss,
                                                  float* __restrict__ loss,
-                                                 bf16* __restrict__ grad, long B, long V,
+                                                 bf16* grad, long B, long V,
                                                  float eps) {
     __shared__ float sm_m[CW], sm_s[CW];
     const long row = blockIdx.x;
     const bf16* z = logits + row * V;
     const long t = targets[row];
     const bool tok = t >= 0 && t < V;
+    // the target's logit, read before anything of the row can be overwritten
+    const float zt = (MODE != CE_BWD && threadIdx.x == 0 && tok) ? (float)z[t] : 0.f;
     float m = -INFINITY, s = 0.f;
     bf16x8 xv[NV > 0 ? NV : 1];
     if constexpr (NV > 0) {
@@ -145,16 +152,16 @@ __global__ void __launch_bounds__(CNT) ce_kernel(const bf16* __restrict__ logits
     ms_reduce(m, s, sm_m, sm_s);
     const float lse = m + __logf(s);
     const float inv_b = 1.0f / (float)B;
-    if constexpr (!BWD) {
+    if constexpr (MODE != CE_BWD) {
         if (threadIdx.x == 0) {
-            const float zt = tok ? (float)z[t] : 0.f;
             const float l = (1.f - eps) * (lse - zt) + eps * logf((float)V);
             loss[row] = tok ? l * inv_b : NAN;
         }
-        return;
-    } else {
+    }
+    if constexpr (MODE != CE_FWD) {
         // softmax_j = exp(z_j - lse); dz_j = coef (softmax_j - [j = t])
-        const float coef = tok ? grad_loss[row] * (1.f - eps) * inv_b : 0.f;
+        const float gl = (MODE == CE_BOTH && !grad_loss) ? 1.f : grad_loss[row];
+        const float coef = tok ? gl * (1.f - eps) * inv_b : 0.f;
         bf16* g = grad + row * V;
         if constexpr (NV > 0) {
 #pragma unroll
@@ -180,21 +187,24 @@ __global__ void __launch_bounds__(CNT) ce_kernel(const bf16* __restrict__ logits
     }
 }
 
-template <bool BWD>
+template <int MODE>
 static int ce_launch(const bf16* z, const int32_t* t, const float* gl, float* loss, bf16* g,
                      long B, long V, float eps, hipStream_t st) {
-    const bool vec = V % 8 == 0 && ((uintptr_t)z & 15) == 0 && (!BWD || ((uintptr_t)g & 15) == 0);
+    const bool vec =
+        V % 8 == 0 && ((uintptr_t)z & 15) == 0 && (MODE == CE_FWD || ((uintptr_t)g & 15) == 0);
     const long nvec = (V / 8 + CNT - 1) / CNT;  // vectors per thread
-    const char* name = BWD ? "cross_entropy_bwd" : "cross_entropy_fwd";
+    const char* name = MODE == CE_FWD   ? "cross_entropy_fwd"
+                       : MODE == CE_BWD ? "cross_entropy_bwd"
+                                        : "cross_entropy_fwd_bwd";
     const dim3 grid((unsigned)B), block(CNT);
-#define CE_CASE(nv)                                                                        \
-    if (vec && nvec <= nv) {                                                               \
-        EFLA_LAUNCH(name, (ce_kernel<nv, BWD>), grid, block, st, z, t, gl, loss, g, B, V, eps); \
-        return (int)hipPeekAtLastError();                                                  \
+#define CE_CASE(nv)                                                                         \
+    if (vec && nvec <= nv) {                                                                \
+        EFLA_LAUNCH(name, (ce_kernel<nv, MODE>), grid, block, st, z, t, gl, loss, g, B, V, eps); \
+        return (int)hipPeekAtLastError();                                                   \
     }
     CE_CASE(1) CE_CASE(2) CE_CASE(4) CE_CASE(8)
 #undef CE_CASE
-    EFLA_LAUNCH(name, (ce_kernel<0, BWD>), grid, block, st, z, t, gl, loss, g, B, V, eps);
+    EFLA_LAUNCH(name, (ce_kernel<0, MODE>), grid, block, st, z, t, gl, loss, g, B, V, eps);
     return (int)hipPeekAtLastError();
 }
 
@@ -266,7 +276,7 @@ extern "C" int cross_entropy_forward_hip(const void* logits, const int32_t* targ
     int rc = lm::ce_check(logits, targets, batch_size, vocab_size, label_smoothing);
     if (rc != kSuccess || batch_size == 0) return rc;
     if (!loss) return kInvalidValue;
-    return lm::ce_launch<false>((const bf16*)logits, targets, nullptr, (float*)loss, nullptr,
+    return lm::ce_launch<lm::CE_FWD>((const bf16*)logits, targets, nullptr, (float*)loss, nullptr,
                                 (long)batch_size, (long)vocab_size, label_smoothing, stream);
 }
 
@@ -277,7 +287,20 @@ extern "C" int cross_entropy_backward_hip(const void* grad_loss, const void* log
     int rc = lm::ce_check(logits, targets, batch_size, vocab_size, label_smoothing);
     if (rc != kSuccess || batch_size == 0) return rc;
     if (!grad_loss || !grad_logits) return kInvalidValue;
-    return lm::ce_launch<true>((const bf16*)logits, targets, (const float*)grad_loss, nullptr,
-                               (bf16*)grad_logits, (long)batch_size, (long)vocab_size,
-                               label_smoothing, stream);
+    return lm::ce_launch<lm::CE_BWD>((const bf16*)logits, targets, (const float*)grad_loss,
+                                     nullptr, (bf16*)grad_logits, (long)batch_size,
+                                     (long)vocab_size, label_smoothing, stream);
+}
+
+extern "C" int cross_entropy_forward_backward_hip(const void* logits, const int32_t* targets,
+                                                  const float* grad_loss, float* loss,
+                                                  void* grad_logits, size_t batch_size,
+                                                  size_t vocab_size, float label_smoothing,
+                                                  hipStream_t stream) {
+    int rc = lm::ce_check(logits, targets, batch_size, vocab_size, label_smoothing);
+    if (rc != kSuccess || batch_size == 0) return rc;
+    if (!loss || !grad_logits) return kInvalidValue;
+    return lm::ce_launch<lm::CE_BOTH>((const bf16*)logits, targets, grad_loss, loss,
+                                      (bf16*)grad_logits, (long)batch_size, (long)vocab_size,
+                                      label_smoothing, stream);
 }

@@ -168,8 +168,12 @@ class EflaLM:
                                           save_stats=True)
         logits = nn.gemm_forward(af, self.w("head"))
         tflat = targets.reshape(-1)
-        loss_rows = nn.cross_entropy_forward(logits, tflat, cfg.label_smoothing)
-        saved.update(x=x, af=af, mf=mf, rf=rf, logits=logits, targets=tflat)
+        # the loss and dL/dlogits of the summed rows from one read of the
+        # logits, the gradient written over them (the backward needs no logits)
+        loss_rows, dlogits = nn.cross_entropy_forward_backward(logits, tflat,
+                                                               cfg.label_smoothing,
+                                                               in_place=True)
+        saved.update(x=x, af=af, mf=mf, rf=rf, dlogits=dlogits, targets=tflat)
         return loss_rows.sum(), saved
 
     # -- backward -------------------------------------------------------------
@@ -180,10 +184,8 @@ class EflaLM:
         N, D, H, dh = B * T, cfg.d_model, cfg.n_heads, cfg.head_dim
         HD = H * dh
         ws = self._workspaces(B, T)
-        ones = torch.ones(N, dtype=torch.float32, device=self.device)
-        dlogits = nn.cross_entropy_backward(ones, saved["logits"], saved["targets"],
-                                            cfg.label_smoothing)
-        saved["logits"] = None
+        dlogits = saved["dlogits"]
+        saved["dlogits"] = None
         daf, _, _ = nn.gemm_backward(dlogits, saved["af"], self.w("head"),
                                      out_b=self.gr("head"))
         del dlogits

@@ -351,6 +351,26 @@ def cross_entropy_forward(logits: torch.Tensor, targets: torch.Tensor,
     return loss
 
 
+def cross_entropy_forward_backward(logits: torch.Tensor, targets: torch.Tensor,
+                                   label_smoothing: float = 0.0,
+                                   grad_loss=None, in_place: bool = False):
+    """(per-row loss / batch fp32 (B,), dL/dlogits bf16) from one read of the
+    logits; dL/dloss[i] = grad_loss[i], or 1 for every row when None.  With
+    in_place the gradient overwrites ``logits``."""
+    _require(logits, "logits", torch.bfloat16)
+    _require(targets, "targets", torch.int32, logits.device)
+    if grad_loss is not None:
+        _require(grad_loss, "grad_loss", torch.float32, logits.device)
+    B, V = logits.shape
+    loss = torch.empty(B, dtype=torch.float32, device=logits.device)
+    g = logits if in_place else torch.empty_like(logits)
+    rc = lib().cross_entropy_forward_backward_hip(_p(logits), _p(targets), _p(grad_loss),
+                                                  _p(loss), _p(g), B, V,
+                                                  float(label_smoothing), _stream(logits))
+    check(rc, "cross_entropy_forward_backward_hip")
+    return loss, g
+
+
 def cross_entropy_backward(grad_loss: torch.Tensor, logits: torch.Tensor, targets: torch.Tensor,
                            label_smoothing: float = 0.0) -> torch.Tensor:
     """dL/dlogits (bf16) given dL/dloss[i] (fp32, (B,))."""

@@ -477,6 +477,17 @@ int cross_entropy_backward_hip(const void* grad_loss, const void* logits, const 
                                void* grad_logits, size_t batch_size, size_t vocab_size,
                                float label_smoothing, hipStream_t stream);
 
+/* No reference counterpart: cross_entropy_forward_hip and
+ * cross_entropy_backward_hip from one read of the logits.  loss[i] as the
+ * forward; grad_logits as the backward with dL/dloss[i] = grad_loss[i]
+ * (grad_loss NULL: 1 for every row, the gradient of the summed rows).
+ * grad_logits may be logits itself (overwritten in place).  Same codes as
+ * the two entries. */
+int cross_entropy_forward_backward_hip(const void* logits, const int32_t* targets,
+                                       const float* grad_loss, float* loss, void* grad_logits,
+                                       size_t batch_size, size_t vocab_size,
+                                       float label_smoothing, hipStream_t stream);
+
 /* ========================================================================
  * Sequence packing (host, no GPU)
  * ======================================================================== */

@@ -299,6 +299,11 @@ def test_embedding_and_cross_entropy_validation(L):
     assert L.cross_entropy_forward_hip(p, p, NULL, 4, 100, 0.0, NULL) == 1
     assert L.cross_entropy_backward_hip(NULL, p, p, p, 4, 100, 0.0, NULL) == 1
     assert L.cross_entropy_backward_hip(p, p, p, p, 4, 100, float("nan"), NULL) == 1
+    assert L.cross_entropy_forward_backward_hip(p, p, NULL, p, p, 0, 100, 0.0, NULL) == 0
+    assert L.cross_entropy_forward_backward_hip(NULL, p, NULL, p, p, 4, 100, 0.0, NULL) == 1
+    assert L.cross_entropy_forward_backward_hip(p, p, NULL, NULL, p, 4, 100, 0.0, NULL) == 1
+    assert L.cross_entropy_forward_backward_hip(p, p, NULL, p, NULL, 4, 100, 0.0, NULL) == 1
+    assert L.cross_entropy_forward_backward_hip(p, p, NULL, p, p, 4, 100, 1.0, NULL) == 1
 
 
 def test_affine_state_scan_validation(L):

@@ -62,6 +62,34 @@ def test_cross_entropy(oracle, B, V, eps):
     assert err <= 1e-5 and eg <= 1e-2
 
 
+@pytest.mark.parametrize("B,V,eps", [(37, 32000, 0.1), (9, 1000, 0.0), (3, 70000, 0.0)])
+def test_cross_entropy_forward_backward_fused(B, V, eps):
+    """The one-pass entry gives the two entries' results bit for bit: with a
+    per-row grad_loss, with grad_loss NULL (= ones) and in place over the
+    logits (the row-in-registers path and the looped path for V = 70000)."""
+    from ceo_amd.nn import (cross_entropy_backward, cross_entropy_forward,
+                            cross_entropy_forward_backward)
+
+    announce(f"cross_entropy fused fwd+bwd B={B} V={V} eps={eps}")
+    g = torch.Generator().manual_seed(B + V)
+    z = (torch.randn(B, V, generator=g) * 4).to(torch.bfloat16).cuda()
+    t = torch.randint(0, V, (B,), generator=g, dtype=torch.int32)
+    t[1] = -1  # invalid target: NaN loss, zero gradient row
+    t = t.cuda()
+    gl = (torch.rand(B, generator=g) + 0.5).cuda()
+    loss_ref = cross_entropy_forward(z, t, eps)
+    grad_ref = cross_entropy_backward(gl, z, t, eps)
+    ones_ref = cross_entropy_backward(torch.ones(B, device="cuda"), z, t, eps)
+    loss, grad = cross_entropy_forward_backward(z, t, eps, grad_loss=gl)
+    assert torch.equal(loss.nan_to_num(), loss_ref.nan_to_num()) and torch.isnan(loss[1])
+    assert torch.equal(grad, grad_ref)
+    zc = z.clone()
+    loss2, grad2 = cross_entropy_forward_backward(zc, t, eps, in_place=True)
+    assert grad2.data_ptr() == zc.data_ptr()
+    assert torch.equal(loss2.nan_to_num(), loss_ref.nan_to_num())
+    assert torch.equal(grad2, ones_ref)
+
+
 def test_cross_entropy_uniform_logits():
     from ceo_amd.nn import cross_entropy_forward
 
