@@ -388,6 +388,10 @@ __global__ void __launch_bounds__(64 * NW) gemm_fast_kernel(Opnd A, Opnd B, long
                 for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
         const long nfull = cur.klen / BK;  // whole k-iterations (direct copies)
         const long niter = (cur.klen + BK - 1) / BK;
+        // on an edge tile a wave whose rows are all past M, or columns all
+        // past N, holds no output: it only copies (the N = 3088 projection's
+        // last tile column is 16 wide and 6 of its 8 waves sit idle)
+        const bool act = cur.m0 + wm < M && cur.n0 + wn < N;
         for (long kt = 0; kt < niter; ++kt) {
             // what the other buffer receives: this item's next k-block, or
             // the next item's first; whole blocks by direct copies, a k-tail
@@ -406,10 +410,12 @@ __global__ void __launch_bounds__(64 * NW) gemm_fast_kernel(Opnd A, Opnd B, long
             // fragments double-buffered in registers: k step ks + 1 is read
             // while the MFMAs of k step ks run
             bf16x8 fb[2][TNI], fa[2][4];
+            if (act) {
 #pragma unroll
-            for (int i = 0; i < TNI; ++i) fb[0][i] = frag<BKC>(bt, wn + 32 * i, 0, l);
+                for (int i = 0; i < TNI; ++i) fb[0][i] = frag<BKC>(bt, wn + 32 * i, 0, l);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) fa[0][j] = frag<AKC>(at, wm + 32 * j, 0, l);
+                for (int j = 0; j < 4; ++j) fa[0][j] = frag<AKC>(at, wm + 32 * j, 0, l);
+            }
             // the next block's copies all go out now, a whole iteration ahead
             // of the wait (the buffer they fill was last read in the previous
             // iteration, which every wave has finished)
@@ -417,34 +423,36 @@ __global__ void __launch_bounds__(64 * NW) gemm_fast_kernel(Opnd A, Opnd B, long
                 copy_tile<AKC, NW>(A, src.m0, k0, As(buf ^ 1), w, l);
                 copy_tile<BKC, NW>(B, src.n0, k0, Bs(buf ^ 1), w, l);
             }
+            if (act) {
 #pragma unroll
-            for (int ks = 0; ks < BK / 16; ++ks) {
-                const int c = ks & 1;
-                if (ks + 1 < BK / 16) {
+                for (int ks = 0; ks < BK / 16; ++ks) {
+                    const int c = ks & 1;
+                    if (ks + 1 < BK / 16) {
+#pragma unroll
+                        for (int i = 0; i < TNI; ++i)
+                            fb[c ^ 1][i] = frag<BKC>(bt, wn + 32 * i, ks + 1, l);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            fa[c ^ 1][j] = frag<AKC>(at, wm + 32 * j, ks + 1, l);
+                    }
 #pragma unroll
                     for (int i = 0; i < TNI; ++i)
-                        fb[c ^ 1][i] = frag<BKC>(bt, wn + 32 * i, ks + 1, l);
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        fa[c ^ 1][j] = frag<AKC>(at, wm + 32 * j, ks + 1, l);
-                }
+                        for (int j = 0; j < 4; ++j)
+                            acc[i][j] = mma32<T>(fb[c][i], fa[c][j], acc[i][j]);
+                    if (ks + 1 < BK / 16) {
+                        // one LDS read between consecutive MFMAs
+                        constexpr int NR = TNI * (BKC ? 1 : 2) + 4 * (AKC ? 1 : 2);
+                        constexpr int NM = 4 * TNI;
+                        constexpr int R = NR < NM ? NR : NM;
 #pragma unroll
-                for (int i = 0; i < TNI; ++i)
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        acc[i][j] = mma32<T>(fb[c][i], fa[c][j], acc[i][j]);
-                if (ks + 1 < BK / 16) {
-                    // one LDS read between consecutive MFMAs
-                    constexpr int NR = TNI * (BKC ? 1 : 2) + 4 * (AKC ? 1 : 2);
-                    constexpr int NM = 4 * TNI;
-                    constexpr int R = NR < NM ? NR : NM;
-#pragma unroll
-                    for (int r = 0; r < R; ++r) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                        for (int r = 0; r < R; ++r) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                        }
+                        if constexpr (NM > R) __builtin_amdgcn_sched_group_barrier(0x008, NM - R, 0);
+                        if constexpr (NR > R) __builtin_amdgcn_sched_group_barrier(0x100, NR - R, 0);
                     }
-                    if constexpr (NM > R) __builtin_amdgcn_sched_group_barrier(0x008, NM - R, 0);
-                    if constexpr (NR > R) __builtin_amdgcn_sched_group_barrier(0x100, NR - R, 0);
                 }
             }
             mf::dma_wait();
