@@ -92,6 +92,7 @@ _SIGS = {
     "layernorm_forward_stats_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     "layernorm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
     "layernorm_backward_residual_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
+    "layernorm_backward_ex_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
     "rmsnorm_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
     "rmsnorm_backward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     "shortconv_forward_hip": (i32, [vp, vp, vp, sz, sz, sz, sz, vp]),
@@ -102,7 +103,7 @@ _SIGS = {
     "gemm_forward_hip": (i32, [vp, vp, vp, vp, sz, sz, sz, i32, i32, i32, vp]),
     "gemm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),
     "gemm_gelu_forward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, sz, vp]),
-    "gemm_gelu_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),
+    "gemm_gelu_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, sz, vp]),
     # GELU, AdamW
     "gemm_ex_hip": (i32, [i32, i32, sz, sz, sz, f32, vp, sz, vp, sz, vp, f32, vp, sz, vp, sz,
                           i32, vp]),

@@ -232,12 +232,25 @@ __global__ void __launch_bounds__(NTH) colsum_part_kernel(const bf16* __restrict
     const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
     const long c0 = (long)blockIdx.x * 128 + 8 * q;
     float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (c0 < N)
-        for (long r = (long)blockIdx.y + (long)rg * CS_RS; r < M; r += 16L * CS_RS) {
-            const bf16x8 v = *reinterpret_cast<const bf16x8*>(x + r * N + c0);
+    if (c0 < N) {
+        // 8 rows' loads in flight before any is added (rows past the end
+        // load the last row and count as zero); the sum stays in row order
+        constexpr int U = 8;
+        constexpr long STEP = 16L * CS_RS;
+        for (long r0 = (long)blockIdx.y + (long)rg * CS_RS; r0 < M; r0 += STEP * U) {
+            bf16x8 v[U];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) s[i] += (float)v[i];
+            for (int u = 0; u < U; ++u) {
+                const long r = r0 + STEP * u < M ? r0 + STEP * u : M - 1;
+                v[u] = *reinterpret_cast<const bf16x8*>(x + r * N + c0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (r0 + STEP * u < M)
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) s[i] += (float)v[u][i];
         }
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[rg][8 * q + i] = s[i];
     __syncthreads();
@@ -260,6 +273,53 @@ __global__ void __launch_bounds__(NTH) colsum_final_kernel(const float* __restri
     y[c] = (bf16)t;
 }
 
+// y[c] = sum over the rows of part (fp32 [rows][N]) as bf16, in a fixed order:
+// row group g (of 16) adds rows g, g + 16, ..., then the 16 groups in turn.
+// Workgroup: 16 row groups x 16 lanes of 4 columns (16-byte loads, all of a
+// lane's rows in flight for the few hundred rows this takes); grid over
+// 64-column blocks.
+__global__ void __launch_bounds__(NTH) colsum_rows_kernel(const float* __restrict__ part,
+                                                          long rows, bf16* __restrict__ y,
+                                                          long N) {
+    __shared__ float acc[16][64 + 1];
+    const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
+    const long c0 = (long)blockIdx.x * 64 + 4 * q;
+    float s[4] = {0.f, 0.f, 0.f, 0.f};
+    if (N % 4 == 0 && c0 + 4 <= N) {
+        // 8 rows' loads in flight before any is added (rows past the end
+        // load the last row and count as zero); the sum stays in row order
+        constexpr int U = 8;
+        for (long r0 = rg; r0 < rows; r0 += 16 * U) {
+            floatx4 v[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const long r = r0 + 16 * u < rows ? r0 + 16 * u : rows - 1;
+                v[u] = *reinterpret_cast<const floatx4*>(part + r * N + c0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (r0 + 16 * u < rows)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[i] += v[u][i];
+        }
+    } else {
+        for (long r = rg; r < rows; r += 16)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (c0 + i < N) s[i] += part[r * N + c0 + i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[rg][4 * q + i] = s[i];
+    __syncthreads();
+    const long c = (long)blockIdx.x * 64 + threadIdx.x;
+    if (threadIdx.x < 64 && c < N) {
+        float t = 0.f;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) t += acc[g][threadIdx.x];
+        y[c] = (bf16)t;
+    }
+}
+
 // k == 0: C = bias (broadcast) or 0
 template <typename TC>
 __global__ void __launch_bounds__(NTH) bias_fill_kernel(TC* __restrict__ C,
@@ -271,6 +331,25 @@ __global__ void __launch_bounds__(NTH) bias_fill_kernel(TC* __restrict__ C,
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// y[c] = sum_r x[r][c] (bf16 [M][N] -> bf16 [N], fp32 sums in a fixed order)
+static int colsum_bf16(const bf16* x, long M, long N, bf16* y, hipStream_t stream) {
+    void* ws = nullptr;
+    WsLease lease;
+    if (N % 8 == 0 && aligned16(x) &&
+        workspace_acquire((size_t)CS_RS * N * sizeof(float), stream, &ws, lease) == kSuccess) {
+        EFLA_LAUNCH("gemm_bwd_dbias", colsum_part_kernel, dim3((unsigned)((N + 127) / 128), CS_RS),
+                    dim3(NTH), stream, x, (float*)ws, M, N);
+        EFLA_LAUNCH("gemm_bwd_dbias_final", colsum_final_kernel,
+                    dim3((unsigned)((N + NTH - 1) / NTH)), dim3(NTH), stream, (const float*)ws, y,
+                    N);
+    } else {
+        EFLA_LAUNCH("gemm_bwd_dbias", colsum_kernel, dim3((unsigned)((N + 63) / 64)), dim3(NTH),
+                    stream, x, y, M, N);
+    }
+    return (int)hipPeekAtLastError();
+}
+
 
 template <typename TA, typename TB, typename TC, typename MT, bool AKM, bool BKM>
 static int launch(const void* a, const void* b, const void* bias, void* c, long M, long N,
@@ -446,7 +525,7 @@ static gf::EpiArgs<T> epi(void* d, long ldd, const void* bias = nullptr, float a
                           float beta = 0.f, const void* c = nullptr, long ldc = 0,
                           void* aux = nullptr, long ldaux = 0) {
     return gf::EpiArgs<T>{(T*)d, ldd, (const T*)bias, (const T*)c, ldc, alpha, beta, (T*)aux,
-                          ldaux, nullptr};
+                          ldaux, nullptr, nullptr};
 }
 
 // ---------------------------------------------------------------------------
@@ -605,6 +684,11 @@ static int lt_forward(const void* a, const void* b, const void* bias, void* c, l
 }
 
 }  // namespace gm
+
+int colsum_bf16_rows(const bf16* x, long M, long N, bf16* y, hipStream_t stream) {
+    return gm::colsum_bf16(x, M, N, y, stream);
+}
+
 }  // namespace efla
 
 using namespace efla;
@@ -731,21 +815,8 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
         if (rc != kSuccess) return rc;
     }
     if (need_bias && m && n) {
-        void* ws = nullptr;
-        WsLease lease;
-        if (N % 8 == 0 && aligned16(grad_c) &&
-            workspace_acquire((size_t)CS_RS * N * sizeof(float), stream, &ws, lease) ==
-                kSuccess) {
-            EFLA_LAUNCH("gemm_bwd_dbias", colsum_part_kernel,
-                        dim3((unsigned)((N + 127) / 128), CS_RS), dim3(NTH), stream,
-                        (const bf16*)grad_c, (float*)ws, M, N);
-            EFLA_LAUNCH("gemm_bwd_dbias_final", colsum_final_kernel,
-                        dim3((unsigned)((N + NTH - 1) / NTH)), dim3(NTH), stream,
-                        (const float*)ws, (bf16*)grad_bias, N);
-        } else {
-            EFLA_LAUNCH("gemm_bwd_dbias", colsum_kernel, dim3((unsigned)((N + 63) / 64)),
-                        dim3(NTH), stream, (const bf16*)grad_c, (bf16*)grad_bias, M, N);
-        }
+        const int rc = colsum_bf16((const bf16*)grad_c, M, N, (bf16*)grad_bias, stream);
+        if (rc != kSuccess) return rc;
     }
     return (int)hipPeekAtLastError();
 }
@@ -856,15 +927,20 @@ extern "C" int gemm_gelu_forward_hip(const void* a, const void* b, const void* b
 
 extern "C" int gemm_gelu_backward_hip(const void* grad_c, const void* a, const void* b,
                                       const void* pre, void* grad_pre, void* grad_b,
-                                      void* grad_bias, size_t m, size_t k, size_t n,
-                                      hipStream_t stream) {
+                                      void* grad_bias, void* grad_pre_bias, size_t m, size_t k,
+                                      size_t n, hipStream_t stream) {
     size_t mk;
     if (!mul_ok(m, k, &mk)) return kInvalidValue;
+    if (grad_pre_bias && !grad_pre) return kInvalidValue;  // the sums are of grad_pre
     if (grad_pre) {
         if (m == 0 || k == 0) {
             // nothing to contract or no rows: gemm_backward_hip's zero fill
             int rc = gemm_backward_hip(grad_c, a, b, grad_pre, nullptr, nullptr, m, k, n, stream);
             if (rc != kSuccess) return rc;
+            if (grad_pre_bias && k) {
+                rc = fill_zero(grad_pre_bias, k * 2, stream);
+                if (rc != kSuccess) return rc;
+            }
         } else {
             if (!grad_c || !b || !pre) return kInvalidValue;
             // grad_pre = (grad_c b^T) * GELU'(pre): contraction over n, both n-contiguous
@@ -872,21 +948,39 @@ extern "C" int gemm_gelu_backward_hip(const void* grad_c, const void* a, const v
             if (n > 0 && backend() == 0 &&
                 fast_ok((long)m, (long)k, (long)n, fa, fb, grad_pre, (long)k, nullptr, nullptr,
                         0, pre, (long)k)) {
-                const int rc = fast_launch<bf16, gf::EPI_DGELU>(
-                    fa, fb, (long)m, (long)k, (long)n,
-                    epi<bf16>(grad_pre, (long)k, nullptr, 1.f, 0.f, nullptr, 0, (void*)pre,
-                              (long)k),
-                    "gemm_gelu_bwd_da", stream);
+                gf::EpiArgs<bf16> ea = epi<bf16>(grad_pre, (long)k, nullptr, 1.f, 0.f, nullptr, 0,
+                                                 (void*)pre, (long)k);
+                // grad_pre's column sums from the epilogue: one fp32 row per
+                // 128 output rows, then their sum
+                void* ws = nullptr;
+                WsLease lease;
+                const long prow = ((long)m + 127) / 128;
+                if (grad_pre_bias) {
+                    EFLA_CHECK((hipError_t)workspace_acquire((size_t)prow * k * sizeof(float),
+                                                             stream, &ws, lease));
+                    ea.cpart = (float*)ws;
+                }
+                int rc = fast_launch<bf16, gf::EPI_DGELU>(fa, fb, (long)m, (long)k, (long)n, ea,
+                                                          "gemm_gelu_bwd_da", stream);
                 if (rc != kSuccess) return rc;
+                if (grad_pre_bias)
+                    EFLA_LAUNCH("gemm_gelu_bwd_dbias", colsum_rows_kernel,
+                                dim3((unsigned)((k + 63) / 64)), dim3(NTH), stream,
+                                (const float*)ws, prow, (bf16*)grad_pre_bias, (long)k);
             } else {
                 int rc = gemm_backward_hip(grad_c, a, b, grad_pre, nullptr, nullptr, m, k, n,
                                            stream);
                 if (rc != kSuccess) return rc;
                 rc = gelu_backward_hip(grad_pre, pre, grad_pre, mk, true, stream);
                 if (rc != kSuccess) return rc;
+                if (grad_pre_bias) {
+                    rc = colsum_bf16((const bf16*)grad_pre, (long)m, (long)k,
+                                     (bf16*)grad_pre_bias, stream);
+                    if (rc != kSuccess) return rc;
+                }
             }
         }
     }
-    if (!grad_b && !grad_bias) return kSuccess;
+    if (!grad_b && !grad_bias) return (int)hipPeekAtLastError();
     return gemm_backward_hip(grad_c, a, b, nullptr, grad_b, grad_bias, m, k, n, stream);
 }

@@ -162,7 +162,9 @@ struct EpiArgs {
     float alpha, beta;
     T* aux;  // GELU_AUX: pre-activation out; DGELU: pre-activation in
     long ldaux;
-    float* part;  // PARTIAL: fp32 partial sums [split][M][N]
+    float* part;   // PARTIAL: fp32 partial sums [split][M][N]
+    float* cpart;  // DGELU: column sums of the output, one fp32 row per 128 output
+                   // rows ([M / 128][N]), or NULL
 };
 
 template <typename T>
@@ -240,6 +242,9 @@ __device__ __forceinline__ void epilogue_wave(const EpiArgs<T>& ea, const floatx
                                               char* wp) {
     constexpr int WC = 32 * TNI;  // columns of the wave's block
     typedef __attribute__((__vector_size__(8 * sizeof(T)))) T t8;
+    // DGELU with column sums: this lane's 8 columns (piece c8 = l % (WC / 8)
+    // of every row it finishes) summed over its rows
+    float csum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const long r0 = mw + 32 * j;
@@ -288,8 +293,10 @@ __device__ __forceinline__ void epilogue_wave(const EpiArgs<T>& ea, const floatx
             } else if constexpr (EPI == EPI_DGELU) {
                 const t8 u = *reinterpret_cast<const t8*>(ea.aux + m * ea.ldaux + n);
 #pragma unroll
-                for (int e = 0; e < 8; ++e)
+                for (int e = 0; e < 8; ++e) {
                     y[e] = (T)((float)(T)v[e] * gelu::gelu_df<true>((float)u[e]));
+                    csum[e] += (float)y[e];
+                }
             } else if constexpr (EPI == EPI_RESID) {
                 const t8 cc = *reinterpret_cast<const t8*>(ea.c + m * ea.ldc + n);
 #pragma unroll
@@ -299,6 +306,23 @@ __device__ __forceinline__ void epilogue_wave(const EpiArgs<T>& ea, const floatx
                 for (int e = 0; e < 8; ++e) y[e] = (T)v[e];
             }
             *reinterpret_cast<t8*>(ea.d + m * ea.ldd + n) = y;
+        }
+    }
+    if constexpr (EPI == EPI_DGELU) {
+        if (ea.cpart && mw < M) {
+            // the lanes sharing a piece index hold different rows: sum them
+            // (fixed order), then one fp32 row of the wave's 128 rows
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+#pragma unroll
+                for (int off = WC / 8; off < 64; off <<= 1) csum[e] += __shfl_xor(csum[e], off);
+            const long n = nw + 8 * l;
+            if (l < WC / 8 && n < N) {
+                float* dst = ea.cpart + (mw / 128) * N + n;
+                *reinterpret_cast<mf::floatx4*>(dst) = mf::floatx4{csum[0], csum[1], csum[2], csum[3]};
+                *reinterpret_cast<mf::floatx4*>(dst + 4) =
+                    mf::floatx4{csum[4], csum[5], csum[6], csum[7]};
+            }
         }
     }
 }

@@ -99,6 +99,8 @@ int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr, WsLease& lea
 // Zero-fill through a kernel (no hipMemsetAsync, so the call is safe inside
 // stream capture).
 int fill_zero(void* ptr, size_t bytes, hipStream_t stream);
+// y[c] = sum_r x[r][c] for bf16 x [M][N] (fp32 sums in a fixed order, bf16 y)
+int colsum_bf16_rows(const __bf16* x, long M, long N, __bf16* y, hipStream_t stream);
 
 // Compute units of the current device (cached per device); 0 if the query fails.
 int device_cu_count();

@@ -172,8 +172,9 @@ __global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
 }
 
 // Register-resident backward for D = NV * 512 (NV <= 4): lane owns columns
-// (j * 64 + lane) * 8 + i.  part[blockIdx.x][0..D) = dw, [D..2D) = db partials.
-template <int NV>
+// (j * 64 + lane) * 8 + i.  part[blockIdx.x][0..D) = dw, [D..2D) = db
+// partials, and with NS = 3 [2D..3D) = the column sums of dx (as written).
+template <int NV, int NS>
 __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ dy,
                                                       const bf16* __restrict__ x,
                                                       const bf16* __restrict__ w,
@@ -184,16 +185,16 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
                                                       float* __restrict__ part, long rows,
                                                       int want_params) {
     constexpr int D = NV * 512;
-    __shared__ float red[NTH / kWave][2 * D];  // 32 KB per 1024 columns
+    __shared__ float red[NTH / kWave][NS * D];  // 32 KB per 1024 columns and sum
     const int lane = lane_id(), wv = wave_id();
-    float wf[NV][8], dwa[NV][8], dba[NV][8];
+    float wf[NV][8], dwa[NV][8], dba[NV][8], dxa[NV][8];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const bf16x8 t = *reinterpret_cast<const bf16x8*>(w + (j * 64 + lane) * 8);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
             wf[j][i] = (float)t[i];
-            dwa[j][i] = dba[j][i] = 0.f;
+            dwa[j][i] = dba[j][i] = dxa[j][i] = 0.f;
         }
     }
     const long waves = (long)gridDim.x * (NTH / kWave);
@@ -241,6 +242,7 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
                 o[i] = (bf16)(rs * (gy * wf[j][i] - sg - xh * sgx) + add);
                 dwa[j][i] += gy * xh;
                 dba[j][i] += gy;
+                if constexpr (NS == 3) dxa[j][i] += (float)o[i];
             }
             *reinterpret_cast<bf16x8*>(dx + row * D + (j * 64 + lane) * 8) = o;
         }
@@ -253,10 +255,11 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
         for (int i = 0; i < 8; ++i) {
             red[wv][(j * 64 + lane) * 8 + i] = dwa[j][i];
             red[wv][D + (j * 64 + lane) * 8 + i] = dba[j][i];
+            if constexpr (NS == 3) red[wv][2 * D + (j * 64 + lane) * 8 + i] = dxa[j][i];
         }
     __syncthreads();
-    float* pr = part + (long)blockIdx.x * 2 * D;
-    for (int c = threadIdx.x; c < 2 * D; c += NTH) {
+    float* pr = part + (long)blockIdx.x * NS * D;
+    for (int c = threadIdx.x; c < NS * D; c += NTH) {
         float s = 0.f;
 #pragma unroll
         for (int k = 0; k < NTH / kWave; ++k) s += red[k][c];
@@ -264,23 +267,35 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
     }
 }
 
-// out[c] = sum_b part[b][c] for c < 2D (dw = out[0..D), db = out[D..2D)).
+// out[c] = sum_b part[b][c] for c < NS D (dw = out[0..D), db = out[D..2D), and
+// with NS = 3 the dx column sums out[2D..3D) as bf16 into dxs).
 // Workgroup: 16 row groups x 16 lanes of 4 columns (16-byte loads); grid over
-// 64-column blocks (2D is a multiple of 4 when D is even; odd D reads scalars).
+// 64-column blocks (NS D is a multiple of 4 when D is even; odd D reads scalars).
 __global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ part, int nblk,
-                                                     int D, float* __restrict__ dw,
-                                                     float* __restrict__ db) {
+                                                     int D, int NS, float* __restrict__ dw,
+                                                     float* __restrict__ db,
+                                                     bf16* __restrict__ dxs) {
     __shared__ float acc[16][64 + 1];
     const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
     const int c0 = blockIdx.x * 64 + 4 * q;
-    const int W = 2 * D;
+    const int W = NS * D;
     float s[4] = {0.f, 0.f, 0.f, 0.f};
     if (W % 4 == 0 && c0 + 4 <= W) {
-#pragma unroll 4
-        for (int b = rg; b < nblk; b += 16) {
-            const floatx4 v = *reinterpret_cast<const floatx4*>(part + (long)b * W + c0);
+        // 8 rows' loads in flight before any is added (rows past the end
+        // load the last row and count as zero); the sum stays in row order
+        constexpr int U = 8;
+        for (int b0 = rg; b0 < nblk; b0 += 16 * U) {
+            floatx4 v[U];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) s[i] += v[i];
+            for (int u = 0; u < U; ++u) {
+                const int b = min(b0 + 16 * u, nblk - 1);
+                v[u] = *reinterpret_cast<const floatx4*>(part + (long)b * W + c0);
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                if (b0 + 16 * u < nblk)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) s[i] += v[u][i];
         }
     } else {
         for (int b = rg; b < nblk; b += 16)
@@ -298,8 +313,10 @@ __global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ p
         for (int k = 0; k < 16; ++k) t += acc[k][threadIdx.x];
         if (c < D) {
             if (dw) dw[c] = t;
-        } else if (c < W && db) {
-            db[c - D] = t;
+        } else if (c < 2 * D) {
+            if (db) db[c - D] = t;
+        } else if (c < W && dxs) {
+            dxs[c - 2 * D] = (bf16)t;
         }
     }
 }
@@ -362,8 +379,9 @@ extern "C" int layernorm_forward_stats_hip(const void* input, const void* weight
 
 static int ln_backward(const void* grad_output, const void* input, const void* weight,
                        const float* mean, const float* rstd, const void* residual,
-                       void* grad_input, float* grad_weight, float* grad_bias, size_t numel,
-                       size_t normalized_shape, hipStream_t stream) {
+                       void* grad_input, float* grad_weight, float* grad_bias,
+                       void* grad_input_colsum, size_t numel, size_t normalized_shape,
+                       hipStream_t stream) {
     const size_t D = normalized_shape;
     if (D == 0) return kInvalidValue;
     const size_t rows = numel / D;
@@ -371,22 +389,28 @@ static int ln_backward(const void* grad_output, const void* input, const void* w
     if (rows == 0) {
         if (grad_weight) EFLA_CHECK((hipError_t)fill_zero(grad_weight, D * 4, stream));
         if (grad_bias) EFLA_CHECK((hipError_t)fill_zero(grad_bias, D * 4, stream));
+        if (grad_input_colsum) EFLA_CHECK((hipError_t)fill_zero(grad_input_colsum, D * 2, stream));
         return kSuccess;
     }
     if (!grad_output || !input || !weight || !mean || !rstd || !grad_input) return kInvalidValue;
-    if ((params && D > 8192) || rows > ((size_t)1 << 40)) return kInvalidConfiguration;
+    if (((params || grad_input_colsum) && D > 8192) || rows > ((size_t)1 << 40))
+        return kInvalidConfiguration;
     const bool aligned = ((uintptr_t)grad_output | (uintptr_t)input | (uintptr_t)weight |
                           (uintptr_t)grad_input | (uintptr_t)residual) % 16 == 0;
     const int nv = (aligned && D % 512 == 0 && D <= 2048) ? (int)(D / 512) : 0;
+    // the register path sums dx's columns with dw and db (a third partial);
+    // the looped path sums them in a pass of their own afterwards
+    const int ns = (nv && grad_input_colsum) ? 3 : 2;
+    const bool parts = params || ns == 3;
     // two workgroups per CU; each wave then takes several rows, which keeps the
     // per-workgroup dw/db partials (and their reduction) small
     size_t nblk = (rows + 3) / 4;
     if (nblk > 512) nblk = 512;
     float* part = nullptr;
     WsLease lease;
-    if (params) {
+    if (parts) {
         void* ws = nullptr;
-        int rc = workspace_acquire(nblk * 2 * D * sizeof(float), stream, &ws, lease);
+        int rc = workspace_acquire(nblk * ns * D * sizeof(float), stream, &ws, lease);
         if (rc != kSuccess) return rc;
         part = (float*)ws;
     }
@@ -394,13 +418,14 @@ static int ln_backward(const void* grad_output, const void* input, const void* w
     const bf16* res = (const bf16*)residual;
     bf16* dx = (bf16*)grad_input;
     const dim3 grid((unsigned)nblk), block(ln::NTH);
-    switch (nv) {
-#define LN_BWD_CASE(n)                                                                        \
-    case n:                                                                                   \
-        EFLA_LAUNCH("layernorm_bwd", ln::bwd_reg_kernel<n>, grid, block, stream, g, x, w, mean, \
-                    rstd, res, dx, part, (long)rows, params ? 1 : 0);                         \
+    switch (nv * 4 + ns) {
+#define LN_BWD_CASE(n, s)                                                                        \
+    case n * 4 + s:                                                                              \
+        EFLA_LAUNCH("layernorm_bwd", (ln::bwd_reg_kernel<n, s>), grid, block, stream, g, x, w, mean, \
+                    rstd, res, dx, part, (long)rows, parts ? 1 : 0);                              \
         break;
-        LN_BWD_CASE(1) LN_BWD_CASE(2) LN_BWD_CASE(3) LN_BWD_CASE(4)
+        LN_BWD_CASE(1, 2) LN_BWD_CASE(2, 2) LN_BWD_CASE(3, 2) LN_BWD_CASE(4, 2)
+        LN_BWD_CASE(1, 3) LN_BWD_CASE(2, 3) LN_BWD_CASE(3, 3) LN_BWD_CASE(4, 3)
 #undef LN_BWD_CASE
         default: {
             const size_t smem = params ? 2 * D * sizeof(float) : 0;
@@ -410,10 +435,18 @@ static int ln_backward(const void* grad_output, const void* input, const void* w
         }
     }
     EFLA_CHECK(hipPeekAtLastError());
-    if (params) {
-        const unsigned gr = (unsigned)((2 * D + 63) / 64);
+    if (parts) {
+        const unsigned gr = (unsigned)((ns * D + 63) / 64);
         EFLA_LAUNCH("layernorm_bwd_reduce", ln::reduce_kernel, dim3(gr), dim3(ln::NTH), stream,
-                    (const float*)part, (int)nblk, (int)D, grad_weight, grad_bias);
+                    (const float*)part, (int)nblk, (int)D, ns, grad_weight, grad_bias,
+                    ns == 3 ? (bf16*)grad_input_colsum : (bf16*)nullptr);
+    }
+    if (grad_input_colsum && ns == 2) {
+        // the column pass leases this stream's workspace itself: hand back the
+        // partials' lease first (its kernels are already queued on the stream)
+        lease.release();
+        EFLA_CHECK((hipError_t)colsum_bf16_rows(dx, (long)rows, (long)D, (bf16*)grad_input_colsum,
+                                                stream));
     }
     return (int)hipPeekAtLastError();
 }
@@ -424,7 +457,7 @@ extern "C" int layernorm_backward_hip(const void* grad_output, const void* input
                                       size_t numel, size_t normalized_shape,
                                       hipStream_t stream) {
     return ln_backward(grad_output, input, weight, mean, rstd, nullptr, grad_input, grad_weight,
-                       grad_bias, numel, normalized_shape, stream);
+                       grad_bias, nullptr, numel, normalized_shape, stream);
 }
 
 extern "C" int layernorm_backward_residual_hip(const void* grad_output, const void* input,
@@ -435,5 +468,15 @@ extern "C" int layernorm_backward_residual_hip(const void* grad_output, const vo
                                                size_t normalized_shape, hipStream_t stream) {
     if (!residual && numel / (normalized_shape ? normalized_shape : 1) > 0) return kInvalidValue;
     return ln_backward(grad_output, input, weight, mean, rstd, residual, grad_input, grad_weight,
-                       grad_bias, numel, normalized_shape, stream);
+                       grad_bias, nullptr, numel, normalized_shape, stream);
+}
+
+extern "C" int layernorm_backward_ex_hip(const void* grad_output, const void* input,
+                                         const void* weight, const float* mean, const float* rstd,
+                                         const void* residual, void* grad_input,
+                                         float* grad_weight, float* grad_bias,
+                                         void* grad_input_colsum, size_t numel,
+                                         size_t normalized_shape, hipStream_t stream) {
+    return ln_backward(grad_output, input, weight, mean, rstd, residual, grad_input, grad_weight,
+                       grad_bias, grad_input_colsum, numel, normalized_shape, stream);
 }

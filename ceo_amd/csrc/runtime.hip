@@ -8,6 +8,7 @@
 #include <memory>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <tuple>
 #include <vector>
 
@@ -280,6 +281,9 @@ namespace efla {
 
 struct WsEntry {
     std::mutex mu;  // held by the lease for as long as a caller uses the buffer
+    // the thread holding mu (default id when free): only that thread stores
+    // its own id here, so it alone can see it and refuse a second lease
+    std::atomic<std::thread::id> owner{};
     void* ptr = nullptr;
     size_t bytes = 0;
 };
@@ -298,7 +302,10 @@ WsEntry* ws_entry(int dev, hipStream_t stream, int slot) {
 }  // namespace
 
 void WsLease::release() {
-    if (entry) entry->mu.unlock();
+    if (entry) {
+        entry->owner.store(std::thread::id());
+        entry->mu.unlock();
+    }
     entry = nullptr;
 }
 
@@ -307,7 +314,11 @@ int workspace_acquire(size_t bytes, hipStream_t stream, void** ptr, WsLease& lea
     int dev = 0;
     EFLA_CHECK(hipGetDevice(&dev));
     WsEntry* e = ws_entry(dev, stream, slot);
+    // a second lease on one (stream, slot) from the holding thread would wait
+    // on itself forever: report the misuse instead
+    if (e->owner.load() == std::this_thread::get_id()) return kInvalidValue;
     e->mu.lock();
+    e->owner.store(std::this_thread::get_id());
     lease.entry = e;
     if (e->bytes < bytes) {
         if (e->ptr) {

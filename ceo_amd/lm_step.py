@@ -189,8 +189,12 @@ class EflaLM:
         daf, _, _ = nn.gemm_backward(dlogits, saved["af"], self.w("head"),
                                      out_b=self.gr("head"))
         del dlogits
-        dx, dw, db = nn.layernorm_backward(daf, saved["x"], self.w("lnf.w"), saved["mf"],
-                                           saved["rf"])
+        # b_down's gradient is the column sum of the layer output's gradient, so each
+        # LayerNorm backward that produces that gradient also sums its columns
+        top = cfg.n_layers - 1
+        dx, dw, db = nn.layernorm_backward(
+            daf, saved["x"], self.w("lnf.w"), saved["mf"], saved["rf"],
+            out_dx_colsum=self.gr(f"l{top}.b_down") if top >= 0 else None)
         self.gr("lnf.w").copy_(dw)
         self.gr("lnf.b").copy_(db)
         for i in reversed(range(cfg.n_layers)):
@@ -198,11 +202,12 @@ class EflaLM:
             s = saved["layers"][i]
             # x2 = x1 + down(gelu(up(ln2(x1))))
             # du = (dx w_down^T) * GELU'(u) from one product (derivative in its epilogue)
+            # and b_up's gradient (du's column sums) comes from the same epilogue
             du, _, _ = nn.gemm_gelu_backward(dx, s["g"], self.w(L + "w_down"), s["u"],
-                                             need_bias=True, out_b=self.gr(L + "w_down"),
-                                             out_bias=self.gr(L + "b_down"))
-            da2, _, _ = nn.gemm_backward(du, s["a2"], self.w(L + "w_up"), need_bias=True,
-                                         out_b=self.gr(L + "w_up"), out_bias=self.gr(L + "b_up"))
+                                             out_b=self.gr(L + "w_down"),
+                                             out_pre_bias=self.gr(L + "b_up"))
+            da2, _, _ = nn.gemm_backward(du, s["a2"], self.w(L + "w_up"),
+                                         out_b=self.gr(L + "w_up"))
             # dx1 = LN2's input gradient + the residual's dx, in one pass
             dx1, dw, db = nn.layernorm_backward(da2, s["x1"], self.w(L + "ln2.w"), s["m2"],
                                                 s["r2"], residual=dx)
@@ -223,8 +228,9 @@ class EflaLM:
             nn.sigmoid_gate_backward(dbeta.view(N, H), s["beta"].view(N, H), dp[:, 3 * HD:])
             da, _, _ = nn.gemm_backward(dp, s["a"], self.w(L + "w_in"), out_b=self.gr(L + "w_in"))
             # dx = dx1 + LN1's input gradient
-            dx, dw, db = nn.layernorm_backward(da, s["x"], self.w(L + "ln1.w"), s["m1"], s["r1"],
-                                               residual=dx1)
+            dx, dw, db = nn.layernorm_backward(
+                da, s["x"], self.w(L + "ln1.w"), s["m1"], s["r1"], residual=dx1,
+                out_dx_colsum=self.gr(f"l{i - 1}.b_down") if i > 0 else None)
             self.gr(L + "ln1.w").copy_(dw)
             self.gr(L + "ln1.b").copy_(db)
             saved["layers"][i] = None

@@ -38,9 +38,10 @@ def layernorm_forward(x: torch.Tensor, weight: torch.Tensor, bias=None, eps: flo
 
 
 def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True,
-                       residual=None):
+                       residual=None, out_dx_colsum=None):
     """(dx bf16, dweight fp32 or None, dbias fp32 or None); with ``residual``
-    (bf16, x's shape) dx is LayerNorm's input gradient plus it."""
+    (bf16, x's shape) dx is LayerNorm's input gradient plus it; with
+    ``out_dx_colsum`` ((D,) bf16) dx's column sums are written there."""
     D = x.shape[-1]
     for t, n in ((dy, "dy"), (x, "x"), (weight, "weight")):
         _require(t, n, torch.bfloat16, x.device)
@@ -49,14 +50,23 @@ def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True,
     dx = torch.empty_like(x)
     dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
     db = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
-    if residual is None:
+    if residual is not None:
+        _require(residual, "residual", torch.bfloat16, x.device)
+        if residual.shape != x.shape:
+            raise ValueError("residual must have x's shape")
+    if out_dx_colsum is not None:
+        _require(out_dx_colsum, "out_dx_colsum", torch.bfloat16, x.device)
+        if out_dx_colsum.numel() != D:
+            raise ValueError("out_dx_colsum must hold normalized_shape values")
+        rc = lib().layernorm_backward_ex_hip(_p(dy), _p(x), _p(weight), _p(mean), _p(rstd),
+                                             _p(residual), _p(dx), _p(dw), _p(db),
+                                             _p(out_dx_colsum), x.numel(), D, _stream(x))
+        check(rc, "layernorm_backward_ex_hip")
+    elif residual is None:
         rc = lib().layernorm_backward_hip(_p(dy), _p(x), _p(weight), _p(mean), _p(rstd), _p(dx),
                                           _p(dw), _p(db), x.numel(), D, _stream(x))
         check(rc, "layernorm_backward_hip")
     else:
-        _require(residual, "residual", torch.bfloat16, x.device)
-        if residual.shape != x.shape:
-            raise ValueError("residual must have x's shape")
         rc = lib().layernorm_backward_residual_hip(_p(dy), _p(x), _p(weight), _p(mean),
                                                    _p(rstd), _p(residual), _p(dx), _p(dw),
                                                    _p(db), x.numel(), D, _stream(x))
@@ -199,27 +209,31 @@ def gemm_gelu_forward(a: torch.Tensor, b: torch.Tensor, bias=None):
 
 
 def gemm_gelu_backward(dc, a, b, pre, need_pre=True, need_b=True, need_bias=False,
-                       out_b=None, out_bias=None):
+                       out_b=None, out_bias=None, out_pre_bias=None):
     """(dpre, db, dbias) for c = a @ b + bias with a = GELU_tanh(pre): dpre =
     (dc @ b^T) * GELU'(pre) from one product with the derivative in its
-    epilogue; bf16."""
+    epilogue; bf16.  With ``out_pre_bias`` ((k,) bf16) the column sums of
+    dpre (the gradient of the bias that made pre) are also written there."""
     m, k = a.shape
     n = b.shape[1]
     for t, nme in ((dc, "dc"), (a, "a"), (b, "b"), (pre, "pre")):
         _require(t, nme, torch.bfloat16, a.device)
     if pre.shape != a.shape:
         raise ValueError("gemm_gelu_backward: pre must have a's shape")
-    for t, nme, shape in ((out_b, "out_b", (k, n)), (out_bias, "out_bias", (n,))):
+    for t, nme, shape in ((out_b, "out_b", (k, n)), (out_bias, "out_bias", (n,)),
+                          (out_pre_bias, "out_pre_bias", (k,))):
         if t is not None:
             _require(t, nme, torch.bfloat16, a.device)
             if tuple(t.shape) != shape:
                 raise ValueError(f"gemm_gelu_backward: {nme} must be {shape}")
+    if out_pre_bias is not None and not need_pre:
+        raise ValueError("gemm_gelu_backward: out_pre_bias needs need_pre")
     dpre = torch.empty_like(a) if need_pre else None
     dbm = (out_b if out_b is not None else torch.empty_like(b)) if need_b else None
     dbias = (out_bias if out_bias is not None else
              torch.empty(n, dtype=torch.bfloat16, device=a.device)) if need_bias else None
     rc = lib().gemm_gelu_backward_hip(_p(dc), _p(a), _p(b), _p(pre), _p(dpre), _p(dbm),
-                                      _p(dbias), m, k, n, _stream(a))
+                                      _p(dbias), _p(out_pre_bias), m, k, n, _stream(a))
     check(rc, "gemm_gelu_backward_hip")
     return dpre, dbm, dbias
 

@@ -251,6 +251,19 @@ int layernorm_backward_residual_hip(const void* grad_output, const void* input,
                                     float* grad_bias, size_t numel, size_t normalized_shape,
                                     hipStream_t stream);
 
+/* No reference counterpart: the general LayerNorm backward.  residual (added
+ * to grad_input) may be NULL; grad_weight, grad_bias and grad_input_colsum
+ * may each be NULL.  grad_input_colsum receives the column sums of
+ * grad_input as written (bf16, normalized_shape values): the gradient of a
+ * bias of the product whose output gradient grad_input is, summed in the
+ * same row pass (D a multiple of 512 up to 2048, 16-byte aligned rows) or in
+ * a pass of its own. */
+int layernorm_backward_ex_hip(const void* grad_output, const void* input, const void* weight,
+                              const float* mean, const float* rstd, const void* residual,
+                              void* grad_input, float* grad_weight, float* grad_bias,
+                              void* grad_input_colsum, size_t numel, size_t normalized_shape,
+                              hipStream_t stream);
+
 /* ========================================================================
  * RMSNorm
  * ======================================================================== */
@@ -375,13 +388,16 @@ int gemm_gelu_forward_hip(const void* a, const void* b, const void* bias, void* 
 
 /* No reference counterpart: gemm_backward_hip for c = GELU_tanh(pre) b + bias
  * with the GELU derivative fused into grad_a's epilogue,
- *   grad_pre  = bf16(grad_c b^T) * GELU'(pre)   (m x k; NULL skips it)
- *   grad_b    = a^T grad_c                      (k x n, a = GELU(pre); NULL skips it)
- *   grad_bias = column sums of grad_c           (n; NULL skips it)
+ *   grad_pre      = bf16(grad_c b^T) * GELU'(pre)   (m x k; NULL skips it)
+ *   grad_b        = a^T grad_c                      (k x n, a = GELU(pre); NULL skips it)
+ *   grad_bias     = column sums of grad_c           (n; NULL skips it)
+ *   grad_pre_bias = column sums of grad_pre         (k; NULL skips it; needs
+ *                   grad_pre): the gradient of the bias of the product that
+ *                   made pre, summed in grad_pre's epilogue
  * bf16, row-major, contiguous.  Same codes as gemm_backward_hip. */
 int gemm_gelu_backward_hip(const void* grad_c, const void* a, const void* b, const void* pre,
-                           void* grad_pre, void* grad_b, void* grad_bias, size_t m, size_t k,
-                           size_t n, hipStream_t stream);
+                           void* grad_pre, void* grad_b, void* grad_bias, void* grad_pre_bias,
+                           size_t m, size_t k, size_t n, hipStream_t stream);
 
 /* ========================================================================
  * GELU and AdamW (the config-4 training step around EFLA)

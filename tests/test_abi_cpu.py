@@ -186,6 +186,10 @@ def test_gemm_validation(L):
     assert L.gemm_forward_hip(p, p, NULL, p, 0, 4, 4, 14, 14, 14, NULL) == 0
     assert L.gemm_backward_hip(p, p, p, NULL, NULL, NULL, 4, 4, 4, NULL) == 0
     assert L.gemm_backward_hip(NULL, p, p, p, NULL, NULL, 4, 4, 4, NULL) == 1
+    # column sums of grad_pre need grad_pre; grad_pre needs grad_c, b and pre
+    assert L.gemm_gelu_backward_hip(p, p, p, p, NULL, NULL, NULL, p, 4, 4, 4, NULL) == 1
+    assert L.gemm_gelu_backward_hip(NULL, p, p, p, p, NULL, NULL, p, 4, 4, 4, NULL) == 1
+    assert L.gemm_gelu_backward_hip(p, p, p, NULL, p, NULL, NULL, NULL, 4, 4, 4, NULL) == 1
 
 
 def test_layernorm_validation(L):
@@ -194,6 +198,12 @@ def test_layernorm_validation(L):
     assert L.layernorm_forward_hip(p, p, NULL, p, 0, 1024, 1e-5, NULL) == 0
     assert L.layernorm_forward_hip(NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1
     assert L.layernorm_forward_stats_hip(p, p, NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1
+    # the _ex backward: D == 0 or a NULL operand -> 1; column sums past 8192 columns -> 9
+    ex = L.layernorm_backward_ex_hip
+    assert ex(p, p, p, p, p, NULL, p, NULL, NULL, p, 1024, 0, NULL) == 1
+    assert ex(p, p, p, p, p, NULL, NULL, NULL, NULL, p, 2048, 1024, NULL) == 1
+    assert ex(p, NULL, p, p, p, NULL, p, NULL, NULL, p, 2048, 1024, NULL) == 1
+    assert ex(p, p, p, p, p, NULL, p, NULL, NULL, p, 32768, 16384, NULL) == 9
 
 
 def test_rmsnorm_validation(L):

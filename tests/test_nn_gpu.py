@@ -199,6 +199,44 @@ def test_layernorm_backward_residual(oracle):
         assert e <= 1e-2 and rel_l2(dw, rdw) <= 1e-4
 
 
+@pytest.mark.parametrize("rows,D", [(300, 1024), (4097, 2048), (513, 1536), (300, 96)])
+def test_layernorm_backward_dx_colsum(rows, D):
+    """layernorm_backward with out_dx_colsum: dx bit-identical to the call
+    without it (dw and db too on the register path, D a multiple of 512 up to
+    2048), and the column sums of the returned dx (from the register kernel's
+    partials, or a separate pass on the looped path)."""
+    from ceo_amd.nn import layernorm_backward, layernorm_forward
+
+    announce(f"layernorm_backward dx colsum rows={rows} D={D}")
+    g = torch.Generator(device="cuda").manual_seed(rows + D)
+    x = torch.randn(rows, D, generator=g, device="cuda").to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(D, generator=g, device="cuda")).to(torch.bfloat16)
+    dy = torch.randn(rows, D, generator=g, device="cuda").to(torch.bfloat16)
+    res = torch.randn(rows, D, generator=g, device="cuda").to(torch.bfloat16)
+    _, mean, rstd = layernorm_forward(x, w, None, 1e-5, save_stats=True)
+    for r in (None, res):
+        dx0, dw0, db0 = layernorm_backward(dy, x, w, mean, rstd, residual=r)
+        cs = torch.full((D,), 7.0, dtype=torch.bfloat16, device="cuda")
+        dx1, dw1, db1 = layernorm_backward(dy, x, w, mean, rstd, residual=r, out_dx_colsum=cs)
+        # without dw / db the sums are still produced
+        cs2 = torch.zeros_like(cs)
+        dx2, _, _ = layernorm_backward(dy, x, w, mean, rstd, need_param_grads=False, residual=r,
+                                       out_dx_colsum=cs2)
+        torch.cuda.synchronize()
+        assert torch.equal(dx0, dx1) and torch.equal(dx0, dx2)
+        if D % 512 == 0:
+            assert torch.equal(dw0, dw1) and torch.equal(db0, db1)
+        else:
+            # the looped kernel adds dw / db with LDS atomics: the order, and
+            # so the last bits, vary from call to call
+            torch.testing.assert_close(dw0, dw1, rtol=1e-5, atol=1e-4)
+            torch.testing.assert_close(db0, db1, rtol=1e-5, atol=1e-4)
+        ref = dx0.double().sum(0)
+        e = rel_l2(cs, ref.cpu().numpy())
+        print(f"  residual={r is not None} rel-L2 colsum {e:.2e}", flush=True)
+        assert e <= 1e-2 and torch.equal(cs, cs2)
+
+
 @pytest.fixture(params=[0, 1, 2], ids=["mfma", "generic", "hipblaslt"])
 def gemm_backend(request):
     """Runs a GEMM test on the library's kernels (the large-tile MFMA kernel
@@ -391,16 +429,23 @@ def test_gemm_gelu_fused(m, k, n):
     # the MLP's second product and its backward through the GELU
     w2 = (0.05 * torch.randn(n, k, generator=g, device="cuda")).to(torch.bfloat16)
     dc = torch.randn(m, k, generator=g, device="cuda").to(torch.bfloat16)
-    dpre, dw2, dbias = nn.gemm_gelu_backward(dc, out, w2, pre, need_bias=True)
+    dpb = torch.full((n,), 3.0, dtype=torch.bfloat16, device="cuda")
+    dpre, dw2, dbias = nn.gemm_gelu_backward(dc, out, w2, pre, need_bias=True,
+                                             out_pre_bias=dpb)
     x = pre.float().requires_grad_(True)
     gl = torch.nn.functional.gelu(x, approximate="tanh")
     (gl * (dc.float() @ w2.float().t()).to(torch.bfloat16).float()).sum().backward()
     e3 = rel_l2(dpre, x.grad.cpu().numpy())
     e4 = rel_l2(dw2, (out.float().t() @ dc.float()).cpu().numpy())
     e5 = rel_l2(dbias, dc.float().sum(0).cpu().numpy())
-    print(f"  rel-L2 pre {e1:.2e} out {e2:.2e} dpre {e3:.2e} dw2 {e4:.2e} dbias {e5:.2e}",
-          flush=True)
-    assert max(e1, e2, e3, e4, e5) <= 1e-2
+    # the pre-activation bias gradient: column sums of the dpre returned
+    e6 = rel_l2(dpb, dpre.double().sum(0).cpu().numpy())
+    dpre2, _, _ = nn.gemm_gelu_backward(dc, out, w2, pre, need_b=False)
+    torch.cuda.synchronize()
+    assert torch.equal(dpre, dpre2)
+    print(f"  rel-L2 pre {e1:.2e} out {e2:.2e} dpre {e3:.2e} dw2 {e4:.2e} dbias {e5:.2e} "
+          f"dpre colsum {e6:.2e}", flush=True)
+    assert max(e1, e2, e3, e4, e5, e6) <= 1e-2
 
 
 @pytest.mark.parametrize("name,m,k,n", [("qkv", 16384, 1024, 3088), ("out", 16384, 1024, 1024),
@@ -445,13 +490,16 @@ def test_gemm_gelu_config4_mlp():
     e1 = rel_l2(pre, pre_ref.float().cpu().numpy())
     e2 = rel_l2(out, torch.nn.functional.gelu(pre_ref.float(), approximate="tanh").cpu().numpy())
     dy = torch.randn(m, d, generator=g, device="cuda").to(torch.bfloat16)
-    dpre, dw, db = nn.gemm_gelu_backward(dy, out, w_down, pre, need_bias=True)
+    db_up = torch.empty(f, dtype=torch.bfloat16, device="cuda")
+    dpre, dw, db = nn.gemm_gelu_backward(dy, out, w_down, pre, need_bias=True,
+                                         out_pre_bias=db_up)
     t = pre.float().requires_grad_(True)
     gl = torch.nn.functional.gelu(t, approximate="tanh")
     (gl * (dy.float() @ w_down.float().t()).to(torch.bfloat16).float()).sum().backward()
     e3 = rel_l2(dpre, t.grad.cpu().numpy())
     e4 = rel_l2(dw, (out.float().t() @ dy.float()).cpu().numpy())
     e5 = rel_l2(db, dy.float().sum(0).cpu().numpy())
-    print(f"  rel-L2 pre {e1:.2e} out {e2:.2e} dpre {e3:.2e} dw {e4:.2e} dbias {e5:.2e}",
-          flush=True)
-    assert max(e1, e2, e3, e4, e5) <= 1e-2
+    e6 = rel_l2(db_up, dpre.double().sum(0).cpu().numpy())
+    print(f"  rel-L2 pre {e1:.2e} out {e2:.2e} dpre {e3:.2e} dw {e4:.2e} dbias {e5:.2e} "
+          f"dpre colsum {e6:.2e}", flush=True)
+    assert max(e1, e2, e3, e4, e5, e6) <= 1e-2
