@@ -22,6 +22,7 @@
 #include "common.hpp"
 #include "efla_coeff.hpp"
 #include "internal.hpp"
+#include "mfma.hpp"
 
 namespace efla {
 namespace r {
@@ -122,6 +123,224 @@ __global__ void __launch_bounds__(NTH) r_forward_kernel(const bf16* __restrict__
         __syncthreads();
     }
     for (int i = threadIdx.x; i < d * d; i += NTH) st[i] = S[(i / d) * lds + i % d];
+}
+
+// ---------------------------------------------------------------------------
+// forward, register-resident state (d = 64 or 128; other d take
+// r_forward_kernel)
+// ---------------------------------------------------------------------------
+// c(beta, |k_t|^2) of every token, [b * H + h][t] (fp32): 16 lanes per
+// (token, head) row of d = 16 P values (P = 4 or 8), 16-byte loads, the
+// squares summed per lane and then across the 16 lanes.
+template <int P>
+__global__ void __launch_bounds__(NTH) r_coeff_kernel(const bf16* __restrict__ k,
+                                                      float* __restrict__ cout, int H, long T,
+                                                      float beta, long n) {
+    const long i = ((long)blockIdx.x * NTH + threadIdx.x) / 16;  // (b, t, h), h fastest
+    const int q = threadIdx.x & 15;
+    float s = 0.f;
+    if (i < n) {
+        typedef __attribute__((__vector_size__(P * sizeof(__bf16)))) __bf16 bfP;
+        const bfP x = *reinterpret_cast<const bfP*>(k + i * (16 * P) + P * q);
+#pragma unroll
+        for (int e = 0; e < P; ++e) s = fmaf((float)x[e], (float)x[e], s);
+    }
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) s += __shfl_xor(s, off);
+    if (i < n && q == 0) {
+        float c, dcl, dcb;
+        efla_coeff(s, beta, c, dcl, dcb);
+        const long h = i % H, bt = i / H, t = bt % T, b = bt / T;
+        cout[(b * H + h) * T + t] = c;
+    }
+}
+
+// The token step with the state in registers: LPC lanes (consecutive) own
+// value column c of S, each holding its RPL rows as packed bf16 pairs.
+// Per token
+//   u_c = sum_row k_row S[row][c]     bf16 dot2 over row pairs, then across
+//                                     the LPC lanes of the column
+//   S[row][c] = bf16(S + (c k_row) (v_c - u_c))       lane-local
+//   o_row = sum_c S[row][c] k_c        the new state's columns go to LDS as
+//                                      [c][row] and 16x16x32 MFMAs contract
+//                                      them with k
+// One barrier per token.  Wave 0 stages token t+1's k (bf16) and c k (fp32,
+// c from r_coeff_kernel) in LDS during token t; k, c and v are loaded two
+// tokens ahead.  The o product of token t reads its fragments right after
+// token t's barrier and runs its MFMAs after token t+1's update, so the reads
+// overlap that work.  OUT writes o_t; CK stores the state before every SEG-th
+// token to ck (the backward's checkpoints).  The bf16 roundings and the
+// (c k) r product are the reference's; the sums run in another order (fp32
+// rounding level before each bf16 rounding).
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+template <int D>
+struct RFastSmem {
+    bf16 Sl[2][D * (D + 8)];  // new state [c][row], double-buffered
+    float ckf[3][D];          // c k (fp32), ring of three tokens
+    bf16 kb[3][D];            // k (bf16)
+};
+
+template <int D>
+constexpr int rfast_threads() {
+    return D == 128 ? 512 : 256;
+}
+
+template <int D, bool OUT, bool CK>
+__global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
+    bf16* __restrict__ state, bf16* __restrict__ out, bf16* __restrict__ ck, int H, long T) {
+    constexpr int NT = rfast_threads<D>(), NW = NT / 64;
+    constexpr int LPC = NT / D, RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
+    static_assert(RPL % 8 == 0 && (D == 64 || D == 128), "d = 64 or 128");
+    __shared__ __attribute__((aligned(16))) RFastSmem<D> sm;
+    const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
+    const int col = tid / LPC, part = tid % LPC, r0 = part * RPL;
+    const int bh = blockIdx.x, b = bh / H, h = bh % H;
+    const long dd = (long)D * D, nseg = (T + SEG - 1) / SEG;
+    const long tstride = (long)H * D;  // elements between tokens
+    const long base0 = (long)b * T * tstride + (long)h * D;
+    const float* cbh = coef + (long)bh * T;
+    bf16* st = state + (long)bh * dd;
+
+    bf16x2 Sp[NP];  // rows r0 + 2p (low half) and r0 + 2p + 1 (high half)
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+        Sp[p] = bf16x2{st[(long)(r0 + 2 * p) * D + col], st[(long)(r0 + 2 * p + 1) * D + col]};
+
+    // v_c per lane; k (D / 64 values per lane) and c in wave 0; two tokens ahead
+    constexpr int KPL = D / 64;
+    bf16 vreg[2], kreg[2][KPL];
+    float creg[2];
+    auto load_v = [&](long tt, int slot) {
+        if (tt < T) vreg[slot] = v[base0 + tt * tstride + col];
+    };
+    auto load_k = [&](long tt, int slot) {
+        if (w == 0 && tt < T) {
+#pragma unroll
+            for (int e = 0; e < KPL; ++e) kreg[slot][e] = k[base0 + tt * tstride + KPL * l + e];
+            creg[slot] = cbh[tt];
+        }
+    };
+    auto stage_k = [&](int slot, int ring) {  // wave 0
+#pragma unroll
+        for (int e = 0; e < KPL; ++e) {
+            sm.ckf[ring][KPL * l + e] = creg[slot] * to_f(kreg[slot][e]);
+            sm.kb[ring][KPL * l + e] = kreg[slot][e];
+        }
+    };
+    if (T > 0) {
+        load_k(0, 0);
+        if (w == 0) stage_k(0, 0);
+        __syncthreads();
+    }
+    load_v(0, 0);
+    load_v(1, 1);
+    load_k(1, 1);
+    load_k(2, 0);
+
+    // the o product of the last token whose fragments are in registers
+    constexpr int MT = D / 16 / NW, NK = D / 32;
+    bf16x8 af[MT][NK], bk[NK];
+    long tp = -1;
+    const int g = l >> 4, j = l & 15;
+    auto o_reads = [&](long t) {
+        const bf16* kb = sm.kb[t % 3];
+        const bf16* slt = sm.Sl[t & 1];
+#pragma unroll
+        for (int q = 0; q < NK; ++q) {
+            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 4 * g);
+            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 16 + 4 * g);
+            bk[q] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+            for (int m = 0; m < MT; ++m) af[m][q] = mf::frag_trc(l, slt, LDS, 32 * q, 16 * (MT * w + m));
+        }
+        tp = t;
+    };
+    // A = S[row][c] (c-order k over c), B = k broadcast over the 16 columns
+    auto o_products = [&]() {
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            mf::floatx4 acc = mf::zero4();
+#pragma unroll
+            for (int q = 0; q < NK; ++q) acc = mf::mma(af[m][q], bk[q], acc);
+            if (j == 0) {
+                bf16x4 ov;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) ov[i] = (bf16)acc[i];
+                *reinterpret_cast<bf16x4*>(out + base0 + tp * tstride + 16 * (MT * w + m) + 4 * g) = ov;
+            }
+        }
+    };
+
+    // token t: its v in vreg[vs]; token t+1's k and c in kreg[ks], creg[ks]
+    auto token = [&](long t, int vs, int ks) {
+        if (CK && t % SEG == 0) {
+            bf16* dst = ck + ((long)bh * nseg + t / SEG) * dd;
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                dst[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
+                dst[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
+            }
+        }
+        const int kslot = (int)(t % 3);
+        // token t+1's k into the ring (read after this token's barrier)
+        if (w == 0 && t + 1 < T) stage_k(ks, (int)((t + 1) % 3));
+        load_k(t + 3, ks);
+        const float vt = to_f(vreg[vs]);
+        load_v(t + 2, vs);
+        // this lane's rows of k (bf16 pairs) and c k, all reads issued first
+        bf16x8 kq[NP / 4];
+        mf::floatx4 cq[RPL / 4];
+#pragma unroll
+        for (int i = 0; i < NP / 4; ++i)
+            kq[i] = *reinterpret_cast<const bf16x8*>(sm.kb[kslot] + r0 + 8 * i);
+#pragma unroll
+        for (int i = 0; i < RPL / 4; ++i)
+            cq[i] = *reinterpret_cast<const mf::floatx4*>(sm.ckf[kslot] + r0 + 4 * i);
+        // u = S^T k for this column (four partial sums, then the lanes of the column)
+        float ua[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
+            ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, Sp[p], ua[p % 4], false);
+        }
+        float u = (ua[0] + ua[1]) + (ua[2] + ua[3]);
+#pragma unroll
+        for (int off = 1; off < LPC; off <<= 1) u += __shfl_xor(u, off);
+        const float rc = vt - u;
+        // S <- bf16(S + (c k) r); the new column piece as bf16 into LDS
+        bf16* sl = sm.Sl[t & 1] + col * LDS + r0;
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float lo = fmaf(cq[p / 2][2 * (p % 2)], rc, (float)Sp[p][0]);
+            const float hi = fmaf(cq[p / 2][2 * (p % 2) + 1], rc, (float)Sp[p][1]);
+            Sp[p] = bf16x2{(bf16)lo, (bf16)hi};
+        }
+        if (OUT) {
+#pragma unroll
+            for (int i = 0; i < NP / 4; ++i)
+                *reinterpret_cast<bf16x8*>(sl + 8 * i) =
+                    bf16x8{Sp[4 * i][0], Sp[4 * i][1], Sp[4 * i + 1][0], Sp[4 * i + 1][1],
+                           Sp[4 * i + 2][0], Sp[4 * i + 2][1], Sp[4 * i + 3][0], Sp[4 * i + 3][1]};
+            if (tp >= 0) o_products();  // the previous token's o
+        }
+        __syncthreads();  // the new state in LDS; token t+1's k staged
+        if (OUT) o_reads(t);
+    };
+    for (long t = 0; t < T; t += 2) {
+        token(t, 0, 1);
+        if (t + 1 < T) token(t + 1, 1, 0);
+    }
+    if (OUT && tp >= 0) o_products();
+    // the forward hands the final state back; the checkpoint pass leaves the
+    // caller's initial state alone
+    if constexpr (!CK)
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            st[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
+            st[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
+        }
 }
 
 // ---------------------------------------------------------------------------
@@ -322,9 +541,41 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
     // the LDS-resident state holds head_dim <= 256 (the reference's bound is
     // its shared-memory limit; see the header)
     if (head_dim > (size_t)MAXD || nbh > (size_t)INT32_MAX) return kInvalidConfiguration;
-    EFLA_LAUNCH("efla_r_forward", r_forward_kernel, dim3((unsigned)nbh), dim3(NTH), stream,
-                (const bf16*)k, (const bf16*)v, (bf16*)state, (bf16*)output, (int)num_heads,
-                (long)seq_len, (int)head_dim, beta);
+    const dim3 grid((unsigned)nbh);
+    // the register-resident path: d = 64 / 128, k aligned for the coefficient
+    // kernel's 2d-byte row loads, at most 2^35 tokens (its grid)
+    const bool fast = (head_dim == 128 || head_dim == 64) &&
+                      (uintptr_t)k % (head_dim / 8) == 0 && nbh * seq_len <= ((size_t)1 << 35);
+    if (fast) {
+        // every token's coefficient first (the stream's workspace), then the
+        // register-resident token loop
+        const size_t ntok = nbh * seq_len;
+        void* ws = nullptr;
+        WsLease lease;
+        int rc = workspace_acquire(ntok * sizeof(float), stream, &ws, lease);
+        if (rc != kSuccess) return rc;
+        const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
+        if (head_dim == 128)
+            EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
+                        (float*)ws, (int)num_heads, (long)seq_len, beta, (long)ntok);
+        else
+            EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
+                        (float*)ws, (int)num_heads, (long)seq_len, beta, (long)ntok);
+        if (head_dim == 128)
+            EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<128, true, false>), grid,
+                        dim3(rfast_threads<128>()), stream, (const bf16*)k, (const bf16*)v,
+                        (const float*)ws, (bf16*)state, (bf16*)output, (bf16*)nullptr,
+                        (int)num_heads, (long)seq_len);
+        else
+            EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<64, true, false>), grid,
+                        dim3(rfast_threads<64>()), stream, (const bf16*)k, (const bf16*)v,
+                        (const float*)ws, (bf16*)state, (bf16*)output, (bf16*)nullptr,
+                        (int)num_heads, (long)seq_len);
+    } else {
+        EFLA_LAUNCH("efla_r_forward", r_forward_kernel, grid, dim3(NTH), stream, (const bf16*)k,
+                    (const bf16*)v, (bf16*)state, (bf16*)output, (int)num_heads, (long)seq_len,
+                    (int)head_dim, beta);
+    }
     return (int)hipPeekAtLastError();
 }
 
@@ -348,9 +599,13 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
         return kInvalidConfiguration;
     const bool gl = head_dim > 128;
     if (gl) g_elems = gse;
+    const bool fast = (head_dim == 128 || head_dim == 64) &&
+                      (uintptr_t)k % (head_dim / 8) == 0 && nbh * seq_len <= ((size_t)1 << 35);
+    const size_t ntok = fast ? nbh * seq_len : 0;  // per-token coefficients
     const size_t off_hist = (ck_elems * 2 + 255) & ~(size_t)255;
     const size_t off_g = (off_hist + hist_elems * 2 + 255) & ~(size_t)255;
-    const size_t need = off_g + g_elems * 4 + 256;
+    const size_t off_c = (off_g + g_elems * 4 + 255) & ~(size_t)255;
+    const size_t need = off_c + ntok * 4 + 256;
     void* ws = nullptr;
     WsLease lease;
     int rc = workspace_acquire(need, stream, &ws, lease);
@@ -358,9 +613,30 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
     bf16* ck = (bf16*)ws;
     bf16* hist = (bf16*)((char*)ws + off_hist);
     float* G = gl ? (float*)((char*)ws + off_g) : nullptr;
-    EFLA_LAUNCH("efla_r_checkpoint", r_checkpoint_kernel, dim3((unsigned)nbh), dim3(NTH), stream,
-                (const bf16*)k, (const bf16*)v, (const bf16*)state, ck, (int)num_heads,
-                (long)seq_len, (int)head_dim, beta);
+    // the state before every SEG-th token (the register-resident forward
+    // where d allows; it does not write `state`)
+    float* coef = (float*)((char*)ws + off_c);
+    const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
+    if (fast && head_dim == 128)
+        EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
+                    coef, (int)num_heads, (long)seq_len, beta, (long)ntok);
+    else if (fast)
+        EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
+                    coef, (int)num_heads, (long)seq_len, beta, (long)ntok);
+    if (fast && head_dim == 128)
+        EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<128, false, true>), dim3((unsigned)nbh),
+                    dim3(rfast_threads<128>()), stream, (const bf16*)k, (const bf16*)v,
+                    (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
+                    (long)seq_len);
+    else if (fast)
+        EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<64, false, true>), dim3((unsigned)nbh),
+                    dim3(rfast_threads<64>()), stream, (const bf16*)k, (const bf16*)v,
+                    (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
+                    (long)seq_len);
+    else
+        EFLA_LAUNCH("efla_r_checkpoint", r_checkpoint_kernel, dim3((unsigned)nbh), dim3(NTH),
+                    stream, (const bf16*)k, (const bf16*)v, (const bf16*)state, ck,
+                    (int)num_heads, (long)seq_len, (int)head_dim, beta);
     if (gl) {
         EFLA_LAUNCH("efla_r_backward", r_backward_kernel<true>, dim3((unsigned)nbh), dim3(NTH),
                     stream, (const bf16*)grad_output, (const bf16*)k, (const bf16*)v, ck, hist,
