@@ -5,17 +5,24 @@
 //   lambda = |k_t|^2, c = c(beta, lambda)
 //   u = S^T k_t, S <- bf16(S + (c k_t)(v_t - u)^T)   (state re-rounded every token)
 //   o_t = S k_t                                        (needs d_k == d_v)
-// One workgroup of 256 threads owns one (b, h).  The bf16 state lives in LDS
-// (row stride d+2 to spread banks) instead of global memory, so a token costs
-// two passes over LDS and four barriers, against three global passes and ~13
-// barriers in the reference.  Reduction order differs from the reference's
-// serial sums; values differ at fp32 rounding level before each bf16 rounding.
+// One workgroup owns one (b, h); the work of a token is serial, so a token's
+// cost is its chain of dependent steps.  For d = 64 and 128 (16-byte aligned
+// k) the state lives in registers: consecutive lanes own one value column,
+// S^T k and the update are lane-local, and o = S k (a sum over columns) is
+// formed by MFMAs from a transposed LDS copy of the new state; one barrier
+// per token, k / v / c loaded two tokens ahead, every token's c(beta, |k|^2)
+// from a separate parallel kernel (r_fast_kernel).  Other d keep the state
+// in LDS (row stride d+2): two LDS passes and four barriers per token against
+// the reference's three global passes and ~13 barriers (r_forward_kernel).
+// Reduction order differs from the reference's serial sums; values differ at
+// fp32 rounding level before each bf16 rounding.
 //
-// The backward recomputes states from bf16 checkpoints taken every 64 tokens
-// (exact, since the states are bf16 values), rebuilds the 65 states of one
-// segment at a time into a workspace, and runs the reference's BPTT
-// (efla.cu:315-454) over the segment in reverse with the fp32 dL/dS in LDS
-// (d <= 128) or in the workspace (d <= 256).
+// The backward recomputes states from bf16 checkpoints (exact, since the
+// states are bf16 values), rebuilds one segment's states at a time into a
+// workspace, and runs the reference's BPTT (efla.cu:315-454) over the segment
+// in reverse: for d = 64 / 128 with 32-token segments and dL/dS in fp32
+// registers (r_bwd_fast_kernel, one barrier per token), otherwise with
+// 64-token segments and dL/dS in LDS (d <= 128) or the workspace (d <= 256).
 #include <hip/hip_runtime.h>
 
 #include "../../include/efla_hip.h"
@@ -29,7 +36,8 @@ namespace r {
 
 constexpr int NTH = 256;
 constexpr int MAXD = 256;
-constexpr int SEG = 64;  // checkpoint spacing of the backward
+constexpr int SEG = 64;   // checkpoint spacing of the backward
+constexpr int SEGF = 32;  // the same for the register-resident backward (d = 64, 128)
 
 __device__ __forceinline__ float block_sum(float x, float* red) {
     // wave reduction then across the 4 waves
@@ -129,12 +137,14 @@ __global__ void __launch_bounds__(NTH) r_forward_kernel(const bf16* __restrict__
 // forward, register-resident state (d = 64 or 128; other d take
 // r_forward_kernel)
 // ---------------------------------------------------------------------------
-// c(beta, |k_t|^2) of every token, [b * H + h][t] (fp32): 16 lanes per
+// c(beta, |k_t|^2) of every token, [b * H + h][t] (fp32), and dc/dlambda
+// when dcout is set: 16 lanes per
 // (token, head) row of d = 16 P values (P = 4 or 8), 16-byte loads, the
 // squares summed per lane and then across the 16 lanes.
 template <int P>
 __global__ void __launch_bounds__(NTH) r_coeff_kernel(const bf16* __restrict__ k,
-                                                      float* __restrict__ cout, int H, long T,
+                                                      float* __restrict__ cout,
+                                                      float* __restrict__ dcout, int H, long T,
                                                       float beta, long n) {
     const long i = ((long)blockIdx.x * NTH + threadIdx.x) / 16;  // (b, t, h), h fastest
     const int q = threadIdx.x & 15;
@@ -152,6 +162,7 @@ __global__ void __launch_bounds__(NTH) r_coeff_kernel(const bf16* __restrict__ k
         efla_coeff(s, beta, c, dcl, dcb);
         const long h = i % H, bt = i / H, t = bt % T, b = bt / T;
         cout[(b * H + h) * T + t] = c;
+        if (dcout) dcout[(b * H + h) * T + t] = dcl;
     }
 }
 
@@ -168,11 +179,36 @@ __global__ void __launch_bounds__(NTH) r_coeff_kernel(const bf16* __restrict__ k
 // c from r_coeff_kernel) in LDS during token t; k, c and v are loaded two
 // tokens ahead.  The o product of token t reads its fragments right after
 // token t's barrier and runs its MFMAs after token t+1's update, so the reads
-// overlap that work.  OUT writes o_t; CK stores the state before every SEG-th
-// token to ck (the backward's checkpoints).  The bf16 roundings and the
+// overlap that work.  OUT writes o_t; CK stores the state before every
+// SEGF-th token to ck, column-major (the register-resident backward's
+// checkpoints).  The bf16 roundings and the
 // (c k) r product are the reference's; the sums run in another order (fp32
 // rounding level before each bf16 rounding).
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
+// Cross-lane moves through DPP (a VALU operand modifier) instead of the LDS
+// permute unit: the lane's partner within its quad (xor 1, xor 2) and a
+// rotation within its row of 16 lanes.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL,
+                                                               0xF, 0xF, true));
+}
+// sum over the L (1, 2 or 4) consecutive lanes of a quad group, in every lane
+template <int L>
+__device__ __forceinline__ float quad_sum(float x) {
+    if constexpr (L >= 2) x += dpp_f<0xB1>(x);  // quad_perm [1, 0, 3, 2]
+    if constexpr (L >= 4) x += dpp_f<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+    return x;
+}
+// sum over the wave of the values in lanes 4i (other lanes hold 0), in every lane
+__device__ __forceinline__ float wave_sum_q4(float x) {
+    x += dpp_f<0x124>(x);  // row_ror:4
+    x += dpp_f<0x128>(x);  // row_ror:8
+    x += __shfl_xor(x, 16);
+    x += __shfl_xor(x, 32);
+    return x;
+}
 
 template <int D>
 struct RFastSmem {
@@ -197,7 +233,7 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
     const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
     const int col = tid / LPC, part = tid % LPC, r0 = part * RPL;
     const int bh = blockIdx.x, b = bh / H, h = bh % H;
-    const long dd = (long)D * D, nseg = (T + SEG - 1) / SEG;
+    const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
     const long tstride = (long)H * D;  // elements between tokens
     const long base0 = (long)b * T * tstride + (long)h * D;
     const float* cbh = coef + (long)bh * T;
@@ -275,13 +311,13 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
 
     // token t: its v in vreg[vs]; token t+1's k and c in kreg[ks], creg[ks]
     auto token = [&](long t, int vs, int ks) {
-        if (CK && t % SEG == 0) {
-            bf16* dst = ck + ((long)bh * nseg + t / SEG) * dd;
+        if (CK && t % SEGF == 0) {  // column-major [c][row]
+            bf16* dst = ck + ((long)bh * nsegf + t / SEGF) * dd + (long)col * D + r0;
 #pragma unroll
-            for (int p = 0; p < NP; ++p) {
-                dst[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
-                dst[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
-            }
+            for (int i = 0; i < NP / 4; ++i)
+                *reinterpret_cast<bf16x8*>(dst + 8 * i) =
+                    bf16x8{Sp[4 * i][0], Sp[4 * i][1], Sp[4 * i + 1][0], Sp[4 * i + 1][1],
+                           Sp[4 * i + 2][0], Sp[4 * i + 2][1], Sp[4 * i + 3][0], Sp[4 * i + 3][1]};
         }
         const int kslot = (int)(t % 3);
         // token t+1's k into the ring (read after this token's barrier)
@@ -305,9 +341,7 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
             const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
             ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, Sp[p], ua[p % 4], false);
         }
-        float u = (ua[0] + ua[1]) + (ua[2] + ua[3]);
-#pragma unroll
-        for (int off = 1; off < LPC; off <<= 1) u += __shfl_xor(u, off);
+        const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
         const float rc = vt - u;
         // S <- bf16(S + (c k) r); the new column piece as bf16 into LDS
         bf16* sl = sm.Sl[t & 1] + col * LDS + r0;
@@ -341,6 +375,312 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
             st[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
             st[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
         }
+}
+
+// ---------------------------------------------------------------------------
+// backward, register-resident (d = 64 or 128)
+// ---------------------------------------------------------------------------
+// The reference BPTT (efla.cu:355-453) per token, last to first, with
+// G = dL/dS (after the token) in fp32 registers in the forward's column-owner
+// layout.  With g = G + dO k^T, u = S^T k, w2 = v - u, sw = g^T k, w1 = c sw:
+//   grad_v = w1,   G <- g - k w1^T
+//   grad_k = 2 grad_lambda k + S_n^T dO + sum_c (c g[:, c] w2_c - S[:, c] w1_c)
+//   grad_lambda = dc/dlambda * sum_c w2_c sw_c       (= sum_row k_row (g w2)_row)
+// where S / S_n are the states before / after the token.  Column sums are
+// lane-local (plus the lanes of the column); the row sum goes through LDS as
+// bf16 high and low parts of each fp32 summand (about 16 bits kept) and
+// 16x16x32 MFMAs against ones.  One barrier per token.
+// Segments of SEGF tokens are taken last to first: each is rebuilt from its
+// checkpoint (ck, column-major) with the forward step, every state stored
+// column-major to the workspace (hist), which the same lanes read back.
+template <int D>
+struct RBwdSmem {
+    bf16 Mh[2][D * (D + 8)];  // the row sum's summands [c][row], high bf16 part
+    bf16 Ml[2][D * (D + 8)];  // low part
+    bf16 fkb[3][D];           // rebuild ring: k (bf16)
+    float fck[3][D];          //   c k (fp32)
+    bf16 rkb[3][D], rgb[3][D];    // reverse ring: k, dO (bf16)
+    float rkf[3][D], rgf[3][D];   //   k, dO (fp32)
+    float rcd[3][4];              //   c, dc/dlambda
+    float gkv[2][D];              // S_n^T dO per column
+    float red[2][16];             // grad_c partials per wave
+};
+
+template <int D>
+__global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
+    const bf16* __restrict__ dO, const bf16* __restrict__ k, const bf16* __restrict__ v,
+    const float* __restrict__ coef, const float* __restrict__ dcoef, const bf16* __restrict__ ck,
+    bf16* __restrict__ hist_all, bf16* __restrict__ grad_k, bf16* __restrict__ grad_v,
+    bf16* __restrict__ grad_state, int H, long T) {
+    constexpr int NT = rfast_threads<D>(), NW = NT / 64;
+    constexpr int LPC = NT / D, RPL = D / LPC, NP = RPL / 2, LDS = D + 8, KPL = D / 64;
+    constexpr int MT = D / 16 / NW, NK = D / 32;
+    static_assert(RPL % 8 == 0 && MT == 1 && LPC == 4, "d = 64 or 128");
+    __shared__ __attribute__((aligned(16))) RBwdSmem<D> sm;
+    const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
+    const int col = tid / LPC, part = tid % LPC, r0 = part * RPL;
+    const int g4 = l >> 4, j16 = l & 15;
+    const int bh = blockIdx.x, b = bh / H, h = bh % H;
+    const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
+    const long tstride = (long)H * D;
+    const long base0 = (long)b * T * tstride + (long)h * D;
+    const float* cbh = coef + (long)bh * T;
+    const float* dcbh = dcoef + (long)bh * T;
+    bf16* hist = hist_all + (long)bh * (SEGF + 1) * dd;
+    auto col_ptr = [&](bf16* basep, long jj) { return basep + jj * dd + (long)col * D + r0; };
+    auto load_col = [&](const bf16* src, bf16x2 (&dst)[NP]) {
+#pragma unroll
+        for (int i = 0; i < NP / 4; ++i) {
+            const bf16x8 x = *reinterpret_cast<const bf16x8*>(src + 8 * i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[4 * i + e] = bf16x2{x[2 * e], x[2 * e + 1]};
+        }
+    };
+    auto pack8 = [&](const bf16x2 (&x)[NP], int i) {
+        return bf16x8{x[4 * i][0], x[4 * i][1], x[4 * i + 1][0], x[4 * i + 1][1],
+                      x[4 * i + 2][0], x[4 * i + 2][1], x[4 * i + 3][0], x[4 * i + 3][1]};
+    };
+    auto store_col = [&](bf16* dst, const bf16x2 (&x)[NP]) {
+#pragma unroll
+        for (int i = 0; i < NP / 4; ++i) *reinterpret_cast<bf16x8*>(dst + 8 * i) = pack8(x, i);
+    };
+
+    float G[RPL];
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) G[i] = 0.f;
+    const bf16x8 ones = bf16x8{(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f,
+                               (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
+
+    for (long seg = nsegf - 1; seg >= 0; --seg) {
+        const long t0 = seg * SEGF, t1 = t0 + SEGF < T ? t0 + SEGF : T;
+        // ---- rebuild: hist[jj] = the state before token t0 + jj
+        bf16x2 S[NP];
+        load_col(ck + ((long)bh * nsegf + seg) * dd + (long)col * D + r0, S);
+        store_col(col_ptr(hist, 0), S);
+        {
+            bf16 vreg[2], kreg[2][KPL];
+            float creg[2];
+            auto load_v = [&](long tt, int slot) {
+                if (tt < t1) vreg[slot] = v[base0 + tt * tstride + col];
+            };
+            auto load_k = [&](long tt, int slot) {
+                if (w == 0 && tt < t1) {
+#pragma unroll
+                    for (int e = 0; e < KPL; ++e) kreg[slot][e] = k[base0 + tt * tstride + KPL * l + e];
+                    creg[slot] = cbh[tt];
+                }
+            };
+            auto stage = [&](int slot, long tt) {  // wave 0
+                const int ring = (int)(tt % 3);
+#pragma unroll
+                for (int e = 0; e < KPL; ++e) {
+                    sm.fck[ring][KPL * l + e] = creg[slot] * to_f(kreg[slot][e]);
+                    sm.fkb[ring][KPL * l + e] = kreg[slot][e];
+                }
+            };
+            load_k(t0, 0);
+            if (w == 0) stage(0, t0);
+            __syncthreads();
+            load_v(t0, 0);
+            load_v(t0 + 1, 1);
+            load_k(t0 + 1, 1);
+            load_k(t0 + 2, 0);
+            auto ftoken = [&](long t, int vs, int ks) {
+                const int kslot = (int)(t % 3);
+                if (w == 0 && t + 1 < t1) stage(ks, t + 1);
+                load_k(t + 3, ks);
+                const float vt = to_f(vreg[vs]);
+                load_v(t + 2, vs);
+                bf16x8 kq[NP / 4];
+                mf::floatx4 cq[RPL / 4];
+#pragma unroll
+                for (int i = 0; i < NP / 4; ++i)
+                    kq[i] = *reinterpret_cast<const bf16x8*>(sm.fkb[kslot] + r0 + 8 * i);
+#pragma unroll
+                for (int i = 0; i < RPL / 4; ++i)
+                    cq[i] = *reinterpret_cast<const mf::floatx4*>(sm.fck[kslot] + r0 + 4 * i);
+                float ua[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
+                    ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, S[p], ua[p % 4], false);
+                }
+                const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
+                const float rc = vt - u;
+#pragma unroll
+                for (int p = 0; p < NP; ++p) {
+                    const float lo = fmaf(cq[p / 2][2 * (p % 2)], rc, (float)S[p][0]);
+                    const float hi = fmaf(cq[p / 2][2 * (p % 2) + 1], rc, (float)S[p][1]);
+                    S[p] = bf16x2{(bf16)lo, (bf16)hi};
+                }
+                store_col(col_ptr(hist, t - t0 + 1), S);
+                __syncthreads();  // token t+1's k staged
+            };
+            for (long t = t0; t < t1; t += 2) {
+                ftoken(t, 0, 1);
+                if (t + 1 < t1) ftoken(t + 1, 1, 0);
+            }
+        }
+        // ---- reverse over the segment
+        {
+            // wave 0: token tt's k, dO (KPL values per lane), c, dc
+            bf16 kd[2][KPL], gd[2][KPL];
+            float cd[2], dcd[2];
+            auto load_kd = [&](long tt, int slot) {
+                if (w == 0 && tt >= t0) {
+#pragma unroll
+                    for (int e = 0; e < KPL; ++e) {
+                        kd[slot][e] = k[base0 + tt * tstride + KPL * l + e];
+                        gd[slot][e] = dO[base0 + tt * tstride + KPL * l + e];
+                    }
+                    cd[slot] = cbh[tt];
+                    dcd[slot] = dcbh[tt];
+                }
+            };
+            auto stage = [&](int slot, long tt) {  // wave 0
+                const int ring = (int)(tt % 3);
+#pragma unroll
+                for (int e = 0; e < KPL; ++e) {
+                    sm.rkb[ring][KPL * l + e] = kd[slot][e];
+                    sm.rgb[ring][KPL * l + e] = gd[slot][e];
+                    sm.rkf[ring][KPL * l + e] = to_f(kd[slot][e]);
+                    sm.rgf[ring][KPL * l + e] = to_f(gd[slot][e]);
+                }
+                if (l == 0) {
+                    sm.rcd[ring][0] = cd[slot];
+                    sm.rcd[ring][1] = dcd[slot];
+                }
+            };
+            // per lane: v_c and the column of the state before the token, one ahead
+            bf16 vR[2];
+            bf16x2 SpR[2][NP], Sn[NP];
+            auto load_lane = [&](long tt, int slot) {
+                if (tt >= t0) {
+                    vR[slot] = v[base0 + tt * tstride + col];
+                    load_col(col_ptr(hist, tt - t0), SpR[slot]);
+                }
+            };
+            load_kd(t1 - 1, 0);
+            if (w == 0) stage(0, t1 - 1);
+            __syncthreads();
+            load_col(col_ptr(hist, t1 - t0), Sn);
+            load_lane(t1 - 1, 0);
+            load_kd(t1 - 2, 0);
+            load_kd(t1 - 3, 1);
+            // token t: its v / state in vR[s], SpR[s]; token t-1's k, dO, c, dc in kd[s] ...
+            auto rtoken = [&](long t, int s) {
+                const int rs = (int)(t % 3), par = (int)(t & 1);
+                if (w == 0 && t - 1 >= t0) stage(s, t - 1);
+                load_kd(t - 3, s);
+                load_lane(t - 1, s ^ 1);
+                const bf16* kb = sm.rkb[rs];
+                const bf16* gb = sm.rgb[rs];
+                const float* kf = sm.rkf[rs];
+                const float* gf = sm.rgf[rs];
+                const float c = sm.rcd[rs][0];
+                const float kc = kf[col];
+                const float vt = to_f(vR[s]);
+                // pass 1, column sums: u = S^T k, gk = S_n^T dO (bf16 pairs),
+                // sw = g^T k with g = G + dO k_c (fp32); eight rows at a time
+                float ua[2] = {0.f, 0.f}, ga[2] = {0.f, 0.f}, sa[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i8 = 0; i8 < RPL / 8; ++i8) {
+                    const bf16x8 kq = *reinterpret_cast<const bf16x8*>(kb + r0 + 8 * i8);
+                    const bf16x8 gq = *reinterpret_cast<const bf16x8*>(gb + r0 + 8 * i8);
+                    const mf::floatx4 k0 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8);
+                    const mf::floatx4 k1 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8 + 4);
+                    const mf::floatx4 o0 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8);
+                    const mf::floatx4 o1 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8 + 4);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int p = 4 * i8 + e;
+                        ua[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{kq[2 * e], kq[2 * e + 1]},
+                                                                    SpR[s][p], ua[e & 1], false);
+                        ga[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{gq[2 * e], gq[2 * e + 1]},
+                                                                    Sn[p], ga[e & 1], false);
+                    }
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float go = e < 4 ? o0[e] : o1[e - 4];
+                        const float kr = e < 4 ? k0[e] : k1[e - 4];
+                        const float gv = fmaf(go, kc, G[8 * i8 + e]);
+                        sa[e & 3] = fmaf(gv, kr, sa[e & 3]);
+                    }
+                }
+                const float u = quad_sum<LPC>(ua[0] + ua[1]);
+                const float gk = quad_sum<LPC>(ga[0] + ga[1]);
+                const float sw = quad_sum<LPC>((sa[0] + sa[1]) + (sa[2] + sa[3]));
+                const float w2 = vt - u, w1 = c * sw, cw2 = c * w2;
+                // pass 2 (k, dO read again, g recomputed as in pass 1): the
+                // row sum's summands c g w2 - S w1 (bf16 high + low parts);
+                // G <- g - k w1^T
+                asm volatile("" ::: "memory");
+                bf16* mh = sm.Mh[par] + col * LDS + r0;
+                bf16* ml = sm.Ml[par] + col * LDS + r0;
+#pragma unroll
+                for (int i8 = 0; i8 < RPL / 8; ++i8) {
+                    const mf::floatx4 k0 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8);
+                    const mf::floatx4 k1 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8 + 4);
+                    const mf::floatx4 o0 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8);
+                    const mf::floatx4 o1 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8 + 4);
+                    bf16x8 hv, lv;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int ii = 8 * i8 + e;
+                        const float go = e < 4 ? o0[e] : o1[e - 4];
+                        const float kr = e < 4 ? k0[e] : k1[e - 4];
+                        const float gv = fmaf(go, kc, G[ii]);
+                        const float sp = (float)SpR[s][ii / 2][ii % 2];
+                        const float m = fmaf(gv, cw2, -(sp * w1));
+                        hv[e] = (bf16)m;
+                        lv[e] = (bf16)(m - (float)hv[e]);
+                        G[ii] = fmaf(-kr, w1, gv);
+                    }
+                    *reinterpret_cast<bf16x8*>(mh + 8 * i8) = hv;
+                    *reinterpret_cast<bf16x8*>(ml + 8 * i8) = lv;
+                }
+                // grad_c = sum_c w2_c sw_c: one value per column, then per wave
+                const float gc = wave_sum_q4(part == 0 ? w2 * sw : 0.f);
+                if (part == 0) {
+                    sm.gkv[par][col] = gk;
+                    grad_v[base0 + t * tstride + col] = (bf16)w1;
+                }
+                if (l == 0) sm.red[par][w] = gc;
+#pragma unroll
+                for (int p = 0; p < NP; ++p) Sn[p] = SpR[s][p];  // the next token's S_n
+                __syncthreads();
+                // rows 16 w .. 16 w + 15: q = sum_c M[row][c] by MFMA against ones
+                const int f0 = 16 * w;
+                mf::floatx4 acc = mf::zero4();
+#pragma unroll
+                for (int q = 0; q < NK; ++q) {
+                    acc = mf::mma(mf::frag_trc(l, sm.Mh[par], LDS, 32 * q, f0), ones, acc);
+                    acc = mf::mma(mf::frag_trc(l, sm.Ml[par], LDS, 32 * q, f0), ones, acc);
+                }
+                if (j16 == 0) {
+                    float gsum = 0.f;
+#pragma unroll
+                    for (int ww = 0; ww < NW; ++ww) gsum += sm.red[par][ww];
+                    const float glam2 = 2.f * gsum * sm.rcd[rs][1];
+                    bf16x4 ov;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int row = f0 + 4 * g4 + i;
+                        ov[i] = (bf16)fmaf(glam2, kf[row], acc[i] + sm.gkv[par][row]);
+                    }
+                    *reinterpret_cast<bf16x4*>(grad_k + base0 + t * tstride + f0 + 4 * g4) = ov;
+                }
+            };
+            for (long t = t1 - 1; t >= t0; t -= 2) {
+                rtoken(t, 0);
+                if (t - 1 >= t0) rtoken(t - 1, 1);
+            }
+        }
+    }
+    // dL/dS_0 in the reference's [row][c] layout
+    bf16* gs = grad_state + (long)bh * dd;
+#pragma unroll
+    for (int i = 0; i < RPL; ++i) gs[(long)(r0 + i) * D + col] = (bf16)G[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -543,9 +883,10 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
     if (head_dim > (size_t)MAXD || nbh > (size_t)INT32_MAX) return kInvalidConfiguration;
     const dim3 grid((unsigned)nbh);
     // the register-resident path: d = 64 / 128, k aligned for the coefficient
-    // kernel's 2d-byte row loads, at most 2^35 tokens (its grid)
+    // kernel's row loads and output for 8-byte row pieces, at most 2^35 tokens
     const bool fast = (head_dim == 128 || head_dim == 64) &&
-                      (uintptr_t)k % (head_dim / 8) == 0 && nbh * seq_len <= ((size_t)1 << 35);
+                      (uintptr_t)k % (head_dim / 8) == 0 && (uintptr_t)output % 8 == 0 &&
+                      nbh * seq_len <= ((size_t)1 << 35);
     if (fast) {
         // every token's coefficient first (the stream's workspace), then the
         // register-resident token loop
@@ -557,10 +898,12 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
         const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
         if (head_dim == 128)
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
-                        (float*)ws, (int)num_heads, (long)seq_len, beta, (long)ntok);
+                        (float*)ws, (float*)nullptr, (int)num_heads, (long)seq_len, beta,
+                        (long)ntok);
         else
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
-                        (float*)ws, (int)num_heads, (long)seq_len, beta, (long)ntok);
+                        (float*)ws, (float*)nullptr, (int)num_heads, (long)seq_len, beta,
+                        (long)ntok);
         if (head_dim == 128)
             EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<128, true, false>), grid,
                         dim3(rfast_threads<128>()), stream, (const bf16*)k, (const bf16*)v,
@@ -593,19 +936,67 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
     if (seq_len == 0) return fill_zero(grad_state, gsb, stream);
     if (!grad_output || !k || !v || !grad_k || !grad_v) return kInvalidValue;
     if (head_dim > (size_t)MAXD || nbh > (size_t)INT32_MAX) return kInvalidConfiguration;
+    // the register-resident path: d = 64 / 128, k aligned for the coefficient
+    // kernel's row loads and grad_k for 8-byte row pieces, at most 2^35 tokens
+    const bool fast = (head_dim == 128 || head_dim == 64) &&
+                      (uintptr_t)k % (head_dim / 8) == 0 && (uintptr_t)grad_k % 8 == 0 &&
+                      nbh * seq_len <= ((size_t)1 << 35);
+    if (fast) {
+        // workspace: checkpoints every SEGF tokens | one segment's states |
+        // c and dc/dlambda per token (all column-major states, bf16)
+        const size_t nsegf = (seq_len + SEGF - 1) / SEGF, ntok = nbh * seq_len;
+        size_t ck_elems, hist_elems;
+        if (!mul_ok(gse, nsegf, &ck_elems) || !mul_ok(gse, SEGF + 1, &hist_elems))
+            return kInvalidConfiguration;
+        const size_t off_hist = (ck_elems * 2 + 255) & ~(size_t)255;
+        const size_t off_c = (off_hist + hist_elems * 2 + 255) & ~(size_t)255;
+        const size_t off_dc = (off_c + ntok * 4 + 255) & ~(size_t)255;
+        const size_t need = off_dc + ntok * 4 + 256;
+        void* ws = nullptr;
+        WsLease lease;
+        int rc = workspace_acquire(need, stream, &ws, lease);
+        if (rc != kSuccess) return rc;
+        bf16* ck = (bf16*)ws;
+        bf16* hist = (bf16*)((char*)ws + off_hist);
+        float* coef = (float*)((char*)ws + off_c);
+        float* dcoef = (float*)((char*)ws + off_dc);
+        const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH)), grid((unsigned)nbh);
+        if (head_dim == 128) {
+            EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
+                        coef, dcoef, (int)num_heads, (long)seq_len, beta, (long)ntok);
+            EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<128, false, true>), grid,
+                        dim3(rfast_threads<128>()), stream, (const bf16*)k, (const bf16*)v,
+                        (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
+                        (long)seq_len);
+            EFLA_LAUNCH("efla_r_backward", r_bwd_fast_kernel<128>, grid,
+                        dim3(rfast_threads<128>()), stream, (const bf16*)grad_output,
+                        (const bf16*)k, (const bf16*)v, (const float*)coef, (const float*)dcoef,
+                        (const bf16*)ck, hist, (bf16*)grad_k, (bf16*)grad_v, (bf16*)grad_state,
+                        (int)num_heads, (long)seq_len);
+        } else {
+            EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
+                        coef, dcoef, (int)num_heads, (long)seq_len, beta, (long)ntok);
+            EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<64, false, true>), grid,
+                        dim3(rfast_threads<64>()), stream, (const bf16*)k, (const bf16*)v,
+                        (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
+                        (long)seq_len);
+            EFLA_LAUNCH("efla_r_backward", r_bwd_fast_kernel<64>, grid,
+                        dim3(rfast_threads<64>()), stream, (const bf16*)grad_output,
+                        (const bf16*)k, (const bf16*)v, (const float*)coef, (const float*)dcoef,
+                        (const bf16*)ck, hist, (bf16*)grad_k, (bf16*)grad_v, (bf16*)grad_state,
+                        (int)num_heads, (long)seq_len);
+        }
+        return (int)hipPeekAtLastError();
+    }
     const size_t nseg = (seq_len + SEG - 1) / SEG;
     size_t ck_elems, hist_elems, g_elems = 0;
     if (!mul_ok(gse, nseg, &ck_elems) || !mul_ok(gse, SEG + 1, &hist_elems))
         return kInvalidConfiguration;
     const bool gl = head_dim > 128;
     if (gl) g_elems = gse;
-    const bool fast = (head_dim == 128 || head_dim == 64) &&
-                      (uintptr_t)k % (head_dim / 8) == 0 && nbh * seq_len <= ((size_t)1 << 35);
-    const size_t ntok = fast ? nbh * seq_len : 0;  // per-token coefficients
     const size_t off_hist = (ck_elems * 2 + 255) & ~(size_t)255;
     const size_t off_g = (off_hist + hist_elems * 2 + 255) & ~(size_t)255;
-    const size_t off_c = (off_g + g_elems * 4 + 255) & ~(size_t)255;
-    const size_t need = off_c + ntok * 4 + 256;
+    const size_t need = off_g + g_elems * 4 + 256;
     void* ws = nullptr;
     WsLease lease;
     int rc = workspace_acquire(need, stream, &ws, lease);
@@ -613,30 +1004,9 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
     bf16* ck = (bf16*)ws;
     bf16* hist = (bf16*)((char*)ws + off_hist);
     float* G = gl ? (float*)((char*)ws + off_g) : nullptr;
-    // the state before every SEG-th token (the register-resident forward
-    // where d allows; it does not write `state`)
-    float* coef = (float*)((char*)ws + off_c);
-    const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
-    if (fast && head_dim == 128)
-        EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
-                    coef, (int)num_heads, (long)seq_len, beta, (long)ntok);
-    else if (fast)
-        EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
-                    coef, (int)num_heads, (long)seq_len, beta, (long)ntok);
-    if (fast && head_dim == 128)
-        EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<128, false, true>), dim3((unsigned)nbh),
-                    dim3(rfast_threads<128>()), stream, (const bf16*)k, (const bf16*)v,
-                    (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
-                    (long)seq_len);
-    else if (fast)
-        EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<64, false, true>), dim3((unsigned)nbh),
-                    dim3(rfast_threads<64>()), stream, (const bf16*)k, (const bf16*)v,
-                    (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
-                    (long)seq_len);
-    else
-        EFLA_LAUNCH("efla_r_checkpoint", r_checkpoint_kernel, dim3((unsigned)nbh), dim3(NTH),
-                    stream, (const bf16*)k, (const bf16*)v, (const bf16*)state, ck,
-                    (int)num_heads, (long)seq_len, (int)head_dim, beta);
+    EFLA_LAUNCH("efla_r_checkpoint", r_checkpoint_kernel, dim3((unsigned)nbh), dim3(NTH), stream,
+                (const bf16*)k, (const bf16*)v, (const bf16*)state, ck, (int)num_heads,
+                (long)seq_len, (int)head_dim, beta);
     if (gl) {
         EFLA_LAUNCH("efla_r_backward", r_backward_kernel<true>, dim3((unsigned)nbh), dim3(NTH),
                     stream, (const bf16*)grad_output, (const bf16*)k, (const bf16*)v, ck, hist,

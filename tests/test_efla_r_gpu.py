@@ -75,6 +75,67 @@ def test_backward_matches_reference(oracle, B, T, H, d):
     assert all(e <= 2e-2 for e in errs.values()), errs
 
 
+@pytest.mark.parametrize("B,T,H,d", [(1, 333, 2, 128), (2, 200, 2, 64)])
+def test_forward_backward_many_segments(oracle, B, T, H, d):
+    """d = 64 / 128 take the register-resident kernels, whose backward
+    rebuilds 32-token segments from checkpoints: T spans ten or more
+    segments and ends in a partial one."""
+    from ceo_amd.efla import efla_backward, efla_forward
+
+    announce(f"efla_forward_hip / efla_backward_hip B={B} T={T} H={H} d={d}")
+    k, v, do, s0 = _inputs(oracle, 800 + d, B, T, H, d, 0.2)
+    beta = 0.6
+    st_ref = s0.copy()
+    rc, o_ref = oracle.r_forward(k, v, st_ref, B, T, H, d, beta)
+    assert rc == 0
+    st = _u16_to_dev(s0)
+    o = efla_forward(_u16_to_dev(k), _u16_to_dev(v), st, beta)
+    rc, gk_ref, gv_ref, gs_ref = oracle.r_backward(do, k, v, s0, B, T, H, d, beta)
+    assert rc == 0
+    gk, gv, gs = efla_backward(_u16_to_dev(do), _u16_to_dev(k), _u16_to_dev(v),
+                               _u16_to_dev(s0), beta)
+    torch.cuda.synchronize()
+    errs = {n: rel_l2(oracle.bf16_to_f32(_dev_to_u16(a)), oracle.bf16_to_f32(r))
+            for n, a, r in (("o", o, o_ref), ("state", st, st_ref), ("grad_k", gk, gk_ref),
+                            ("grad_v", gv, gv_ref), ("grad_state", gs, gs_ref))}
+    print("  rel-L2:", {k: f"{e:.2e}" for k, e in errs.items()}, flush=True)
+    assert all(e <= 2e-2 for e in errs.values()), errs
+
+
+def test_misaligned_k_takes_the_generic_kernels(oracle):
+    """A k whose address is not 16-byte aligned (a view one element into a
+    buffer) runs the LDS-resident kernels; both paths match the oracle and
+    each other to the bf16 bound."""
+    from ceo_amd.efla import efla_backward, efla_forward
+
+    B, T, H, d = 1, 90, 2, 128
+    announce(f"efla_forward_hip / efla_backward_hip misaligned k B={B} T={T} H={H} d={d}")
+    k, v, do, s0 = _inputs(oracle, 900, B, T, H, d, 0.2)
+    beta = 0.7
+    kd = _u16_to_dev(k)
+    buf = torch.empty(kd.numel() + 1, dtype=torch.bfloat16, device="cuda")
+    km = buf[1:].view(B, T, H, d)
+    km.copy_(kd)
+    assert km.data_ptr() % 16 != 0
+    outs = []
+    for kk in (kd, km):
+        st = _u16_to_dev(s0)
+        o = efla_forward(kk, _u16_to_dev(v), st, beta)
+        grads = efla_backward(_u16_to_dev(do), kk, _u16_to_dev(v), _u16_to_dev(s0), beta)
+        outs.append((o, st) + grads)
+    torch.cuda.synchronize()
+    st_ref = s0.copy()
+    _, o_ref = oracle.r_forward(k, v, st_ref, B, T, H, d, beta)
+    _, gk_ref, gv_ref, gs_ref = oracle.r_backward(do, k, v, s0, B, T, H, d, beta)
+    refs = (o_ref, st_ref, gk_ref, gv_ref, gs_ref)
+    for path, res in zip(("aligned", "misaligned"), outs):
+        errs = [rel_l2(oracle.bf16_to_f32(_dev_to_u16(a)), oracle.bf16_to_f32(r))
+                for a, r in zip(res, refs)]
+        print(f"  {path}: rel-L2 o, state, grad_k, grad_v, grad_state =",
+              " ".join(f"{e:.2e}" for e in errs), flush=True)
+        assert max(errs) <= 2e-2
+
+
 def test_backward_zero_length_zeroes_grad_state(oracle):
     from ceo_amd._lib import lib
 
