@@ -92,7 +92,7 @@ _SIGS = {
     "layernorm_forward_stats_hip": (i32, [vp, vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     "layernorm_backward_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
     "layernorm_backward_residual_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
-    "layernorm_backward_ex_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, vp]),
+    "layernorm_backward_ex_hip": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, sz, i32, vp]),
     "rmsnorm_forward_hip": (i32, [vp, vp, vp, sz, sz, f32, vp]),
     "rmsnorm_backward_hip": (i32, [vp, vp, vp, vp, vp, sz, sz, f32, vp]),
     "shortconv_forward_hip": (i32, [vp, vp, vp, sz, sz, sz, sz, vp]),

@@ -267,13 +267,14 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
     }
 }
 
-// out[c] = sum_b part[b][c] for c < NS D (dw = out[0..D), db = out[D..2D), and
-// with NS = 3 the dx column sums out[2D..3D) as bf16 into dxs).
+// out[c] = sum_b part[b][c] for c < NS D (dw = out[0..D), db = out[D..2D),
+// fp32 or with pbf bf16, and with NS = 3 the dx column sums out[2D..3D) as
+// bf16 into dxs).
 // Workgroup: 16 row groups x 16 lanes of 4 columns (16-byte loads); grid over
 // 64-column blocks (NS D is a multiple of 4 when D is even; odd D reads scalars).
 __global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ part, int nblk,
-                                                     int D, int NS, float* __restrict__ dw,
-                                                     float* __restrict__ db,
+                                                     int D, int NS, void* __restrict__ dw,
+                                                     void* __restrict__ db, int pbf,
                                                      bf16* __restrict__ dxs) {
     __shared__ float acc[16][64 + 1];
     const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
@@ -312,9 +313,11 @@ __global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ p
 #pragma unroll
         for (int k = 0; k < 16; ++k) t += acc[k][threadIdx.x];
         if (c < D) {
-            if (dw) dw[c] = t;
+            if (dw && pbf) static_cast<bf16*>(dw)[c] = (bf16)t;
+            else if (dw) static_cast<float*>(dw)[c] = t;
         } else if (c < 2 * D) {
-            if (db) db[c - D] = t;
+            if (db && pbf) static_cast<bf16*>(db)[c - D] = (bf16)t;
+            else if (db) static_cast<float*>(db)[c - D] = t;
         } else if (c < W && dxs) {
             dxs[c - 2 * D] = (bf16)t;
         }
@@ -379,16 +382,17 @@ extern "C" int layernorm_forward_stats_hip(const void* input, const void* weight
 
 static int ln_backward(const void* grad_output, const void* input, const void* weight,
                        const float* mean, const float* rstd, const void* residual,
-                       void* grad_input, float* grad_weight, float* grad_bias,
+                       void* grad_input, void* grad_weight, void* grad_bias,
                        void* grad_input_colsum, size_t numel, size_t normalized_shape,
-                       hipStream_t stream) {
+                       bool pbf, hipStream_t stream) {
     const size_t D = normalized_shape;
     if (D == 0) return kInvalidValue;
     const size_t rows = numel / D;
     const bool params = grad_weight || grad_bias;
     if (rows == 0) {
-        if (grad_weight) EFLA_CHECK((hipError_t)fill_zero(grad_weight, D * 4, stream));
-        if (grad_bias) EFLA_CHECK((hipError_t)fill_zero(grad_bias, D * 4, stream));
+        const size_t pb = pbf ? 2 : 4;
+        if (grad_weight) EFLA_CHECK((hipError_t)fill_zero(grad_weight, D * pb, stream));
+        if (grad_bias) EFLA_CHECK((hipError_t)fill_zero(grad_bias, D * pb, stream));
         if (grad_input_colsum) EFLA_CHECK((hipError_t)fill_zero(grad_input_colsum, D * 2, stream));
         return kSuccess;
     }
@@ -438,7 +442,7 @@ static int ln_backward(const void* grad_output, const void* input, const void* w
     if (parts) {
         const unsigned gr = (unsigned)((ns * D + 63) / 64);
         EFLA_LAUNCH("layernorm_bwd_reduce", ln::reduce_kernel, dim3(gr), dim3(ln::NTH), stream,
-                    (const float*)part, (int)nblk, (int)D, ns, grad_weight, grad_bias,
+                    (const float*)part, (int)nblk, (int)D, ns, grad_weight, grad_bias, pbf ? 1 : 0,
                     ns == 3 ? (bf16*)grad_input_colsum : (bf16*)nullptr);
     }
     if (grad_input_colsum && ns == 2) {
@@ -457,7 +461,7 @@ extern "C" int layernorm_backward_hip(const void* grad_output, const void* input
                                       size_t numel, size_t normalized_shape,
                                       hipStream_t stream) {
     return ln_backward(grad_output, input, weight, mean, rstd, nullptr, grad_input, grad_weight,
-                       grad_bias, nullptr, numel, normalized_shape, stream);
+                       grad_bias, nullptr, numel, normalized_shape, false, stream);
 }
 
 extern "C" int layernorm_backward_residual_hip(const void* grad_output, const void* input,
@@ -468,15 +472,17 @@ extern "C" int layernorm_backward_residual_hip(const void* grad_output, const vo
                                                size_t normalized_shape, hipStream_t stream) {
     if (!residual && numel / (normalized_shape ? normalized_shape : 1) > 0) return kInvalidValue;
     return ln_backward(grad_output, input, weight, mean, rstd, residual, grad_input, grad_weight,
-                       grad_bias, nullptr, numel, normalized_shape, stream);
+                       grad_bias, nullptr, numel, normalized_shape, false, stream);
 }
 
 extern "C" int layernorm_backward_ex_hip(const void* grad_output, const void* input,
                                          const void* weight, const float* mean, const float* rstd,
                                          const void* residual, void* grad_input,
-                                         float* grad_weight, float* grad_bias,
+                                         void* grad_weight, void* grad_bias,
                                          void* grad_input_colsum, size_t numel,
-                                         size_t normalized_shape, hipStream_t stream) {
+                                         size_t normalized_shape, int param_grads_bf16,
+                                         hipStream_t stream) {
     return ln_backward(grad_output, input, weight, mean, rstd, residual, grad_input, grad_weight,
-                       grad_bias, grad_input_colsum, numel, normalized_shape, stream);
+                       grad_bias, grad_input_colsum, numel, normalized_shape,
+                       param_grads_bf16 != 0, stream);
 }

@@ -192,11 +192,11 @@ class EflaLM:
         # b_down's gradient is the column sum of the layer output's gradient, so each
         # LayerNorm backward that produces that gradient also sums its columns
         top = cfg.n_layers - 1
-        dx, dw, db = nn.layernorm_backward(
+        # parameter gradients straight into the bf16 gradient buffer
+        dx, _, _ = nn.layernorm_backward(
             daf, saved["x"], self.w("lnf.w"), saved["mf"], saved["rf"],
-            out_dx_colsum=self.gr(f"l{top}.b_down") if top >= 0 else None)
-        self.gr("lnf.w").copy_(dw)
-        self.gr("lnf.b").copy_(db)
+            out_dx_colsum=self.gr(f"l{top}.b_down") if top >= 0 else None,
+            out_dw=self.gr("lnf.w"), out_db=self.gr("lnf.b"))
         for i in reversed(range(cfg.n_layers)):
             L = f"l{i}."
             s = saved["layers"][i]
@@ -209,10 +209,9 @@ class EflaLM:
             da2, _, _ = nn.gemm_backward(du, s["a2"], self.w(L + "w_up"),
                                          out_b=self.gr(L + "w_up"))
             # dx1 = LN2's input gradient + the residual's dx, in one pass
-            dx1, dw, db = nn.layernorm_backward(da2, s["x1"], self.w(L + "ln2.w"), s["m2"],
-                                                s["r2"], residual=dx)
-            self.gr(L + "ln2.w").copy_(dw)
-            self.gr(L + "ln2.b").copy_(db)
+            dx1, _, _ = nn.layernorm_backward(da2, s["x1"], self.w(L + "ln2.w"), s["m2"],
+                                              s["r2"], residual=dx, out_dw=self.gr(L + "ln2.w"),
+                                              out_db=self.gr(L + "ln2.b"))
             # x1 = x + o w_o, o = EFLA(q, k, v, beta)
             do, _, _ = nn.gemm_backward(dx1, s["o"], self.w(L + "w_o"), out_b=self.gr(L + "w_o"))
             # dq, dk, dv are written in place into the fused projection's gradient
@@ -228,11 +227,10 @@ class EflaLM:
             nn.sigmoid_gate_backward(dbeta.view(N, H), s["beta"].view(N, H), dp[:, 3 * HD:])
             da, _, _ = nn.gemm_backward(dp, s["a"], self.w(L + "w_in"), out_b=self.gr(L + "w_in"))
             # dx = dx1 + LN1's input gradient
-            dx, dw, db = nn.layernorm_backward(
+            dx, _, _ = nn.layernorm_backward(
                 da, s["x"], self.w(L + "ln1.w"), s["m1"], s["r1"], residual=dx1,
-                out_dx_colsum=self.gr(f"l{i - 1}.b_down") if i > 0 else None)
-            self.gr(L + "ln1.w").copy_(dw)
-            self.gr(L + "ln1.b").copy_(db)
+                out_dx_colsum=self.gr(f"l{i - 1}.b_down") if i > 0 else None,
+                out_dw=self.gr(L + "ln1.w"), out_db=self.gr(L + "ln1.b"))
             saved["layers"][i] = None
         self.embed_grad.zero_()
         nn.embedding_backward(dx, saved["tokens"].reshape(-1), self.embed_grad)

@@ -38,9 +38,11 @@ def layernorm_forward(x: torch.Tensor, weight: torch.Tensor, bias=None, eps: flo
 
 
 def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True,
-                       residual=None, out_dx_colsum=None):
-    """(dx bf16, dweight fp32 or None, dbias fp32 or None); with ``residual``
-    (bf16, x's shape) dx is LayerNorm's input gradient plus it; with
+                       residual=None, out_dx_colsum=None, out_dw=None, out_db=None):
+    """(dx bf16, dweight, dbias); dweight / dbias are fp32 (None without
+    need_param_grads), or the given ``out_dw`` / ``out_db`` ((D,) bf16, written
+    in place, e.g. views of a bf16 gradient buffer).  With ``residual`` (bf16,
+    x's shape) dx is LayerNorm's input gradient plus it; with
     ``out_dx_colsum`` ((D,) bf16) dx's column sums are written there."""
     D = x.shape[-1]
     for t, n in ((dy, "dy"), (x, "x"), (weight, "weight")):
@@ -48,8 +50,18 @@ def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True,
     _require(mean, "mean", torch.float32, x.device)
     _require(rstd, "rstd", torch.float32, x.device)
     dx = torch.empty_like(x)
-    dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
-    db = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
+    pbf = out_dw is not None or out_db is not None
+    if pbf:
+        if out_dw is None or out_db is None or not need_param_grads:
+            raise ValueError("out_dw and out_db go together (and need need_param_grads)")
+        for t, n in ((out_dw, "out_dw"), (out_db, "out_db")):
+            _require(t, n, torch.bfloat16, x.device)
+            if t.numel() != D:
+                raise ValueError(f"{n} must hold normalized_shape values")
+        dw, db = out_dw, out_db
+    else:
+        dw = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
+        db = torch.empty(D, dtype=torch.float32, device=x.device) if need_param_grads else None
     if residual is not None:
         _require(residual, "residual", torch.bfloat16, x.device)
         if residual.shape != x.shape:
@@ -58,9 +70,11 @@ def layernorm_backward(dy, x, weight, mean, rstd, need_param_grads: bool = True,
         _require(out_dx_colsum, "out_dx_colsum", torch.bfloat16, x.device)
         if out_dx_colsum.numel() != D:
             raise ValueError("out_dx_colsum must hold normalized_shape values")
+    if out_dx_colsum is not None or pbf:
         rc = lib().layernorm_backward_ex_hip(_p(dy), _p(x), _p(weight), _p(mean), _p(rstd),
                                              _p(residual), _p(dx), _p(dw), _p(db),
-                                             _p(out_dx_colsum), x.numel(), D, _stream(x))
+                                             _p(out_dx_colsum), x.numel(), D, int(pbf),
+                                             _stream(x))
         check(rc, "layernorm_backward_ex_hip")
     elif residual is None:
         rc = lib().layernorm_backward_hip(_p(dy), _p(x), _p(weight), _p(mean), _p(rstd), _p(dx),

@@ -253,16 +253,18 @@ int layernorm_backward_residual_hip(const void* grad_output, const void* input,
 
 /* No reference counterpart: the general LayerNorm backward.  residual (added
  * to grad_input) may be NULL; grad_weight, grad_bias and grad_input_colsum
- * may each be NULL.  grad_input_colsum receives the column sums of
- * grad_input as written (bf16, normalized_shape values): the gradient of a
- * bias of the product whose output gradient grad_input is, summed in the
- * same row pass (D a multiple of 512 up to 2048, 16-byte aligned rows) or in
- * a pass of its own. */
+ * may each be NULL.  grad_weight / grad_bias are fp32, or bf16 when
+ * param_grads_bf16 is non-zero (written straight into a bf16 gradient
+ * buffer, the sums still taken in fp32).  grad_input_colsum receives the
+ * column sums of grad_input as written (bf16, normalized_shape values): the
+ * gradient of a bias of the product whose output gradient grad_input is,
+ * summed in the same row pass (D a multiple of 512 up to 2048, 16-byte
+ * aligned rows) or in a pass of its own. */
 int layernorm_backward_ex_hip(const void* grad_output, const void* input, const void* weight,
                               const float* mean, const float* rstd, const void* residual,
-                              void* grad_input, float* grad_weight, float* grad_bias,
+                              void* grad_input, void* grad_weight, void* grad_bias,
                               void* grad_input_colsum, size_t numel, size_t normalized_shape,
-                              hipStream_t stream);
+                              int param_grads_bf16, hipStream_t stream);
 
 /* ========================================================================
  * RMSNorm

@@ -200,10 +200,11 @@ def test_layernorm_validation(L):
     assert L.layernorm_forward_stats_hip(p, p, NULL, p, NULL, p, 2048, 1024, 1e-5, NULL) == 1
     # the _ex backward: D == 0 or a NULL operand -> 1; column sums past 8192 columns -> 9
     ex = L.layernorm_backward_ex_hip
-    assert ex(p, p, p, p, p, NULL, p, NULL, NULL, p, 1024, 0, NULL) == 1
-    assert ex(p, p, p, p, p, NULL, NULL, NULL, NULL, p, 2048, 1024, NULL) == 1
-    assert ex(p, NULL, p, p, p, NULL, p, NULL, NULL, p, 2048, 1024, NULL) == 1
-    assert ex(p, p, p, p, p, NULL, p, NULL, NULL, p, 32768, 16384, NULL) == 9
+    assert ex(p, p, p, p, p, NULL, p, NULL, NULL, p, 1024, 0, 0, NULL) == 1
+    assert ex(p, p, p, p, p, NULL, NULL, NULL, NULL, p, 2048, 1024, 0, NULL) == 1
+    assert ex(p, NULL, p, p, p, NULL, p, NULL, NULL, p, 2048, 1024, 1, NULL) == 1
+    assert ex(p, p, p, p, p, NULL, p, NULL, NULL, p, 32768, 16384, 0, NULL) == 9
+    assert ex(p, p, p, p, p, NULL, p, p, p, NULL, 32768, 16384, 1, NULL) == 9
 
 
 def test_rmsnorm_validation(L):

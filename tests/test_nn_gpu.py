@@ -235,6 +235,16 @@ def test_layernorm_backward_dx_colsum(rows, D):
         e = rel_l2(cs, ref.cpu().numpy())
         print(f"  residual={r is not None} rel-L2 colsum {e:.2e}", flush=True)
         assert e <= 1e-2 and torch.equal(cs, cs2)
+        # dw / db straight into bf16 buffers: the fp32 sums rounded once
+        bw = torch.zeros(D, dtype=torch.bfloat16, device="cuda")
+        bb = torch.zeros_like(bw)
+        dx3, _, _ = layernorm_backward(dy, x, w, mean, rstd, residual=r, out_dw=bw, out_db=bb)
+        torch.cuda.synchronize()
+        assert torch.equal(dx3, dx0)
+        if D % 512 == 0:
+            assert torch.equal(bw, dw0.to(torch.bfloat16)) and torch.equal(bb, db0.to(torch.bfloat16))
+        else:
+            assert rel_l2(bw, dw0.cpu().numpy()) <= 1e-2 and rel_l2(bb, db0.cpu().numpy()) <= 1e-2
 
 
 @pytest.fixture(params=[0, 1, 2], ids=["mfma", "generic", "hipblaslt"])
