@@ -175,13 +175,14 @@ __global__ void __launch_bounds__(NTH) r_coeff_kernel(const bf16* __restrict__ k
 //   o_row = sum_c S[row][c] k_c        the new state's columns go to LDS as
 //                                      [c][row] and 16x16x32 MFMAs contract
 //                                      them with k
-// One barrier per token.  Wave 0 stages token t+1's k (bf16) and c k (fp32,
-// c from r_coeff_kernel) in LDS during token t; k, c and v are loaded two
-// tokens ahead.  The o product of token t reads its fragments right after
-// token t's barrier and runs its MFMAs after token t+1's update, so the reads
-// overlap that work.  OUT writes o_t; CK stores the state before every
-// SEGF-th token to ck, column-major (the register-resident backward's
-// checkpoints).  The bf16 roundings and the
+// The updates need only the lane's own column, so tokens go in pairs: both
+// updates, both new states to LDS, one barrier, then both o products.  Wave 0
+// stages pair P+1's k (bf16) and c k (fp32, c from r_coeff_kernel) in LDS
+// during pair P; k, c and v are loaded two pairs ahead.  The o products of
+// pair P read their fragments right after P's barrier and run their MFMAs
+// after pair P+1's updates, so the reads overlap that work.  OUT writes o_t;
+// CK stores the state before every SEGF-th token to ck, column-major (the
+// register-resident backward's checkpoints).  The bf16 roundings and the
 // (c k) r product are the reference's; the sums run in another order (fp32
 // rounding level before each bf16 rounding).
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
@@ -212,9 +213,9 @@ __device__ __forceinline__ float wave_sum_q4(float x) {
 
 template <int D>
 struct RFastSmem {
-    bf16 Sl[2][D * (D + 8)];  // new state [c][row], double-buffered
-    float ckf[3][D];          // c k (fp32), ring of three tokens
-    bf16 kb[3][D];            // k (bf16)
+    bf16 Sl[4][D * (D + 8)];  // new states [c][row]: two tokens, double-buffered
+    float ckf[3][2][D];       // c k (fp32), ring of three token pairs
+    bf16 kb[3][2][D];         // k (bf16)
 };
 
 template <int D>
@@ -238,32 +239,45 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
     const long base0 = (long)b * T * tstride + (long)h * D;
     const float* cbh = coef + (long)bh * T;
     bf16* st = state + (long)bh * dd;
+    const long npair = (T + 1) / 2;
 
     bf16x2 Sp[NP];  // rows r0 + 2p (low half) and r0 + 2p + 1 (high half)
 #pragma unroll
     for (int p = 0; p < NP; ++p)
         Sp[p] = bf16x2{st[(long)(r0 + 2 * p) * D + col], st[(long)(r0 + 2 * p + 1) * D + col]};
 
-    // v_c per lane; k (D / 64 values per lane) and c in wave 0; two tokens ahead
+    // per token pair: v_c per lane; k (D / 64 values per lane) and c in wave
+    // 0; loaded two pairs ahead into slot (pair & 1)
     constexpr int KPL = D / 64;
-    bf16 vreg[2], kreg[2][KPL];
-    float creg[2];
-    auto load_v = [&](long tt, int slot) {
-        if (tt < T) vreg[slot] = v[base0 + tt * tstride + col];
-    };
-    auto load_k = [&](long tt, int slot) {
-        if (w == 0 && tt < T) {
+    bf16 vreg[2][2], kreg[2][2][KPL];
+    float creg[2][2];
+    auto load_v = [&](long P, int slot) {
 #pragma unroll
-            for (int e = 0; e < KPL; ++e) kreg[slot][e] = k[base0 + tt * tstride + KPL * l + e];
-            creg[slot] = cbh[tt];
-        }
+        for (int i = 0; i < 2; ++i)
+            if (2 * P + i < T) vreg[slot][i] = v[base0 + (2 * P + i) * tstride + col];
     };
-    auto stage_k = [&](int slot, int ring) {  // wave 0
+    auto load_k = [&](long P, int slot) {
+        if (w == 0)
 #pragma unroll
-        for (int e = 0; e < KPL; ++e) {
-            sm.ckf[ring][KPL * l + e] = creg[slot] * to_f(kreg[slot][e]);
-            sm.kb[ring][KPL * l + e] = kreg[slot][e];
-        }
+            for (int i = 0; i < 2; ++i) {
+                const long tt = 2 * P + i;
+                if (tt < T) {
+#pragma unroll
+                    for (int e = 0; e < KPL; ++e)
+                        kreg[slot][i][e] = k[base0 + tt * tstride + KPL * l + e];
+                    creg[slot][i] = cbh[tt];
+                }
+            }
+    };
+    auto stage_k = [&](int slot, long P) {  // wave 0: pair P into ring slot P % 3
+        const int ring = (int)(P % 3);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < KPL; ++e) {
+                sm.ckf[ring][i][KPL * l + e] = creg[slot][i] * to_f(kreg[slot][i][e]);
+                sm.kb[ring][i][KPL * l + e] = kreg[slot][i][e];
+            }
     };
     if (T > 0) {
         load_k(0, 0);
@@ -275,65 +289,67 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
     load_k(1, 1);
     load_k(2, 0);
 
-    // the o product of the last token whose fragments are in registers
+    // o products of the last pair, fragments in registers
     constexpr int MT = D / 16 / NW, NK = D / 32;
-    bf16x8 af[MT][NK], bk[NK];
-    long tp = -1;
+    bf16x8 af[2][MT][NK], bk[2][NK];
+    long pp = -1;
     const int g = l >> 4, j = l & 15;
-    auto o_reads = [&](long t) {
-        const bf16* kb = sm.kb[t % 3];
-        const bf16* slt = sm.Sl[t & 1];
+    auto o_reads = [&](long P) {
 #pragma unroll
-        for (int q = 0; q < NK; ++q) {
-            const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 4 * g);
-            const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 16 + 4 * g);
-            bk[q] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        for (int i = 0; i < 2; ++i) {
+            const bf16* kb = sm.kb[P % 3][i];
+            const bf16* slt = sm.Sl[2 * (P & 1) + i];
 #pragma unroll
-            for (int m = 0; m < MT; ++m) af[m][q] = mf::frag_trc(l, slt, LDS, 32 * q, 16 * (MT * w + m));
+            for (int q = 0; q < NK; ++q) {
+                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 4 * g);
+                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 16 + 4 * g);
+                bk[i][q] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    af[i][m][q] = mf::frag_trc(l, slt, LDS, 32 * q, 16 * (MT * w + m));
+            }
         }
-        tp = t;
+        pp = P;
     };
     // A = S[row][c] (c-order k over c), B = k broadcast over the 16 columns
     auto o_products = [&]() {
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            mf::floatx4 acc = mf::zero4();
+        for (int i = 0; i < 2; ++i) {
+            const long t = 2 * pp + i;
+            if (t >= T) break;
 #pragma unroll
-            for (int q = 0; q < NK; ++q) acc = mf::mma(af[m][q], bk[q], acc);
-            if (j == 0) {
-                bf16x4 ov;
+            for (int m = 0; m < MT; ++m) {
+                mf::floatx4 acc = mf::zero4();
 #pragma unroll
-                for (int i = 0; i < 4; ++i) ov[i] = (bf16)acc[i];
-                *reinterpret_cast<bf16x4*>(out + base0 + tp * tstride + 16 * (MT * w + m) + 4 * g) = ov;
+                for (int q = 0; q < NK; ++q) acc = mf::mma(af[i][m][q], bk[i][q], acc);
+                if (j == 0) {
+                    bf16x4 ov;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ov[e] = (bf16)acc[e];
+                    *reinterpret_cast<bf16x4*>(out + base0 + t * tstride + 16 * (MT * w + m) + 4 * g) = ov;
+                }
             }
         }
     };
-
-    // token t: its v in vreg[vs]; token t+1's k and c in kreg[ks], creg[ks]
-    auto token = [&](long t, int vs, int ks) {
+    // one token's update: its k, c k in ring slot `ring`, token i of the pair
+    auto update = [&](long t, int ring, int i, float vt, bf16* sl) {
         if (CK && t % SEGF == 0) {  // column-major [c][row]
             bf16* dst = ck + ((long)bh * nsegf + t / SEGF) * dd + (long)col * D + r0;
 #pragma unroll
-            for (int i = 0; i < NP / 4; ++i)
-                *reinterpret_cast<bf16x8*>(dst + 8 * i) =
-                    bf16x8{Sp[4 * i][0], Sp[4 * i][1], Sp[4 * i + 1][0], Sp[4 * i + 1][1],
-                           Sp[4 * i + 2][0], Sp[4 * i + 2][1], Sp[4 * i + 3][0], Sp[4 * i + 3][1]};
+            for (int q = 0; q < NP / 4; ++q)
+                *reinterpret_cast<bf16x8*>(dst + 8 * q) =
+                    bf16x8{Sp[4 * q][0], Sp[4 * q][1], Sp[4 * q + 1][0], Sp[4 * q + 1][1],
+                           Sp[4 * q + 2][0], Sp[4 * q + 2][1], Sp[4 * q + 3][0], Sp[4 * q + 3][1]};
         }
-        const int kslot = (int)(t % 3);
-        // token t+1's k into the ring (read after this token's barrier)
-        if (w == 0 && t + 1 < T) stage_k(ks, (int)((t + 1) % 3));
-        load_k(t + 3, ks);
-        const float vt = to_f(vreg[vs]);
-        load_v(t + 2, vs);
         // this lane's rows of k (bf16 pairs) and c k, all reads issued first
         bf16x8 kq[NP / 4];
         mf::floatx4 cq[RPL / 4];
 #pragma unroll
-        for (int i = 0; i < NP / 4; ++i)
-            kq[i] = *reinterpret_cast<const bf16x8*>(sm.kb[kslot] + r0 + 8 * i);
+        for (int q = 0; q < NP / 4; ++q)
+            kq[q] = *reinterpret_cast<const bf16x8*>(sm.kb[ring][i] + r0 + 8 * q);
 #pragma unroll
-        for (int i = 0; i < RPL / 4; ++i)
-            cq[i] = *reinterpret_cast<const mf::floatx4*>(sm.ckf[kslot] + r0 + 4 * i);
+        for (int q = 0; q < RPL / 4; ++q)
+            cq[q] = *reinterpret_cast<const mf::floatx4*>(sm.ckf[ring][i] + r0 + 4 * q);
         // u = S^T k for this column (four partial sums, then the lanes of the column)
         float ua[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -344,7 +360,6 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
         const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
         const float rc = vt - u;
         // S <- bf16(S + (c k) r); the new column piece as bf16 into LDS
-        bf16* sl = sm.Sl[t & 1] + col * LDS + r0;
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             const float lo = fmaf(cq[p / 2][2 * (p % 2)], rc, (float)Sp[p][0]);
@@ -353,20 +368,31 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
         }
         if (OUT) {
 #pragma unroll
-            for (int i = 0; i < NP / 4; ++i)
-                *reinterpret_cast<bf16x8*>(sl + 8 * i) =
-                    bf16x8{Sp[4 * i][0], Sp[4 * i][1], Sp[4 * i + 1][0], Sp[4 * i + 1][1],
-                           Sp[4 * i + 2][0], Sp[4 * i + 2][1], Sp[4 * i + 3][0], Sp[4 * i + 3][1]};
-            if (tp >= 0) o_products();  // the previous token's o
+            for (int q = 0; q < NP / 4; ++q)
+                *reinterpret_cast<bf16x8*>(sl + 8 * q) =
+                    bf16x8{Sp[4 * q][0], Sp[4 * q][1], Sp[4 * q + 1][0], Sp[4 * q + 1][1],
+                           Sp[4 * q + 2][0], Sp[4 * q + 2][1], Sp[4 * q + 3][0], Sp[4 * q + 3][1]};
         }
-        __syncthreads();  // the new state in LDS; token t+1's k staged
-        if (OUT) o_reads(t);
     };
-    for (long t = 0; t < T; t += 2) {
-        token(t, 0, 1);
-        if (t + 1 < T) token(t + 1, 1, 0);
+    // pair P: its v in vreg[s], pair P+1's k and c in kreg[s ^ 1]
+    auto pair = [&](long P, int s) {
+        const int ring = (int)(P % 3);
+        // pair P+1's k into the ring (read after this pair's barrier)
+        if (w == 0 && P + 1 < npair) stage_k(s ^ 1, P + 1);
+        load_k(P + 3, s ^ 1);
+        const float v0 = to_f(vreg[s][0]), v1 = to_f(vreg[s][1]);
+        load_v(P + 2, s);
+        update(2 * P, ring, 0, v0, sm.Sl[2 * (P & 1)] + col * LDS + r0);
+        if (2 * P + 1 < T) update(2 * P + 1, ring, 1, v1, sm.Sl[2 * (P & 1) + 1] + col * LDS + r0);
+        if (OUT && pp >= 0) o_products();  // the previous pair's o
+        __syncthreads();  // the new states in LDS; pair P+1's k staged
+        if (OUT) o_reads(P);
+    };
+    for (long P = 0; P < npair; P += 2) {
+        pair(P, 0);
+        if (P + 1 < npair) pair(P + 1, 1);
     }
-    if (OUT && tp >= 0) o_products();
+    if (OUT && pp >= 0) o_products();
     // the forward hands the final state back; the checkpoint pass leaves the
     // caller's initial state alone
     if constexpr (!CK)

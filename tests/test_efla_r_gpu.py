@@ -36,7 +36,8 @@ def _inputs(oracle, seed, B, T, H, d, s0_scale):
 
 
 @pytest.mark.parametrize("B,T,H,d", [(2, 100, 2, 64), (1, 130, 3, 128), (1, 40, 1, 256),
-                                     (2, 1, 2, 32), (1, 70, 2, 96)])
+                                     (2, 1, 2, 32), (1, 70, 2, 96), (1, 1, 2, 128),
+                                     (2, 3, 1, 64)])
 def test_forward_matches_reference(oracle, B, T, H, d):
     from ceo_amd.efla import efla_forward
 
@@ -56,7 +57,7 @@ def test_forward_matches_reference(oracle, B, T, H, d):
 
 
 @pytest.mark.parametrize("B,T,H,d", [(2, 100, 2, 64), (1, 150, 2, 128), (1, 70, 1, 256),
-                                     (1, 64, 2, 48)])
+                                     (1, 64, 2, 48), (1, 1, 2, 128), (2, 33, 1, 64)])
 def test_backward_matches_reference(oracle, B, T, H, d):
     from ceo_amd.efla import efla_backward
 
