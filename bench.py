@@ -540,6 +540,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-recompute", action="store_true",
                     help="skip the pass timing the recompute variant")
+    ap.add_argument("--no-ref-abi", action="store_true",
+                    help="skip timing the reference ABI's efla_forward_hip / efla_backward_hip "
+                         "(cfg3 only)")
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU-baseline work (whole sequences, at least one)")
     ap.add_argument("--seed", type=int, default=0xEF1A0002)
@@ -650,6 +653,35 @@ def main() -> int:
         print(f"[bench] recompute variant: median {recompute:.4f} ms/step", file=sys.stderr,
               flush=True)
 
+    ref_abi = None
+    if args.config == "cfg3" and not args.no_ref_abi:
+        # the reference ABI's own entries on the same k, v, dO: the token-by-token
+        # recurrence with the bf16 state re-rounded every token (efla.cu:154-233,
+        # 315-454; no chunked form reproduces it), scalar beta, zero initial state
+        s0 = torch.zeros(B * H, K, K, dtype=torch.bfloat16, device=dev)
+        st = s0.clone()
+
+        def fwd_r():
+            efla.efla_forward(x["k"], x["v"], st.copy_(s0), 0.5, C)
+
+        def bwd_r():
+            efla.efla_backward(x["do"], x["k"], x["v"], s0, 0.5)
+
+        fwd_r()
+        bwd_r()
+        per_f, _ = timed(fwd_r, 3)
+        per_b, _ = timed(bwd_r, 3)
+        mf_, mb_ = median(per_f), median(per_b)
+        ref_abi = {
+            "what": "efla_forward_hip / efla_backward_hip (the reference's token-serial "
+                    "recurrence, state re-rounded to bf16 per token), median of 3 calls",
+            "forward_ms": round(mf_, 3), "backward_ms": round(mb_, 3),
+            "forward_tokens_per_s": round(ntok / (mf_ * 1e-3), 1),
+            "backward_tokens_per_s": round(ntok / (mb_ * 1e-3), 1),
+        }
+        print(f"[bench] reference ABI: forward {mf_:.3f} ms, backward {mb_:.3f} ms",
+              file=sys.stderr, flush=True)
+
     # FLOPs / bytes
     if cu is not None:
         lens = (cu[1:] - cu[:-1]).tolist()
@@ -736,6 +768,7 @@ def main() -> int:
         "step_io_gbs": round(io / (ms_step * 1e-3) / 1e9, 1),
         "roofline": roof,
         "recompute": recompute,
+        "reference_abi": ref_abi,
         "kernels": kernels,
         "cpu_baseline": cpu,
         "device": {"arch": info["arch"], "cus": info["compute_units"],
