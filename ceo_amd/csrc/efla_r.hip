@@ -426,7 +426,6 @@ struct RBwdSmem {
     bf16 fkb[3][D];           // rebuild ring: k (bf16)
     float fck[3][D];          //   c k (fp32)
     bf16 rkb[3][D], rgb[3][D];    // reverse ring: k, dO (bf16)
-    float rkf[3][D], rgf[3][D];   //   k, dO (fp32)
     float rcd[3][4];              //   c, dc/dlambda
     float gkv[2][D];              // S_n^T dO per column
     float red[2][16];             // grad_c partials per wave
@@ -569,8 +568,6 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
                 for (int e = 0; e < KPL; ++e) {
                     sm.rkb[ring][KPL * l + e] = kd[slot][e];
                     sm.rgb[ring][KPL * l + e] = gd[slot][e];
-                    sm.rkf[ring][KPL * l + e] = to_f(kd[slot][e]);
-                    sm.rgf[ring][KPL * l + e] = to_f(gd[slot][e]);
                 }
                 if (l == 0) {
                     sm.rcd[ring][0] = cd[slot];
@@ -601,66 +598,56 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
                 load_lane(t - 1, s ^ 1);
                 const bf16* kb = sm.rkb[rs];
                 const bf16* gb = sm.rgb[rs];
-                const float* kf = sm.rkf[rs];
-                const float* gf = sm.rgf[rs];
                 const float c = sm.rcd[rs][0];
-                const float kc = kf[col];
+                const float kc = (float)kb[col];
                 const float vt = to_f(vR[s]);
+                // this lane's rows of k and dO (bf16), read once for both passes;
+                // each pass widens them to fp32 where it needs them
+                bf16x8 kq[RPL / 8], gq[RPL / 8];
+#pragma unroll
+                for (int i8 = 0; i8 < RPL / 8; ++i8) {
+                    kq[i8] = *reinterpret_cast<const bf16x8*>(kb + r0 + 8 * i8);
+                    gq[i8] = *reinterpret_cast<const bf16x8*>(gb + r0 + 8 * i8);
+                }
                 // pass 1, column sums: u = S^T k, gk = S_n^T dO (bf16 pairs),
-                // sw = g^T k with g = G + dO k_c (fp32); eight rows at a time
+                // sw = g^T k with g = G + dO k_c (fp32)
                 float ua[2] = {0.f, 0.f}, ga[2] = {0.f, 0.f}, sa[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int i8 = 0; i8 < RPL / 8; ++i8) {
-                    const bf16x8 kq = *reinterpret_cast<const bf16x8*>(kb + r0 + 8 * i8);
-                    const bf16x8 gq = *reinterpret_cast<const bf16x8*>(gb + r0 + 8 * i8);
-                    const mf::floatx4 k0 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8);
-                    const mf::floatx4 k1 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8 + 4);
-                    const mf::floatx4 o0 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8);
-                    const mf::floatx4 o1 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8 + 4);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const int p = 4 * i8 + e;
-                        ua[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{kq[2 * e], kq[2 * e + 1]},
-                                                                    SpR[s][p], ua[e & 1], false);
-                        ga[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{gq[2 * e], gq[2 * e + 1]},
-                                                                    Sn[p], ga[e & 1], false);
+                        ua[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(
+                            bf16x2{kq[i8][2 * e], kq[i8][2 * e + 1]}, SpR[s][p], ua[e & 1], false);
+                        ga[e & 1] = __builtin_amdgcn_fdot2_f32_bf16(
+                            bf16x2{gq[i8][2 * e], gq[i8][2 * e + 1]}, Sn[p], ga[e & 1], false);
                     }
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float go = e < 4 ? o0[e] : o1[e - 4];
-                        const float kr = e < 4 ? k0[e] : k1[e - 4];
-                        const float gv = fmaf(go, kc, G[8 * i8 + e]);
-                        sa[e & 3] = fmaf(gv, kr, sa[e & 3]);
+                        const float gv = fmaf((float)gq[i8][e], kc, G[8 * i8 + e]);
+                        sa[e & 3] = fmaf(gv, (float)kq[i8][e], sa[e & 3]);
                     }
                 }
                 const float u = quad_sum<LPC>(ua[0] + ua[1]);
                 const float gk = quad_sum<LPC>(ga[0] + ga[1]);
                 const float sw = quad_sum<LPC>((sa[0] + sa[1]) + (sa[2] + sa[3]));
                 const float w2 = vt - u, w1 = c * sw, cw2 = c * w2;
-                // pass 2 (k, dO read again, g recomputed as in pass 1): the
-                // row sum's summands c g w2 - S w1 (bf16 high + low parts);
-                // G <- g - k w1^T
-                asm volatile("" ::: "memory");
+                // pass 2 (g recomputed as in pass 1): the row sum's summands
+                // c g w2 - S w1 (bf16 high + low parts); G <- g - k w1^T
                 bf16* mh = sm.Mh[par] + col * LDS + r0;
                 bf16* ml = sm.Ml[par] + col * LDS + r0;
 #pragma unroll
                 for (int i8 = 0; i8 < RPL / 8; ++i8) {
-                    const mf::floatx4 k0 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8);
-                    const mf::floatx4 k1 = *reinterpret_cast<const mf::floatx4*>(kf + r0 + 8 * i8 + 4);
-                    const mf::floatx4 o0 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8);
-                    const mf::floatx4 o1 = *reinterpret_cast<const mf::floatx4*>(gf + r0 + 8 * i8 + 4);
                     bf16x8 hv, lv;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int ii = 8 * i8 + e;
-                        const float go = e < 4 ? o0[e] : o1[e - 4];
-                        const float kr = e < 4 ? k0[e] : k1[e - 4];
-                        const float gv = fmaf(go, kc, G[ii]);
+                        const float gv = fmaf((float)gq[i8][e], kc, G[ii]);
                         const float sp = (float)SpR[s][ii / 2][ii % 2];
                         const float m = fmaf(gv, cw2, -(sp * w1));
                         hv[e] = (bf16)m;
                         lv[e] = (bf16)(m - (float)hv[e]);
-                        G[ii] = fmaf(-kr, w1, gv);
+                        G[ii] = fmaf(-(float)kq[i8][e], w1, gv);
                     }
                     *reinterpret_cast<bf16x8*>(mh + 8 * i8) = hv;
                     *reinterpret_cast<bf16x8*>(ml + 8 * i8) = lv;
@@ -692,7 +679,7 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int row = f0 + 4 * g4 + i;
-                        ov[i] = (bf16)fmaf(glam2, kf[row], acc[i] + sm.gkv[par][row]);
+                        ov[i] = (bf16)fmaf(glam2, (float)kb[row], acc[i] + sm.gkv[par][row]);
                     }
                     *reinterpret_cast<bf16x4*>(grad_k + base0 + t * tstride + f0 + 4 * g4) = ov;
                 }
