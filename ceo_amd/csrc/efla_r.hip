@@ -195,11 +195,12 @@ __device__ __forceinline__ float dpp_f(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL,
                                                                0xF, 0xF, true));
 }
-// sum over the L (1, 2 or 4) consecutive lanes of a quad group, in every lane
+// sum over the L (1, 2, 4 or 8) consecutive lanes of an aligned group, in every lane
 template <int L>
 __device__ __forceinline__ float quad_sum(float x) {
-    if constexpr (L >= 2) x += dpp_f<0xB1>(x);  // quad_perm [1, 0, 3, 2]
-    if constexpr (L >= 4) x += dpp_f<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+    if constexpr (L >= 2) x += dpp_f<0xB1>(x);   // quad_perm [1, 0, 3, 2]
+    if constexpr (L >= 4) x += dpp_f<0x4E>(x);   // quad_perm [2, 3, 0, 1]
+    if constexpr (L >= 8) x += dpp_f<0x141>(x);  // row_half_mirror: lane 7 - i of its 8
     return x;
 }
 // sum over the wave of the values in lanes 4i (other lanes hold 0), in every lane
@@ -211,29 +212,41 @@ __device__ __forceinline__ float wave_sum_q4(float x) {
     return x;
 }
 
-template <int D>
+// Column split: the state's value columns evolve independently (the update
+// and S^T k touch only their own column), so one (b, h) may be spread over NS
+// workgroups of D / NS columns each, LPC lanes per column.  Only the row sums
+// (o, and the backward's grad_k) span columns: with NS > 1 each workgroup
+// writes its part in fp32 to `part` (NS slices of `pstride` elements, the
+// output's layout) and r_combine_kernel adds the slices and rounds once.
+// NS = 1, LPC = 4 is one workgroup per (b, h); NS = 2, LPC = 8 gives a grid of
+// 2 B H with half the rows per lane (for B H below the CU count).
+template <int D, int NS>
 struct RFastSmem {
-    bf16 Sl[4][D * (D + 8)];  // new states [c][row]: two tokens, double-buffered
-    float ckf[3][2][D];       // c k (fp32), ring of three token pairs
-    bf16 kb[3][2][D];         // k (bf16)
+    bf16 Sl[4][(D / NS) * (D + 8)];  // new states [c][row]: two tokens, double-buffered
+    float ckf[3][2][D];              // c k (fp32), ring of three token pairs
+    bf16 kb[3][2][D];                // k (bf16)
 };
 
-template <int D>
+template <int D, int NS, int LPC>
 constexpr int rfast_threads() {
-    return D == 128 ? 512 : 256;
+    return D / NS * LPC;
 }
 
-template <int D, bool OUT, bool CK>
-__global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
+template <int D, int NS, int LPC, bool OUT, bool CK>
+__global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
-    bf16* __restrict__ state, bf16* __restrict__ out, bf16* __restrict__ ck, int H, long T) {
-    constexpr int NT = rfast_threads<D>(), NW = NT / 64;
-    constexpr int LPC = NT / D, RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
-    static_assert(RPL % 8 == 0 && (D == 64 || D == 128), "d = 64 or 128");
-    __shared__ __attribute__((aligned(16))) RFastSmem<D> sm;
+    bf16* __restrict__ state, bf16* __restrict__ out, float* __restrict__ part_out, long pstride,
+    bf16* __restrict__ ck, int H, long T) {
+    constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
+    constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
+    static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
+                      NT <= 1024 && D % (16 * NW) == 0,
+                  "d = 64 or 128, 32-column multiples per workgroup");
+    __shared__ __attribute__((aligned(16))) RFastSmem<D, NS> sm;
     const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
-    const int col = tid / LPC, part = tid % LPC, r0 = part * RPL;
-    const int bh = blockIdx.x, b = bh / H, h = bh % H;
+    const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
+    const int col = cb * NC + tid / LPC, lcol = tid / LPC, part = tid % LPC, r0 = part * RPL;
+    const int b = bh / H, h = bh % H;
     const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
     const long tstride = (long)H * D;  // elements between tokens
     const long base0 = (long)b * T * tstride + (long)h * D;
@@ -290,7 +303,7 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
     load_k(2, 0);
 
     // o products of the last pair, fragments in registers
-    constexpr int MT = D / 16 / NW, NK = D / 32;
+    constexpr int MT = D / 16 / NW, NK = NC / 32;
     bf16x8 af[2][MT][NK], bk[2][NK];
     long pp = -1;
     const int g = l >> 4, j = l & 15;
@@ -301,8 +314,8 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
             const bf16* slt = sm.Sl[2 * (P & 1) + i];
 #pragma unroll
             for (int q = 0; q < NK; ++q) {
-                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 4 * g);
-                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kb + 32 * q + 16 + 4 * g);
+                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kb + cb * NC + 32 * q + 4 * g);
+                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kb + cb * NC + 32 * q + 16 + 4 * g);
                 bk[i][q] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
                 for (int m = 0; m < MT; ++m)
@@ -323,10 +336,15 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
 #pragma unroll
                 for (int q = 0; q < NK; ++q) acc = mf::mma(af[i][m][q], bk[i][q], acc);
                 if (j == 0) {
-                    bf16x4 ov;
+                    const long o = base0 + t * tstride + 16 * (MT * w + m) + 4 * g;
+                    if constexpr (NS == 1) {
+                        bf16x4 ov;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) ov[e] = (bf16)acc[e];
-                    *reinterpret_cast<bf16x4*>(out + base0 + t * tstride + 16 * (MT * w + m) + 4 * g) = ov;
+                        for (int e = 0; e < 4; ++e) ov[e] = (bf16)acc[e];
+                        *reinterpret_cast<bf16x4*>(out + o) = ov;
+                    } else {
+                        *reinterpret_cast<mf::floatx4*>(part_out + cb * pstride + o) = acc;
+                    }
                 }
             }
         }
@@ -382,8 +400,8 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
         load_k(P + 3, s ^ 1);
         const float v0 = to_f(vreg[s][0]), v1 = to_f(vreg[s][1]);
         load_v(P + 2, s);
-        update(2 * P, ring, 0, v0, sm.Sl[2 * (P & 1)] + col * LDS + r0);
-        if (2 * P + 1 < T) update(2 * P + 1, ring, 1, v1, sm.Sl[2 * (P & 1) + 1] + col * LDS + r0);
+        update(2 * P, ring, 0, v0, sm.Sl[2 * (P & 1)] + lcol * LDS + r0);
+        if (2 * P + 1 < T) update(2 * P + 1, ring, 1, v1, sm.Sl[2 * (P & 1) + 1] + lcol * LDS + r0);
         if (OUT && pp >= 0) o_products();  // the previous pair's o
         __syncthreads();  // the new states in LDS; pair P+1's k staged
         if (OUT) o_reads(P);
@@ -415,37 +433,48 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_fast_kernel(
 // where S / S_n are the states before / after the token.  Column sums are
 // lane-local (plus the lanes of the column); the row sum goes through LDS as
 // bf16 high and low parts of each fp32 summand (about 16 bits kept) and
-// 16x16x32 MFMAs against ones.  One barrier per token.
-// Segments of SEGF tokens are taken last to first: each is rebuilt from its
-// checkpoint (ck, column-major) with the forward step, every state stored
-// column-major to the workspace (hist), which the same lanes read back.
-template <int D>
+// 16x16x32 MFMAs against ones.
+// Segments of SEGF tokens are taken last to first.  A segment's k, dO, c and
+// dc/dlambda (and c k in fp32 where LDS allows) are staged in LDS by the whole
+// workgroup at once; the segment is then rebuilt from its checkpoint (ck,
+// column-major) with the forward step without barriers (each lane's column
+// needs only its own rows), every state stored column-major to the workspace
+// (hist), which the same lanes read back in the reverse pass (one barrier per
+// token, for the row sum).
+template <int D, int NS>
 struct RBwdSmem {
-    bf16 Mh[2][D * (D + 8)];  // the row sum's summands [c][row], high bf16 part
-    bf16 Ml[2][D * (D + 8)];  // low part
-    bf16 fkb[3][D];           // rebuild ring: k (bf16)
-    float fck[3][D];          //   c k (fp32)
-    bf16 rkb[3][D], rgb[3][D];    // reverse ring: k, dO (bf16)
-    float rcd[3][4];              //   c, dc/dlambda
-    float gkv[2][D];              // S_n^T dO per column
-    float red[2][16];             // grad_c partials per wave
+    static constexpr bool CKS = NS > 1;  // c k staged (fp32); else formed per row
+    bf16 Mh[2][(D / NS) * (D + 8)];      // the row sum's summands [c][row], high bf16 part
+    bf16 Ml[2][(D / NS) * (D + 8)];      // low part
+    bf16 kb[SEGF][D];                    // the segment's k
+    bf16 gb[SEGF][D];                    //   dO
+    float ckf[CKS ? SEGF : 1][D];        //   c k
+    float cc[SEGF], dcc[SEGF];           //   c, dc/dlambda
+    float gkv[2][D / NS];                // S_n^T dO per column
+    float red[2][16];                    // grad_c partials per wave
 };
 
-template <int D>
-__global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
+template <int D, int NS, int LPC>
+__global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kernel(
     const bf16* __restrict__ dO, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ coef, const float* __restrict__ dcoef, const bf16* __restrict__ ck,
-    bf16* __restrict__ hist_all, bf16* __restrict__ grad_k, bf16* __restrict__ grad_v,
-    bf16* __restrict__ grad_state, int H, long T) {
-    constexpr int NT = rfast_threads<D>(), NW = NT / 64;
-    constexpr int LPC = NT / D, RPL = D / LPC, NP = RPL / 2, LDS = D + 8, KPL = D / 64;
-    constexpr int MT = D / 16 / NW, NK = D / 32;
-    static_assert(RPL % 8 == 0 && MT == 1 && LPC == 4, "d = 64 or 128");
-    __shared__ __attribute__((aligned(16))) RBwdSmem<D> sm;
+    bf16* __restrict__ hist_all, bf16* __restrict__ grad_k, float* __restrict__ part_gk,
+    long pstride, bf16* __restrict__ grad_v, bf16* __restrict__ grad_state, int H, long T) {
+    constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
+    constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
+    constexpr int MT = D / 16 / NW, NK = NC / 32;
+    constexpr int VW = D / 16;  // staging vector: 16 bytes (d = 128) or 8 (d = 64, k 8-byte aligned)
+    constexpr bool CKS = RBwdSmem<D, NS>::CKS;
+    static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
+                      NT <= 1024 && D % (16 * NW) == 0 && LPC % 4 == 0 && NW <= 16,
+                  "d = 64 or 128, 32-column multiples per workgroup, 4 or 8 lanes per column");
+    typedef __attribute__((__vector_size__(VW * sizeof(__bf16)))) __bf16 bfV;
+    __shared__ __attribute__((aligned(16))) RBwdSmem<D, NS> sm;
     const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
-    const int col = tid / LPC, part = tid % LPC, r0 = part * RPL;
+    const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
+    const int col = cb * NC + tid / LPC, lcol = tid / LPC, part = tid % LPC, r0 = part * RPL;
     const int g4 = l >> 4, j16 = l & 15;
-    const int bh = blockIdx.x, b = bh / H, h = bh % H;
+    const int b = bh / H, h = bh % H;
     const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
     const long tstride = (long)H * D;
     const long base0 = (long)b * T * tstride + (long)h * D;
@@ -478,131 +507,94 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
 
     for (long seg = nsegf - 1; seg >= 0; --seg) {
         const long t0 = seg * SEGF, t1 = t0 + SEGF < T ? t0 + SEGF : T;
+        const int n = (int)(t1 - t0);
+        // ---- the segment's k, dO, c, dc (and c k) into LDS; the previous
+        // segment's last readers are done (barrier at the end of its reverse)
+        for (int i = tid; i < SEGF * D / VW; i += NT) {
+            const int j = i / (D / VW), e0 = (i % (D / VW)) * VW;
+            if (j < n) {
+                const long o = base0 + (t0 + j) * tstride + e0;
+                const bfV kx = *reinterpret_cast<const bfV*>(k + o);
+                *reinterpret_cast<bfV*>(&sm.kb[j][e0]) = kx;
+                *reinterpret_cast<bfV*>(&sm.gb[j][e0]) = *reinterpret_cast<const bfV*>(dO + o);
+                if constexpr (CKS) {
+                    const float cj = cbh[t0 + j];
+#pragma unroll
+                    for (int e = 0; e < VW; ++e) sm.ckf[j][e0 + e] = cj * (float)kx[e];
+                }
+            }
+        }
+        if (tid < n) {
+            sm.cc[tid] = cbh[t0 + tid];
+            sm.dcc[tid] = dcbh[t0 + tid];
+        }
         // ---- rebuild: hist[jj] = the state before token t0 + jj
         bf16x2 S[NP];
         load_col(ck + ((long)bh * nsegf + seg) * dd + (long)col * D + r0, S);
         store_col(col_ptr(hist, 0), S);
-        {
-            bf16 vreg[2], kreg[2][KPL];
-            float creg[2];
-            auto load_v = [&](long tt, int slot) {
-                if (tt < t1) vreg[slot] = v[base0 + tt * tstride + col];
-            };
-            auto load_k = [&](long tt, int slot) {
-                if (w == 0 && tt < t1) {
+        bf16 vreg[2];
+        vreg[0] = v[base0 + t0 * tstride + col];
+        if (n > 1) vreg[1] = v[base0 + (t0 + 1) * tstride + col];
+        __syncthreads();
+        for (int j = 0; j < n; ++j) {
+            const float vt = to_f(vreg[j & 1]);
+            if (j + 2 < n) vreg[j & 1] = v[base0 + (t0 + j + 2) * tstride + col];
+            bf16x8 kq[NP / 4];
 #pragma unroll
-                    for (int e = 0; e < KPL; ++e) kreg[slot][e] = k[base0 + tt * tstride + KPL * l + e];
-                    creg[slot] = cbh[tt];
+            for (int i = 0; i < NP / 4; ++i)
+                kq[i] = *reinterpret_cast<const bf16x8*>(&sm.kb[j][r0 + 8 * i]);
+            float ckr[RPL];
+            if constexpr (CKS) {
+#pragma unroll
+                for (int i = 0; i < RPL / 4; ++i) {
+                    const mf::floatx4 x = *reinterpret_cast<const mf::floatx4*>(&sm.ckf[j][r0 + 4 * i]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ckr[4 * i + e] = x[e];
                 }
-            };
-            auto stage = [&](int slot, long tt) {  // wave 0
-                const int ring = (int)(tt % 3);
+            } else {
+                const float cj = sm.cc[j];
 #pragma unroll
-                for (int e = 0; e < KPL; ++e) {
-                    sm.fck[ring][KPL * l + e] = creg[slot] * to_f(kreg[slot][e]);
-                    sm.fkb[ring][KPL * l + e] = kreg[slot][e];
-                }
-            };
-            load_k(t0, 0);
-            if (w == 0) stage(0, t0);
-            __syncthreads();
-            load_v(t0, 0);
-            load_v(t0 + 1, 1);
-            load_k(t0 + 1, 1);
-            load_k(t0 + 2, 0);
-            auto ftoken = [&](long t, int vs, int ks) {
-                const int kslot = (int)(t % 3);
-                if (w == 0 && t + 1 < t1) stage(ks, t + 1);
-                load_k(t + 3, ks);
-                const float vt = to_f(vreg[vs]);
-                load_v(t + 2, vs);
-                bf16x8 kq[NP / 4];
-                mf::floatx4 cq[RPL / 4];
-#pragma unroll
-                for (int i = 0; i < NP / 4; ++i)
-                    kq[i] = *reinterpret_cast<const bf16x8*>(sm.fkb[kslot] + r0 + 8 * i);
-#pragma unroll
-                for (int i = 0; i < RPL / 4; ++i)
-                    cq[i] = *reinterpret_cast<const mf::floatx4*>(sm.fck[kslot] + r0 + 4 * i);
-                float ua[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
-                    ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, S[p], ua[p % 4], false);
-                }
-                const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
-                const float rc = vt - u;
-#pragma unroll
-                for (int p = 0; p < NP; ++p) {
-                    const float lo = fmaf(cq[p / 2][2 * (p % 2)], rc, (float)S[p][0]);
-                    const float hi = fmaf(cq[p / 2][2 * (p % 2) + 1], rc, (float)S[p][1]);
-                    S[p] = bf16x2{(bf16)lo, (bf16)hi};
-                }
-                store_col(col_ptr(hist, t - t0 + 1), S);
-                __syncthreads();  // token t+1's k staged
-            };
-            for (long t = t0; t < t1; t += 2) {
-                ftoken(t, 0, 1);
-                if (t + 1 < t1) ftoken(t + 1, 1, 0);
+                for (int i = 0; i < RPL; ++i) ckr[i] = cj * (float)kq[i / 8][i % 8];
             }
+            float ua[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
+                ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, S[p], ua[p % 4], false);
+            }
+            const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
+            const float rc = vt - u;
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const float lo = fmaf(ckr[2 * p], rc, (float)S[p][0]);
+                const float hi = fmaf(ckr[2 * p + 1], rc, (float)S[p][1]);
+                S[p] = bf16x2{(bf16)lo, (bf16)hi};
+            }
+            store_col(col_ptr(hist, j + 1), S);
         }
         // ---- reverse over the segment
         {
-            // wave 0: token tt's k, dO (KPL values per lane), c, dc
-            bf16 kd[2][KPL], gd[2][KPL];
-            float cd[2], dcd[2];
-            auto load_kd = [&](long tt, int slot) {
-                if (w == 0 && tt >= t0) {
-#pragma unroll
-                    for (int e = 0; e < KPL; ++e) {
-                        kd[slot][e] = k[base0 + tt * tstride + KPL * l + e];
-                        gd[slot][e] = dO[base0 + tt * tstride + KPL * l + e];
-                    }
-                    cd[slot] = cbh[tt];
-                    dcd[slot] = dcbh[tt];
-                }
-            };
-            auto stage = [&](int slot, long tt) {  // wave 0
-                const int ring = (int)(tt % 3);
-#pragma unroll
-                for (int e = 0; e < KPL; ++e) {
-                    sm.rkb[ring][KPL * l + e] = kd[slot][e];
-                    sm.rgb[ring][KPL * l + e] = gd[slot][e];
-                }
-                if (l == 0) {
-                    sm.rcd[ring][0] = cd[slot];
-                    sm.rcd[ring][1] = dcd[slot];
-                }
-            };
             // per lane: v_c and the column of the state before the token, one ahead
             bf16 vR[2];
             bf16x2 SpR[2][NP], Sn[NP];
-            auto load_lane = [&](long tt, int slot) {
-                if (tt >= t0) {
-                    vR[slot] = v[base0 + tt * tstride + col];
-                    load_col(col_ptr(hist, tt - t0), SpR[slot]);
+            auto load_lane = [&](int j, int slot) {
+                if (j >= 0) {
+                    vR[slot] = v[base0 + (t0 + j) * tstride + col];
+                    load_col(col_ptr(hist, j), SpR[slot]);
                 }
             };
-            load_kd(t1 - 1, 0);
-            if (w == 0) stage(0, t1 - 1);
-            __syncthreads();
-            load_col(col_ptr(hist, t1 - t0), Sn);
-            load_lane(t1 - 1, 0);
-            load_kd(t1 - 2, 0);
-            load_kd(t1 - 3, 1);
-            // token t: its v / state in vR[s], SpR[s]; token t-1's k, dO, c, dc in kd[s] ...
-            auto rtoken = [&](long t, int s) {
-                const int rs = (int)(t % 3), par = (int)(t & 1);
-                if (w == 0 && t - 1 >= t0) stage(s, t - 1);
-                load_kd(t - 3, s);
-                load_lane(t - 1, s ^ 1);
-                const bf16* kb = sm.rkb[rs];
-                const bf16* gb = sm.rgb[rs];
-                const float c = sm.rcd[rs][0];
+            load_col(col_ptr(hist, n), Sn);
+            load_lane(n - 1, 0);
+            // token t0 + j: its v / state in vR[s], SpR[s]
+            auto rtoken = [&](int j, int s) {
+                const int par = j & 1;
+                load_lane(j - 1, s ^ 1);
+                const bf16* kb = sm.kb[j];
+                const bf16* gb = sm.gb[j];
+                const float c = sm.cc[j];
                 const float kc = (float)kb[col];
                 const float vt = to_f(vR[s]);
-                // this lane's rows of k and dO (bf16), read once for both passes;
-                // each pass widens them to fp32 where it needs them
+                // this lane's rows of k and dO (bf16), read once for both passes
                 bf16x8 kq[RPL / 8], gq[RPL / 8];
 #pragma unroll
                 for (int i8 = 0; i8 < RPL / 8; ++i8) {
@@ -610,8 +602,9 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
                     gq[i8] = *reinterpret_cast<const bf16x8*>(gb + r0 + 8 * i8);
                 }
                 // pass 1, column sums: u = S^T k, gk = S_n^T dO (bf16 pairs),
-                // sw = g^T k with g = G + dO k_c (fp32)
+                // sw = g^T k with g = G + dO k_c (fp32, left in G)
                 float ua[2] = {0.f, 0.f}, ga[2] = {0.f, 0.f}, sa[4] = {0.f, 0.f, 0.f, 0.f};
+                float kf[RPL];
 #pragma unroll
                 for (int i8 = 0; i8 < RPL / 8; ++i8) {
 #pragma unroll
@@ -624,30 +617,31 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
                     }
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const float gv = fmaf((float)gq[i8][e], kc, G[8 * i8 + e]);
-                        sa[e & 3] = fmaf(gv, (float)kq[i8][e], sa[e & 3]);
+                        const int ii = 8 * i8 + e;
+                        kf[ii] = (float)kq[i8][e];
+                        G[ii] = fmaf((float)gq[i8][e], kc, G[ii]);
+                        sa[e & 3] = fmaf(G[ii], kf[ii], sa[e & 3]);
                     }
                 }
                 const float u = quad_sum<LPC>(ua[0] + ua[1]);
                 const float gk = quad_sum<LPC>(ga[0] + ga[1]);
                 const float sw = quad_sum<LPC>((sa[0] + sa[1]) + (sa[2] + sa[3]));
                 const float w2 = vt - u, w1 = c * sw, cw2 = c * w2;
-                // pass 2 (g recomputed as in pass 1): the row sum's summands
-                // c g w2 - S w1 (bf16 high + low parts); G <- g - k w1^T
-                bf16* mh = sm.Mh[par] + col * LDS + r0;
-                bf16* ml = sm.Ml[par] + col * LDS + r0;
+                // pass 2: the row sum's summands c g w2 - S w1 (bf16 high + low
+                // parts); G <- g - k w1^T
+                bf16* mh = sm.Mh[par] + lcol * LDS + r0;
+                bf16* ml = sm.Ml[par] + lcol * LDS + r0;
 #pragma unroll
                 for (int i8 = 0; i8 < RPL / 8; ++i8) {
                     bf16x8 hv, lv;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int ii = 8 * i8 + e;
-                        const float gv = fmaf((float)gq[i8][e], kc, G[ii]);
                         const float sp = (float)SpR[s][ii / 2][ii % 2];
-                        const float m = fmaf(gv, cw2, -(sp * w1));
+                        const float m = fmaf(G[ii], cw2, -(sp * w1));
                         hv[e] = (bf16)m;
                         lv[e] = (bf16)(m - (float)hv[e]);
-                        G[ii] = fmaf(-(float)kq[i8][e], w1, gv);
+                        G[ii] = fmaf(-kf[ii], w1, G[ii]);
                     }
                     *reinterpret_cast<bf16x8*>(mh + 8 * i8) = hv;
                     *reinterpret_cast<bf16x8*>(ml + 8 * i8) = lv;
@@ -655,45 +649,131 @@ __global__ void __launch_bounds__(rfast_threads<D>()) r_bwd_fast_kernel(
                 // grad_c = sum_c w2_c sw_c: one value per column, then per wave
                 const float gc = wave_sum_q4(part == 0 ? w2 * sw : 0.f);
                 if (part == 0) {
-                    sm.gkv[par][col] = gk;
-                    grad_v[base0 + t * tstride + col] = (bf16)w1;
+                    sm.gkv[par][lcol] = gk;
+                    grad_v[base0 + (t0 + j) * tstride + col] = (bf16)w1;
                 }
                 if (l == 0) sm.red[par][w] = gc;
 #pragma unroll
                 for (int p = 0; p < NP; ++p) Sn[p] = SpR[s][p];  // the next token's S_n
                 __syncthreads();
-                // rows 16 w .. 16 w + 15: q = sum_c M[row][c] by MFMA against ones
-                const int f0 = 16 * w;
-                mf::floatx4 acc = mf::zero4();
+                // rows 16 (MT w + m) ..: q = sum_c M[row][c] by MFMA against ones
+                // (this workgroup's columns; grad_lambda from its columns' grad_c)
 #pragma unroll
-                for (int q = 0; q < NK; ++q) {
-                    acc = mf::mma(mf::frag_trc(l, sm.Mh[par], LDS, 32 * q, f0), ones, acc);
-                    acc = mf::mma(mf::frag_trc(l, sm.Ml[par], LDS, 32 * q, f0), ones, acc);
-                }
-                if (j16 == 0) {
-                    float gsum = 0.f;
+                for (int m = 0; m < MT; ++m) {
+                    const int f0 = 16 * (MT * w + m);
+                    mf::floatx4 acc = mf::zero4();
 #pragma unroll
-                    for (int ww = 0; ww < NW; ++ww) gsum += sm.red[par][ww];
-                    const float glam2 = 2.f * gsum * sm.rcd[rs][1];
-                    bf16x4 ov;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int row = f0 + 4 * g4 + i;
-                        ov[i] = (bf16)fmaf(glam2, (float)kb[row], acc[i] + sm.gkv[par][row]);
+                    for (int q = 0; q < NK; ++q) {
+                        acc = mf::mma(mf::frag_trc(l, sm.Mh[par], LDS, 32 * q, f0), ones, acc);
+                        acc = mf::mma(mf::frag_trc(l, sm.Ml[par], LDS, 32 * q, f0), ones, acc);
                     }
-                    *reinterpret_cast<bf16x4*>(grad_k + base0 + t * tstride + f0 + 4 * g4) = ov;
+                    if (j16 == 0) {
+                        float gsum = 0.f;
+#pragma unroll
+                        for (int ww = 0; ww < NW; ++ww) gsum += sm.red[par][ww];
+                        const float glam2 = 2.f * gsum * sm.dcc[j];
+                        mf::floatx4 gv4;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int row = f0 + 4 * g4 + i, lr = row - cb * NC;
+                            const float sn = (NS == 1 || (lr >= 0 && lr < NC)) ? sm.gkv[par][lr] : 0.f;
+                            gv4[i] = fmaf(glam2, (float)kb[row], acc[i] + sn);
+                        }
+                        const long o = base0 + (t0 + j) * tstride + f0 + 4 * g4;
+                        if constexpr (NS == 1) {
+                            *reinterpret_cast<bf16x4*>(grad_k + o) =
+                                bf16x4{(bf16)gv4[0], (bf16)gv4[1], (bf16)gv4[2], (bf16)gv4[3]};
+                        } else {
+                            *reinterpret_cast<mf::floatx4*>(part_gk + cb * pstride + o) = gv4;
+                        }
+                    }
                 }
             };
-            for (long t = t1 - 1; t >= t0; t -= 2) {
-                rtoken(t, 0);
-                if (t - 1 >= t0) rtoken(t - 1, 1);
+            for (int j = n - 1; j >= 0; j -= 2) {
+                rtoken(j, 0);
+                if (j - 1 >= 0) rtoken(j - 1, 1);
             }
         }
+        __syncthreads();  // the segment's staged data and last row sums read
     }
     // dL/dS_0 in the reference's [row][c] layout
     bf16* gs = grad_state + (long)bh * dd;
 #pragma unroll
     for (int i = 0; i < RPL; ++i) gs[(long)(r0 + i) * D + col] = (bf16)G[i];
+}
+
+// out[i] = bf16(sum_s part[s * pstride + i]) over the NS fp32 slices written
+// by the column-split kernels, four elements per thread, slices in order
+__global__ void __launch_bounds__(NTH) r_combine_kernel(const float* __restrict__ part,
+                                                        long pstride, int ns,
+                                                        bf16* __restrict__ out, long n4) {
+    for (long i = (long)blockIdx.x * NTH + threadIdx.x; i < n4; i += (long)gridDim.x * NTH) {
+        mf::floatx4 a = reinterpret_cast<const mf::floatx4*>(part)[i];
+        for (int sl = 1; sl < ns; ++sl) {
+            const mf::floatx4 b = reinterpret_cast<const mf::floatx4*>(part + sl * pstride)[i];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] += b[e];
+        }
+        reinterpret_cast<bf16x4*>(out)[i] = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
+    }
+}
+
+// Workgroups per (b, h) for the register-resident kernels: 2 (d = 64, 128)
+// when B H would leave at least half of the CUs without one.
+// (Four workgroups of 32 columns, two per CU, measured slower at B H = 128:
+// forward 5.5 against 5.2 ms, backward 26.5 against 24.7 ms.)
+inline int r_split(size_t nbh) {
+    const int ncu = device_cu_count();
+    return ncu > 0 && nbh * 2 <= (size_t)ncu ? 2 : 1;
+}
+
+template <int D, int NS, int LPC>
+void r_launch_fwd(bool checkpoints, const void* k, const void* v, const float* coef, void* state,
+                  void* out, float* part, long pstride, bf16* ck, int H, long T, size_t nbh,
+                  hipStream_t stream) {
+    const dim3 grid((unsigned)(nbh * NS)), block(rfast_threads<D, NS, LPC>());
+    if (checkpoints)
+        EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<D, NS, LPC, false, true>), grid, block,
+                    stream, (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)nullptr,
+                    (float*)nullptr, 0L, ck, H, T);
+    else
+        EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, true, false>), grid, block,
+                    stream, (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part,
+                    pstride, (bf16*)nullptr, H, T);
+}
+
+template <int D, int NS, int LPC>
+void r_launch_bwd(const void* dO, const void* k, const void* v, const float* coef,
+                  const float* dcoef, const bf16* ck, bf16* hist, void* grad_k, float* part,
+                  long pstride, void* grad_v, void* grad_state, int H, long T, size_t nbh,
+                  hipStream_t stream) {
+    EFLA_LAUNCH("efla_r_backward", (r_bwd_fast_kernel<D, NS, LPC>), dim3((unsigned)(nbh * NS)),
+                dim3(rfast_threads<D, NS, LPC>()), stream, (const bf16*)dO, (const bf16*)k,
+                (const bf16*)v, coef, dcoef, ck, hist, (bf16*)grad_k, part, pstride,
+                (bf16*)grad_v, (bf16*)grad_state, H, T);
+}
+
+// the register-resident forward (checkpoints = false) or checkpoint pass for
+// head_dim d and split ns
+inline void r_fwd_fast(int d, int ns, bool checkpoints, const void* k, const void* v,
+                       const float* coef, void* state, void* out, float* part, long pstride,
+                       bf16* ck, int H, long T, size_t nbh, hipStream_t stream) {
+    if (d == 128 && ns == 1)
+        r_launch_fwd<128, 1, 4>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+    else if (d == 128)
+        r_launch_fwd<128, 2, 8>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+    else if (ns == 1)
+        r_launch_fwd<64, 1, 4>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+    else
+        r_launch_fwd<64, 2, 8>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+}
+
+inline void r_combine(const float* part, long pstride, int ns, void* out, size_t elems,
+                      hipStream_t stream) {
+    const long n4 = (long)(elems / 4);
+    const long nb = (n4 + NTH - 1) / NTH;
+    EFLA_LAUNCH("efla_r_combine", r_combine_kernel, dim3((unsigned)(nb < (1L << 20) ? nb : (1L << 20))),
+                dim3(NTH), stream, part, pstride, ns, (bf16*)out, n4);
 }
 
 // ---------------------------------------------------------------------------
@@ -902,12 +982,17 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
                       nbh * seq_len <= ((size_t)1 << 35);
     if (fast) {
         // every token's coefficient first (the stream's workspace), then the
-        // register-resident token loop
+        // register-resident token loop; with the column split its fp32 row-sum
+        // slices follow the coefficients in the workspace
         const size_t ntok = nbh * seq_len;
+        const int ns = r_split(nbh);
+        const size_t off_p = (ntok * sizeof(float) + 255) & ~(size_t)255;
+        const size_t need = ns > 1 ? off_p + ns * elems * sizeof(float) : ntok * sizeof(float);
         void* ws = nullptr;
         WsLease lease;
-        int rc = workspace_acquire(ntok * sizeof(float), stream, &ws, lease);
+        int rc = workspace_acquire(need, stream, &ws, lease);
         if (rc != kSuccess) return rc;
+        float* part = ns > 1 ? (float*)((char*)ws + off_p) : nullptr;
         const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
         if (head_dim == 128)
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
@@ -917,16 +1002,9 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
                         (float*)ws, (float*)nullptr, (int)num_heads, (long)seq_len, beta,
                         (long)ntok);
-        if (head_dim == 128)
-            EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<128, true, false>), grid,
-                        dim3(rfast_threads<128>()), stream, (const bf16*)k, (const bf16*)v,
-                        (const float*)ws, (bf16*)state, (bf16*)output, (bf16*)nullptr,
-                        (int)num_heads, (long)seq_len);
-        else
-            EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<64, true, false>), grid,
-                        dim3(rfast_threads<64>()), stream, (const bf16*)k, (const bf16*)v,
-                        (const float*)ws, (bf16*)state, (bf16*)output, (bf16*)nullptr,
-                        (int)num_heads, (long)seq_len);
+        r_fwd_fast((int)head_dim, ns, false, k, v, (const float*)ws, state, output, part,
+                   (long)elems, nullptr, (int)num_heads, (long)seq_len, nbh, stream);
+        if (ns > 1) r_combine(part, (long)elems, ns, output, elems, stream);
     } else {
         EFLA_LAUNCH("efla_r_forward", r_forward_kernel, grid, dim3(NTH), stream, (const bf16*)k,
                     (const bf16*)v, (bf16*)state, (bf16*)output, (int)num_heads, (long)seq_len,
@@ -949,10 +1027,12 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
     if (seq_len == 0) return fill_zero(grad_state, gsb, stream);
     if (!grad_output || !k || !v || !grad_k || !grad_v) return kInvalidValue;
     if (head_dim > (size_t)MAXD || nbh > (size_t)INT32_MAX) return kInvalidConfiguration;
-    // the register-resident path: d = 64 / 128, k aligned for the coefficient
-    // kernel's row loads and grad_k for 8-byte row pieces, at most 2^35 tokens
+    // the register-resident path: d = 64 / 128, k and dO aligned for d / 8-byte
+    // row loads (the coefficient kernel's, the segment staging's) and grad_k
+    // for 8-byte row pieces, at most 2^35 tokens
     const bool fast = (head_dim == 128 || head_dim == 64) &&
-                      (uintptr_t)k % (head_dim / 8) == 0 && (uintptr_t)grad_k % 8 == 0 &&
+                      (uintptr_t)k % (head_dim / 8) == 0 &&
+                      (uintptr_t)grad_output % (head_dim / 8) == 0 && (uintptr_t)grad_k % 8 == 0 &&
                       nbh * seq_len <= ((size_t)1 << 35);
     if (fast) {
         // workspace: checkpoints every SEGF tokens | one segment's states |
@@ -964,7 +1044,12 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
         const size_t off_hist = (ck_elems * 2 + 255) & ~(size_t)255;
         const size_t off_c = (off_hist + hist_elems * 2 + 255) & ~(size_t)255;
         const size_t off_dc = (off_c + ntok * 4 + 255) & ~(size_t)255;
-        const size_t need = off_dc + ntok * 4 + 256;
+        // with the column split: grad_k's fp32 slices
+        const int ns = r_split(nbh);
+        size_t elems = 0;
+        if (!mul_ok(ntok, head_dim, &elems)) return kInvalidConfiguration;
+        const size_t off_p = (off_dc + ntok * 4 + 255) & ~(size_t)255;
+        const size_t need = ns > 1 ? off_p + ns * elems * 4 : off_dc + ntok * 4 + 256;
         void* ws = nullptr;
         WsLease lease;
         int rc = workspace_acquire(need, stream, &ws, lease);
@@ -973,32 +1058,31 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
         bf16* hist = (bf16*)((char*)ws + off_hist);
         float* coef = (float*)((char*)ws + off_c);
         float* dcoef = (float*)((char*)ws + off_dc);
-        const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH)), grid((unsigned)nbh);
-        if (head_dim == 128) {
+        float* part = ns > 1 ? (float*)((char*)ws + off_p) : nullptr;
+        const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
+        if (head_dim == 128)
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
                         coef, dcoef, (int)num_heads, (long)seq_len, beta, (long)ntok);
-            EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<128, false, true>), grid,
-                        dim3(rfast_threads<128>()), stream, (const bf16*)k, (const bf16*)v,
-                        (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
-                        (long)seq_len);
-            EFLA_LAUNCH("efla_r_backward", r_bwd_fast_kernel<128>, grid,
-                        dim3(rfast_threads<128>()), stream, (const bf16*)grad_output,
-                        (const bf16*)k, (const bf16*)v, (const float*)coef, (const float*)dcoef,
-                        (const bf16*)ck, hist, (bf16*)grad_k, (bf16*)grad_v, (bf16*)grad_state,
-                        (int)num_heads, (long)seq_len);
-        } else {
+        else
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
                         coef, dcoef, (int)num_heads, (long)seq_len, beta, (long)ntok);
-            EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<64, false, true>), grid,
-                        dim3(rfast_threads<64>()), stream, (const bf16*)k, (const bf16*)v,
-                        (const float*)coef, (bf16*)state, (bf16*)nullptr, ck, (int)num_heads,
-                        (long)seq_len);
-            EFLA_LAUNCH("efla_r_backward", r_bwd_fast_kernel<64>, grid,
-                        dim3(rfast_threads<64>()), stream, (const bf16*)grad_output,
-                        (const bf16*)k, (const bf16*)v, (const float*)coef, (const float*)dcoef,
-                        (const bf16*)ck, hist, (bf16*)grad_k, (bf16*)grad_v, (bf16*)grad_state,
-                        (int)num_heads, (long)seq_len);
-        }
+        r_fwd_fast((int)head_dim, ns, true, k, v, coef, (void*)state, nullptr, nullptr, 0, ck,
+                   (int)num_heads, (long)seq_len, nbh, stream);
+        const int H = (int)num_heads;
+        const long T = (long)seq_len, ps = (long)elems;
+        if (head_dim == 128 && ns == 1)
+            r_launch_bwd<128, 1, 4>(grad_output, k, v, coef, dcoef, ck, hist, grad_k, part, ps,
+                                    grad_v, grad_state, H, T, nbh, stream);
+        else if (head_dim == 128)
+            r_launch_bwd<128, 2, 8>(grad_output, k, v, coef, dcoef, ck, hist, grad_k, part, ps,
+                                    grad_v, grad_state, H, T, nbh, stream);
+        else if (ns == 1)
+            r_launch_bwd<64, 1, 4>(grad_output, k, v, coef, dcoef, ck, hist, grad_k, part, ps,
+                                   grad_v, grad_state, H, T, nbh, stream);
+        else
+            r_launch_bwd<64, 2, 8>(grad_output, k, v, coef, dcoef, ck, hist, grad_k, part, ps,
+                                   grad_v, grad_state, H, T, nbh, stream);
+        if (ns > 1) r_combine(part, ps, ns, grad_k, elems, stream);
         return (int)hipPeekAtLastError();
     }
     const size_t nseg = (seq_len + SEG - 1) / SEG;

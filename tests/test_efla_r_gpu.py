@@ -35,9 +35,12 @@ def _inputs(oracle, seed, B, T, H, d, s0_scale):
     return k, v, do, s0
 
 
+# B H at most half the CU count (256 on MI355X) takes the column-split kernels
+# (two workgroups per (b, h), fp32 row-sum slices); the two shapes with B H >
+# 128 take one workgroup per (b, h).
 @pytest.mark.parametrize("B,T,H,d", [(2, 100, 2, 64), (1, 130, 3, 128), (1, 40, 1, 256),
                                      (2, 1, 2, 32), (1, 70, 2, 96), (1, 1, 2, 128),
-                                     (2, 3, 1, 64)])
+                                     (2, 3, 1, 64), (2, 37, 65, 128), (1, 40, 150, 64)])
 def test_forward_matches_reference(oracle, B, T, H, d):
     from ceo_amd.efla import efla_forward
 
@@ -57,7 +60,8 @@ def test_forward_matches_reference(oracle, B, T, H, d):
 
 
 @pytest.mark.parametrize("B,T,H,d", [(2, 100, 2, 64), (1, 150, 2, 128), (1, 70, 1, 256),
-                                     (1, 64, 2, 48), (1, 1, 2, 128), (2, 33, 1, 64)])
+                                     (1, 64, 2, 48), (1, 1, 2, 128), (2, 33, 1, 64),
+                                     (2, 37, 65, 128), (1, 40, 150, 64)])
 def test_backward_matches_reference(oracle, B, T, H, d):
     from ceo_amd.efla import efla_backward
 
@@ -104,32 +108,40 @@ def test_forward_backward_many_segments(oracle, B, T, H, d):
 
 
 def test_misaligned_k_takes_the_generic_kernels(oracle):
-    """A k whose address is not 16-byte aligned (a view one element into a
-    buffer) runs the LDS-resident kernels; both paths match the oracle and
-    each other to the bf16 bound."""
+    """A k (or, for the backward, a dO) whose address is not 16-byte aligned
+    (a view one element into a buffer) runs the LDS-resident kernels; all
+    paths match the oracle to the bf16 bound."""
     from ceo_amd.efla import efla_backward, efla_forward
 
     B, T, H, d = 1, 90, 2, 128
     announce(f"efla_forward_hip / efla_backward_hip misaligned k B={B} T={T} H={H} d={d}")
     k, v, do, s0 = _inputs(oracle, 900, B, T, H, d, 0.2)
     beta = 0.7
-    kd = _u16_to_dev(k)
-    buf = torch.empty(kd.numel() + 1, dtype=torch.bfloat16, device="cuda")
-    km = buf[1:].view(B, T, H, d)
-    km.copy_(kd)
-    assert km.data_ptr() % 16 != 0
+    def misaligned(x):
+        buf = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device="cuda")
+        xm = buf[1:].view(x.shape)
+        xm.copy_(x)
+        assert xm.data_ptr() % 16 != 0
+        return xm
+
+    kd, dod = _u16_to_dev(k), _u16_to_dev(do)
+    km = misaligned(kd)
     outs = []
     for kk in (kd, km):
         st = _u16_to_dev(s0)
         o = efla_forward(kk, _u16_to_dev(v), st, beta)
-        grads = efla_backward(_u16_to_dev(do), kk, _u16_to_dev(v), _u16_to_dev(s0), beta)
+        grads = efla_backward(dod, kk, _u16_to_dev(v), _u16_to_dev(s0), beta)
         outs.append((o, st) + grads)
+    # a misaligned dO alone also takes the generic backward
+    st = _u16_to_dev(s0)
+    o = efla_forward(kd, _u16_to_dev(v), st, beta)
+    outs.append((o, st) + efla_backward(misaligned(dod), kd, _u16_to_dev(v), _u16_to_dev(s0), beta))
     torch.cuda.synchronize()
     st_ref = s0.copy()
     _, o_ref = oracle.r_forward(k, v, st_ref, B, T, H, d, beta)
     _, gk_ref, gv_ref, gs_ref = oracle.r_backward(do, k, v, s0, B, T, H, d, beta)
     refs = (o_ref, st_ref, gk_ref, gv_ref, gs_ref)
-    for path, res in zip(("aligned", "misaligned"), outs):
+    for path, res in zip(("aligned", "misaligned k", "misaligned dO"), outs):
         errs = [rel_l2(oracle.bf16_to_f32(_dev_to_u16(a)), oracle.bf16_to_f32(r))
                 for a, r in zip(res, refs)]
         print(f"  {path}: rel-L2 o, state, grad_k, grad_v, grad_state =",
