@@ -180,11 +180,9 @@ __global__ void __launch_bounds__(NTH) r_coeff_kernel(const bf16* __restrict__ k
 // stages pair P+1's k (bf16) and c k (fp32, c from r_coeff_kernel) in LDS
 // during pair P; k, c and v are loaded two pairs ahead.  The o products of
 // pair P read their fragments right after P's barrier and run their MFMAs
-// after pair P+1's updates, so the reads overlap that work.  OUT writes o_t;
-// CK stores the state before every SEGF-th token to ck, column-major (the
-// register-resident backward's checkpoints).  The bf16 roundings and the
-// (c k) r product are the reference's; the sums run in another order (fp32
-// rounding level before each bf16 rounding).
+// after pair P+1's updates, so the reads overlap that work.  The bf16
+// roundings and the (c k) r product are the reference's; the sums run in
+// another order (fp32 rounding level before each bf16 rounding).
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 
 // Cross-lane moves through DPP (a VALU operand modifier) instead of the LDS
@@ -232,11 +230,12 @@ constexpr int rfast_threads() {
     return D / NS * LPC;
 }
 
-template <int D, int NS, int LPC, bool OUT, bool CK>
+template <int D, int NS, int LPC>
 __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
     bf16* __restrict__ state, bf16* __restrict__ out, float* __restrict__ part_out, long pstride,
-    bf16* __restrict__ ck, int H, long T) {
+    int H, long T) {
+    constexpr bool OUT = true;
     constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
     constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
     static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
@@ -247,7 +246,7 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
     const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
     const int col = cb * NC + tid / LPC, lcol = tid / LPC, part = tid % LPC, r0 = part * RPL;
     const int b = bh / H, h = bh % H;
-    const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
+    const long dd = (long)D * D;
     const long tstride = (long)H * D;  // elements between tokens
     const long base0 = (long)b * T * tstride + (long)h * D;
     const float* cbh = coef + (long)bh * T;
@@ -351,14 +350,6 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
     };
     // one token's update: its k, c k in ring slot `ring`, token i of the pair
     auto update = [&](long t, int ring, int i, float vt, bf16* sl) {
-        if (CK && t % SEGF == 0) {  // column-major [c][row]
-            bf16* dst = ck + ((long)bh * nsegf + t / SEGF) * dd + (long)col * D + r0;
-#pragma unroll
-            for (int q = 0; q < NP / 4; ++q)
-                *reinterpret_cast<bf16x8*>(dst + 8 * q) =
-                    bf16x8{Sp[4 * q][0], Sp[4 * q][1], Sp[4 * q + 1][0], Sp[4 * q + 1][1],
-                           Sp[4 * q + 2][0], Sp[4 * q + 2][1], Sp[4 * q + 3][0], Sp[4 * q + 3][1]};
-        }
         // this lane's rows of k (bf16 pairs) and c k, all reads issued first
         bf16x8 kq[NP / 4];
         mf::floatx4 cq[RPL / 4];
@@ -411,14 +402,171 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
         if (P + 1 < npair) pair(P + 1, 1);
     }
     if (OUT && pp >= 0) o_products();
-    // the forward hands the final state back; the checkpoint pass leaves the
-    // caller's initial state alone
-    if constexpr (!CK)
+    // the final state back to the caller
 #pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            st[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
-            st[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
+    for (int p = 0; p < NP; ++p) {
+        st[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
+        st[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// segment staging (checkpoint pass and backward)
+// ---------------------------------------------------------------------------
+// A segment's (SEGF tokens) per-token rows in LDS: k, c k in fp32 (CKS), dO
+// (DO), this workgroup's NC value columns of v (VS), c and dc/dlambda (DC).
+template <int D, int NC, bool DO, bool CKS, bool VS, bool DC>
+struct SegLds {
+    bf16 kb[SEGF][D];
+    bf16 gb[DO ? SEGF : 1][D];
+    float ckf[CKS ? SEGF : 1][D];
+    bf16 vb[VS ? SEGF : 1][NC];
+    float cc[SEGF], dcc[DC ? SEGF : 1];
+};
+
+// The same rows on their way in: load() issues the global reads of a segment
+// into registers (a segment ahead of use, so their latency overlaps the
+// current segment's work); store() writes them to SegLds once the current
+// segment's readers are done.  Pieces of VW = d / 16 elements (d / 8 bytes,
+// the alignment the host checks for k, dO and v) spread over the NT threads.
+template <int D, int NC, int NT, bool DO, bool CKS, bool VS, bool DC>
+struct SegRows {
+    static constexpr int VW = D / 16;
+    static constexpr int NKP = SEGF * D / VW, IK = (NKP + NT - 1) / NT;   // k / dO pieces
+    static constexpr int NVP = SEGF * NC / VW, IV = (NVP + NT - 1) / NT;  // v pieces
+    typedef __attribute__((__vector_size__(VW * sizeof(__bf16)))) __bf16 bfV;
+    bfV kx[IK], gx[DO ? IK : 1], vx[VS ? IV : 1];
+    float cx[CKS ? IK : 1], cs, dcs;
+
+    __device__ __forceinline__ void load(const bf16* __restrict__ k, const bf16* __restrict__ dO,
+                                         const bf16* __restrict__ v, const float* __restrict__ cbh,
+                                         const float* __restrict__ dcbh, long base0, long tstride,
+                                         long t0, int n, int vcol0, int tid) {
+#pragma unroll
+        for (int it = 0; it < IK; ++it) {
+            const int i = tid + it * NT, j = i / (D / VW), e0 = (i % (D / VW)) * VW;
+            if (i < NKP && j < n) {
+                const long o = base0 + (t0 + j) * tstride + e0;
+                kx[it] = *reinterpret_cast<const bfV*>(k + o);
+                if constexpr (DO) gx[it] = *reinterpret_cast<const bfV*>(dO + o);
+                if constexpr (CKS) cx[it] = cbh[t0 + j];
+            }
         }
+        if constexpr (VS)
+#pragma unroll
+            for (int it = 0; it < IV; ++it) {
+                const int i = tid + it * NT, j = i / (NC / VW), e0 = (i % (NC / VW)) * VW;
+                if (i < NVP && j < n)
+                    vx[it] = *reinterpret_cast<const bfV*>(v + base0 + (t0 + j) * tstride + vcol0 + e0);
+            }
+        if (tid < n) {
+            cs = cbh[t0 + tid];
+            if constexpr (DC) dcs = dcbh[t0 + tid];
+        }
+    }
+
+    __device__ __forceinline__ void store(SegLds<D, NC, DO, CKS, VS, DC>& sl, int n, int tid) const {
+#pragma unroll
+        for (int it = 0; it < IK; ++it) {
+            const int i = tid + it * NT, j = i / (D / VW), e0 = (i % (D / VW)) * VW;
+            if (i < NKP && j < n) {
+                *reinterpret_cast<bfV*>(&sl.kb[j][e0]) = kx[it];
+                if constexpr (DO) *reinterpret_cast<bfV*>(&sl.gb[j][e0]) = gx[it];
+                if constexpr (CKS)
+#pragma unroll
+                    for (int e = 0; e < VW; ++e) sl.ckf[j][e0 + e] = cx[it] * (float)kx[it][e];
+            }
+        }
+        if constexpr (VS)
+#pragma unroll
+            for (int it = 0; it < IV; ++it) {
+                const int i = tid + it * NT, j = i / (NC / VW), e0 = (i % (NC / VW)) * VW;
+                if (i < NVP && j < n) *reinterpret_cast<bfV*>(&sl.vb[j][e0]) = vx[it];
+            }
+        if (tid < n) {
+            sl.cc[tid] = cs;
+            if constexpr (DC) sl.dcc[tid] = dcs;
+        }
+    }
+};
+
+// The checkpoint pass of the register-resident backward: the forward's state
+// update (as r_fast_kernel, same roundings) with no outputs but the state
+// before every SEGF-th token, stored column-major to ck.  Each lane's column
+// needs only its own rows of k and c k, so a segment runs without barriers
+// from staged rows (two barriers per segment, the next segment's reads in
+// flight meanwhile).
+template <int D, int NS, int LPC>
+__global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_ckpt_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
+    const bf16* __restrict__ state, bf16* __restrict__ ck, int H, long T) {
+    constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>();
+    constexpr int RPL = D / LPC, NP = RPL / 2;
+    static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
+                      NT <= 1024,
+                  "d = 64 or 128, 32-column multiples per workgroup");
+    __shared__ __attribute__((aligned(16))) SegLds<D, NC, false, true, true, false> sm;
+    const int tid = threadIdx.x;
+    const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
+    const int col = cb * NC + tid / LPC, lcol = tid / LPC, part = tid % LPC, r0 = part * RPL;
+    const int b = bh / H, h = bh % H;
+    const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
+    const long tstride = (long)H * D;
+    const long base0 = (long)b * T * tstride + (long)h * D;
+    const float* cbh = coef + (long)bh * T;
+    const bf16* st = state + (long)bh * dd;
+
+    bf16x2 S[NP];  // rows r0 + 2p (low half) and r0 + 2p + 1 (high half)
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+        S[p] = bf16x2{st[(long)(r0 + 2 * p) * D + col], st[(long)(r0 + 2 * p + 1) * D + col]};
+    SegRows<D, NC, NT, false, true, true, false> rows;
+    rows.load(k, nullptr, v, cbh, nullptr, base0, tstride, 0, (int)(T < SEGF ? T : SEGF), cb * NC,
+              tid);
+    for (long seg = 0; seg < nsegf; ++seg) {
+        const long t0 = seg * SEGF;
+        const int n = (int)(T - t0 < SEGF ? T - t0 : SEGF);
+        rows.store(sm, n, tid);
+        __syncthreads();
+        if (seg + 1 < nsegf) {
+            const long t2 = t0 + SEGF;
+            rows.load(k, nullptr, v, cbh, nullptr, base0, tstride, t2,
+                      (int)(T - t2 < SEGF ? T - t2 : SEGF), cb * NC, tid);
+        }
+        // the state before token t0, column-major [c][row]
+        bf16* dst = ck + ((long)bh * nsegf + seg) * dd + (long)col * D + r0;
+#pragma unroll
+        for (int q = 0; q < NP / 4; ++q)
+            *reinterpret_cast<bf16x8*>(dst + 8 * q) =
+                bf16x8{S[4 * q][0], S[4 * q][1], S[4 * q + 1][0], S[4 * q + 1][1],
+                       S[4 * q + 2][0], S[4 * q + 2][1], S[4 * q + 3][0], S[4 * q + 3][1]};
+        for (int j = 0; j < n; ++j) {
+            bf16x8 kq[NP / 4];
+            mf::floatx4 cq[RPL / 4];
+#pragma unroll
+            for (int q = 0; q < NP / 4; ++q)
+                kq[q] = *reinterpret_cast<const bf16x8*>(&sm.kb[j][r0 + 8 * q]);
+#pragma unroll
+            for (int q = 0; q < RPL / 4; ++q)
+                cq[q] = *reinterpret_cast<const mf::floatx4*>(&sm.ckf[j][r0 + 4 * q]);
+            const float vt = to_f(sm.vb[j][lcol]);
+            float ua[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
+                ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, S[p], ua[p % 4], false);
+            }
+            const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
+            const float rc = vt - u;
+#pragma unroll
+            for (int p = 0; p < NP; ++p) {
+                const float lo = fmaf(cq[p / 2][2 * (p % 2)], rc, (float)S[p][0]);
+                const float hi = fmaf(cq[p / 2][2 * (p % 2) + 1], rc, (float)S[p][1]);
+                S[p] = bf16x2{(bf16)lo, (bf16)hi};
+            }
+        }
+        __syncthreads();  // the segment's rows read
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -435,21 +583,19 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
 // bf16 high and low parts of each fp32 summand (about 16 bits kept) and
 // 16x16x32 MFMAs against ones.
 // Segments of SEGF tokens are taken last to first.  A segment's k, dO, c and
-// dc/dlambda (and c k in fp32 where LDS allows) are staged in LDS by the whole
-// workgroup at once; the segment is then rebuilt from its checkpoint (ck,
-// column-major) with the forward step without barriers (each lane's column
-// needs only its own rows), every state stored column-major to the workspace
-// (hist), which the same lanes read back in the reverse pass (one barrier per
-// token, for the row sum).
+// dc/dlambda (and c k in fp32 and this workgroup's v columns where LDS allows:
+// the split kernels) are staged in LDS by the whole workgroup at once, their
+// global reads issued during the previous segment's reverse pass; the segment
+// is then rebuilt from its checkpoint (ck, column-major) with the forward step
+// without barriers (each lane's column needs only its own rows), every state
+// stored column-major to the workspace (hist), which the same lanes read back
+// in the reverse pass (one barrier per token, for the row sum).
 template <int D, int NS>
 struct RBwdSmem {
-    static constexpr bool CKS = NS > 1;  // c k staged (fp32); else formed per row
+    static constexpr bool CKS = NS > 1;  // c k and v staged; else formed per row / read per lane
     bf16 Mh[2][(D / NS) * (D + 8)];      // the row sum's summands [c][row], high bf16 part
     bf16 Ml[2][(D / NS) * (D + 8)];      // low part
-    bf16 kb[SEGF][D];                    // the segment's k
-    bf16 gb[SEGF][D];                    //   dO
-    float ckf[CKS ? SEGF : 1][D];        //   c k
-    float cc[SEGF], dcc[SEGF];           //   c, dc/dlambda
+    SegLds<D, D / NS, true, CKS, CKS, true> seg;
     float gkv[2][D / NS];                // S_n^T dO per column
     float red[2][16];                    // grad_c partials per wave
 };
@@ -463,12 +609,10 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
     constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
     constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
     constexpr int MT = D / 16 / NW, NK = NC / 32;
-    constexpr int VW = D / 16;  // staging vector: 16 bytes (d = 128) or 8 (d = 64, k 8-byte aligned)
     constexpr bool CKS = RBwdSmem<D, NS>::CKS;
     static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
                       NT <= 1024 && D % (16 * NW) == 0 && LPC % 4 == 0 && NW <= 16,
                   "d = 64 or 128, 32-column multiples per workgroup, 4 or 8 lanes per column");
-    typedef __attribute__((__vector_size__(VW * sizeof(__bf16)))) __bf16 bfV;
     __shared__ __attribute__((aligned(16))) RBwdSmem<D, NS> sm;
     const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
     const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
@@ -505,54 +649,50 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
     const bf16x8 ones = bf16x8{(bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f,
                                (bf16)1.f, (bf16)1.f, (bf16)1.f, (bf16)1.f};
 
+    SegRows<D, NC, NT, true, CKS, CKS, true> rows;
+    {
+        const long t0 = (nsegf - 1) * SEGF;
+        rows.load(k, dO, v, cbh, dcbh, base0, tstride, t0, (int)(T - t0), cb * NC, tid);
+    }
     for (long seg = nsegf - 1; seg >= 0; --seg) {
         const long t0 = seg * SEGF, t1 = t0 + SEGF < T ? t0 + SEGF : T;
         const int n = (int)(t1 - t0);
-        // ---- the segment's k, dO, c, dc (and c k) into LDS; the previous
-        // segment's last readers are done (barrier at the end of its reverse)
-        for (int i = tid; i < SEGF * D / VW; i += NT) {
-            const int j = i / (D / VW), e0 = (i % (D / VW)) * VW;
-            if (j < n) {
-                const long o = base0 + (t0 + j) * tstride + e0;
-                const bfV kx = *reinterpret_cast<const bfV*>(k + o);
-                *reinterpret_cast<bfV*>(&sm.kb[j][e0]) = kx;
-                *reinterpret_cast<bfV*>(&sm.gb[j][e0]) = *reinterpret_cast<const bfV*>(dO + o);
-                if constexpr (CKS) {
-                    const float cj = cbh[t0 + j];
-#pragma unroll
-                    for (int e = 0; e < VW; ++e) sm.ckf[j][e0 + e] = cj * (float)kx[e];
-                }
-            }
-        }
-        if (tid < n) {
-            sm.cc[tid] = cbh[t0 + tid];
-            sm.dcc[tid] = dcbh[t0 + tid];
-        }
+        // ---- the segment's rows into LDS (the previous segment's last
+        // readers are done: barrier at the end of its reverse pass)
+        rows.store(sm.seg, n, tid);
         // ---- rebuild: hist[jj] = the state before token t0 + jj
         bf16x2 S[NP];
         load_col(ck + ((long)bh * nsegf + seg) * dd + (long)col * D + r0, S);
         store_col(col_ptr(hist, 0), S);
         bf16 vreg[2];
-        vreg[0] = v[base0 + t0 * tstride + col];
-        if (n > 1) vreg[1] = v[base0 + (t0 + 1) * tstride + col];
+        if constexpr (!CKS) {
+            vreg[0] = v[base0 + t0 * tstride + col];
+            if (n > 1) vreg[1] = v[base0 + (t0 + 1) * tstride + col];
+        }
         __syncthreads();
         for (int j = 0; j < n; ++j) {
-            const float vt = to_f(vreg[j & 1]);
-            if (j + 2 < n) vreg[j & 1] = v[base0 + (t0 + j + 2) * tstride + col];
+            float vt;
+            if constexpr (CKS) {
+                vt = to_f(sm.seg.vb[j][lcol]);
+            } else {
+                vt = to_f(vreg[j & 1]);
+                if (j + 2 < n) vreg[j & 1] = v[base0 + (t0 + j + 2) * tstride + col];
+            }
             bf16x8 kq[NP / 4];
 #pragma unroll
             for (int i = 0; i < NP / 4; ++i)
-                kq[i] = *reinterpret_cast<const bf16x8*>(&sm.kb[j][r0 + 8 * i]);
+                kq[i] = *reinterpret_cast<const bf16x8*>(&sm.seg.kb[j][r0 + 8 * i]);
             float ckr[RPL];
             if constexpr (CKS) {
 #pragma unroll
                 for (int i = 0; i < RPL / 4; ++i) {
-                    const mf::floatx4 x = *reinterpret_cast<const mf::floatx4*>(&sm.ckf[j][r0 + 4 * i]);
+                    const mf::floatx4 x =
+                        *reinterpret_cast<const mf::floatx4*>(&sm.seg.ckf[j][r0 + 4 * i]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) ckr[4 * i + e] = x[e];
                 }
             } else {
-                const float cj = sm.cc[j];
+                const float cj = sm.seg.cc[j];
 #pragma unroll
                 for (int i = 0; i < RPL; ++i) ckr[i] = cj * (float)kq[i / 8][i % 8];
             }
@@ -574,26 +714,29 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
         }
         // ---- reverse over the segment
         {
-            // per lane: v_c and the column of the state before the token, one ahead
+            // per lane: (v_c and) the column of the state before the token, one ahead
             bf16 vR[2];
             bf16x2 SpR[2][NP], Sn[NP];
             auto load_lane = [&](int j, int slot) {
                 if (j >= 0) {
-                    vR[slot] = v[base0 + (t0 + j) * tstride + col];
+                    if constexpr (!CKS) vR[slot] = v[base0 + (t0 + j) * tstride + col];
                     load_col(col_ptr(hist, j), SpR[slot]);
                 }
             };
             load_col(col_ptr(hist, n), Sn);
             load_lane(n - 1, 0);
-            // token t0 + j: its v / state in vR[s], SpR[s]
+            // the next segment's rows: reads in flight during this reverse pass
+            if (seg > 0)
+                rows.load(k, dO, v, cbh, dcbh, base0, tstride, t0 - SEGF, SEGF, cb * NC, tid);
+            // token t0 + j: its (v and) state in vR[s], SpR[s]
             auto rtoken = [&](int j, int s) {
                 const int par = j & 1;
                 load_lane(j - 1, s ^ 1);
-                const bf16* kb = sm.kb[j];
-                const bf16* gb = sm.gb[j];
-                const float c = sm.cc[j];
+                const bf16* kb = sm.seg.kb[j];
+                const bf16* gb = sm.seg.gb[j];
+                const float c = sm.seg.cc[j];
                 const float kc = (float)kb[col];
-                const float vt = to_f(vR[s]);
+                const float vt = CKS ? to_f(sm.seg.vb[j][lcol]) : to_f(vR[s]);
                 // this lane's rows of k and dO (bf16), read once for both passes
                 bf16x8 kq[RPL / 8], gq[RPL / 8];
 #pragma unroll
@@ -671,7 +814,7 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
                         float gsum = 0.f;
 #pragma unroll
                         for (int ww = 0; ww < NW; ++ww) gsum += sm.red[par][ww];
-                        const float glam2 = 2.f * gsum * sm.dcc[j];
+                        const float glam2 = 2.f * gsum * sm.seg.dcc[j];
                         mf::floatx4 gv4;
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
@@ -733,13 +876,12 @@ void r_launch_fwd(bool checkpoints, const void* k, const void* v, const float* c
                   hipStream_t stream) {
     const dim3 grid((unsigned)(nbh * NS)), block(rfast_threads<D, NS, LPC>());
     if (checkpoints)
-        EFLA_LAUNCH("efla_r_checkpoint", (r_fast_kernel<D, NS, LPC, false, true>), grid, block,
-                    stream, (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)nullptr,
-                    (float*)nullptr, 0L, ck, H, T);
+        EFLA_LAUNCH("efla_r_checkpoint", (r_ckpt_kernel<D, NS, LPC>), grid, block, stream,
+                    (const bf16*)k, (const bf16*)v, coef, (const bf16*)state, ck, H, T);
     else
-        EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, true, false>), grid, block,
-                    stream, (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part,
-                    pstride, (bf16*)nullptr, H, T);
+        EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC>), grid, block, stream,
+                    (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part, pstride,
+                    H, T);
 }
 
 template <int D, int NS, int LPC>
@@ -1027,13 +1169,13 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
     if (seq_len == 0) return fill_zero(grad_state, gsb, stream);
     if (!grad_output || !k || !v || !grad_k || !grad_v) return kInvalidValue;
     if (head_dim > (size_t)MAXD || nbh > (size_t)INT32_MAX) return kInvalidConfiguration;
-    // the register-resident path: d = 64 / 128, k and dO aligned for d / 8-byte
+    // the register-resident path: d = 64 / 128, k, dO and v aligned for d / 8-byte
     // row loads (the coefficient kernel's, the segment staging's) and grad_k
     // for 8-byte row pieces, at most 2^35 tokens
-    const bool fast = (head_dim == 128 || head_dim == 64) &&
-                      (uintptr_t)k % (head_dim / 8) == 0 &&
-                      (uintptr_t)grad_output % (head_dim / 8) == 0 && (uintptr_t)grad_k % 8 == 0 &&
-                      nbh * seq_len <= ((size_t)1 << 35);
+    const size_t ra = head_dim / 8;
+    const bool fast = (head_dim == 128 || head_dim == 64) && (uintptr_t)k % ra == 0 &&
+                      (uintptr_t)grad_output % ra == 0 && (uintptr_t)v % ra == 0 &&
+                      (uintptr_t)grad_k % 8 == 0 && nbh * seq_len <= ((size_t)1 << 35);
     if (fast) {
         // workspace: checkpoints every SEGF tokens | one segment's states |
         // c and dc/dlambda per token (all column-major states, bf16)
