@@ -176,13 +176,14 @@ __global__ void __launch_bounds__(NTH) r_coeff_kernel(const bf16* __restrict__ k
 //                                      [c][row] and 16x16x32 MFMAs contract
 //                                      them with k
 // The updates need only the lane's own column, so tokens go in pairs: both
-// updates, both new states to LDS, one barrier, then both o products.  Wave 0
-// stages pair P+1's k (bf16) and c k (fp32, c from r_coeff_kernel) in LDS
-// during pair P; k, c and v are loaded two pairs ahead.  The o products of
-// pair P read their fragments right after P's barrier and run their MFMAs
-// after pair P+1's updates, so the reads overlap that work.  The bf16
-// roundings and the (c k) r product are the reference's; the sums run in
-// another order (fp32 rounding level before each bf16 rounding).
+// updates, both new states to LDS, one barrier, then both o products.  Each
+// segment of SEGF tokens has its k (bf16), c k (fp32, c from r_coeff_kernel)
+// and v columns staged in LDS at once (SegRows, the global reads a segment
+// ahead).  The o products of a pair read their fragments right after its
+// barrier and run their MFMAs after the next pair's updates, so the reads
+// overlap that work.  The bf16 roundings and the (c k) r product are the
+// reference's; the sums run in another order (fp32 rounding level before each
+// bf16 rounding).
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
 
 // Cross-lane moves through DPP (a VALU operand modifier) instead of the LDS
@@ -201,13 +202,23 @@ __device__ __forceinline__ float quad_sum(float x) {
     if constexpr (L >= 8) x += dpp_f<0x141>(x);  // row_half_mirror: lane 7 - i of its 8
     return x;
 }
-// sum over the wave of the values in lanes 4i (other lanes hold 0), in every lane
+// x from lane (row r, i) of the rows in ROWMASK (the DPP source lane), 0 elsewhere
+template <int CTRL, int ROWMASK>
+__device__ __forceinline__ float dpp_rows(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x),
+                                                                  CTRL, ROWMASK, 0xF, false));
+}
+// sum over the wave of the values in lanes 4i (other lanes are ignored),
+// uniform; all VALU: lane 4i's value to its quad, rotations within each row of
+// 16 (every lane then holds its row's sum), then the GFX9 row broadcasts (lane
+// 15 into rows 1 and 3, lane 31 into rows 2 and 3) leave the total in lane 63
 __device__ __forceinline__ float wave_sum_q4(float x) {
-    x += dpp_f<0x124>(x);  // row_ror:4
-    x += dpp_f<0x128>(x);  // row_ror:8
-    x += __shfl_xor(x, 16);
-    x += __shfl_xor(x, 32);
-    return x;
+    x = dpp_f<0x00>(x);            // quad_perm [0, 0, 0, 0]
+    x += dpp_f<0x124>(x);          // row_ror:4
+    x += dpp_f<0x128>(x);          // row_ror:8
+    x += dpp_rows<0x142, 0xA>(x);  // row_bcast:15
+    x += dpp_rows<0x143, 0xC>(x);  // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
 // Column split: the state's value columns evolve independently (the update
@@ -218,200 +229,13 @@ __device__ __forceinline__ float wave_sum_q4(float x) {
 // output's layout) and r_combine_kernel adds the slices and rounds once.
 // NS = 1, LPC = 4 is one workgroup per (b, h); NS = 2, LPC = 8 gives a grid of
 // 2 B H with half the rows per lane (for B H below the CU count).
-template <int D, int NS>
-struct RFastSmem {
-    bf16 Sl[4][(D / NS) * (D + 8)];  // new states [c][row]: two tokens, double-buffered
-    float ckf[3][2][D];              // c k (fp32), ring of three token pairs
-    bf16 kb[3][2][D];                // k (bf16)
-};
-
 template <int D, int NS, int LPC>
 constexpr int rfast_threads() {
     return D / NS * LPC;
 }
 
-template <int D, int NS, int LPC>
-__global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
-    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
-    bf16* __restrict__ state, bf16* __restrict__ out, float* __restrict__ part_out, long pstride,
-    int H, long T) {
-    constexpr bool OUT = true;
-    constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
-    constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
-    static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
-                      NT <= 1024 && D % (16 * NW) == 0,
-                  "d = 64 or 128, 32-column multiples per workgroup");
-    __shared__ __attribute__((aligned(16))) RFastSmem<D, NS> sm;
-    const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
-    const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
-    const int col = cb * NC + tid / LPC, lcol = tid / LPC, part = tid % LPC, r0 = part * RPL;
-    const int b = bh / H, h = bh % H;
-    const long dd = (long)D * D;
-    const long tstride = (long)H * D;  // elements between tokens
-    const long base0 = (long)b * T * tstride + (long)h * D;
-    const float* cbh = coef + (long)bh * T;
-    bf16* st = state + (long)bh * dd;
-    const long npair = (T + 1) / 2;
-
-    bf16x2 Sp[NP];  // rows r0 + 2p (low half) and r0 + 2p + 1 (high half)
-#pragma unroll
-    for (int p = 0; p < NP; ++p)
-        Sp[p] = bf16x2{st[(long)(r0 + 2 * p) * D + col], st[(long)(r0 + 2 * p + 1) * D + col]};
-
-    // per token pair: v_c per lane; k (D / 64 values per lane) and c in wave
-    // 0; loaded two pairs ahead into slot (pair & 1)
-    constexpr int KPL = D / 64;
-    bf16 vreg[2][2], kreg[2][2][KPL];
-    float creg[2][2];
-    auto load_v = [&](long P, int slot) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-            if (2 * P + i < T) vreg[slot][i] = v[base0 + (2 * P + i) * tstride + col];
-    };
-    auto load_k = [&](long P, int slot) {
-        if (w == 0)
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const long tt = 2 * P + i;
-                if (tt < T) {
-#pragma unroll
-                    for (int e = 0; e < KPL; ++e)
-                        kreg[slot][i][e] = k[base0 + tt * tstride + KPL * l + e];
-                    creg[slot][i] = cbh[tt];
-                }
-            }
-    };
-    auto stage_k = [&](int slot, long P) {  // wave 0: pair P into ring slot P % 3
-        const int ring = (int)(P % 3);
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int e = 0; e < KPL; ++e) {
-                sm.ckf[ring][i][KPL * l + e] = creg[slot][i] * to_f(kreg[slot][i][e]);
-                sm.kb[ring][i][KPL * l + e] = kreg[slot][i][e];
-            }
-    };
-    if (T > 0) {
-        load_k(0, 0);
-        if (w == 0) stage_k(0, 0);
-        __syncthreads();
-    }
-    load_v(0, 0);
-    load_v(1, 1);
-    load_k(1, 1);
-    load_k(2, 0);
-
-    // o products of the last pair, fragments in registers
-    constexpr int MT = D / 16 / NW, NK = NC / 32;
-    bf16x8 af[2][MT][NK], bk[2][NK];
-    long pp = -1;
-    const int g = l >> 4, j = l & 15;
-    auto o_reads = [&](long P) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const bf16* kb = sm.kb[P % 3][i];
-            const bf16* slt = sm.Sl[2 * (P & 1) + i];
-#pragma unroll
-            for (int q = 0; q < NK; ++q) {
-                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kb + cb * NC + 32 * q + 4 * g);
-                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kb + cb * NC + 32 * q + 16 + 4 * g);
-                bk[i][q] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-                for (int m = 0; m < MT; ++m)
-                    af[i][m][q] = mf::frag_trc(l, slt, LDS, 32 * q, 16 * (MT * w + m));
-            }
-        }
-        pp = P;
-    };
-    // A = S[row][c] (c-order k over c), B = k broadcast over the 16 columns
-    auto o_products = [&]() {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const long t = 2 * pp + i;
-            if (t >= T) break;
-#pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                mf::floatx4 acc = mf::zero4();
-#pragma unroll
-                for (int q = 0; q < NK; ++q) acc = mf::mma(af[i][m][q], bk[i][q], acc);
-                if (j == 0) {
-                    const long o = base0 + t * tstride + 16 * (MT * w + m) + 4 * g;
-                    if constexpr (NS == 1) {
-                        bf16x4 ov;
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) ov[e] = (bf16)acc[e];
-                        *reinterpret_cast<bf16x4*>(out + o) = ov;
-                    } else {
-                        *reinterpret_cast<mf::floatx4*>(part_out + cb * pstride + o) = acc;
-                    }
-                }
-            }
-        }
-    };
-    // one token's update: its k, c k in ring slot `ring`, token i of the pair
-    auto update = [&](long t, int ring, int i, float vt, bf16* sl) {
-        // this lane's rows of k (bf16 pairs) and c k, all reads issued first
-        bf16x8 kq[NP / 4];
-        mf::floatx4 cq[RPL / 4];
-#pragma unroll
-        for (int q = 0; q < NP / 4; ++q)
-            kq[q] = *reinterpret_cast<const bf16x8*>(sm.kb[ring][i] + r0 + 8 * q);
-#pragma unroll
-        for (int q = 0; q < RPL / 4; ++q)
-            cq[q] = *reinterpret_cast<const mf::floatx4*>(sm.ckf[ring][i] + r0 + 4 * q);
-        // u = S^T k for this column (four partial sums, then the lanes of the column)
-        float ua[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
-            ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, Sp[p], ua[p % 4], false);
-        }
-        const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
-        const float rc = vt - u;
-        // S <- bf16(S + (c k) r); the new column piece as bf16 into LDS
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-            const float lo = fmaf(cq[p / 2][2 * (p % 2)], rc, (float)Sp[p][0]);
-            const float hi = fmaf(cq[p / 2][2 * (p % 2) + 1], rc, (float)Sp[p][1]);
-            Sp[p] = bf16x2{(bf16)lo, (bf16)hi};
-        }
-        if (OUT) {
-#pragma unroll
-            for (int q = 0; q < NP / 4; ++q)
-                *reinterpret_cast<bf16x8*>(sl + 8 * q) =
-                    bf16x8{Sp[4 * q][0], Sp[4 * q][1], Sp[4 * q + 1][0], Sp[4 * q + 1][1],
-                           Sp[4 * q + 2][0], Sp[4 * q + 2][1], Sp[4 * q + 3][0], Sp[4 * q + 3][1]};
-        }
-    };
-    // pair P: its v in vreg[s], pair P+1's k and c in kreg[s ^ 1]
-    auto pair = [&](long P, int s) {
-        const int ring = (int)(P % 3);
-        // pair P+1's k into the ring (read after this pair's barrier)
-        if (w == 0 && P + 1 < npair) stage_k(s ^ 1, P + 1);
-        load_k(P + 3, s ^ 1);
-        const float v0 = to_f(vreg[s][0]), v1 = to_f(vreg[s][1]);
-        load_v(P + 2, s);
-        update(2 * P, ring, 0, v0, sm.Sl[2 * (P & 1)] + lcol * LDS + r0);
-        if (2 * P + 1 < T) update(2 * P + 1, ring, 1, v1, sm.Sl[2 * (P & 1) + 1] + lcol * LDS + r0);
-        if (OUT && pp >= 0) o_products();  // the previous pair's o
-        __syncthreads();  // the new states in LDS; pair P+1's k staged
-        if (OUT) o_reads(P);
-    };
-    for (long P = 0; P < npair; P += 2) {
-        pair(P, 0);
-        if (P + 1 < npair) pair(P + 1, 1);
-    }
-    if (OUT && pp >= 0) o_products();
-    // the final state back to the caller
-#pragma unroll
-    for (int p = 0; p < NP; ++p) {
-        st[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
-        st[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
-    }
-}
-
 // ---------------------------------------------------------------------------
-// segment staging (checkpoint pass and backward)
+// segment staging (forward, checkpoint pass, backward)
 // ---------------------------------------------------------------------------
 // A segment's (SEGF tokens) per-token rows in LDS: k, c k in fp32 (CKS), dO
 // (DO), this workgroup's NC value columns of v (VS), c and dc/dlambda (DC).
@@ -489,6 +313,167 @@ struct SegRows {
         }
     }
 };
+
+template <int D, int NS>
+struct RFastSmem {
+    static constexpr bool CKS = NS > 1;  // c k staged (fp32); else formed per row
+    bf16 Sl[4][(D / NS) * (D + 8)];      // new states [c][row]: two tokens, double-buffered
+    SegLds<D, D / NS, false, CKS, true, false> seg;
+};
+
+template <int D, int NS, int LPC>
+__global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
+    const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
+    bf16* __restrict__ state, bf16* __restrict__ out, float* __restrict__ part_out, long pstride,
+    int H, long T) {
+    constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
+    constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
+    constexpr bool CKS = RFastSmem<D, NS>::CKS;
+    static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
+                      NT <= 1024 && D % (16 * NW) == 0,
+                  "d = 64 or 128, 32-column multiples per workgroup");
+    __shared__ __attribute__((aligned(16))) RFastSmem<D, NS> sm;
+    const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
+    const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
+    const int col = cb * NC + tid / LPC, lcol = tid / LPC, part = tid % LPC, r0 = part * RPL;
+    const int b = bh / H, h = bh % H;
+    const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
+    const long tstride = (long)H * D;  // elements between tokens
+    const long base0 = (long)b * T * tstride + (long)h * D;
+    const float* cbh = coef + (long)bh * T;
+    bf16* st = state + (long)bh * dd;
+
+    bf16x2 Sp[NP];  // rows r0 + 2p (low half) and r0 + 2p + 1 (high half)
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+        Sp[p] = bf16x2{st[(long)(r0 + 2 * p) * D + col], st[(long)(r0 + 2 * p + 1) * D + col]};
+
+    // o products of the last pair, fragments in registers
+    constexpr int MT = D / 16 / NW, NK = NC / 32;
+    bf16x8 af[2][MT][NK], bk[2][NK];
+    long pp = -1;  // that pair's first token
+    const int g = l >> 4, j = l & 15;
+    auto o_reads = [&](long t, int jj, int sb) {  // token t (segment row jj), Sl buffer sb
+        pp = t;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            if (t + i >= T) break;
+            const bf16* kb = sm.seg.kb[jj + i];
+            const bf16* slt = sm.Sl[sb + i];
+#pragma unroll
+            for (int q = 0; q < NK; ++q) {
+                const bf16x4 lo = *reinterpret_cast<const bf16x4*>(kb + cb * NC + 32 * q + 4 * g);
+                const bf16x4 hi = *reinterpret_cast<const bf16x4*>(kb + cb * NC + 32 * q + 16 + 4 * g);
+                bk[i][q] = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+                for (int m = 0; m < MT; ++m)
+                    af[i][m][q] = mf::frag_trc(l, slt, LDS, 32 * q, 16 * (MT * w + m));
+            }
+        }
+    };
+    // A = S[row][c] (c-order k over c), B = k broadcast over the 16 columns
+    auto o_products = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const long t = pp + i;
+            if (t >= T) break;
+#pragma unroll
+            for (int m = 0; m < MT; ++m) {
+                mf::floatx4 acc = mf::zero4();
+#pragma unroll
+                for (int q = 0; q < NK; ++q) acc = mf::mma(af[i][m][q], bk[i][q], acc);
+                if (j == 0) {
+                    const long o = base0 + t * tstride + 16 * (MT * w + m) + 4 * g;
+                    if constexpr (NS == 1) {
+                        bf16x4 ov;
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) ov[e] = (bf16)acc[e];
+                        *reinterpret_cast<bf16x4*>(out + o) = ov;
+                    } else {
+                        *reinterpret_cast<mf::floatx4*>(part_out + cb * pstride + o) = acc;
+                    }
+                }
+            }
+        }
+    };
+    // one token's update from segment row jj; the new column piece to sl
+    auto update = [&](int jj, bf16* sl) {
+        // this lane's rows of k (bf16 pairs) and c k, all reads issued first
+        bf16x8 kq[NP / 4];
+        float ckr[RPL];
+#pragma unroll
+        for (int q = 0; q < NP / 4; ++q)
+            kq[q] = *reinterpret_cast<const bf16x8*>(&sm.seg.kb[jj][r0 + 8 * q]);
+        if constexpr (CKS) {
+#pragma unroll
+            for (int q = 0; q < RPL / 4; ++q) {
+                const mf::floatx4 x = *reinterpret_cast<const mf::floatx4*>(&sm.seg.ckf[jj][r0 + 4 * q]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) ckr[4 * q + e] = x[e];
+            }
+        } else {
+            const float cj = sm.seg.cc[jj];
+#pragma unroll
+            for (int i = 0; i < RPL; ++i) ckr[i] = cj * (float)kq[i / 8][i % 8];
+        }
+        const float vt = to_f(sm.seg.vb[jj][lcol]);
+        // u = S^T k for this column (four partial sums, then the lanes of the column)
+        float ua[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const bf16x2 kp = bf16x2{kq[p / 4][2 * (p % 4)], kq[p / 4][2 * (p % 4) + 1]};
+            ua[p % 4] = __builtin_amdgcn_fdot2_f32_bf16(kp, Sp[p], ua[p % 4], false);
+        }
+        const float u = quad_sum<LPC>((ua[0] + ua[1]) + (ua[2] + ua[3]));
+        const float rc = vt - u;
+        // S <- bf16(S + (c k) r); the new column piece as bf16 into LDS
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            const float lo = fmaf(ckr[2 * p], rc, (float)Sp[p][0]);
+            const float hi = fmaf(ckr[2 * p + 1], rc, (float)Sp[p][1]);
+            Sp[p] = bf16x2{(bf16)lo, (bf16)hi};
+        }
+#pragma unroll
+        for (int q = 0; q < NP / 4; ++q)
+            *reinterpret_cast<bf16x8*>(sl + 8 * q) =
+                bf16x8{Sp[4 * q][0], Sp[4 * q][1], Sp[4 * q + 1][0], Sp[4 * q + 1][1],
+                       Sp[4 * q + 2][0], Sp[4 * q + 2][1], Sp[4 * q + 3][0], Sp[4 * q + 3][1]};
+    };
+
+    SegRows<D, NC, NT, false, CKS, true, false> rows;
+    rows.load(k, nullptr, v, cbh, nullptr, base0, tstride, 0, (int)(T < SEGF ? T : SEGF), cb * NC,
+              tid);
+    long P = 0;  // token pairs so far (selects the Sl buffers)
+    for (long seg = 0; seg < nsegf; ++seg) {
+        const long t0 = seg * SEGF;
+        const int n = (int)(T - t0 < SEGF ? T - t0 : SEGF);
+        __syncthreads();  // the previous segment's rows read (its last o_reads)
+        rows.store(sm.seg, n, tid);
+        __syncthreads();
+        if (seg + 1 < nsegf) {
+            const long t2 = t0 + SEGF;
+            rows.load(k, nullptr, v, cbh, nullptr, base0, tstride, t2,
+                      (int)(T - t2 < SEGF ? T - t2 : SEGF), cb * NC, tid);
+        }
+        // pairs of tokens: both updates, both new states to LDS, the previous
+        // pair's o products, one barrier, this pair's o fragments
+        for (int jj = 0; jj < n; jj += 2, ++P) {
+            const int sb = 2 * (int)(P & 1);
+            update(jj, sm.Sl[sb] + lcol * LDS + r0);
+            if (jj + 1 < n) update(jj + 1, sm.Sl[sb + 1] + lcol * LDS + r0);
+            if (pp >= 0) o_products();
+            __syncthreads();
+            o_reads(t0 + jj, jj, sb);
+        }
+    }
+    if (pp >= 0) o_products();
+    // the final state back to the caller
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+        st[(long)(r0 + 2 * p) * D + col] = Sp[p][0];
+        st[(long)(r0 + 2 * p + 1) * D + col] = Sp[p][1];
+    }
+}
 
 // The checkpoint pass of the register-resident backward: the forward's state
 // update (as r_fast_kernel, same roundings) with no outputs but the state
@@ -1117,11 +1102,12 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
     // its shared-memory limit; see the header)
     if (head_dim > (size_t)MAXD || nbh > (size_t)INT32_MAX) return kInvalidConfiguration;
     const dim3 grid((unsigned)nbh);
-    // the register-resident path: d = 64 / 128, k aligned for the coefficient
-    // kernel's row loads and output for 8-byte row pieces, at most 2^35 tokens
+    // the register-resident path: d = 64 / 128, k and v aligned for d / 8-byte
+    // row loads (the coefficient kernel's, the segment staging's) and output
+    // for 8-byte row pieces, at most 2^35 tokens
     const bool fast = (head_dim == 128 || head_dim == 64) &&
-                      (uintptr_t)k % (head_dim / 8) == 0 && (uintptr_t)output % 8 == 0 &&
-                      nbh * seq_len <= ((size_t)1 << 35);
+                      (uintptr_t)k % (head_dim / 8) == 0 && (uintptr_t)v % (head_dim / 8) == 0 &&
+                      (uintptr_t)output % 8 == 0 && nbh * seq_len <= ((size_t)1 << 35);
     if (fast) {
         // every token's coefficient first (the stream's workspace), then the
         // register-resident token loop; with the column split its fp32 row-sum
