@@ -979,23 +979,26 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
             if (c > 0 && (ncu <= 0 || c < ncu)) ncu = c;
         }
         const dim3 grad_grid((unsigned)(ncu > 0 && ncu < nitems ? ncu : nitems));
-        // the forward that saved the states also saved each chunk's P
+        // the forward that saved the states also saved each chunk's P.  The
+        // gradient kernel runs 16 waves (four per SIMD) where its registers
+        // allow it without spills (d_v <= 128), else 8
+        constexpr int NG = V <= 128 ? 4 : 2;
         if (reuse_states) {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, true>), scan_grid,
                         dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)w.Pc, si, H, dST, dS0, w.dh, p.ld);
-            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true>), grad_grid,
-                        dim3(fast::NT8), st, q, k, v, dO, (const bf16*)w.Tc, (const float*)w.bc,
-                        (const float*)w.dcc, (const bf16*)w.Pc, w.h, w.dh, si, H, nitems, dq, dk, dv,
-                        dbeta, p.ld);
+            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true, NG>), grad_grid,
+                        dim3(fast::grad_threads<NG>()), st, q, k, v, dO, (const bf16*)w.Tc,
+                        (const float*)w.bc, (const float*)w.dcc, (const bf16*)w.Pc, w.h, w.dh,
+                        si, H, nitems, dq, dk, dv, dbeta, p.ld);
         } else {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, false>), scan_grid,
                         dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)nullptr, si, H, dST, dS0, w.dh, p.ld);
-            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false>), grad_grid,
-                        dim3(fast::NT8), st, q, k, v, dO, (const bf16*)w.Tc, (const float*)w.bc,
-                        (const float*)w.dcc, (const bf16*)nullptr, w.h, w.dh, si, H, nitems, dq, dk, dv,
-                        dbeta, p.ld);
+            EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false, NG>), grad_grid,
+                        dim3(fast::grad_threads<NG>()), st, q, k, v, dO, (const bf16*)w.Tc,
+                        (const float*)w.bc, (const float*)w.dcc, (const bf16*)nullptr, w.h, w.dh,
+                        si, H, nitems, dq, dk, dv, dbeta, p.ld);
         }
         return (int)hipPeekAtLastError();
     } else if (!reuse) {

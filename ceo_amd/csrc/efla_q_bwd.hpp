@@ -288,7 +288,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
 // ---------------------------------------------------------------------------
 // per-chunk gradients
 // ---------------------------------------------------------------------------
-template <int K>
+template <int K, int NG>
 struct GradSmem {
     bf16 Qs[64 * ldb<K>()];
     bf16 Ks[64 * ldb<K>()];
@@ -297,7 +297,7 @@ struct GradSmem {
     // b, dc/dlambda, dc/dbeta per token for items of even / odd position in
     // this workgroup's sequence (the next item's arrive during the closing)
     float coef[2][3][64];
-    float dbh[2][64];    // per-half partial dL/db
+    float dbh[NG][64];   // per-group partial dL/db
     // one 64-wide value slice's inputs; during an item's closing products the
     // next item's first slice is copied in here
     bf16 V[64 * LD64];   // v[:, slice]; each wave's (rows, value tiles) later hold D Y
@@ -323,12 +323,11 @@ struct GradSmem {
     } u;
 };
 
-constexpr int NT8 = 512;  // grad_kernel: 8 waves
-
-// Wave (tb, hf): tb = wave & 3 owns tokens 16tb .. 16tb+15 (the columns of
-// every transposed tile it computes); hf = wave >> 2 picks half of the value
-// tiles (slice phase), of the key tiles (dq / dk) and of the 16-token blocks
-// of the 64 x 64 chunk matrices.
+// Wave (tb, gq): tb = wave & 3 owns tokens 16tb .. 16tb+15 (the columns of
+// every transposed tile it computes); gq = wave >> 2 picks one of NG groups of
+// the value tiles (slice phase), of the key tiles (dq / dk) and of the 16-token
+// blocks of the 64 x 64 chunk matrices: 4 / NG of each.  NG = 2 is 8 waves, NG
+// = 4 is 16 (four per SIMD, half the tiles per wave).
 //
 // Persistent: workgroup b (one per CU) takes the (chunk, head) items b,
 // b + gridDim.x, ... in heads-fastest order (the heads of one chunk are
@@ -339,19 +338,31 @@ constexpr int NT8 = 512;  // grad_kernel: 8 waves
 // longer reads Q, T once it no longer reads T, and k after the last product
 // that reads K.  Nothing of the next item passes through registers, so the
 // copies never make a wave wait.
-template <int K, int V, bool PS>
-__global__ void __launch_bounds__(NT8) grad_kernel(
+template <int NG>
+constexpr int grad_threads() {
+    return 256 * NG;
+}
+
+template <int K, int V, bool PS, int NG>
+__global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const bf16* __restrict__ dO, const bf16* __restrict__ Tws, const float* __restrict__ bws,
     const float* __restrict__ dcws, const bf16* __restrict__ Pws, const bf16* __restrict__ hist,
     const bf16* __restrict__ dhist, SeqInfo si, int H, int nitems,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
     bf16* __restrict__ dbeta, TokLd ld) {
-    constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 32;  // NF key tiles per half
-    __shared__ __attribute__((aligned(16))) GradSmem<K> sm;
+    constexpr int NT8 = grad_threads<NG>(), NW = NT8 / 64;
+    constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 16 / NG;  // NF key tiles per group
+    constexpr int EG = 4 / NG;  // value tiles / 16-token blocks per group
+    // threads holding the v, dO slice and the h, dh slice prefetches (one
+    // 16-byte piece each at most)
+    constexpr int NTV = NT8 < 64 * VS / 8 ? NT8 : 64 * VS / 8;
+    constexpr int NTH = NT8 < 64 * K / 8 ? NT8 : 64 * K / 8;
+    static_assert(NG == 2 || NG == 4, "8 or 16 waves");
+    __shared__ __attribute__((aligned(16))) GradSmem<K, NG> sm;
     const int w8 = mf::wave(), tb = w8 & 3, hf = w8 >> 2;
     const int nks = tb >= 2 ? 1 : 0;  // first k-step (of 32) that reaches t'' >= t
-    const int f0 = hf * NF;            // first key tile of this half
+    const int f0 = hf * NF;            // first key tile of this group
 
     struct Item {
         int h, slot, len;
@@ -366,25 +377,25 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     // copies into LDS (l: lane); each is issued by all waves
     auto copy_slice0 = [&](const Item& I, int par, int l) {
         const long cid = (long)I.slot * H + I.h, chb = cid * V * K;
-        mf::dma_tile<64, VS, LD64, 8>(sm.V, v + I.bos * ld.v + (long)I.h * V, ld.v, I.len, 0, l);
-        mf::dma_tile<64, VS, LD64, 8>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
-        mf::dma_tile<64, K, LDK, 8>(sm.h, hist + chb, K, 64, 4, l);
-        mf::dma_tile<64, K, LDK, 8>(sm.dh, dhist + chb, K, 64, 6, l);
+        mf::dma_tile<64, VS, LD64, NW>(sm.V, v + I.bos * ld.v + (long)I.h * V, ld.v, I.len, 0, l);
+        mf::dma_tile<64, VS, LD64, NW>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
+        mf::dma_tile<64, K, LDK, NW>(sm.h, hist + chb, K, 64, 4, l);
+        mf::dma_tile<64, K, LDK, NW>(sm.dh, dhist + chb, K, 64, 6, l);
         if constexpr (PS)
-            mf::dma_tile<64, 64, LD64, 8>(sm.Ps, Pws + cid * 64 * 64, 64, 64, 2, l);
+            mf::dma_tile<64, 64, LD64, NW>(sm.Ps, Pws + cid * 64 * 64, 64, 64, 2, l);
         // b (16 chunks of 16 bytes) and dc/dlambda, dc/dbeta (32 chunks)
-        if (w8 == 7 && l < 16) mf::dma16(bws + cid * 64, 16u * l, sm.coef[par][0]);
-        if (w8 == 6 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
+        if (w8 == NW - 1 && l < 16) mf::dma16(bws + cid * 64, 16u * l, sm.coef[par][0]);
+        if (w8 == NW - 2 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
     };
     auto copy_q = [&](const Item& I, int l) {
-        mf::dma_tile<64, K, LDK, 8>(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
+        mf::dma_tile<64, K, LDK, NW>(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
     };
     auto copy_t = [&](const Item& I, int l) {
-        mf::dma_tile<64, 64, LD64, 8>(sm.Tb, Tws + ((long)I.slot * H + I.h) * 64 * 64, 64, 64, 5,
+        mf::dma_tile<64, 64, LD64, NW>(sm.Tb, Tws + ((long)I.slot * H + I.h) * 64 * 64, 64, 64, 5,
                                       l);
     };
     auto copy_k = [&](const Item& I, int l) {
-        mf::dma_tile<64, K, LDK, 8>(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);
+        mf::dma_tile<64, K, LDK, NW>(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);
     };
 
     int it = blockIdx.x, par = 0;
@@ -406,14 +417,18 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     const long chb = ((long)slot * H + h) * V * K;  // this chunk's h / dh block
     const float* cf = sm.coef[par][0];  // b, dc/dlambda, dc/dbeta at cf[0, 64, 128 + t]
 
-    mf::TileRegs<64, VS, NT8> rv, rd;
-    mf::TileRegs<64, K, NT8> rh, rdh;
+    mf::TileRegs<64, VS, NTV> rv, rd;
+    mf::TileRegs<64, K, NTH> rh, rdh;
     auto prefetch = [&](int s) {
         const int vv = s * VS;
-        rv.load(v + bos * ld.v + (long)h * V + vv, ld.v, len, tid);
-        rd.load(dO + (bos * H + h) * V + vv, (long)H * V, len, tid);
-        rh.load(hist + chb + (long)vv * K, K, 64, tid);
-        rdh.load(dhist + chb + (long)vv * K, K, 64, tid);
+        if (NTV == NT8 || tid < NTV) {
+            rv.load(v + bos * ld.v + (long)h * V + vv, ld.v, len, tid);
+            rd.load(dO + (bos * H + h) * V + vv, (long)H * V, len, tid);
+        }
+        if (NTH == NT8 || tid < NTH) {
+            rh.load(hist + chb + (long)vv * K, K, 64, tid);
+            rdh.load(dhist + chb + (long)vv * K, K, 64, tid);
+        }
     };
     // ---- item setup: every input of the item's first slice is in flight
     mf::dma_wait();
@@ -436,7 +451,7 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         __syncthreads();
     }
     if constexpr (!PS) {
-        for (int n = w8; n < 10; n += 8) {
+        for (int n = w8; n < 10; n += NW) {
             int I, J;
             lower_tile(n, I, J);
             floatx4 accp = zero4();
@@ -455,29 +470,36 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     const float bt = cf[t];
 
     // ---- value slices ----
-    floatx4 dqa[NF], dka[NF], dma[2], dta[2];
+    floatx4 dqa[NF], dka[NF], dma[EG], dta[EG];
 #pragma unroll
     for (int fb = 0; fb < NF; ++fb) dqa[fb] = dka[fb] = zero4();
-    dma[0] = dma[1] = dta[0] = dta[1] = zero4();
-    const bool jlive = hf == 0 || tb >= 2;  // this half's t' blocks reach t' <= t
+#pragma unroll
+    for (int e = 0; e < EG; ++e) dma[e] = dta[e] = zero4();
+    // this group's t' blocks reach t' <= t: block J holds tokens of
+    // 32 (J >> 1) .. 32 (J >> 1) + 31 (pim interleaves J and J ^ 1)
+    const bool jlive = 32 * ((EG * hf) >> 1) <= 16 * tb + 15;
     float dbp = 0.f;
     for (int s = 0; s < NS; ++s) {
         const int vv = s * VS;
         if (s > 0) {  // slice 0 was copied in with the item's other inputs
             __syncthreads();
-            rv.store_rows(sm.V, LD64);
-            rd.store_rows(sm.dO, LD64);
-            rh.store_rows(sm.h, LDK);
-            rdh.store_rows(sm.dh, LDK);
+            if (NTV == NT8 || tid < NTV) {
+                rv.store_rows(sm.V, LD64);
+                rd.store_rows(sm.dO, LD64);
+            }
+            if (NTH == NT8 || tid < NTH) {
+                rh.store_rows(sm.h, LDK);
+                rdh.store_rows(sm.dh, LDK);
+            }
             __syncthreads();
         }
         if (s + 1 < NS) prefetch(s + 1);
-        // R^T = V^T - h K^T and dVn^T = dO^T P + dh K^T for value tiles 2hf, 2hf+1:
-        // tile (value 16vb + 4g + i, token t)
-        floatx4 rT[2];
+        // R^T = V^T - h K^T and dVn^T = dO^T P + dh K^T for value tiles
+        // EG hf .. EG hf + EG - 1: tile (value 16vb + 4g + i, token t)
+        floatx4 rT[EG];
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int vb = 2 * hf + e;
+        for (int e = 0; e < EG; ++e) {
+            const int vb = EG * hf + e;
             floatx4 ra = load4(sm.V + t * LD64 + 16 * vb + 4 * g);
             floatx4 da = zero4();
 #pragma unroll
@@ -496,8 +518,8 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         __syncthreads();
         // Vn^T = (D R)^T T^T; Y^T = dVn^T T; db += sum_v Y R; D Y -> V (and dv)
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int vb = 2 * hf + e;
+        for (int e = 0; e < EG; ++e) {
+            const int vb = EG * hf + e;
             floatx4 vn = mma(frag_tr(l, sm.u.s.DR, LD64, 0, 16 * vb), tfr0, zero4());
             if (tb >= 2) vn = mma(frag_tr(l, sm.u.s.DR, LD64, 32, 16 * vb), tfr1, vn);
             store4(sm.u.s.Vn + t * LD64 + 16 * vb + 4 * g, vn);
@@ -510,8 +532,8 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
             store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
         __syncthreads();
-        {  // dv = D Y of this slice from its bf16 copy in V, as whole 16-byte row pieces
-            static_assert(NT8 == 64 * (VS / 8), "one piece per thread");
+        if (NTV == NT8 || tid < NTV) {  // dv = D Y of this slice from its bf16 copy in V, as whole 16-byte row pieces
+            static_assert(NTV == 64 * (VS / 8), "one piece per thread");
             const int tt = tid / (VS / 8), f = 8 * (tid % (VS / 8));
             if (tt < len)
                 *reinterpret_cast<bf16x8*>(dv + (bos + tt) * ld.dv + (long)h * V + vv + f) =
@@ -534,8 +556,8 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
             if (jlive) {
                 const bf16x8 dvb = frag_nat(l, sm.u.s.dVn, LD64, 16 * tb, 32 * ks);
 #pragma unroll
-                for (int e = 0; e < 2; ++e) {
-                    const int J = 2 * hf + e;
+                for (int e = 0; e < EG; ++e) {
+                    const int J = EG * hf + e;
                     dta[e] = mma(frag_row(l, sm.u.s.DR, LD64, pim(J, r), 32 * ks), dvb, dta[e]);
                     dma[e] = mma(frag_row(l, sm.u.s.Vn, LD64, pim(J, r), 32 * ks), dob, dma[e]);
                 }
@@ -551,8 +573,8 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     // ---- closing products ----
     // Dm[t][t'] keeps t' <= t, dT[t][t'] keeps t' < t; share both [t][t']
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int J = 2 * hf + e;
+    for (int e = 0; e < EG; ++e) {
+        const int J = EG * hf + e;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int tp = pim(J, 4 * g + i);
@@ -566,12 +588,12 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     // the next item's first slice, P and coefficients into the free slice
     // buffers (the closing products touch neither)
     if (more) copy_slice0(nxt, par ^ 1, l);
-    // X^T[t''][t] = sum_t' T[t''][t'] dT[t][t'] for t'' blocks 2hf, 2hf+1
+    // X^T[t''][t] = sum_t' T[t''][t'] dT[t][t'] for this group's t'' blocks
     {
         const bf16x8 d0 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 0), d1 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 32);
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int J = 2 * hf + e;
+        for (int e = 0; e < EG; ++e) {
+            const int J = EG * hf + e;
             floatx4 x = mma(frag_nat(l, sm.Tb, LD64, 16 * J, 0), d0, zero4());
             x = mma(frag_nat(l, sm.Tb, LD64, 16 * J, 32), d1, x);
             store4(sm.u.e.X + t * LD64 + 16 * J + 4 * g, x);
@@ -594,12 +616,13 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
     }
     __syncthreads();
     if (more) copy_q(nxt, l);  // Q is not read again in this item
-    // M^T[j][i] = sum_t X[t][j] T[t][i] (i = t owned here, j in blocks 2hf, 2hf+1, j < i);
-    // dA = -M, G recomputed: db += sum_j dA G; dG = b_i dA -> shared [i][j]
+    // M^T[j][i] = sum_t X[t][j] T[t][i] (i = t owned here, j in this group's
+    // blocks, j < i); dA = -M, G recomputed: db += sum_j dA G; dG = b_i dA ->
+    // shared [i][j]
     float dbg = 0.f;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
-        const int J = 2 * hf + e;
+    for (int e = 0; e < EG; ++e) {
+        const int J = EG * hf + e;
         floatx4 dg = zero4();
         if (jlive) {
             const int c0 = 32 * (J >> 1) + 4 * (J & 1);
@@ -648,7 +671,9 @@ __global__ void __launch_bounds__(NT8) grad_kernel(
         kfin[fb] = *reinterpret_cast<const bf16x4*>(sm.Ks + t * LDK + 16 * (f0 + fb) + 4 * g);
     __syncthreads();
     if (more) copy_k(nxt, l);
-    const float dbt = sm.dbh[0][t] + sm.dbh[1][t];  // dL/db for token t
+    float dbt = sm.dbh[0][t];  // dL/db for token t
+#pragma unroll
+    for (int gg = 1; gg < NG; ++gg) dbt += sm.dbh[gg][t];
     // dk += 2 db c'(lambda) k; dq, dk (this half's key tiles) into LDS (the
     // closing buffers are free), then written out as whole 16-byte row pieces
     {
