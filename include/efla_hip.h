@@ -50,6 +50,11 @@ extern "C" {
  * overwritten with S_T.  chunk_size is accepted and ignored, as in the
  * reference.  Validation order: B, H or d == 0 -> 1; T == 0 -> 0; any null
  * pointer -> 1; B*H or sizes overflowing -> 9.
+ * Scratch comes from the stream's cached workspace (leased per call): 4 bytes
+ * per (b, t, h) for the coefficients, and for d = 64 / 128 with B*H at most
+ * half the device's CU count (two workgroups per (b, h), each owning half of
+ * the state's columns) 8 bytes per output element more for the fp32 partial
+ * row sums (cfg3's B=4, T=8192, H=32, d=128: 1.07 GB).
  */
 int efla_forward_hip(const void* k, const void* v, void* state, void* output,
                      size_t batch_size, size_t seq_len, size_t num_heads, size_t head_dim,
@@ -60,7 +65,11 @@ int efla_forward_hip(const void* k, const void* v, void* state, void* output,
  * S_0.  Outputs grad_k, grad_v (B, T, H, d) bf16 and grad_state = dL/dS_0
  * (B*H, d, d) bf16 for the loss sum(output * grad_output).  T == 0 zeroes
  * grad_state and returns 0.  State history is recomputed from checkpoints in a
- * cached workspace instead of the reference's per-call (T+1)*d*d allocation.
+ * cached workspace instead of the reference's per-call (T+1)*d*d allocation:
+ * one bf16 d*d checkpoint per 32 tokens (64 on the LDS-resident path) and one
+ * segment's states per (b, h), 8 bytes per (b, t, h) of coefficients, and with
+ * the column split (as efla_forward_hip) 8 bytes per grad_k element for the
+ * fp32 partial row sums.
  */
 int efla_backward_hip(const void* grad_output, const void* k, const void* v, const void* state,
                       void* grad_k, void* grad_v, void* grad_state, size_t batch_size,
