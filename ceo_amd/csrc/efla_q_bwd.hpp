@@ -353,6 +353,27 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     bf16* __restrict__ dbeta, TokLd ld) {
     constexpr int NT8 = grad_threads<NG>(), NW = NT8 / 64;
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 16 / NG;  // NF key tiles per group
+    // K-wide operand tiles (Qs, Ks, h, dh) are kept as K / 64 column halves of
+    // 64 with row stride LDH (72 for K = 128: the same 64 x LDK elements, but
+    // 16-byte row reads of a 64-wide half with a 144-byte stride run about
+    // 1.45x the rate of a 288-byte stride on gfx950); every fragment's k or
+    // line range lies inside one half.  kh(base, c) is the half holding
+    // column c, read at column c % 64.
+    // (The 8-wave d_v = 256 instantiation keeps [64][LDK] tiles: with the
+    // halves, hipcc's register allocation fails on it.)
+    constexpr int KH = NG == 4 ? K / 64 : 1, LDH = KH > 1 ? 72 : LDK, HALF = 64 * LDH;
+    static_assert(K % 64 == 0 && KH * HALF <= 64 * LDK, "K = 64 or 128");
+    auto kh = [](const bf16* base, int c) { return KH > 1 ? base + (c >> 6) * HALF : base; };
+    auto kcol = [](int c) { return KH > 1 ? (c & 63) : c; };
+    auto kcopy = [&](bf16* dst, const bf16* src, long ld, int nvalid, int rot, int l) {
+        if constexpr (KH == 1) {
+            mf::dma_tile<64, K, LDK, NW>(dst, src, ld, nvalid, rot, l);
+        } else {
+#pragma unroll
+            for (int hh = 0; hh < KH; ++hh)
+                mf::dma_tile<64, 64, LDH, NW>(dst + hh * HALF, src + 64 * hh, ld, nvalid, rot + hh, l);
+        }
+    };
     constexpr int EG = 4 / NG;  // value tiles / 16-token blocks per group
     // threads holding the v, dO slice and the h, dh slice prefetches (one
     // 16-byte piece each at most)
@@ -379,8 +400,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         const long cid = (long)I.slot * H + I.h, chb = cid * V * K;
         mf::dma_tile<64, VS, LD64, NW>(sm.V, v + I.bos * ld.v + (long)I.h * V, ld.v, I.len, 0, l);
         mf::dma_tile<64, VS, LD64, NW>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
-        mf::dma_tile<64, K, LDK, NW>(sm.h, hist + chb, K, 64, 4, l);
-        mf::dma_tile<64, K, LDK, NW>(sm.dh, dhist + chb, K, 64, 6, l);
+        kcopy(sm.h, hist + chb, K, 64, 4, l);
+        kcopy(sm.dh, dhist + chb, K, 64, 6, l);
         if constexpr (PS)
             mf::dma_tile<64, 64, LD64, NW>(sm.Ps, Pws + cid * 64 * 64, 64, 64, 2, l);
         // b (16 chunks of 16 bytes) and dc/dlambda, dc/dbeta (32 chunks)
@@ -388,14 +409,14 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         if (w8 == NW - 2 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
     };
     auto copy_q = [&](const Item& I, int l) {
-        mf::dma_tile<64, K, LDK, NW>(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
+        kcopy(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
     };
     auto copy_t = [&](const Item& I, int l) {
         mf::dma_tile<64, 64, LD64, NW>(sm.Tb, Tws + ((long)I.slot * H + I.h) * 64 * 64, 64, 64, 5,
                                       l);
     };
     auto copy_k = [&](const Item& I, int l) {
-        mf::dma_tile<64, K, LDK, NW>(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);
+        kcopy(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);
     };
 
     int it = blockIdx.x, par = 0;
@@ -439,7 +460,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     __syncthreads();  // every wave's copies have landed
     if (len < 64) {  // a sequence's last chunk: token rows past its end read as zero
         for (int i = tid; i < (64 - len) * (K / 8); i += NT8) {
-            const int o = (len + i / (K / 8)) * LDK + 8 * (i % (K / 8));
+            const int c = 8 * (i % (K / 8));
+            const int o = (KH > 1 ? (c >> 6) * HALF : 0) + (len + i / (K / 8)) * LDH + kcol(c);
             *reinterpret_cast<bf16x8*>(sm.Qs + o) = bf16x8{};
             *reinterpret_cast<bf16x8*>(sm.Ks + o) = bf16x8{};
         }
@@ -457,7 +479,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             floatx4 accp = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)
-                accp = mma(frag_nat(l, sm.Ks, LDK, 16 * J, k0), frag_nat(l, sm.Qs, LDK, 16 * I, k0), accp);
+                accp = mma(frag_nat(l, kh(sm.Ks, k0), LDH, 16 * J, kcol(k0)),
+                           frag_nat(l, kh(sm.Qs, k0), LDH, 16 * I, kcol(k0)), accp);
             const int tq = 16 * I + r, tk = 16 * J + 4 * g;
             *reinterpret_cast<bf16x4*>(sm.Ps + tq * LD64 + tk) =
                 bf16x4{(bf16)(tk + 0 <= tq ? accp[0] : 0.f), (bf16)(tk + 1 <= tq ? accp[1] : 0.f),
@@ -488,8 +511,13 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
                 rd.store_rows(sm.dO, LD64);
             }
             if (NTH == NT8 || tid < NTH) {
-                rh.store_rows(sm.h, LDK);
-                rdh.store_rows(sm.dh, LDK);
+                if constexpr (KH > 1) {
+                    rh.store_rows_split(sm.h, LDH, HALF);
+                    rdh.store_rows_split(sm.dh, LDH, HALF);
+                } else {
+                    rh.store_rows(sm.h, LDK);
+                    rdh.store_rows(sm.dh, LDK);
+                }
             }
             __syncthreads();
         }
@@ -504,9 +532,10 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             floatx4 da = zero4();
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb) {
-                const bf16x8 kt = frag_nat(l, sm.Ks, LDK, 16 * tb, 32 * kb);
-                ra = mma(frag_nat(l, sm.h, LDK, 16 * vb, 32 * kb), mf::neg(kt), ra);
-                da = mma(frag_nat(l, sm.dh, LDK, 16 * vb, 32 * kb), kt, da);
+                const int kc = 32 * kb;
+                const bf16x8 kt = frag_nat(l, kh(sm.Ks, kc), LDH, 16 * tb, kcol(kc));
+                ra = mma(frag_nat(l, kh(sm.h, kc), LDH, 16 * vb, kcol(kc)), mf::neg(kt), ra);
+                da = mma(frag_nat(l, kh(sm.dh, kc), LDH, 16 * vb, kcol(kc)), kt, da);
             }
             // (both operands transposed: c-order rows, see mf::frag_trc)
             if (nks == 0) da = mma(frag_trc(l, sm.dO, LD64, 0, 16 * vb), frag_trc(l, sm.Ps, LD64, 0, 16 * tb), da);
@@ -548,10 +577,11 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             const bf16x8 vnb = frag_nat(l, sm.u.s.Vn, LD64, 16 * tb, 32 * ks);
 #pragma unroll
             for (int fb = 0; fb < NF; ++fb) {
-                const bf16x8 ha = frag_tr(l, sm.h, LDK, 32 * ks, 16 * (f0 + fb));
+                const int fcl = 16 * (f0 + fb);
+                const bf16x8 ha = frag_tr(l, kh(sm.h, fcl), LDH, 32 * ks, kcol(fcl));
                 dqa[fb] = mma(ha, dob, dqa[fb]);
                 dka[fb] = mma(ha, dyb, dka[fb]);
-                dka[fb] = mma(frag_tr(l, sm.dh, LDK, 32 * ks, 16 * (f0 + fb)), vnb, dka[fb]);
+                dka[fb] = mma(frag_tr(l, kh(sm.dh, fcl), LDH, 32 * ks, kcol(fcl)), vnb, dka[fb]);
             }
             if (jlive) {
                 const bf16x8 dvb = frag_nat(l, sm.u.s.dVn, LD64, 16 * tb, 32 * ks);
@@ -608,10 +638,10 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
-            dqa[fb] = mma(frag_tr(l, sm.Ks, LDK, 0, fc), m0, dqa[fb]);
-            if (tb >= 2) dqa[fb] = mma(frag_tr(l, sm.Ks, LDK, 32, fc), m1, dqa[fb]);
-            if (nks == 0) dka[fb] = mma(frag_trc(l, sm.Qs, LDK, 0, fc), c0, dka[fb]);
-            dka[fb] = mma(frag_trc(l, sm.Qs, LDK, 32, fc), c1, dka[fb]);
+            dqa[fb] = mma(frag_tr(l, kh(sm.Ks, fc), LDH, 0, kcol(fc)), m0, dqa[fb]);
+            if (tb >= 2) dqa[fb] = mma(frag_tr(l, kh(sm.Ks, fc), LDH, 32, kcol(fc)), m1, dqa[fb]);
+            if (nks == 0) dka[fb] = mma(frag_trc(l, kh(sm.Qs, fc), LDH, 0, kcol(fc)), c0, dka[fb]);
+            dka[fb] = mma(frag_trc(l, kh(sm.Qs, fc), LDH, 32, kcol(fc)), c1, dka[fb]);
         }
     }
     __syncthreads();
@@ -632,7 +662,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             floatx4 gg = zero4();
 #pragma unroll
             for (int k0 = 0; k0 < K; k0 += 32)
-                gg = mma(frag_row(l, sm.Ks, LDK, pim(J, r), k0), frag_nat(l, sm.Ks, LDK, 16 * tb, k0), gg);
+                gg = mma(frag_row(l, kh(sm.Ks, k0), LDH, pim(J, r), kcol(k0)),
+                         frag_nat(l, kh(sm.Ks, k0), LDH, 16 * tb, kcol(k0)), gg);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int j = pim(J, 4 * g + i);
@@ -657,7 +688,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
-            const bf16x8 k0 = frag_tr(l, sm.Ks, LDK, 0, fc), k1 = frag_tr(l, sm.Ks, LDK, 32, fc);
+            const bf16x8 k0 = frag_tr(l, kh(sm.Ks, fc), LDH, 0, kcol(fc)),
+                         k1 = frag_tr(l, kh(sm.Ks, fc), LDH, 32, kcol(fc));
             dka[fb] = mma(k0, a0, dka[fb]);
             if (tb >= 2) dka[fb] = mma(k1, a1, dka[fb]);
             if (nks == 0) dka[fb] = mma(k0, b0, dka[fb]);
@@ -668,7 +700,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     bf16x4 kfin[NF];
 #pragma unroll
     for (int fb = 0; fb < NF; ++fb)
-        kfin[fb] = *reinterpret_cast<const bf16x4*>(sm.Ks + t * LDK + 16 * (f0 + fb) + 4 * g);
+        kfin[fb] = *reinterpret_cast<const bf16x4*>(kh(sm.Ks, 16 * (f0 + fb)) + t * LDH +
+                                                    kcol(16 * (f0 + fb)) + 4 * g);
     __syncthreads();
     if (more) copy_k(nxt, l);
     float dbt = sm.dbh[0][t];  // dL/db for token t

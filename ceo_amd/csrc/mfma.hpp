@@ -230,6 +230,15 @@ struct TileRegs {
 #pragma unroll
         for (int j = 0; j < TPT; ++j) *reinterpret_cast<bf16x8*>(dst + (t + j) * ldr + 8 * f) = x[j];
     }
+    // row-major copy into column halves of 64: element (t, c) at
+    // dst + (c / 64) * half + t * ldr + c % 64
+    __device__ __forceinline__ void store_rows_split(bf16* dst, int ldr, int half) {
+        mask();
+        const int f = fg(), t = t0();
+#pragma unroll
+        for (int j = 0; j < TPT; ++j)
+            *reinterpret_cast<bf16x8*>(dst + (8 * f >> 6) * half + (t + j) * ldr + (8 * f & 63)) = x[j];
+    }
     // transposed [d][t] copy, row stride ldt (TPT consecutive tokens per write)
     __device__ __forceinline__ void store_cols(bf16* dst, int ldt) {
         mask();
