@@ -239,13 +239,13 @@ constexpr int rfast_threads() {
 // ---------------------------------------------------------------------------
 // A segment's (SEGF tokens) per-token rows in LDS: k, c k in fp32 (CKS), dO
 // (DO), this workgroup's NC value columns of v (VS), c and dc/dlambda (DC).
-template <int D, int NC, bool DO, bool CKS, bool VS, bool DC>
+template <int D, int NC, bool DO, bool CKS, bool VS, bool DC, int SG = SEGF>
 struct SegLds {
-    bf16 kb[SEGF][D];
-    bf16 gb[DO ? SEGF : 1][D];
-    float ckf[CKS ? SEGF : 1][D];
-    bf16 vb[VS ? SEGF : 1][NC];
-    float cc[SEGF], dcc[DC ? SEGF : 1];
+    bf16 kb[SG][D];
+    bf16 gb[DO ? SG : 1][D];
+    float ckf[CKS ? SG : 1][D];
+    bf16 vb[VS ? SG : 1][NC];
+    float cc[SG], dcc[DC ? SG : 1];
 };
 
 // The same rows on their way in: load() issues the global reads of a segment
@@ -253,11 +253,11 @@ struct SegLds {
 // current segment's work); store() writes them to SegLds once the current
 // segment's readers are done.  Pieces of VW = d / 16 elements (d / 8 bytes,
 // the alignment the host checks for k, dO and v) spread over the NT threads.
-template <int D, int NC, int NT, bool DO, bool CKS, bool VS, bool DC>
+template <int D, int NC, int NT, bool DO, bool CKS, bool VS, bool DC, int SG = SEGF>
 struct SegRows {
     static constexpr int VW = D / 16;
-    static constexpr int NKP = SEGF * D / VW, IK = (NKP + NT - 1) / NT;   // k / dO pieces
-    static constexpr int NVP = SEGF * NC / VW, IV = (NVP + NT - 1) / NT;  // v pieces
+    static constexpr int NKP = SG * D / VW, IK = (NKP + NT - 1) / NT;   // k / dO pieces
+    static constexpr int NVP = SG * NC / VW, IV = (NVP + NT - 1) / NT;  // v pieces
     typedef __attribute__((__vector_size__(VW * sizeof(__bf16)))) __bf16 bfV;
     bfV kx[IK], gx[DO ? IK : 1], vx[VS ? IV : 1];
     float cx[CKS ? IK : 1], cs, dcs;
@@ -289,7 +289,7 @@ struct SegRows {
         }
     }
 
-    __device__ __forceinline__ void store(SegLds<D, NC, DO, CKS, VS, DC>& sl, int n, int tid) const {
+    __device__ __forceinline__ void store(SegLds<D, NC, DO, CKS, VS, DC, SG>& sl, int n, int tid) const {
 #pragma unroll
         for (int it = 0; it < IK; ++it) {
             const int i = tid + it * NT, j = i / (D / VW), e0 = (i % (D / VW)) * VW;
@@ -314,30 +314,32 @@ struct SegRows {
     }
 };
 
-template <int D, int NS>
+template <int D, int NS, int SG>
 struct RFastSmem {
     static constexpr bool CKS = NS > 1;  // c k staged (fp32); else formed per row
     bf16 Sl[4][(D / NS) * (D + 8)];      // new states [c][row]: two tokens, double-buffered
-    SegLds<D, D / NS, false, CKS, true, false> seg;
+    SegLds<D, D / NS, false, CKS, true, false, SG> seg;
 };
 
-template <int D, int NS, int LPC>
+// SG: tokens staged per segment (chunk_size's tuning hint; the results do not
+// depend on it)
+template <int D, int NS, int LPC, int SG>
 __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
     bf16* __restrict__ state, bf16* __restrict__ out, float* __restrict__ part_out, long pstride,
     int H, long T) {
     constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
     constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
-    constexpr bool CKS = RFastSmem<D, NS>::CKS;
+    constexpr bool CKS = RFastSmem<D, NS, SG>::CKS;
     static_assert(RPL % 8 == 0 && (D == 64 || D == 128) && NC % 32 == 0 && NT % 64 == 0 &&
-                      NT <= 1024 && D % (16 * NW) == 0,
+                      NT <= 1024 && D % (16 * NW) == 0 && SG % 2 == 0,
                   "d = 64 or 128, 32-column multiples per workgroup");
-    __shared__ __attribute__((aligned(16))) RFastSmem<D, NS> sm;
+    __shared__ __attribute__((aligned(16))) RFastSmem<D, NS, SG> sm;
     const int tid = threadIdx.x, w = mf::wave(), l = mf::lane();
     const int bh = blockIdx.x / NS, cb = blockIdx.x % NS;
     const int col = cb * NC + tid / LPC, lcol = tid / LPC, part = tid % LPC, r0 = part * RPL;
     const int b = bh / H, h = bh % H;
-    const long dd = (long)D * D, nsegf = (T + SEGF - 1) / SEGF;
+    const long dd = (long)D * D, nsegf = (T + SG - 1) / SG;
     const long tstride = (long)H * D;  // elements between tokens
     const long base0 = (long)b * T * tstride + (long)h * D;
     const float* cbh = coef + (long)bh * T;
@@ -440,20 +442,20 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
                        Sp[4 * q + 2][0], Sp[4 * q + 2][1], Sp[4 * q + 3][0], Sp[4 * q + 3][1]};
     };
 
-    SegRows<D, NC, NT, false, CKS, true, false> rows;
-    rows.load(k, nullptr, v, cbh, nullptr, base0, tstride, 0, (int)(T < SEGF ? T : SEGF), cb * NC,
+    SegRows<D, NC, NT, false, CKS, true, false, SG> rows;
+    rows.load(k, nullptr, v, cbh, nullptr, base0, tstride, 0, (int)(T < SG ? T : SG), cb * NC,
               tid);
     long P = 0;  // token pairs so far (selects the Sl buffers)
     for (long seg = 0; seg < nsegf; ++seg) {
-        const long t0 = seg * SEGF;
-        const int n = (int)(T - t0 < SEGF ? T - t0 : SEGF);
+        const long t0 = seg * SG;
+        const int n = (int)(T - t0 < SG ? T - t0 : SG);
         __syncthreads();  // the previous segment's rows read (its last o_reads)
         rows.store(sm.seg, n, tid);
         __syncthreads();
         if (seg + 1 < nsegf) {
-            const long t2 = t0 + SEGF;
+            const long t2 = t0 + SG;
             rows.load(k, nullptr, v, cbh, nullptr, base0, tstride, t2,
-                      (int)(T - t2 < SEGF ? T - t2 : SEGF), cb * NC, tid);
+                      (int)(T - t2 < SG ? T - t2 : SG), cb * NC, tid);
         }
         // pairs of tokens: both updates, both new states to LDS, the previous
         // pair's o products, one barrier, this pair's o fragments
@@ -856,15 +858,23 @@ inline int r_split(size_t nbh) {
 }
 
 template <int D, int NS, int LPC>
-void r_launch_fwd(bool checkpoints, const void* k, const void* v, const float* coef, void* state,
-                  void* out, float* part, long pstride, bf16* ck, int H, long T, size_t nbh,
-                  hipStream_t stream) {
+void r_launch_fwd(bool checkpoints, int sg, const void* k, const void* v, const float* coef,
+                  void* state, void* out, float* part, long pstride, bf16* ck, int H, long T,
+                  size_t nbh, hipStream_t stream) {
     const dim3 grid((unsigned)(nbh * NS)), block(rfast_threads<D, NS, LPC>());
     if (checkpoints)
         EFLA_LAUNCH("efla_r_checkpoint", (r_ckpt_kernel<D, NS, LPC>), grid, block, stream,
                     (const bf16*)k, (const bf16*)v, coef, (const bf16*)state, ck, H, T);
+    else if (sg == 16)
+        EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, 16>), grid, block, stream,
+                    (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part, pstride,
+                    H, T);
+    else if (sg == 64 && (NS > 1 || D == 64))  // the LDS of the other shapes holds 32 at most
+        EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, (NS > 1 || D == 64) ? 64 : 32>),
+                    grid, block, stream, (const bf16*)k, (const bf16*)v, coef, (bf16*)state,
+                    (bf16*)out, part, pstride, H, T);
     else
-        EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC>), grid, block, stream,
+        EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, 32>), grid, block, stream,
                     (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part, pstride,
                     H, T);
 }
@@ -882,17 +892,24 @@ void r_launch_bwd(const void* dO, const void* k, const void* v, const float* coe
 
 // the register-resident forward (checkpoints = false) or checkpoint pass for
 // head_dim d and split ns
-inline void r_fwd_fast(int d, int ns, bool checkpoints, const void* k, const void* v,
+inline void r_fwd_fast(int d, int ns, bool checkpoints, int sg, const void* k, const void* v,
                        const float* coef, void* state, void* out, float* part, long pstride,
                        bf16* ck, int H, long T, size_t nbh, hipStream_t stream) {
     if (d == 128 && ns == 1)
-        r_launch_fwd<128, 1, 4>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+        r_launch_fwd<128, 1, 4>(checkpoints, sg, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
     else if (d == 128)
-        r_launch_fwd<128, 2, 8>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+        r_launch_fwd<128, 2, 8>(checkpoints, sg, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
     else if (ns == 1)
-        r_launch_fwd<64, 1, 4>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+        r_launch_fwd<64, 1, 4>(checkpoints, sg, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
     else
-        r_launch_fwd<64, 2, 8>(checkpoints, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+        r_launch_fwd<64, 2, 8>(checkpoints, sg, k, v, coef, state, out, part, pstride, ck, H, T, nbh, stream);
+}
+
+// chunk_size as the forward's segment length: 16, 32 or 64 tokens staged in
+// LDS at once (the largest not above it, at least 16; 0 picks 32)
+inline int r_segment(size_t chunk_size) {
+    if (chunk_size == 0) return SEGF;
+    return chunk_size >= 64 ? 64 : chunk_size >= 32 ? 32 : 16;
 }
 
 inline void r_combine(const float* part, long pstride, int ns, void* out, size_t elems,
@@ -1090,7 +1107,8 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
                                 size_t batch_size, size_t seq_len, size_t num_heads,
                                 size_t head_dim, float beta, size_t chunk_size,
                                 hipStream_t stream) {
-    (void)chunk_size;  // accepted and ignored, as efla.cu:495
+    // chunk_size (ignored by the reference, efla.cu:495) is the register-resident
+    // forward's segment length hint; the results do not depend on it
     if (batch_size == 0 || num_heads == 0 || head_dim == 0) return kInvalidValue;
     if (seq_len == 0) return kSuccess;
     if (!k || !v || !state || !output) return kInvalidValue;
@@ -1130,8 +1148,8 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
                         (float*)ws, (float*)nullptr, (int)num_heads, (long)seq_len, beta,
                         (long)ntok);
-        r_fwd_fast((int)head_dim, ns, false, k, v, (const float*)ws, state, output, part,
-                   (long)elems, nullptr, (int)num_heads, (long)seq_len, nbh, stream);
+        r_fwd_fast((int)head_dim, ns, false, r_segment(chunk_size), k, v, (const float*)ws, state,
+                   output, part, (long)elems, nullptr, (int)num_heads, (long)seq_len, nbh, stream);
         if (ns > 1) r_combine(part, (long)elems, ns, output, elems, stream);
     } else {
         EFLA_LAUNCH("efla_r_forward", r_forward_kernel, grid, dim3(NTH), stream, (const bf16*)k,
@@ -1194,7 +1212,7 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
         else
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<4>, cg, dim3(NTH), stream, (const bf16*)k,
                         coef, dcoef, (int)num_heads, (long)seq_len, beta, (long)ntok);
-        r_fwd_fast((int)head_dim, ns, true, k, v, coef, (void*)state, nullptr, nullptr, 0, ck,
+        r_fwd_fast((int)head_dim, ns, true, SEGF, k, v, coef, (void*)state, nullptr, nullptr, 0, ck,
                    (int)num_heads, (long)seq_len, nbh, stream);
         const int H = (int)num_heads;
         const long T = (long)seq_len, ps = (long)elems;

@@ -52,7 +52,11 @@ def _require(t, name, dtype=None, device=None, contiguous=True):
 # ---------------------------------------------------------------------------
 def efla_forward(k: torch.Tensor, v: torch.Tensor, state: torch.Tensor, beta: float,
                  chunk_size: int = 64) -> torch.Tensor:
-    """eflaForwardCuda: o_t = S_t k_t; ``state`` (B*H, d, d) bf16 is updated in place."""
+    """eflaForwardCuda: o_t = S_t k_t; ``state`` (B*H, d, d) bf16 is updated in place.
+
+    ``chunk_size`` (ignored by the reference) is a tuning hint: for d = 64 / 128
+    the number of tokens (16, 32 or 64) staged in LDS at once; the results do
+    not depend on it."""
     B, T, H, d = k.shape
     for t, n in ((k, "k"), (v, "v"), (state, "state")):
         _require(t, n, torch.bfloat16, k.device)

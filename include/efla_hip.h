@@ -47,8 +47,10 @@ extern "C" {
  *   lambda = |k_t|^2, c = (1 - exp(-beta lambda)) / lambda,
  *   S <- bf16(S + c k_t (v_t - S^T k_t)^T), o_t = S k_t   (requires d_k == d_v)
  * k, v, output: (B, T, H, d) bf16.  state: (B*H, d, d) bf16, read as S_0 and
- * overwritten with S_T.  chunk_size is accepted and ignored, as in the
- * reference.  Validation order: B, H or d == 0 -> 1; T == 0 -> 0; any null
+ * overwritten with S_T.  chunk_size (ignored by the reference) is a tuning
+ * hint: for d = 64 / 128 the number of tokens staged in LDS at once (16, 32 or
+ * 64: the largest not above it, at least 16; 0 -> 32); the results do not
+ * depend on it.  Validation order: B, H or d == 0 -> 1; T == 0 -> 0; any null
  * pointer -> 1; B*H or sizes overflowing -> 9.
  * Scratch comes from the stream's cached workspace (leased per call): 4 bytes
  * per (b, t, h) for the coefficients, and for d = 64 / 128 with B*H at most

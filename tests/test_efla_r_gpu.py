@@ -149,6 +149,31 @@ def test_misaligned_k_takes_the_generic_kernels(oracle):
         assert max(errs) <= 2e-2
 
 
+@pytest.mark.parametrize("B,T,H,d", [(1, 150, 2, 128), (2, 100, 65, 128), (2, 77, 2, 64)])
+def test_forward_chunk_size_hint_leaves_results_unchanged(oracle, B, T, H, d):
+    """chunk_size picks how many tokens the register-resident forward stages in
+    LDS at once (16, 32, 64; 0 -> 32); the per-token arithmetic is the same, so
+    output and final state are bit-identical for every value."""
+    from ceo_amd.efla import efla_forward
+
+    announce(f"efla_forward_hip chunk_size hint B={B} T={T} H={H} d={d}")
+    k, v, _, s0 = _inputs(oracle, 1300 + d + H, B, T, H, d, 0.2)
+    kd, vd = _u16_to_dev(k), _u16_to_dev(v)
+    res = []
+    for cs in (0, 16, 32, 64, 100):
+        st = _u16_to_dev(s0)
+        o = efla_forward(kd, vd, st, 0.6, cs)
+        torch.cuda.synchronize()
+        res.append((_dev_to_u16(o), _dev_to_u16(st)))
+    for o, st in res[1:]:
+        assert np.array_equal(o, res[0][0]) and np.array_equal(st, res[0][1])
+    st_ref = s0.copy()
+    _, o_ref = oracle.r_forward(k, v, st_ref, B, T, H, d, 0.6)
+    eo = rel_l2(oracle.bf16_to_f32(res[0][0]), oracle.bf16_to_f32(o_ref))
+    print(f"  bit-identical over chunk_size 0/16/32/64/100; rel-L2 o={eo:.2e}", flush=True)
+    assert eo <= 2e-2
+
+
 def test_backward_zero_length_zeroes_grad_state(oracle):
     from ceo_amd._lib import lib
 
