@@ -5,24 +5,30 @@
 //   lambda = |k_t|^2, c = c(beta, lambda)
 //   u = S^T k_t, S <- bf16(S + (c k_t)(v_t - u)^T)   (state re-rounded every token)
 //   o_t = S k_t                                        (needs d_k == d_v)
-// One workgroup owns one (b, h); the work of a token is serial, so a token's
-// cost is its chain of dependent steps.  For d = 64 and 128 (16-byte aligned
-// k) the state lives in registers: consecutive lanes own one value column,
-// S^T k and the update are lane-local, and o = S k (a sum over columns) is
-// formed by MFMAs from a transposed LDS copy of the new state; one barrier
-// per token, k / v / c loaded two tokens ahead, every token's c(beta, |k|^2)
-// from a separate parallel kernel (r_fast_kernel).  Other d keep the state
-// in LDS (row stride d+2): two LDS passes and four barriers per token against
-// the reference's three global passes and ~13 barriers (r_forward_kernel).
+// The work of a token is serial per (b, h), so a token's cost is its chain of
+// dependent steps.  For d = 64 and 128 (k, v, dO aligned to d / 8 bytes) the
+// state lives in registers (r_fast_kernel): consecutive lanes own one value
+// column, S^T k and the update are lane-local, and o = S k (a sum over
+// columns) is formed by MFMAs from a transposed LDS copy of the new state, one
+// barrier per token pair.  The value columns evolve independently, so when
+// B H leaves half of the CUs idle each (b, h) is split over two workgroups of
+// half the columns (fp32 row-sum slices added by r_combine_kernel).  Each
+// segment's k, c k and v are staged in LDS at once, the next segment's reads
+// in flight; every token's c(beta, |k|^2) comes from a separate parallel
+// kernel.  Other d keep one workgroup per (b, h) and the state in LDS (row
+// stride d+2): two LDS passes and four barriers per token against the
+// reference's three global passes and ~13 barriers (r_forward_kernel).
 // Reduction order differs from the reference's serial sums; values differ at
 // fp32 rounding level before each bf16 rounding.
 //
 // The backward recomputes states from bf16 checkpoints (exact, since the
 // states are bf16 values), rebuilds one segment's states at a time into a
 // workspace, and runs the reference's BPTT (efla.cu:315-454) over the segment
-// in reverse: for d = 64 / 128 with 32-token segments and dL/dS in fp32
-// registers (r_bwd_fast_kernel, one barrier per token), otherwise with
-// 64-token segments and dL/dS in LDS (d <= 128) or the workspace (d <= 256).
+// in reverse: for d = 64 / 128 with 32-token segments, dL/dS in fp32
+// registers and the same column split (r_ckpt_kernel for the checkpoints,
+// r_bwd_fast_kernel: a barrier-free rebuild, one barrier per reverse token),
+// otherwise with 64-token segments and dL/dS in LDS (d <= 128) or the
+// workspace (d <= 256).
 #include <hip/hip_runtime.h>
 
 #include "../../include/efla_hip.h"
