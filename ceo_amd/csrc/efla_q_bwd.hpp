@@ -351,7 +351,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     const bf16* __restrict__ dhist, SeqInfo si, int H, int nitems,
     bf16* __restrict__ dq, bf16* __restrict__ dk, bf16* __restrict__ dv,
     bf16* __restrict__ dbeta, TokLd ld) {
-    constexpr int NT8 = grad_threads<NG>(), NW = NT8 / 64;
+    constexpr int NTG = grad_threads<NG>(), NW = NTG / 64;  // threads, waves
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 16 / NG;  // NF key tiles per group
     // K-wide operand tiles (Qs, Ks, h, dh) are kept as K / 64 column halves of
     // 64 with row stride LDH (72 for K = 128: the same 64 x LDK elements, but
@@ -377,8 +377,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     constexpr int EG = 4 / NG;  // value tiles / 16-token blocks per group
     // threads holding the v, dO slice and the h, dh slice prefetches (one
     // 16-byte piece each at most)
-    constexpr int NTV = NT8 < 64 * VS / 8 ? NT8 : 64 * VS / 8;
-    constexpr int NTH = NT8 < 64 * K / 8 ? NT8 : 64 * K / 8;
+    constexpr int NTV = NTG < 64 * VS / 8 ? NTG : 64 * VS / 8;
+    constexpr int NTH = NTG < 64 * K / 8 ? NTG : 64 * K / 8;
     static_assert(NG == 2 || NG == 4, "8 or 16 waves");
     __shared__ __attribute__((aligned(16))) GradSmem<K, NG> sm;
     const int w8 = mf::wave(), tb = w8 & 3, hf = w8 >> 2;
@@ -423,7 +423,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     Item cur;
     if (!locate(it, cur)) return;  // uniform over the workgroup
     if constexpr (!PS)  // P's tiles above the diagonal are never written
-        for (int i = threadIdx.x; i < 64 * LD64; i += NT8) sm.Ps[i] = (bf16)0.f;
+        for (int i = threadIdx.x; i < 64 * LD64; i += NTG) sm.Ps[i] = (bf16)0.f;
     copy_slice0(cur, par, mf::lane());
     copy_q(cur, mf::lane());
     copy_t(cur, mf::lane());
@@ -442,11 +442,11 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     mf::TileRegs<64, K, NTH> rh, rdh;
     auto prefetch = [&](int s) {
         const int vv = s * VS;
-        if (NTV == NT8 || tid < NTV) {
+        if (NTV == NTG || tid < NTV) {
             rv.load(v + bos * ld.v + (long)h * V + vv, ld.v, len, tid);
             rd.load(dO + (bos * H + h) * V + vv, (long)H * V, len, tid);
         }
-        if (NTH == NT8 || tid < NTH) {
+        if (NTH == NTG || tid < NTH) {
             rh.load(hist + chb + (long)vv * K, K, 64, tid);
             rdh.load(dhist + chb + (long)vv * K, K, 64, tid);
         }
@@ -459,13 +459,13 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     const bool more = locate(it + (int)gridDim.x, nxt);
     __syncthreads();  // every wave's copies have landed
     if (len < 64) {  // a sequence's last chunk: token rows past its end read as zero
-        for (int i = tid; i < (64 - len) * (K / 8); i += NT8) {
+        for (int i = tid; i < (64 - len) * (K / 8); i += NTG) {
             const int c = 8 * (i % (K / 8));
             const int o = (KH > 1 ? (c >> 6) * HALF : 0) + (len + i / (K / 8)) * LDH + kcol(c);
             *reinterpret_cast<bf16x8*>(sm.Qs + o) = bf16x8{};
             *reinterpret_cast<bf16x8*>(sm.Ks + o) = bf16x8{};
         }
-        for (int i = tid; i < (64 - len) * (VS / 8); i += NT8) {
+        for (int i = tid; i < (64 - len) * (VS / 8); i += NTG) {
             const int o = (len + i / (VS / 8)) * LD64 + 8 * (i % (VS / 8));
             *reinterpret_cast<bf16x8*>(sm.V + o) = bf16x8{};
             *reinterpret_cast<bf16x8*>(sm.dO + o) = bf16x8{};
@@ -506,11 +506,11 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         const int vv = s * VS;
         if (s > 0) {  // slice 0 was copied in with the item's other inputs
             __syncthreads();
-            if (NTV == NT8 || tid < NTV) {
+            if (NTV == NTG || tid < NTV) {
                 rv.store_rows(sm.V, LD64);
                 rd.store_rows(sm.dO, LD64);
             }
-            if (NTH == NT8 || tid < NTH) {
+            if (NTH == NTG || tid < NTH) {
                 if constexpr (KH > 1) {
                     rh.store_rows_split(sm.h, LDH, HALF);
                     rdh.store_rows_split(sm.dh, LDH, HALF);
@@ -561,7 +561,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
         __syncthreads();
-        if (NTV == NT8 || tid < NTV) {  // dv = D Y of this slice from its bf16 copy in V, as whole 16-byte row pieces
+        if (NTV == NTG || tid < NTV) {  // dv = D Y of this slice from its bf16 copy in V, as whole 16-byte row pieces
             static_assert(NTV == 64 * (VS / 8), "one piece per thread");
             const int tt = tid / (VS / 8), f = 8 * (tid % (VS / 8));
             if (tt < len)
@@ -724,7 +724,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         }
         if (t < len && hf == 0 && g == 0) dbeta[(bos + t) * H + h] = (bf16)(dbt * cf[128 + t]);
         __syncthreads();
-        for (int i = tid; i < 64 * (K / 8); i += NT8) {
+        for (int i = tid; i < 64 * (K / 8); i += NTG) {
             const int tt = i / (K / 8), f = 8 * (i % (K / 8));
             if (tt < len) {
                 const long o = (long)h * K + f;
