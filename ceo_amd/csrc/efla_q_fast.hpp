@@ -73,13 +73,13 @@ __device__ __forceinline__ void store_state_frag(bf16* __restrict__ hist, const 
 // prep
 // ---------------------------------------------------------------------------
 // G = K K^T and T = (I + strict_lower(D G))^{-1} are kept as their ten lower
-// 16x16 tiles, packed, fp32 (row stride 17 for G, 20 for T), T in the space k
-// occupies until G is formed: 29 KB of LDS, so five workgroups fit on a CU
-// (the kernel is a chain of short dependent phases and runs as fast as it has
-// workgroups in flight).
+// 16x16 tiles, packed, fp32 (row stride 17 for G, 16 for T), both in the space
+// k occupies until G is formed: 21 KB of LDS for K = 128, so seven workgroups
+// fit on a CU (the kernel is a chain of short dependent phases and runs as
+// fast as it has workgroups in flight).
 constexpr int PT_LD = 17;  // G tiles
 constexpr int PT_SZ = 16 * PT_LD;
-constexpr int PTT_LD = 20;  // T tiles: 16-byte aligned rows for the bf16 write-out
+constexpr int PTT_LD = 16;  // T tiles: 16-byte aligned rows for the bf16 write-out
 constexpr int PTT_SZ = 16 * PTT_LD;
 
 // packed offset of lower tile (I, J), I >= J, for tiles of `sz` floats
@@ -91,9 +91,11 @@ template <int K>
 struct PrepSmem {
     union {
         bf16 Kr[64 * ldb<K>()];  // k, until K K^T is formed
-        float T[10 * PTT_SZ];    // lower tiles of (I + A)^{-1}
+        struct {
+            float G[10 * PT_SZ];   // lower tiles of K K^T
+            float T[10 * PTT_SZ];  // lower tiles of (I + A)^{-1}
+        } f;
     } u;
-    float G[10 * PT_SZ];  // lower tiles of K K^T
     float lam[64];
     float b[64];
 };
@@ -138,23 +140,39 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
             dcout[cid * 128 + 64 + t] = dcb;
         }
     }
-    // G = K K^T, lower tiles
-    for (int n = w; n < 10; n += 4) {
-        int I, J;
-        lower_tile(n, I, J);
-        floatx4 acc = zero4();
+    // G = K K^T, lower tiles (wave w: tiles w, w + 4, w + 8), held in
+    // registers until every wave is done with k, whose space G and T take
+    floatx4 gacc[3];
 #pragma unroll
-        for (int k0 = 0; k0 < K; k0 += 32)
-            acc = mma(frag_nat(sm.u.Kr, LDK, 16 * I, k0), frag_nat(sm.u.Kr, LDK, 16 * J, k0), acc);
-        float* Gt = sm.G + ptile(I, J);
+    for (int u = 0; u < 3; ++u) {
+        const int n = w + 4 * u;
+        gacc[u] = zero4();
+        if (n < 10) {
+            int I, J;
+            lower_tile(n, I, J);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Gt[(4 * g + i) * PT_LD + r] = acc[i];
+            for (int k0 = 0; k0 < K; k0 += 32)
+                gacc[u] = mma(frag_nat(sm.u.Kr, LDK, 16 * I, k0),
+                              frag_nat(sm.u.Kr, LDK, 16 * J, k0), gacc[u]);
+        }
     }
-    __syncthreads();  // k is dead from here; T takes its place
+    __syncthreads();  // k is dead from here
+#pragma unroll
+    for (int u = 0; u < 3; ++u) {
+        const int n = w + 4 * u;
+        if (n < 10) {
+            int I, J;
+            lower_tile(n, I, J);
+            float* Gt = sm.u.f.G + ptile(I, J);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) Gt[(4 * g + i) * PT_LD + r] = gacc[u][i];
+        }
+    }
+    __syncthreads();
     // diagonal 16x16 blocks of T by forward substitution (lane = column)
     if (l < 16) {
         const int base = 16 * w;
-        const float* Gd = sm.G + ptile(w, w);
+        const float* Gd = sm.u.f.G + ptile(w, w);
         float x[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
@@ -163,7 +181,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
             for (int j = 0; j < i; ++j) s += Gd[i * PT_LD + j] * x[j];
             x[i] = (i == l ? 1.f : 0.f) - sm.b[base + i] * s;
         }
-        float* Td = sm.u.T + ptile(w, w, PTT_SZ);
+        float* Td = sm.u.f.T + ptile(w, w, PTT_SZ);
 #pragma unroll
         for (int i = 0; i < 16; ++i) Td[i * PTT_LD + l] = x[i];
     }
@@ -176,14 +194,14 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
             floatx4 y = zero4();
             for (int m = 16 * J; m < 16 * I; m += 4) {
                 const int mb = m >> 4, mo = (m & 15) + g;
-                y = mma_f32(bi * sm.G[ptile(I, mb) + r * PT_LD + mo],
-                            sm.u.T[ptile(mb, J, PTT_SZ) + mo * PTT_LD + r], y);
+                y = mma_f32(bi * sm.u.f.G[ptile(I, mb) + r * PT_LD + mo],
+                            sm.u.f.T[ptile(mb, J, PTT_SZ) + mo * PTT_LD + r], y);
             }
-            const float* Tii = sm.u.T + ptile(I, I, PTT_SZ) + r * PTT_LD + 4 * g;
+            const float* Tii = sm.u.f.T + ptile(I, I, PTT_SZ) + r * PTT_LD + 4 * g;
             floatx4 t = zero4();
 #pragma unroll
             for (int i = 0; i < 4; ++i) t = mma_f32(Tii[i], y[i], t);
-            float* Tij = sm.u.T + ptile(I, J, PTT_SZ);
+            float* Tij = sm.u.f.T + ptile(I, J, PTT_SZ);
 #pragma unroll
             for (int i = 0; i < 4; ++i) Tij[(4 * g + i) * PTT_LD + r] = -t[i];
         }
@@ -195,7 +213,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
         bf16x8 lo, hi;
         if (J <= I) {
             const floatx4* src =
-                reinterpret_cast<const floatx4*>(sm.u.T + ptile(I, J, PTT_SZ) + i * PTT_LD);
+                reinterpret_cast<const floatx4*>(sm.u.f.T + ptile(I, J, PTT_SZ) + i * PTT_LD);
             float v[16];
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
