@@ -199,6 +199,51 @@ def test_packed_batch_runs_sequences_independently(oracle):
             assert torch.equal(big[:, a:b], small), s
 
 
+@pytest.mark.parametrize("reuse", [False, True], ids=["recompute", "reuse-states"])
+def test_many_sequences_scans_match_per_sequence_runs(oracle, reuse):
+    """A varlen batch whose state scans have more (sequence, head, value
+    slice) workgroups than the GPU has CUs, so they run in several rounds,
+    and whose gradient kernel meets sequence boundaries inside its items'
+    loop: each sequence's outputs and gradients must match its own run bit
+    for bit, with the forward's states reused and recomputed."""
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd, new_workspace
+
+    H, K, V = 4, 128, 128
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    nseq = cus // (H * V // 64) + 9  # scan grid above the CU count
+    announce(f"{nseq} sequences (scan grid {nseq * H * V // 64} > {cus} CUs) == per-sequence runs")
+    rng = np.random.default_rng(21)
+    lens = [int(x) for x in rng.integers(1, 200, nseq)]
+    ntok = sum(lens)
+    cu_np = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    x = oracle.make_efla_inputs(6, ntok, H, K, V, bf16=True)
+    g = {n: to_dev(a, torch.bfloat16, (1, ntok, H, K) if n in "qk" else
+                   (1, ntok, H) if n == "beta" else (1, ntok, H, V)) for n, a in x.items()}
+    cu = torch.from_numpy(cu_np).to("cuda")
+
+    def run(t, cu_t):
+        if reuse:
+            ws = new_workspace(t["q"], t["v"], cu_t)
+            o, _ = chunk_efla_fwd(t["q"], t["k"], t["v"], t["beta"], cu_seqlens=cu_t, workspace=ws,
+                                  save_states=True)
+            gr = chunk_efla_bwd(t["q"], t["k"], t["v"], t["beta"], t["do"], cu_seqlens=cu_t,
+                                workspace=ws, reuse_forward=True, reuse_states=True)
+        else:
+            o, _ = chunk_efla_fwd(t["q"], t["k"], t["v"], t["beta"], cu_seqlens=cu_t)
+            gr = chunk_efla_bwd(t["q"], t["k"], t["v"], t["beta"], t["do"], cu_seqlens=cu_t)
+        torch.cuda.synchronize()
+        return o.clone(), [u.clone() for u in gr[:4]]
+
+    o, grads = run(g, cu)
+    for s in range(nseq):
+        a, b = int(cu_np[s]), int(cu_np[s + 1])
+        one = {n: t[:, a:b].contiguous() for n, t in g.items()}
+        o1, g1 = run(one, None)
+        assert torch.equal(o[:, a:b], o1), s
+        for big, small in zip(grads, g1):
+            assert torch.equal(big[:, a:b], small), s
+
+
 # The gradient kernel is persistent: min(#CUs, items) workgroups each loop over
 # (chunk, head) items, copying the next item's inputs into LDS while the
 # current one finishes.  At test sizes every workgroup would get one item, so
