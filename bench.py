@@ -96,6 +96,20 @@ def io_bytes(ntok: int, H: int, K: int, V: int, bwd: bool, esize: int = 2) -> fl
     return float(ntok) * per_tok
 
 
+def kernel_io_bytes_per_token_head(K: int, V: int, esize: int = 2) -> dict:
+    """The op's own I/O bytes each kernel accounts for, per (token, head):
+    what it reads of the op's inputs and writes of its outputs.  Intermediates
+    (T, b, chunk states, P) are not algorithmic bytes; the gradient kernel is
+    charged the whole backward I/O (q, k, v, dO, beta in; dq, dk, dv, dbeta
+    out), the forward scan the forward's (q, k, v in, o out)."""
+    return {
+        "efla_q_fwd_prep": (K + 1) * esize,
+        "efla_q_fwd_scan": (2 * K + 2 * V) * esize,
+        "efla_q_bwd_state": (2 * K + V) * esize,
+        "efla_q_bwd_grad": (4 * K + 4 * V + 2) * esize,
+    }
+
+
 # ---------------------------------------------------------------------------
 # inputs
 # ---------------------------------------------------------------------------
@@ -710,18 +724,23 @@ def main() -> int:
         avg_ms = tot_ms / launches
         fl = per_chunk.get(dom, 0.0) * n_chunks * H
         ach = fl / (avg_ms * 1e-3) / 1e12
+        alg_bytes = kernel_io_bytes_per_token_head(
+            K, V, 2 if cfg["dtype"] == "bf16" else 4).get(dom, 0) * ntok * H
+        gbs = alg_bytes / (avg_ms * 1e-3) / 1e9
         traffic = measured_traffic(args.config, dom)
-        roof = {"kernel": dom, "bound": "mfma", "achieved": round(ach, 2),
-                "peak": peak, "unit": "TFLOP/s",
-                "frac": round(ach / peak, 4),
-                "traffic": traffic,
-                "avg_ms": round(avg_ms, 4),
-                "flops_per_launch": fl}
+        mfma = {"achieved": round(ach, 2), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(ach / peak, 4), "flops_per_launch": fl}
+        hbm = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+               "frac": round(gbs / PEAK_HBM_GBS, 4), "algorithmic_bytes_per_launch": alg_bytes}
         if traffic:
-            # the same launch against the HBM roof: its measured bytes over its time
-            gbs = traffic / (avg_ms * 1e-3) / 1e9
-            roof["hbm"] = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                           "frac": round(gbs / PEAK_HBM_GBS, 4)}
+            # what the launch moves (FETCH_SIZE + WRITE_SIZE) over its time
+            hbm["measured_gbs"] = round(traffic / (avg_ms * 1e-3) / 1e9, 1)
+        # the bound is the roof the kernel is closer to
+        bound = "hbm" if hbm["frac"] > mfma["frac"] else "mfma"
+        top = hbm if bound == "hbm" else mfma
+        roof = {"kernel": dom, "bound": bound, "achieved": top["achieved"],
+                "peak": top["peak"], "unit": top["unit"], "frac": top["frac"],
+                "traffic": traffic, "avg_ms": round(avg_ms, 4), "mfma": mfma, "hbm": hbm}
     step_tflops = step_flops / (ms_step * 1e-3) / 1e12
     io = io_bytes(ntok, H, K, V, cfg["bwd"], esize=2 if cfg["dtype"] == "bf16" else 4)
     if recompute is not None:

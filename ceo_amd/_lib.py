@@ -150,6 +150,7 @@ _SIGS = {
     "efla_rt_event_elapsed_ms": (i32, [ctypes.POINTER(f32), vp, vp]),
     "efla_rt_workspace_bytes": (sz, []),
     "efla_rt_workspace_release": (i32, []),
+    "efla_rt_workspace_release_stream": (i32, [vp]),
     "efla_prof_enable": (None, [i32]),
     "efla_prof_reset": (None, []),
     "efla_prof_collect": (i32, []),

@@ -12,7 +12,8 @@
 // columns) is formed by MFMAs from a transposed LDS copy of the new state, one
 // barrier per token pair.  The value columns evolve independently, so when
 // B H leaves half of the CUs idle each (b, h) is split over two workgroups of
-// half the columns (fp32 row-sum slices added by r_combine_kernel).  Each
+// half the columns (their fp32 row sums meet in one zeroed fp32 buffer by
+// atomic adds, rounded once by r_combine_kernel).  Each
 // segment's k, c k and v are staged in LDS at once, the next segment's reads
 // in flight; every token's c(beta, |k|^2) comes from a separate parallel
 // kernel.  Other d keep one workgroup per (b, h) and the state in LDS (row
@@ -230,11 +231,20 @@ __device__ __forceinline__ float wave_sum_q4(float x) {
 // Column split: the state's value columns evolve independently (the update
 // and S^T k touch only their own column), so one (b, h) may be spread over NS
 // workgroups of D / NS columns each, LPC lanes per column.  Only the row sums
-// (o, and the backward's grad_k) span columns: with NS > 1 each workgroup
-// writes its part in fp32 to `part` (NS slices of `pstride` elements, the
-// output's layout) and r_combine_kernel adds the slices and rounds once.
+// (o, and the backward's grad_k) span columns: with NS = 2 each workgroup
+// adds its part into `part` (one zeroed fp32 buffer in the output's layout)
+// with fp32 atomics, and r_combine_kernel rounds the sum once to bf16.  Each
+// element receives exactly two addends onto zero, and fl(fl(0 + x) + y) =
+// fl(x + y) = fl(fl(0 + y) + x), so the result does not depend on which
+// workgroup adds first (4 bytes of scratch per output element).
 // NS = 1, LPC = 4 is one workgroup per (b, h); NS = 2, LPC = 8 gives a grid of
 // 2 B H with half the rows per lane (for B H below the CU count).
+// p[0..3] += a with vector-memory fp32 atomics (no return value)
+__device__ __forceinline__ void atomic_add4(float* p, const mf::floatx4& a) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) unsafeAtomicAdd(p + e, a[e]);
+}
+
 template <int D, int NS, int LPC>
 constexpr int rfast_threads() {
     return D / NS * LPC;
@@ -332,7 +342,7 @@ struct RFastSmem {
 template <int D, int NS, int LPC, int SG>
 __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
     const bf16* __restrict__ k, const bf16* __restrict__ v, const float* __restrict__ coef,
-    bf16* __restrict__ state, bf16* __restrict__ out, float* __restrict__ part_out, long pstride,
+    bf16* __restrict__ state, bf16* __restrict__ out, float* __restrict__ part_out,
     int H, long T) {
     constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
     constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
@@ -398,7 +408,7 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
                         for (int e = 0; e < 4; ++e) ov[e] = (bf16)acc[e];
                         *reinterpret_cast<bf16x4*>(out + o) = ov;
                     } else {
-                        *reinterpret_cast<mf::floatx4*>(part_out + cb * pstride + o) = acc;
+                        atomic_add4(part_out + o, acc);
                     }
                 }
             }
@@ -598,7 +608,7 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
     const bf16* __restrict__ dO, const bf16* __restrict__ k, const bf16* __restrict__ v,
     const float* __restrict__ coef, const float* __restrict__ dcoef, const bf16* __restrict__ ck,
     bf16* __restrict__ hist_all, bf16* __restrict__ grad_k, float* __restrict__ part_gk,
-    long pstride, bf16* __restrict__ grad_v, bf16* __restrict__ grad_state, int H, long T) {
+    bf16* __restrict__ grad_v, bf16* __restrict__ grad_state, int H, long T) {
     constexpr int NC = D / NS, NT = rfast_threads<D, NS, LPC>(), NW = NT / 64;
     constexpr int RPL = D / LPC, NP = RPL / 2, LDS = D + 8;
     constexpr int MT = D / 16 / NW, NK = NC / 32;
@@ -820,7 +830,7 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
                             *reinterpret_cast<bf16x4*>(grad_k + o) =
                                 bf16x4{(bf16)gv4[0], (bf16)gv4[1], (bf16)gv4[2], (bf16)gv4[3]};
                         } else {
-                            *reinterpret_cast<mf::floatx4*>(part_gk + cb * pstride + o) = gv4;
+                            atomic_add4(part_gk + o, gv4);
                         }
                     }
                 }
@@ -838,8 +848,9 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
     for (int i = 0; i < RPL; ++i) gs[(long)(r0 + i) * D + col] = (bf16)G[i];
 }
 
-// out[i] = bf16(sum_s part[s * pstride + i]) over the NS fp32 slices written
-// by the column-split kernels, four elements per thread, slices in order
+// out[i] = bf16(sum_s part[s * pstride + i]) over `ns` fp32 slices, four
+// elements per thread, slices in order (the column-split kernels leave one
+// slice holding the whole fp32 sum: ns = 1)
 __global__ void __launch_bounds__(NTH) r_combine_kernel(const float* __restrict__ part,
                                                         long pstride, int ns,
                                                         bf16* __restrict__ out, long n4) {
@@ -873,15 +884,15 @@ void r_launch_fwd(bool checkpoints, int sg, const void* k, const void* v, const 
                     (const bf16*)k, (const bf16*)v, coef, (const bf16*)state, ck, H, T);
     else if (sg == 16)
         EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, 16>), grid, block, stream,
-                    (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part, pstride,
+                    (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part,
                     H, T);
     else if (sg == 64 && (NS > 1 || D == 64))  // the LDS of the other shapes holds 32 at most
         EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, (NS > 1 || D == 64) ? 64 : 32>),
                     grid, block, stream, (const bf16*)k, (const bf16*)v, coef, (bf16*)state,
-                    (bf16*)out, part, pstride, H, T);
+                    (bf16*)out, part, H, T);
     else
         EFLA_LAUNCH("efla_r_forward", (r_fast_kernel<D, NS, LPC, 32>), grid, block, stream,
-                    (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part, pstride,
+                    (const bf16*)k, (const bf16*)v, coef, (bf16*)state, (bf16*)out, part,
                     H, T);
 }
 
@@ -892,7 +903,7 @@ void r_launch_bwd(const void* dO, const void* k, const void* v, const float* coe
                   hipStream_t stream) {
     EFLA_LAUNCH("efla_r_backward", (r_bwd_fast_kernel<D, NS, LPC>), dim3((unsigned)(nbh * NS)),
                 dim3(rfast_threads<D, NS, LPC>()), stream, (const bf16*)dO, (const bf16*)k,
-                (const bf16*)v, coef, dcoef, ck, hist, (bf16*)grad_k, part, pstride,
+                (const bf16*)v, coef, dcoef, ck, hist, (bf16*)grad_k, part,
                 (bf16*)grad_v, (bf16*)grad_state, H, T);
 }
 
@@ -1134,17 +1145,22 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
                       (uintptr_t)output % 8 == 0 && nbh * seq_len <= ((size_t)1 << 35);
     if (fast) {
         // every token's coefficient first (the stream's workspace), then the
-        // register-resident token loop; with the column split its fp32 row-sum
-        // slices follow the coefficients in the workspace
+        // register-resident token loop; with the column split the fp32 row
+        // sums (one zeroed buffer both halves add into) follow the
+        // coefficients in the workspace
         const size_t ntok = nbh * seq_len;
         const int ns = r_split(nbh);
         const size_t off_p = (ntok * sizeof(float) + 255) & ~(size_t)255;
-        const size_t need = ns > 1 ? off_p + ns * elems * sizeof(float) : ntok * sizeof(float);
+        const size_t need = ns > 1 ? off_p + elems * sizeof(float) : ntok * sizeof(float);
         void* ws = nullptr;
         WsLease lease;
         int rc = workspace_acquire(need, stream, &ws, lease);
         if (rc != kSuccess) return rc;
         float* part = ns > 1 ? (float*)((char*)ws + off_p) : nullptr;
+        if (part) {
+            rc = fill_zero(part, elems * sizeof(float), stream);
+            if (rc != kSuccess) return rc;
+        }
         const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
         if (head_dim == 128)
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
@@ -1156,7 +1172,7 @@ extern "C" int efla_forward_hip(const void* k, const void* v, void* state, void*
                         (long)ntok);
         r_fwd_fast((int)head_dim, ns, false, r_segment(chunk_size), k, v, (const float*)ws, state,
                    output, part, (long)elems, nullptr, (int)num_heads, (long)seq_len, nbh, stream);
-        if (ns > 1) r_combine(part, (long)elems, ns, output, elems, stream);
+        if (ns > 1) r_combine(part, (long)elems, 1, output, elems, stream);
     } else {
         EFLA_LAUNCH("efla_r_forward", r_forward_kernel, grid, dim3(NTH), stream, (const bf16*)k,
                     (const bf16*)v, (bf16*)state, (bf16*)output, (int)num_heads, (long)seq_len,
@@ -1196,12 +1212,12 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
         const size_t off_hist = (ck_elems * 2 + 255) & ~(size_t)255;
         const size_t off_c = (off_hist + hist_elems * 2 + 255) & ~(size_t)255;
         const size_t off_dc = (off_c + ntok * 4 + 255) & ~(size_t)255;
-        // with the column split: grad_k's fp32 slices
+        // with the column split: grad_k's fp32 sums (one zeroed buffer)
         const int ns = r_split(nbh);
         size_t elems = 0;
         if (!mul_ok(ntok, head_dim, &elems)) return kInvalidConfiguration;
         const size_t off_p = (off_dc + ntok * 4 + 255) & ~(size_t)255;
-        const size_t need = ns > 1 ? off_p + ns * elems * 4 : off_dc + ntok * 4 + 256;
+        const size_t need = ns > 1 ? off_p + elems * 4 : off_dc + ntok * 4 + 256;
         void* ws = nullptr;
         WsLease lease;
         int rc = workspace_acquire(need, stream, &ws, lease);
@@ -1211,6 +1227,10 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
         float* coef = (float*)((char*)ws + off_c);
         float* dcoef = (float*)((char*)ws + off_dc);
         float* part = ns > 1 ? (float*)((char*)ws + off_p) : nullptr;
+        if (part) {
+            rc = fill_zero(part, elems * 4, stream);
+            if (rc != kSuccess) return rc;
+        }
         const dim3 cg((unsigned)((ntok * 16 + NTH - 1) / NTH));
         if (head_dim == 128)
             EFLA_LAUNCH("efla_r_coeff", r_coeff_kernel<8>, cg, dim3(NTH), stream, (const bf16*)k,
@@ -1234,7 +1254,7 @@ extern "C" int efla_backward_hip(const void* grad_output, const void* k, const v
         else
             r_launch_bwd<64, 2, 8>(grad_output, k, v, coef, dcoef, ck, hist, grad_k, part, ps,
                                    grad_v, grad_state, H, T, nbh, stream);
-        if (ns > 1) r_combine(part, ps, ns, grad_k, elems, stream);
+        if (ns > 1) r_combine(part, ps, 1, grad_k, elems, stream);
         return (int)hipPeekAtLastError();
     }
     const size_t nseg = (seq_len + SEG - 1) / SEG;

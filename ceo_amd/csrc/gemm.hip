@@ -1,25 +1,24 @@
 // Row-major GEMM for gfx950, replacing the reference's cuBLAS calls
-// (kernels/cuda/gemm.cu:182-234, 303-548).
-//
-// Matching bf16 / fp16 / fp32 operands go to hipBLASLt (a plain library GEMM,
-// as the reference's cuBLAS call is): one handle per device, created on first
-// use and kept, and the library's cached workspace of the calling stream; the chosen algorithm and descriptors
-// are cached per (shape, transposes, dtype, bias) so a steady-state call does
-// no heuristic query and no device allocation.  The row-major product
-// C = A B is issued as the column-major C^T = B^T A^T, the bias as the
-// epilogue's per-row bias of C^T.  Mixed dtypes, shapes for which hipBLASLt
-// offers no algorithm, and efla_rt_set_gemm_backend(1) take the hand-written
-// MFMA kernel below.
+// (kernels/cuda/gemm.cu:182-234, 303-548).  Every product runs on the
+// hand-written MFMA kernels of this library; no vendor BLAS is linked.
 //
 //   forward:  C[m,n] = sum_k A[m,k] B[k,n] (+ bias[n])     any of fp32/fp16/bf16
 //   backward: dA = dC B^T, dB = A^T dC, dbias = column sums of dC   (bf16)
 //
-// One kernel template covers all three products.  Operands are described as
-// (m,k) and (k,n) matrices whose contiguous index is either k ("K-major") or
-// the other one; tiles are staged in LDS k-contiguous so MFMA fragments are
-// single 16-byte reads, transposing on the way in when the source is not
-// K-major.  Workgroup tile 128x128x32, 4 waves each owning 64x64 (16 MFMA
-// 16x16 tiles), one-stage register prefetch of the next k-tile, fp32
+// Matching bf16 / fp16 operands take the large-tile kernel of gemm_fast.hpp
+// (256 x 256 workgroup tiles of v_mfma_f32_32x32x16, operands copied straight
+// into LDS, persistent grid in XCD bands, split-K for short grids, fused
+// bias / residual / GELU epilogues) wherever its shape and alignment checks
+// pass (fast_ok).  Everything else -- fp32 and mixed dtypes, odd strides,
+// shapes it does not take, and efla_rt_set_gemm_backend(1) -- runs the generic
+// kernel below.
+//
+// The generic kernel covers all three products with one template.  Operands
+// are described as (m,k) and (k,n) matrices whose contiguous index is either k
+// ("K-major") or the other one; tiles are staged in LDS k-contiguous so MFMA
+// fragments are single 16-byte reads, transposing on the way in when the
+// source is not K-major.  Workgroup tile 128x128x32, 4 waves each owning 64x64
+// (16 MFMA 16x16 tiles), one-stage register prefetch of the next k-tile, fp32
 // accumulation, bias fused into the epilogue (the reference adds it in a
 // second pass with a second rounding).  Tiles are ordered in groups of 8 rows
 // of tiles, and consecutive tile ids are spread so that each XCD works on a
@@ -27,7 +26,6 @@
 // re-reads).  Matching dtypes run on bf16 / fp16 MFMA; mixed dtypes on fp32
 // MFMA after conversion.
 #include <hip/hip_runtime.h>
-#include <hipblaslt/hipblaslt.h>
 
 #include <algorithm>
 #include <map>
@@ -528,160 +526,10 @@ static gf::EpiArgs<T> epi(void* d, long ldd, const void* bias = nullptr, float a
                           ldaux, nullptr, nullptr};
 }
 
-// ---------------------------------------------------------------------------
-// hipBLASLt path
-// ---------------------------------------------------------------------------
-constexpr size_t kLtWorkspace = (size_t)128 << 20;
-constexpr int kMaxDev = 64;
-
-struct LtDevice {
-    hipblasLtHandle_t handle = nullptr;
-    bool broken = false;  // creation failed: always use the native kernel
-};
-
-// (opA, opB, M, N, K, lda, ldb, ldd, dtype, has_bias, ldc or 0 without C)
-typedef std::tuple<int, int, long, long, long, long, long, long, int, int, long> LtKey;
-
-struct LtPlan {
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr, d = nullptr;
-    hipblasLtMatmulAlgo_t algo;
-    size_t ws_bytes = 0;
-    bool ok = false;  // false: hipBLASLt offers no algorithm for this problem
-};
-
-static std::mutex g_lt_mu;
-static LtDevice g_lt_dev[kMaxDev];
-static std::map<std::pair<int, LtKey>, LtPlan> g_lt_plans;
 // 0: the hand-written kernels (large-tile where it takes the problem, else the
-// generic one); 1: the generic hand-written kernel only; 2: hipBLASLt where it
-// takes the problem, else the hand-written kernels
+// generic one); 1: the generic hand-written kernel only
+static std::mutex g_backend_mu;
 static int g_backend = 0;
-
-static hipDataType lt_type(int dt) {
-    return dt == kDtypeF32 ? HIP_R_32F : dt == kDtypeF16 ? HIP_R_16F : HIP_R_16BF;
-}
-
-// Caller holds g_lt_mu.  nullptr when hipBLASLt is unusable on this device.
-static LtDevice* lt_device(int dev) {
-    if (dev < 0 || dev >= kMaxDev) return nullptr;
-    LtDevice& d = g_lt_dev[dev];
-    if (d.broken) return nullptr;
-    if (!d.handle) {
-        if (hipblasLtCreate(&d.handle) != HIPBLAS_STATUS_SUCCESS) {
-            d.handle = nullptr;
-            d.broken = true;
-            return nullptr;
-        }
-    }
-    return &d;
-}
-
-static bool lt_plan(LtDevice* d, const LtKey& k, LtPlan* p) {
-    const hipblasOperation_t ta = (hipblasOperation_t)std::get<0>(k);
-    const hipblasOperation_t tb = (hipblasOperation_t)std::get<1>(k);
-    const long M = std::get<2>(k), N = std::get<3>(k), K = std::get<4>(k);
-    const long lda = std::get<5>(k), ldb = std::get<6>(k), ldd = std::get<7>(k);
-    const hipDataType t = lt_type(std::get<8>(k));
-    const bool bias = std::get<9>(k) != 0;
-    const long ldc = std::get<10>(k);
-    if (hipblasLtMatmulDescCreate(&p->desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) !=
-        HIPBLAS_STATUS_SUCCESS)
-        return false;
-    int32_t opa = ta, opb = tb;
-    hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSA, &opa, sizeof(opa));
-    hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_TRANSB, &opb, sizeof(opb));
-    if (bias) {
-        hipblasLtEpilogue_t ep = HIPBLASLT_EPILOGUE_BIAS;
-        int32_t bt = t;
-        hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_EPILOGUE, &ep, sizeof(ep));
-        hipblasLtMatmulDescSetAttribute(p->desc, HIPBLASLT_MATMUL_DESC_BIAS_DATA_TYPE, &bt,
-                                        sizeof(bt));
-    }
-    // column-major layouts: op(A) is M x K, op(B) is K x N, D is M x N
-    const long ar = ta == HIPBLAS_OP_N ? M : K, ac = ta == HIPBLAS_OP_N ? K : M;
-    const long br = tb == HIPBLAS_OP_N ? K : N, bc = tb == HIPBLAS_OP_N ? N : K;
-    if (hipblasLtMatrixLayoutCreate(&p->a, t, ar, ac, lda) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatrixLayoutCreate(&p->b, t, br, bc, ldb) != HIPBLAS_STATUS_SUCCESS ||
-        hipblasLtMatrixLayoutCreate(&p->d, t, M, N, ldd) != HIPBLAS_STATUS_SUCCESS)
-        return false;
-    p->c = p->d;
-    if (ldc != 0 && ldc != ldd &&
-        hipblasLtMatrixLayoutCreate(&p->c, t, M, N, ldc) != HIPBLAS_STATUS_SUCCESS)
-        return false;
-    hipblasLtMatmulPreference_t pref;
-    if (hipblasLtMatmulPreferenceCreate(&pref) != HIPBLAS_STATUS_SUCCESS) return false;
-    uint64_t wsb = kLtWorkspace;
-    hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb,
-                                          sizeof(wsb));
-    hipblasLtMatmulHeuristicResult_t res[8];
-    int n = 0;
-    const hipblasStatus_t st = hipblasLtMatmulAlgoGetHeuristic(d->handle, p->desc, p->a, p->b,
-                                                               p->c, p->d, pref, 8, res, &n);
-    hipblasLtMatmulPreferenceDestroy(pref);
-    if (st != HIPBLAS_STATUS_SUCCESS) return false;
-    for (int i = 0; i < n; ++i) {  // best-ranked first
-        if (res[i].state != HIPBLAS_STATUS_SUCCESS || res[i].workspaceSize > kLtWorkspace)
-            continue;
-        p->algo = res[i].algo;
-        p->ws_bytes = res[i].workspaceSize;
-        return true;
-    }
-    return false;
-}
-
-// Column-major D[M x N] = alpha op(A) op(B) (+ bias[M] per row) (+ beta C),
-// all of dtype dt, fp32 accumulation; C (leading dimension ldc) is read only
-// when beta != 0 and may be D itself.  Returns kSuccess, a launch error, or -1
-// when hipBLASLt cannot take the problem (the caller then runs the native
-// kernel, or reports it).
-static int lt_matmul(hipblasOperation_t ta, hipblasOperation_t tb, long M, long N, long K,
-                     const void* A, long lda, const void* B, long ldb, void* D, long ldd,
-                     const void* bias, int dt, hipStream_t stream, float alpha = 1.f,
-                     float beta = 0.f, const void* C = nullptr, long ldc = 0) {
-    std::lock_guard<std::mutex> lk(g_lt_mu);
-    if (g_backend != 2) return -1;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return -1;
-    LtDevice* d = lt_device(dev);
-    if (!d) return -1;
-    if (beta == 0.f) {
-        C = nullptr;
-        ldc = 0;
-    }
-    const LtKey key(ta, tb, M, N, K, lda, ldb, ldd, dt, bias ? 1 : 0, C ? ldc : 0);
-    auto it = g_lt_plans.find({dev, key});
-    if (it == g_lt_plans.end()) {
-        LtPlan p;
-        p.ok = lt_plan(d, key, &p);
-        it = g_lt_plans.emplace(std::make_pair(dev, key), p).first;
-    }
-    LtPlan& p = it->second;
-    if (!p.ok) return -1;
-    // the library workspace of this stream (slot 1), held while the product is queued
-    void* ws = nullptr;
-    WsLease lease;
-    if (p.ws_bytes) {
-        const int rc = workspace_acquire(p.ws_bytes, stream, &ws, lease, 1);
-        if (rc != kSuccess) return rc;
-    }
-    if (bias)
-        hipblasLtMatmulDescSetAttribute(p.desc, HIPBLASLT_MATMUL_DESC_BIAS_POINTER, &bias,
-                                        sizeof(bias));
-    ::efla::ProfScope ps("gemm_hipblaslt", stream);
-    const hipblasStatus_t st =
-        hipblasLtMatmul(d->handle, p.desc, &alpha, A, p.a, B, p.b, &beta, C ? C : D, p.c, D, p.d,
-                        &p.algo, ws, p.ws_bytes, stream);
-    if (st != HIPBLAS_STATUS_SUCCESS) return kInvalidValue;
-    return (int)hipPeekAtLastError();
-}
-
-// Row-major C[m x n] = A[m x k] B[k x n] (+ bias[n]) as column-major
-// C^T = B^T A^T: A' = B (n x k, ld n), B' = A (k x m, ld k), bias per row of C^T.
-static int lt_forward(const void* a, const void* b, const void* bias, void* c, long m, long k,
-                      long n, int dt, hipStream_t st) {
-    return lt_matmul(HIPBLAS_OP_N, HIPBLAS_OP_N, n, m, k, b, n, a, k, c, n, bias, dt, st);
-}
 
 }  // namespace gm
 
@@ -695,13 +543,13 @@ using namespace efla;
 using namespace efla::gm;
 
 static int backend() {
-    std::lock_guard<std::mutex> lk(g_lt_mu);
+    std::lock_guard<std::mutex> lk(g_backend_mu);
     return g_backend;
 }
 
 extern "C" int efla_rt_set_gemm_backend(int backend) {
-    if (backend < 0 || backend > 2) return kInvalidValue;
-    std::lock_guard<std::mutex> lk(g_lt_mu);
+    if (backend < 0 || backend > 1) return kInvalidValue;
+    std::lock_guard<std::mutex> lk(g_backend_mu);
     g_backend = backend;
     return kSuccess;
 }
@@ -724,8 +572,6 @@ extern "C" int gemm_forward_hip(const void* a, const void* b, const void* bias, 
         }
     }
     if (dtype_a == dtype_b && dtype_b == dtype_c) {
-        const int rc = lt_forward(a, b, bias, c, (long)m, (long)k, (long)n, dtype_a, stream);
-        if (rc >= 0) return rc;
         // C[m, n] = A[m, k] B[k, n]: A k-contiguous, B line (n) contiguous
         const FastOp fa{a, (long)k, true}, fb{b, (long)n, false};
         if (dtype_a != kDtypeF32 && backend() != 1 &&
@@ -785,11 +631,10 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
     if (need_a && m && k && n) {
         // dA[m, k] = sum_n dC[m, n] B[k, n]; column-major dA^T = op_T(B') dC^T
         // with B' = B as (n x k, ld n) and dC^T as (n x m, ld n)
-        int rc = lt_matmul(HIPBLAS_OP_T, HIPBLAS_OP_N, K, M, N, b, N, grad_c, N, grad_a, K,
-                           nullptr, kDtypeBF16, stream);
+        int rc = -1;
         // dA = dC B^T: contraction over n, both operands n-contiguous
         const FastOp fa{grad_c, N, true}, fb{b, N, true};
-        if (rc < 0 && backend() != 1 &&
+        if (backend() != 1 &&
             fast_ok(M, K, N, fa, fb, grad_a, K, nullptr, nullptr, 0, nullptr, 0))
             rc = fast_launch<bf16, gf::EPI_PLAIN>(fa, fb, M, K, N, epi<bf16>(grad_a, K),
                                                   "gemm_bwd_da", stream);
@@ -801,11 +646,10 @@ extern "C" int gemm_backward_hip(const void* grad_c, const void* a, const void* 
     if (need_b && m && k && n) {
         // dB[k, n] = sum_m A[m, k] dC[m, n]; column-major dB^T = dC^T op_T(A')
         // with dC^T as (n x m, ld n) and A' = A as (k x m, ld k)
-        int rc = lt_matmul(HIPBLAS_OP_N, HIPBLAS_OP_T, N, K, M, grad_c, N, a, K, grad_b, N,
-                           nullptr, kDtypeBF16, stream);
+        int rc = -1;
         // dB = A^T dC: contraction over m, A k- (line-) contiguous, dC n-contiguous
         const FastOp fa{a, K, false}, fb{grad_c, N, false};
-        if (rc < 0 && backend() != 1 &&
+        if (backend() != 1 &&
             fast_ok(K, N, M, fa, fb, grad_b, N, nullptr, nullptr, 0, nullptr, 0))
             rc = fast_launch<bf16, gf::EPI_PLAIN>(fa, fb, K, N, M, epi<bf16>(grad_b, N),
                                                   "gemm_bwd_db", stream);
@@ -853,13 +697,6 @@ extern "C" int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t 
     if (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n) || ldd < n ||
         (beta != 0.f && ldc < n))
         return kInvalidValue;
-    // row-major D = op(A) op(B) as column-major D^T = op(B)^T op(A)^T: a row-major
-    // matrix is its own transpose read column-major with the same leading dimension
-    int rc = k == 0 ? -1 : lt_matmul(trans_b ? HIPBLAS_OP_T : HIPBLAS_OP_N,
-                       trans_a ? HIPBLAS_OP_T : HIPBLAS_OP_N, (long)n, (long)m, (long)k, b,
-                       (long)ldb, a, (long)lda, d, (long)ldd, bias, dtype, stream, alpha, beta, c,
-                       (long)ldc);
-    if (rc >= 0) return rc;
     // op(A) is A (k-contiguous) or A^T of a stored k x m (m-contiguous); op(B)
     // is B of a stored k x n (n-contiguous) or B^T of a stored n x k
     const FastOp fa{a, (long)lda, trans_a == 0}, fb{b, (long)ldb, trans_b != 0};

@@ -35,15 +35,16 @@ __global__ void __launch_bounds__(256) fill_f16_kernel(_Float16* __restrict__ p,
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
 }
 
-// Zeroes [p, p + bytes): unaligned head and tail bytes, 4-byte words between.
+// Zeroes [p, p + bytes): head bytes up to 16-byte alignment, 16-byte words,
+// then the tail bytes.
 __global__ void __launch_bounds__(256) zero_kernel(uint8_t* __restrict__ p, size_t head,
                                                    size_t nwords, size_t tail) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     const size_t i0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    uint32_t* w = reinterpret_cast<uint32_t*>(p + head);
-    for (size_t i = i0; i < nwords; i += stride) w[i] = 0u;
+    uint4* w = reinterpret_cast<uint4*>(p + head);
+    for (size_t i = i0; i < nwords; i += stride) w[i] = uint4{0u, 0u, 0u, 0u};
     if (i0 < head) p[i0] = 0;
-    if (i0 < tail) p[head + nwords * 4 + i0] = 0;
+    if (i0 < tail) p[head + nwords * 16 + i0] = 0;
 }
 
 static unsigned grid_for(size_t n) {
@@ -55,10 +56,10 @@ static unsigned grid_for(size_t n) {
 
 int fill_zero(void* ptr, size_t bytes, hipStream_t stream) {
     if (bytes == 0) return kSuccess;
-    size_t head = (4 - ((uintptr_t)ptr & 3u)) & 3u;
+    size_t head = (16 - ((uintptr_t)ptr & 15u)) & 15u;
     if (head > bytes) head = bytes;
-    const size_t nwords = (bytes - head) / 4;
-    const size_t tail = bytes - head - nwords * 4;
+    const size_t nwords = (bytes - head) / 16;
+    const size_t tail = bytes - head - nwords * 16;
     EFLA_LAUNCH("fill_zero", zero_kernel, dim3(grid_for(nwords)), dim3(256), stream,
                 (uint8_t*)ptr, head, nwords, tail);
     return (int)hipPeekAtLastError();
@@ -260,7 +261,12 @@ int efla_rt_fill(void* ptr, float value, size_t numel, int dtype, hipStream_t st
 
 // --- streams / events ---------------------------------------------------------
 int efla_rt_stream_create(hipStream_t* stream) { return (int)hipStreamCreate(stream); }
-int efla_rt_stream_destroy(hipStream_t stream) { return (int)hipStreamDestroy(stream); }
+int efla_rt_stream_destroy(hipStream_t stream) {
+    // the stream's cached workspaces go first, while its handle still names it
+    const int rc = efla_rt_workspace_release_stream(stream);
+    if (rc != kSuccess) return rc;
+    return (int)hipStreamDestroy(stream);
+}
 int efla_rt_stream_synchronize(hipStream_t stream) { return (int)hipStreamSynchronize(stream); }
 int efla_rt_event_create(hipEvent_t* event) { return (int)hipEventCreate(event); }
 int efla_rt_event_destroy(hipEvent_t event) { return (int)hipEventDestroy(event); }
@@ -293,11 +299,14 @@ typedef std::tuple<int, hipStream_t, int> WsKey;  // (device, stream, slot)
 std::mutex g_ws_mu;                                // guards the map, not the entries
 std::map<WsKey, std::unique_ptr<WsEntry>> g_ws;
 
+// An entry is erased only by efla_rt_workspace_release_stream, whose caller
+// guarantees that no other thread uses that stream meanwhile, so the pointer
+// stays valid for as long as its (device, stream) is in use.
 WsEntry* ws_entry(int dev, hipStream_t stream, int slot) {
     std::lock_guard<std::mutex> g(g_ws_mu);
     std::unique_ptr<WsEntry>& e = g_ws[WsKey(dev, stream, slot)];
     if (!e) e.reset(new WsEntry);
-    return e.get();  // entries are never erased, so the pointer stays valid
+    return e.get();
 }
 }  // namespace
 
@@ -376,6 +385,33 @@ extern "C" size_t efla_rt_workspace_bytes(void) {
         total += e->bytes;
     }
     return total;
+}
+
+extern "C" int efla_rt_workspace_release_stream(hipStream_t stream) {
+    int dev = 0;
+    EFLA_CHECK(hipGetDevice(&dev));
+    std::vector<efla::WsKey> keys;
+    std::vector<efla::WsEntry*> entries;
+    {
+        std::lock_guard<std::mutex> g(efla::g_ws_mu);
+        for (auto& kv : efla::g_ws)
+            if (std::get<0>(kv.first) == dev && std::get<1>(kv.first) == stream) {
+                keys.push_back(kv.first);
+                entries.push_back(kv.second.get());
+            }
+    }
+    if (keys.empty()) return kSuccess;
+    // everything queued on the stream, which may still read these buffers
+    EFLA_CHECK(hipStreamSynchronize(stream));
+    for (efla::WsEntry* e : entries) {
+        std::lock_guard<std::mutex> ge(e->mu);  // a lease still launching finishes first
+        if (e->ptr) EFLA_CHECK(hipFree(e->ptr));
+        e->ptr = nullptr;
+        e->bytes = 0;
+    }
+    std::lock_guard<std::mutex> g(efla::g_ws_mu);
+    for (const efla::WsKey& k : keys) efla::g_ws.erase(k);
+    return kSuccess;
 }
 
 extern "C" int efla_rt_workspace_release(void) {

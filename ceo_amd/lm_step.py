@@ -133,8 +133,13 @@ class EflaLM:
         return self._ws
 
     # -- forward --------------------------------------------------------------
-    def forward(self, tokens: torch.Tensor, targets: torch.Tensor):
-        """tokens, targets: (B, T) int32.  Returns (mean loss tensor, saved)."""
+    def forward(self, tokens: torch.Tensor, targets: torch.Tensor, train: bool = True):
+        """tokens, targets: (B, T) int32.  Returns (mean loss tensor, saved).
+
+        With ``train`` (the step's forward) the cross-entropy also writes
+        dL/dlogits over the logits in place, and ``saved`` holds what
+        backward() needs.  With ``train=False`` (evaluation) the logits are
+        kept (``saved["logits"]``) and no activation or gradient is stored."""
         cfg = self.cfg
         B, T = tokens.shape
         N, D, H, dh = B * T, cfg.d_model, cfg.n_heads, cfg.head_dim
@@ -151,7 +156,7 @@ class EflaLM:
             # (copied out when the row width is not whole 16-byte pieces)
             q, k, v = (self._io(p[:, j * HD:(j + 1) * HD]).view(B, T, H, dh) for j in range(3))
             beta = nn.sigmoid_gate_forward(p[:, 3 * HD:]).view(B, T, H)
-            o, _ = efla.chunk_efla_fwd(q, k, v, beta, workspace=ws[i], save_states=True)
+            o, _ = efla.chunk_efla_fwd(q, k, v, beta, workspace=ws[i], save_states=train)
             o2 = o.view(N, HD)
             # x1 = x + o w_o with the residual added by the product's epilogue
             x1 = nn.gemm_ex(o2, self.w(L + "w_o"), torch.empty_like(x), c=x, beta=1.0)
@@ -161,13 +166,18 @@ class EflaLM:
             u, gl = nn.gemm_gelu_forward(a2, self.w(L + "w_up"), self.w(L + "b_up"))
             x2 = nn.gemm_ex(gl, self.w(L + "w_down"), torch.empty_like(x),
                             bias=self.w(L + "b_down"), c=x1, beta=1.0)
-            saved["layers"].append(dict(x=x, a=a, m1=m1, r1=r1, q=q, k=k, v=v, beta=beta,
-                                        o=o2, x1=x1, a2=a2, m2=m2, r2=r2, u=u, g=gl))
+            if train:
+                saved["layers"].append(dict(x=x, a=a, m1=m1, r1=r1, q=q, k=k, v=v, beta=beta,
+                                            o=o2, x1=x1, a2=a2, m2=m2, r2=r2, u=u, g=gl))
             x = x2
         af, mf, rf = nn.layernorm_forward(x, self.w("lnf.w"), self.w("lnf.b"), cfg.ln_eps,
                                           save_stats=True)
         logits = nn.gemm_forward(af, self.w("head"))
         tflat = targets.reshape(-1)
+        if not train:
+            loss_rows = nn.cross_entropy_forward(logits, tflat, cfg.label_smoothing)
+            saved.update(logits=logits)
+            return loss_rows.sum(), saved
         # the loss and dL/dlogits of the summed rows from one read of the
         # logits, the gradient written over them (the backward needs no logits)
         loss_rows, dlogits = nn.cross_entropy_forward_backward(logits, tflat,

@@ -358,8 +358,8 @@ int prism_backward_hip(const void* grad_output, const void* u, const void* v, co
  * Hand-written MFMA kernels: bf16 / fp16 problems whose k, output columns
  * and strides are multiples of 8 elements (16-byte rows) run a 256 x 256 x 64
  * tile kernel; everything else (fp32, mixed dtypes, other shapes) a generic
- * 128 x 128 one.  efla_rt_set_gemm_backend selects hipBLASLt instead, for
- * comparison.
+ * 128 x 128 one (efla_rt_set_gemm_backend(1) forces it).  No vendor BLAS
+ * is linked.
  * ======================================================================== */
 
 /* Replaces gemm_forward_cuda (kernels.h:211-223, gemm.cu:303-398):

@@ -47,6 +47,8 @@ int efla_rt_fill(void* ptr, float value, size_t numel, int dtype, hipStream_t st
 
 /* --- streams (CudaStream, cuda.zig:291-314) --- */
 int efla_rt_stream_create(hipStream_t* stream);
+/* Releases the stream's cached library workspaces
+ * (efla_rt_workspace_release_stream), then destroys it. */
 int efla_rt_stream_destroy(hipStream_t stream);
 int efla_rt_stream_synchronize(hipStream_t stream);
 
@@ -67,12 +69,20 @@ int efla_rt_event_elapsed_ms(float* ms, hipEvent_t start, hipEvent_t stop);
 size_t efla_rt_workspace_bytes(void);
 /* Release the cached workspaces of the current device (synchronises it). */
 int efla_rt_workspace_release(void);
+/* Release the cached workspaces of one stream on the current device: waits
+ * for the stream, frees its buffers and forgets it, so a later stream that
+ * receives the same handle value starts with none.  Call it before
+ * hipStreamDestroy on any stream the library's entry points were given
+ * (efla_rt_stream_destroy does so itself), and not while another thread
+ * issues library calls on that stream.  No counterpart in the reference (its
+ * entry points allocate and free scratch per call, efla.cu:631-647,
+ * 695-696). */
+int efla_rt_workspace_release_stream(hipStream_t stream);
 
 /* GEMM backend of the gemm_* entries for this process: 0 (default) the
  * library's hand-written kernels (the large-tile kernel where it takes the
- * problem, else the generic one); 1 the generic hand-written kernel only;
- * 2 hipBLASLt where it takes the problem (for comparison), else the
- * hand-written kernels.  Other values -> 1. */
+ * problem, else the generic one); 1 the generic hand-written kernel only.
+ * Other values -> 1.  No vendor BLAS is linked. */
 int efla_rt_set_gemm_backend(int backend);
 
 /* --- launch profiler ---

@@ -338,7 +338,7 @@ def test_runtime_validation(L):
     assert L.efla_rt_fill(NULL, f, 5, 14, NULL) == 1  # NULL with elements
     for dt in (1, 3, 99, -1):  # only fp32 (0), fp16 (2), bf16 (14)
         assert L.efla_rt_fill(p, f, 5, dt, NULL) == 1
-    assert L.efla_rt_set_gemm_backend(3) == 1
+    assert L.efla_rt_set_gemm_backend(2) == 1
     assert L.efla_rt_set_gemm_backend(-1) == 1
     assert L.efla_rt_set_gemm_backend(0) == 0
 

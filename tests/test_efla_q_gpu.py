@@ -15,13 +15,15 @@ pytestmark = pytest.mark.gpu
 TOL = {torch.float32: 1e-4, torch.bfloat16: 2e-2}
 
 
-def _case(oracle, seed, B, T, H, K, V, dtype, *, s0=False, dst=False, cu=None):
+def _case(oracle, seed, B, T, H, K, V, dtype, *, s0=False, dst=False, cu=None, xform=None):
     from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd
 
     announce(f"chunk_efla B={B} T={T} H={H} K={K} V={V} {dtype} s0={s0} dst={dst} "
-             f"varlen={cu is not None}")
+             f"varlen={cu is not None}" + (f" {xform.__name__}" if xform else ""))
     ntok = B * T
     x = oracle.make_efla_inputs(seed, ntok, H, K, V, bf16=dtype == torch.bfloat16)
+    if xform is not None:
+        x = xform(oracle, x, dtype == torch.bfloat16)
     N = B if cu is None else len(cu) - 1
     rng = np.random.default_rng(seed)
     S0 = (rng.standard_normal((N, H, K, V)) * 0.3).astype(np.float32) if s0 else None
@@ -77,6 +79,83 @@ def test_bf16_long_sequence(oracle, K, V):
     # full benchmark sequence length: rounding must not accumulate over 128
     # chunks of the state recurrence
     _case(oracle, 0xEF1A0002 + V, 1, 8192, 2, K, V, torch.bfloat16, s0=True, dst=True)
+
+
+# lambda = |k|^2 per token, cycling over the coefficient's regimes: below the
+# reference's series branch point (lambda <= 1e-6, efla.cu:93-115), inside this
+# library's series range (beta lambda < 0.03, beta < 1), and one all-zero k per
+# head (lambda = 0, where c = beta and dc/dlambda = -beta^2 / 2 exactly).
+SMALL_K_SCALES = (3e-4, 9e-4, 0.05, 0.15, 0.1)
+
+
+def small_lambda(oracle, x, bf16):
+    k = x["k"].astype(np.float64).copy()
+    scale = np.array([SMALL_K_SCALES[i % len(SMALL_K_SCALES)] for i in range(k.shape[0])])
+    k *= scale[:, None, None]
+    k[5] = 0.0
+    x = dict(x)
+    x["k"] = oracle.round_bf16(k) if bf16 else k.astype(np.float32)
+    lam = (x["k"].astype(np.float64) ** 2).sum(-1)
+    assert lam.max() < 0.03 and (lam[1::len(SMALL_K_SCALES)] <= 1e-6).all() and lam[5].max() == 0
+    return x
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_small_lambda_coefficient_branch(oracle, dtype):
+    """Every token's coefficient comes from the short-lambda series (and the
+    lambda -> 0 limit of dc/dlambda drives dk): the fp32 path must hold
+    1e-4 against the fp64 oracle, which evaluates c with expm1."""
+    _case(oracle, 0x5A11, 2, 150, 2, 64, 64, dtype, s0=True, dst=True, xform=small_lambda)
+
+
+@pytest.mark.parametrize("K,V", [(128, 128), (64, 64)])
+def test_small_lambda_bf16_fast_kernels(oracle, K, V):
+    _case(oracle, 0x5A12 + K, 2, 200, 2, K, V, torch.bfloat16, s0=True, dst=True,
+          xform=small_lambda)
+
+
+def test_nan_inf_stay_in_their_sequence_and_head(oracle):
+    """A NaN in one token's k and an Inf in another sequence's v contaminate
+    only their own (sequence, head): every other (sequence, head) gets outputs
+    and gradients bit-identical to a clean run, and finite; the contaminated
+    ones carry non-finite values from the next chunk on (SURVEY's failure-
+    detection row: NaN/Inf injected into the inputs must propagate)."""
+    from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd
+
+    B, T, H, K, V = 3, 200, 2, 128, 128
+    announce(f"chunk_efla NaN/Inf isolation B={B} T={T} H={H} K={K} V={V}")
+    x = oracle.make_efla_inputs(0xBAD, B * T, H, K, V, bf16=True)
+    g = {n: to_dev(a, torch.bfloat16, (B, T, H, K) if n in "qk" else
+                   (B, T, H) if n == "beta" else (B, T, H, V)) for n, a in x.items()}
+
+    def run(gg):
+        o, st = chunk_efla_fwd(gg["q"], gg["k"], gg["v"], gg["beta"], None, True)
+        grads = chunk_efla_bwd(gg["q"], gg["k"], gg["v"], gg["beta"], gg["do"])
+        torch.cuda.synchronize()
+        return [o, st] + list(grads[:4])
+
+    clean = run(g)
+    bad = {n: t.clone() for n, t in g.items()}
+    bad["k"][0, 70, 0, 3] = float("nan")
+    bad["v"][2, 150, 1, 5] = float("inf")
+    dirty = run(bad)
+    names = ["o", "S_T", "dq", "dk", "dv", "dbeta"]
+    hit = {(0, 0), (2, 1)}
+    for n, a, b in zip(names, clean, dirty):
+        for bb in range(B):
+            for hh in range(H):
+                sa, sb = (a[bb, hh], b[bb, hh]) if n == "S_T" else (a[bb, :, hh], b[bb, :, hh])
+                if (bb, hh) in hit:
+                    continue
+                assert torch.isfinite(sb.float()).all(), (n, bb, hh)
+                assert torch.equal(sa, sb), (n, bb, hh)
+    # propagation: from the chunk after the bad token on, the output is not finite
+    assert not torch.isfinite(dirty[0][0, 128:, 0].float()).any()
+    assert not torch.isfinite(dirty[0][2, 192:, 1].float()).all()
+    assert not torch.isfinite(dirty[1][0, 0].float()).all()
+    for i in range(2, 6):  # every gradient of the NaN's (sequence, head) is hit
+        d = dirty[i]
+        assert not torch.isfinite(d[0, :, 0].float()).all(), names[i]
 
 
 def test_varlen_bf16(oracle):

@@ -173,3 +173,58 @@ def test_workspace_bytes_and_release(L):
     assert runtime.workspace_bytes() == 2 * one  # a second stream gets its own buffer
     runtime.release_workspace()
     assert runtime.workspace_bytes() == 0
+
+
+def test_workspace_released_with_its_stream(L):
+    """Four library streams each run the reference ABI's forward at the bench
+    shape (B H = 128 takes the column split: one zeroed fp32 row-sum buffer,
+    4 bytes per output element, after the per-token coefficients) and a
+    chunked forward; destroying each stream through efla_rt_stream_destroy
+    frees its cached buffers, and the device's total returns to zero."""
+    from ceo_amd import efla, runtime
+
+    announce("runtime: per-stream workspaces freed by efla_rt_stream_destroy")
+    runtime.release_workspace()
+    assert runtime.workspace_bytes() == 0
+    B, T, H, d = 4, 8192, 32, 128
+    g = torch.Generator(device="cuda:0").manual_seed(2)
+    k = (0.08 * torch.randn(B, T, H, d, generator=g, device="cuda:0")).to(torch.bfloat16)
+    v = torch.randn(B, T, H, d, generator=g, device="cuda:0").to(torch.bfloat16)
+    q = torch.randn(1, 256, 2, 64, generator=g, device="cuda:0").to(torch.bfloat16)
+    beta = torch.rand(1, 256, 2, generator=g, device="cuda:0").to(torch.bfloat16)
+    states = [torch.zeros(B * H, d, d, dtype=torch.bfloat16, device="cuda:0") for _ in range(4)]
+    ref_state = states[0].clone()
+    ref_o = efla.efla_forward(k, v, ref_state, 0.5)
+    torch.cuda.synchronize()
+    runtime.release_workspace()
+    ntok, elems = B * T * H, B * T * H * d
+    step = 64 << 20
+    bound = -(-(ntok * 4 + 256 + elems * 4) // step) * step  # the 64 MiB growth step
+    streams, outs, totals = [], [], []
+    try:
+        for i in range(4):
+            s = ctypes.c_void_p()
+            assert L.efla_rt_stream_create(ctypes.byref(s)) == 0
+            streams.append(s)
+            with torch.cuda.stream(torch.cuda.ExternalStream(s.value)):
+                outs.append(efla.efla_forward(k, v, states[i], 0.5))
+                efla.chunk_efla_fwd(q, q, q, beta)
+            assert L.efla_rt_stream_synchronize(s) == 0
+            totals.append(runtime.workspace_bytes())
+        per = [totals[0]] + [b - a for a, b in zip(totals, totals[1:])]
+        print(f"  per-stream cached bytes {per}, Mode R bound {bound}", flush=True)
+        assert all(p == per[0] for p in per)
+        # the chunked forward reuses the stream's (larger) Mode R buffer
+        assert per[0] <= bound
+        for o, st in zip(outs, states):  # the same bits on every stream
+            assert torch.equal(o, ref_o) and torch.equal(st, ref_state)
+    finally:
+        outs.clear()
+        torch.cuda.synchronize()
+        left = []
+        for s in streams:
+            left.append((L.efla_rt_stream_destroy(s), runtime.workspace_bytes()))
+    print(f"  after each destroy: {left}", flush=True)
+    assert all(rc == 0 for rc, _ in left)
+    assert [b for _, b in left] == [(3 - j) * totals[0] for j in range(4)]
+    assert runtime.workspace_bytes() == 0
