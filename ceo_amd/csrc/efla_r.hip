@@ -239,10 +239,9 @@ __device__ __forceinline__ float wave_sum_q4(float x) {
 // workgroup adds first (4 bytes of scratch per output element).
 // NS = 1, LPC = 4 is one workgroup per (b, h); NS = 2, LPC = 8 gives a grid of
 // 2 B H with half the rows per lane (for B H below the CU count).
-// p[0..3] += a with vector-memory fp32 atomics (no return value)
-__device__ __forceinline__ void atomic_add4(float* p, const mf::floatx4& a) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) unsafeAtomicAdd(p + e, a[e]);
+// a[i] for a lane-dependent i in 0..3 (a select chain, no scratch indexing)
+__device__ __forceinline__ float pick4(const mf::floatx4& a, int i) {
+    return i == 0 ? a[0] : i == 1 ? a[1] : i == 2 ? a[2] : a[3];
 }
 
 template <int D, int NS, int LPC>
@@ -400,16 +399,19 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_fast_kernel(
                 mf::floatx4 acc = mf::zero4();
 #pragma unroll
                 for (int q = 0; q < NK; ++q) acc = mf::mma(af[i][m][q], bk[i][q], acc);
-                if (j == 0) {
-                    const long o = base0 + t * tstride + 16 * (MT * w + m) + 4 * g;
-                    if constexpr (NS == 1) {
+                // the 16 columns of acc are equal (B is a broadcast of k)
+                const long o = base0 + t * tstride + 16 * (MT * w + m) + 4 * g;
+                if constexpr (NS == 1) {
+                    if (j == 0) {
                         bf16x4 ov;
 #pragma unroll
                         for (int e = 0; e < 4; ++e) ov[e] = (bf16)acc[e];
                         *reinterpret_cast<bf16x4*>(out + o) = ov;
-                    } else {
-                        atomic_add4(part_out + o, acc);
                     }
+                } else if (j < 4) {
+                    // lanes 0..3 of each row group add one row each: the wave's
+                    // 16 rows in one atomic instruction on one 64-byte line
+                    unsafeAtomicAdd(part_out + o + j, pick4(acc, j));
                 }
             }
         }
@@ -813,24 +815,29 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
                         acc = mf::mma(mf::frag_trc(l, sm.Mh[par], LDS, 32 * q, f0), ones, acc);
                         acc = mf::mma(mf::frag_trc(l, sm.Ml[par], LDS, 32 * q, f0), ones, acc);
                     }
-                    if (j16 == 0) {
+                    // the 16 columns of acc are equal (B is ones); with the
+                    // column split lanes 0..3 of each row group add one row each
+                    // (one atomic instruction per wave on one 64-byte line)
+                    if (NS == 1 ? j16 == 0 : j16 < 4) {
                         float gsum = 0.f;
 #pragma unroll
                         for (int ww = 0; ww < NW; ++ww) gsum += sm.red[par][ww];
                         const float glam2 = 2.f * gsum * sm.seg.dcc[j];
-                        mf::floatx4 gv4;
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int row = f0 + 4 * g4 + i, lr = row - cb * NC;
-                            const float sn = (NS == 1 || (lr >= 0 && lr < NC)) ? sm.gkv[par][lr] : 0.f;
-                            gv4[i] = fmaf(glam2, (float)kb[row], acc[i] + sn);
-                        }
                         const long o = base0 + (t0 + j) * tstride + f0 + 4 * g4;
                         if constexpr (NS == 1) {
+                            mf::floatx4 gv4;
+#pragma unroll
+                            for (int i = 0; i < 4; ++i) {
+                                const int row = f0 + 4 * g4 + i;
+                                gv4[i] = fmaf(glam2, (float)kb[row], acc[i] + sm.gkv[par][row]);
+                            }
                             *reinterpret_cast<bf16x4*>(grad_k + o) =
                                 bf16x4{(bf16)gv4[0], (bf16)gv4[1], (bf16)gv4[2], (bf16)gv4[3]};
                         } else {
-                            atomic_add4(part_gk + o, gv4);
+                            const int row = f0 + 4 * g4 + j16, lr = row - cb * NC;
+                            const float sn = (lr >= 0 && lr < NC) ? sm.gkv[par][lr] : 0.f;
+                            unsafeAtomicAdd(part_gk + o + j16,
+                                            fmaf(glam2, (float)kb[row], pick4(acc, j16) + sn));
                         }
                     }
                 }

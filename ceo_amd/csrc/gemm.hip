@@ -693,8 +693,9 @@ extern "C" int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t 
     const size_t lim = (size_t)1 << 40;
     if (m > lim || n > lim || k > lim || lda > lim || ldb > lim || ldc > lim || ldd > lim)
         return kInvalidValue;
-    // row strides: op(A) is m x k (A stored m x k, or k x m when transposed), etc.
-    if (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n) || ldd < n ||
+    // row strides: op(A) is m x k (A stored m x k, or k x m when transposed),
+    // etc.; with k == 0 neither A nor B is read, nor are their strides
+    if ((k > 0 && (lda < (trans_a ? m : k) || ldb < (trans_b ? k : n))) || ldd < n ||
         (beta != 0.f && ldc < n))
         return kInvalidValue;
     // op(A) is A (k-contiguous) or A^T of a stored k x m (m-contiguous); op(B)

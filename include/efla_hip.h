@@ -384,8 +384,9 @@ int gemm_backward_hip(const void* grad_c, const void* a, const void* b, void* gr
  * row-major with row strides lda, ldb, ldc, ldd; op(A) is A (stored m x k) or,
  * with trans_a, A^T (A stored k x m); op(B) likewise (k x n or, transposed,
  * n x k).  One dtype for every operand, fp32 accumulation.  C is read only
- * when beta != 0 and may be D; k == 0 gives D = bias + beta C.  m or n == 0
- * -> 0; bad strides or pointers -> 1. */
+ * when beta != 0 and may be D; k == 0 gives D = bias + beta C without
+ * reading A or B (they may be NULL, their strides are not checked).  m or
+ * n == 0 -> 0; bad strides or pointers -> 1. */
 int gemm_ex_hip(int trans_a, int trans_b, size_t m, size_t n, size_t k, float alpha,
                 const void* a, size_t lda, const void* b, size_t ldb, const void* bias,
                 float beta, const void* c, size_t ldc, void* d, size_t ldd, int dtype,

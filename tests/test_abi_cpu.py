@@ -260,6 +260,9 @@ def test_gemm_ex_and_residual_validation(L):
     assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 4, p, 8, NULL, 0.0, NULL, 0, p, 8, bf, NULL) == 1
     assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 0.0, NULL, 0, p, 4, bf, NULL) == 1
     assert L.gemm_ex_hip(0, 0, 8, 8, 8, 1.0, p, 8, p, 8, NULL, 1.0, NULL, 8, p, 8, bf, NULL) == 1
+    # k == 0 reads neither operand, but D's stride is still checked
+    assert L.gemm_ex_hip(0, 0, 8, 8, 0, 1.0, NULL, 0, NULL, 0, NULL, 0.0, NULL, 0, p, 4, bf,
+                         NULL) == 1
     assert L.layernorm_backward_residual_hip(p, p, p, p, p, NULL, p, NULL, NULL, 2048, 1024,
                                              NULL) == 1
 
