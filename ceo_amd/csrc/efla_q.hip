@@ -855,12 +855,12 @@ static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** c
     *h = *Vn = nullptr;
     *Pc = nullptr;
     if (__is_same(T, bf16)) {
-        *Tc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
+        *Tc = c.take<bf16>((size_t)p.slots * p.H * fast::TRI_ELEMS);
         *bc = c.take<float>((size_t)p.slots * p.H * 64);
         *dcc = c.take<float>((size_t)p.slots * p.H * 128);
         if (with_h) {
             *h = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
-            *Pc = c.take<bf16>((size_t)p.slots * p.H * 64 * 64);
+            *Pc = c.take<bf16>((size_t)p.slots * p.H * fast::TRI_ELEMS);
         }
     } else {
         *W = c.take<T>((size_t)p.ntok * p.H * p.K);

@@ -41,6 +41,19 @@ using mf::tr_rows4;
 
 constexpr int LD64 = ldb<64>();
 
+// A packed lower-triangular matrix (tri_off) straight into a [64][LD64] LDS
+// tile, as mf::dma_tile copies a full one: every 16-byte LDS chunk is written,
+// the upper and pad chunks from the zero stub.
+template <int NW>
+__device__ __forceinline__ void dma_tri(bf16* lds, const bf16* src, int rot, int l) {
+    constexpr int CPR = LD64 / 8, NI = 64 * CPR / 64;
+    const int w = mf::wave();
+    for (int i = (w + NW - rot % NW) % NW; i < NI; i += NW) {
+        const int c = 64 * i + l, row = c / CPR, col = c - row * CPR;
+        mf::dma16(src, (unsigned)(col < 8 ? tri_off(row, col) : TRI_ZERO) * 2u, lds + 512 * i);
+    }
+}
+
 __device__ __forceinline__ void store4s(bf16* p, floatx4 a, float s) {
     *reinterpret_cast<bf16x4*>(p) =
         bf16x4{(bf16)(a[0] * s), (bf16)(a[1] * s), (bf16)(a[2] * s), (bf16)(a[3] * s)};
@@ -193,7 +206,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         const int len = (int)min((long)64, slen - (long)n * 64);
         const long cid = (long)(slot0 + n) * H + h;
         pre.load(q, k, dO, Tc, bc, bos, len, h, V, v0, cid, ld.q, ld.k, (long)H * V);
-        if constexpr (PS) rp.load(Pc + cid * 64 * 64, 64, 64);
+        if constexpr (PS) load_tri(rp, Pc + cid * TRI_ELEMS);
     };
     auto stage = [&](ScanDhBuf<K, PS>& bf) {
         pre.stage(bf);
@@ -403,7 +416,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         kcopy(sm.h, hist + chb, K, 64, 4, l);
         kcopy(sm.dh, dhist + chb, K, 64, 6, l);
         if constexpr (PS)
-            mf::dma_tile<64, 64, LD64, NW>(sm.Ps, Pws + cid * 64 * 64, 64, 64, 2, l);
+            dma_tri<NW>(sm.Ps, Pws + cid * TRI_ELEMS, 2, l);
         // b (16 chunks of 16 bytes) and dc/dlambda, dc/dbeta (32 chunks)
         if (w8 == NW - 1 && l < 16) mf::dma16(bws + cid * 64, 16u * l, sm.coef[par][0]);
         if (w8 == NW - 2 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
@@ -412,8 +425,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         kcopy(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
     };
     auto copy_t = [&](const Item& I, int l) {
-        mf::dma_tile<64, 64, LD64, NW>(sm.Tb, Tws + ((long)I.slot * H + I.h) * 64 * 64, 64, 64, 5,
-                                      l);
+        dma_tri<NW>(sm.Tb, Tws + ((long)I.slot * H + I.h) * TRI_ELEMS, 5, l);
     };
     auto copy_k = [&](const Item& I, int l) {
         kcopy(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);

@@ -55,6 +55,47 @@ constexpr int ldb() {  // bf16 row stride: D + 16 keeps b128, b64 and tr16 reads
     return D + 16;
 }
 
+// The per-chunk lower-triangular 64 x 64 bf16 matrices T and P live in the
+// workspace packed: the ten lower 16 x 16 tiles (I >= J) in lower_tile order,
+// each row-major (16 rows of 32 bytes), then a zero stub that loads of the
+// upper tiles read, so the LDS copies stay whole 64 x 64 tiles while HBM
+// moves 5184 instead of 8192 bytes per (chunk, head).
+constexpr int TRI_ZERO = 10 * 256;         // element offset of the zero stub
+constexpr int TRI_ELEMS = TRI_ZERO + 32;  // bf16 per (chunk, head): 81 64-byte lines
+
+// Element offset of the 8-column piece f (0..7) of row `row` (the zero stub
+// for pieces above the diagonal tiles).
+__device__ __forceinline__ int tri_off(int row, int f) {
+    const int I = row >> 4, J = f >> 1;
+    return J <= I ? (I * (I + 1) / 2 + J) * 256 + (row & 15) * 16 + (f & 1) * 8 : TRI_ZERO;
+}
+
+// Writes row `row`, column tile J (16 values as two 8-value pieces) of a
+// packed matrix; the upper tiles are not stored, and the thread holding row 0,
+// tile 1 writes the zero stub instead.
+__device__ __forceinline__ void tri_store_piece(bf16* __restrict__ base, int row, int J,
+                                                const bf16x8& lo, const bf16x8& hi) {
+    if (J <= (row >> 4)) {
+        bf16* dst = base + tri_off(row, 2 * J);
+        *reinterpret_cast<bf16x8*>(dst) = lo;
+        *reinterpret_cast<bf16x8*>(dst + 8) = hi;
+    } else if (row == 0 && J == 1) {
+        *reinterpret_cast<bf16x8*>(base + TRI_ZERO) = bf16x8{};
+        *reinterpret_cast<bf16x8*>(base + TRI_ZERO + 8) = bf16x8{};
+    }
+}
+
+// A packed matrix into the registers of a 64 x 64 tile loader, as
+// TileRegs::load would hold the full matrix (upper pieces read as zeros).
+template <int NT>
+__device__ __forceinline__ void load_tri(mf::TileRegs<64, 64, NT>& r, const bf16* __restrict__ src) {
+    r.tid = (int)threadIdx.x;
+    r.valid = 64;
+    const int f = r.fg(), t = r.t0();
+#pragma unroll
+    for (int j = 0; j < r.TPT; ++j) r.x[j] = *reinterpret_cast<const bf16x8*>(src + tri_off(t + j, f));
+}
+
 __device__ __forceinline__ void store4(bf16* p, floatx4 a) {
     *reinterpret_cast<bf16x4*>(p) = bf16x4{(bf16)a[0], (bf16)a[1], (bf16)a[2], (bf16)a[3]};
 }
@@ -230,9 +271,7 @@ __global__ void __launch_bounds__(NT) prep_kernel(const bf16* __restrict__ k,
 #pragma unroll
             for (int c = 0; c < 8; ++c) lo[c] = hi[c] = (bf16)0.f;
         }
-        bf16* dst = Tout + cid * 64 * 64 + tr * 64 + 16 * J;
-        *reinterpret_cast<bf16x8*>(dst) = lo;
-        *reinterpret_cast<bf16x8*>(dst + 8) = hi;
+        tri_store_piece(Tout + cid * TRI_ELEMS, tr, J, lo, hi);
     }
 }
 
@@ -284,7 +323,7 @@ struct ChunkRegs {
         if (WITH_Q) rq.load(q + bos * lq + (long)h * K, lq, len);
         rk.load(k + bos * lk + (long)h * K, lk, len);
         rv.load(vsl + bos * lv + (long)h * V + v0, lv, len);
-        rt.load(Tc + cid * 64 * 64, 64, 64);
+        load_tri(rt, Tc + cid * TRI_ELEMS);
         if (threadIdx.x < 64) b = bc[cid * 64 + threadIdx.x];
     }
     template <typename Buf>
@@ -409,12 +448,11 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         }
         __syncthreads();  // P complete
         if (pout && vsl == 0) {
-            // hand P to the backward: [t][t'] bf16, zero above the diagonal
-            const int tr = threadIdx.x >> 2, c0 = 16 * (threadIdx.x & 3);
-            bf16* dst = pout + ((long)(slot0 + n) * H + h) * 64 * 64 + tr * 64 + c0;
-            *reinterpret_cast<bf16x8*>(dst) = *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + c0);
-            *reinterpret_cast<bf16x8*>(dst + 8) =
-                *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + c0 + 8);
+            // hand P to the backward (packed lower tiles)
+            const int tr = threadIdx.x >> 2, J = threadIdx.x & 3;
+            tri_store_piece(pout + ((long)(slot0 + n) * H + h) * TRI_ELEMS, tr, J,
+                            *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + 16 * J),
+                            *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + 16 * J + 8));
         }
         const bf16x8 vb0 = frag_from_c(vn[0], vn[1]), vb1 = frag_from_c(vn[2], vn[3]);
         // o^T = S^T Q^T + Vn^T P^T: tile tb holds (value 16w + 4g + i, token 16tb + r)

@@ -169,11 +169,12 @@ def test_workspace_sizes(L):
     fw = f(4, 8192, 0, 32, 128, 128, 14)
     bw = b(4, 8192, 0, 32, 128, 128, 14)
     slots, H = 4 * 8192 // 64, 32
-    t_bytes = slots * H * 64 * 64 * 2        # bf16 T per chunk
+    t_bytes = slots * H * (10 * 256 + 32) * 2  # bf16 T per chunk: ten lower 16x16 tiles
     state_bytes = slots * H * 128 * 128 * 2  # bf16 chunk states
     assert fw >= t_bytes
     assert fw < t_bytes + state_bytes        # no states unless asked for
     assert bw >= fw + 2 * state_bytes        # h and dh
+    assert bw < fw + 2 * state_bytes + 2 * t_bytes  # P packed as T is
     assert bw < 16 * 2**30                   # fits comfortably in 288 GB
     assert f(4, 8192, 0, 32, 96, 128, 14) == 0
     assert f(1, 65536, 40, 16, 128, 256, 14) > 0   # packed, cfg5 shape

@@ -100,7 +100,7 @@ def test_noalloc_runs_just_inside_scratch():
     L = _lib.lib()
     announce("noalloc forward: problem just inside the fixed scratch")
     limit = 64 << 20  # EFLA_NOALLOC_SCRATCH_BYTES
-    x = _inputs(5, 1, 64 * 7000 // 16, 16, 64, 64, torch.bfloat16)
+    x = _inputs(5, 1, 64 * 11000 // 16, 16, 64, 64, torch.bfloat16)  # 11,000 chunk-heads
     assert efla.workspace_bytes("fwd", 1, x["T"], 16, 64, 64, torch.bfloat16) <= limit
     rc, o, _ = _call(L, x, True)
     assert rc == 0
