@@ -109,6 +109,7 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
         for (int fb = 0; fb < K / 16; ++fb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) S[fb][i] = S0[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
+        mf::dma_wait();  // retired here, not by a vmcnt(0) inside the chunk loop
     }
     ChunkRegs<K, false, true> pre;
     auto prefetch = [&](int n) {
@@ -196,6 +197,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
         for (int fb = 0; fb < K / 16; ++fb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) dS[fb][i] = dST[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
+        mf::dma_wait();  // retired here, not by a vmcnt(0) inside the chunk loop
     }
     if constexpr (!PS)
         for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;

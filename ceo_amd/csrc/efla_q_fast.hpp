@@ -401,6 +401,10 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         for (int fb = 0; fb < K / 16; ++fb)
 #pragma unroll
             for (int i = 0; i < 4; ++i) S[fb][i] = S0[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
+        // retire these loads here: left pending, their waits land inside the
+        // chunk loop as vmcnt(0), which every chunk would then pay for the
+        // next chunk's prefetch and the last chunk's stores
+        mf::dma_wait();
     }
     for (int i = threadIdx.x; i < 64 * LDP; i += NT) sm.P[i] = (bf16)0.f;
 
