@@ -199,26 +199,32 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
     }
     const long waves = (long)gridDim.x * (NTH / kWave);
     long row = (long)blockIdx.x * (NTH / kWave) + wv;
-    // the next row's x, dy (and the residual gradient) are loaded while this one computes
-    bf16x8 xn[NV], gn[NV], rn[NV] = {};
-    auto fetch = [&](long r) {
+    // the next two rows' x, dy (and the residual gradient) are in flight while
+    // this one computes: with one row a wave kept too few bytes in flight to
+    // cover the loaded memory latency
+    bf16x8 xn[2][NV], gn[2][NV], rn[2][NV] = {};
+    auto fetch = [&](long r, int sl) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            xn[j] = *reinterpret_cast<const bf16x8*>(x + r * D + (j * 64 + lane) * 8);
-            gn[j] = *reinterpret_cast<const bf16x8*>(dy + r * D + (j * 64 + lane) * 8);
-            if (res) rn[j] = *reinterpret_cast<const bf16x8*>(res + r * D + (j * 64 + lane) * 8);
+            xn[sl][j] = *reinterpret_cast<const bf16x8*>(x + r * D + (j * 64 + lane) * 8);
+            gn[sl][j] = *reinterpret_cast<const bf16x8*>(dy + r * D + (j * 64 + lane) * 8);
+            if (res) rn[sl][j] = *reinterpret_cast<const bf16x8*>(res + r * D + (j * 64 + lane) * 8);
         }
     };
-    if (row < rows) fetch(row);
+    if (row < rows) fetch(row, 0);
+    if (row + waves < rows) fetch(row + waves, 1);
     for (; row < rows; row += waves) {
         bf16x8 xv[NV], gv[NV], rv[NV];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            xv[j] = xn[j];
-            gv[j] = gn[j];
-            rv[j] = rn[j];
+            xv[j] = xn[0][j];
+            gv[j] = gn[0][j];
+            rv[j] = rn[0][j];
+            xn[0][j] = xn[1][j];
+            gn[0][j] = gn[1][j];
+            rn[0][j] = rn[1][j];
         }
-        if (row + waves < rows) fetch(row + waves);
+        if (row + 2 * waves < rows) fetch(row + 2 * waves, 1);
         const float mu = mean[row], rs = rstd[row];
         float sg = 0.f, sgx = 0.f;
 #pragma unroll
@@ -270,36 +276,37 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
 // out[c] = sum_b part[b][c] for c < NS D (dw = out[0..D), db = out[D..2D),
 // fp32 or with pbf bf16, and with NS = 3 the dx column sums out[2D..3D) as
 // bf16 into dxs).
-// Workgroup: 16 row groups x 16 lanes of 4 columns (16-byte loads); grid over
-// 64-column blocks (NS D is a multiple of 4 when D is even; odd D reads scalars).
+// Workgroup: 64 row groups x 4 lanes of 4 columns (16-byte loads), 16 columns
+// per workgroup, so the grid has NS D / 16 workgroups and each thread's rows
+// (b = rg, rg + 64, ...; at most 8 for the 512 partial rows) are all in flight
+// at once.  Row group rg sums its rows in increasing b, then the 64 group
+// sums are added in increasing rg: a fixed order.  Odd D reads scalars.
+constexpr int RED_RG = 64, RED_U = 8;
 __global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ part, int nblk,
                                                      int D, int NS, void* __restrict__ dw,
                                                      void* __restrict__ db, int pbf,
                                                      bf16* __restrict__ dxs) {
-    __shared__ float acc[16][64 + 1];
-    const int q = threadIdx.x & 15, rg = threadIdx.x >> 4;
-    const int c0 = blockIdx.x * 64 + 4 * q;
+    __shared__ float acc[RED_RG][16 + 1];
+    const int q = threadIdx.x & 3, rg = threadIdx.x >> 2;
+    const int c0 = blockIdx.x * 16 + 4 * q;
     const int W = NS * D;
     float s[4] = {0.f, 0.f, 0.f, 0.f};
     if (W % 4 == 0 && c0 + 4 <= W) {
-        // 8 rows' loads in flight before any is added (rows past the end
-        // load the last row and count as zero); the sum stays in row order
-        constexpr int U = 8;
-        for (int b0 = rg; b0 < nblk; b0 += 16 * U) {
-            floatx4 v[U];
+        for (int b0 = rg; b0 < nblk; b0 += RED_RG * RED_U) {
+            floatx4 v[RED_U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int b = min(b0 + 16 * u, nblk - 1);
+            for (int u = 0; u < RED_U; ++u) {  // rows past the end re-read the last row
+                const int b = min(b0 + RED_RG * u, nblk - 1);
                 v[u] = *reinterpret_cast<const floatx4*>(part + (long)b * W + c0);
             }
 #pragma unroll
-            for (int u = 0; u < U; ++u)
-                if (b0 + 16 * u < nblk)
+            for (int u = 0; u < RED_U; ++u)
+                if (b0 + RED_RG * u < nblk)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) s[i] += v[u][i];
         }
     } else {
-        for (int b = rg; b < nblk; b += 16)
+        for (int b = rg; b < nblk; b += RED_RG)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 if (c0 + i < W) s[i] += part[(long)b * W + c0 + i];
@@ -307,11 +314,11 @@ __global__ void __launch_bounds__(NTH) reduce_kernel(const float* __restrict__ p
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[rg][4 * q + i] = s[i];
     __syncthreads();
-    if (threadIdx.x < 64) {
-        const int c = blockIdx.x * 64 + threadIdx.x;
+    if (threadIdx.x < 16) {
+        const int c = blockIdx.x * 16 + threadIdx.x;
         float t = 0.f;
-#pragma unroll
-        for (int k = 0; k < 16; ++k) t += acc[k][threadIdx.x];
+#pragma unroll 8
+        for (int k = 0; k < RED_RG; ++k) t += acc[k][threadIdx.x];
         if (c < D) {
             if (dw && pbf) static_cast<bf16*>(dw)[c] = (bf16)t;
             else if (dw) static_cast<float*>(dw)[c] = t;
@@ -440,7 +447,7 @@ static int ln_backward(const void* grad_output, const void* input, const void* w
     }
     EFLA_CHECK(hipPeekAtLastError());
     if (parts) {
-        const unsigned gr = (unsigned)((ns * D + 63) / 64);
+        const unsigned gr = (unsigned)((ns * D + 15) / 16);
         EFLA_LAUNCH("layernorm_bwd_reduce", ln::reduce_kernel, dim3(gr), dim3(ln::NTH), stream,
                     (const float*)part, (int)nblk, (int)D, ns, grad_weight, grad_bias, pbf ? 1 : 0,
                     ns == 3 ? (bf16*)grad_input_colsum : (bf16*)nullptr);
