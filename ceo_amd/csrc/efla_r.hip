@@ -603,6 +603,9 @@ struct RBwdSmem {
     SegLds<D, D / NS, true, CKS, CKS, true> seg;
     float gkv[2][D / NS];                // S_n^T dO per column
     float red[2][16];                    // grad_c partials per wave
+    // NS > 1: this workgroup's fp32 grad_k row sums of a segment [token][row],
+    // added into the output buffer once per segment (by segment parity)
+    float gks[NS > 1 ? 2 : 1][NS > 1 ? SEGF : 1][NS > 1 ? D : 1];
 };
 
 template <int D, int NS, int LPC>
@@ -836,8 +839,7 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
                         } else {
                             const int row = f0 + 4 * g4 + j16, lr = row - cb * NC;
                             const float sn = (lr >= 0 && lr < NC) ? sm.gkv[par][lr] : 0.f;
-                            unsafeAtomicAdd(part_gk + o + j16,
-                                            fmaf(glam2, (float)kb[row], pick4(acc, j16) + sn));
+                            sm.gks[seg & 1][j][row] = fmaf(glam2, (float)kb[row], pick4(acc, j16) + sn);
                         }
                     }
                 }
@@ -848,6 +850,19 @@ __global__ void __launch_bounds__((rfast_threads<D, NS, LPC>())) r_bwd_fast_kern
             }
         }
         __syncthreads();  // the segment's staged data and last row sums read
+        if constexpr (NS > 1) {
+            // the segment's grad_k row sums into the shared fp32 buffer: whole
+            // 256-byte rows of atomics, off the token chain (issued per token,
+            // each atomic's round trip landed in the next token's wait for its
+            // state loads, which share the in-order vector-memory counter).
+            // Segment seg - 1 writes the other buffer; seg - 2 writes this one
+            // only after the barriers of seg - 1's rebuild.
+            const float* src = &sm.gks[seg & 1][0][0];
+            for (int i = tid; i < n * D; i += NT) {
+                const int jj = i / D, row = i - jj * D;
+                unsafeAtomicAdd(part_gk + base0 + (t0 + jj) * tstride + row, src[i]);
+            }
+        }
     }
     // dL/dS_0 in the reference's [row][c] layout
     bf16* gs = grad_state + (long)bh * dd;
