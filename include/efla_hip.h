@@ -55,8 +55,9 @@ extern "C" {
  * Scratch comes from the stream's cached workspace (leased per call): 4 bytes
  * per (b, t, h) for the coefficients, and for d = 64 / 128 with B*H at most
  * half the device's CU count (two workgroups per (b, h), each owning half of
- * the state's columns) 8 bytes per output element more for the fp32 partial
- * row sums (cfg3's B=4, T=8192, H=32, d=128: 1.07 GB).
+ * the state's columns) 4 bytes per output element more: one fp32 buffer of
+ * row sums both workgroups add into (cfg3's B=4, T=8192, H=32, d=128:
+ * 0.54 GB).  `efla_rt_workspace_release_stream` frees a stream's share.
  */
 int efla_forward_hip(const void* k, const void* v, void* state, void* output,
                      size_t batch_size, size_t seq_len, size_t num_heads, size_t head_dim,
@@ -70,8 +71,8 @@ int efla_forward_hip(const void* k, const void* v, void* state, void* output,
  * cached workspace instead of the reference's per-call (T+1)*d*d allocation:
  * one bf16 d*d checkpoint per 32 tokens (64 on the LDS-resident path) and one
  * segment's states per (b, h), 8 bytes per (b, t, h) of coefficients, and with
- * the column split (as efla_forward_hip) 8 bytes per grad_k element for the
- * fp32 partial row sums.
+ * the column split (as efla_forward_hip) 4 bytes per grad_k element for the
+ * fp32 row sums.
  */
 int efla_backward_hip(const void* grad_output, const void* k, const void* v, const void* state,
                       void* grad_k, void* grad_v, void* grad_state, size_t batch_size,
