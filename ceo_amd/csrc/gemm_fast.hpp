@@ -236,15 +236,44 @@ __device__ __forceinline__ unsigned ep_off(int row, int col) {  // col % 4 == 0
     return (unsigned)(row * (128 * TNI) + (((col >> 2) ^ (row & 15)) << 4));
 }
 
-template <typename T, int EPI, int TNI>
+template <typename T, int EPI, int TNI, bool AHEAD>
 __device__ __forceinline__ void epilogue_wave(const EpiArgs<T>& ea, const floatx16 (&acc)[TNI][4],
                                               int split, long mw, long nw, long M, long N, int l,
                                               char* wp) {
     constexpr int WC = 32 * TNI;  // columns of the wave's block
+    constexpr int NP = WC / 16;   // 8-element pieces per lane and 32-row pass
     typedef __attribute__((__vector_size__(8 * sizeof(T)))) T t8;
     // DGELU with column sums: this lane's 8 columns (piece c8 = l % (WC / 8)
     // of every row it finishes) summed over its rows
     float csum[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // A lane's pieces keep their columns from pass to pass (piece s: row
+    // (64 s + l) / (WC / 8) of the pass, columns 8 ((64 s + l) % (WC / 8))).
+    // The pre-activation (DGELU) or residual (RESID) pieces are read ahead of
+    // their use: with AHEAD those of pass j + 1 while pass j is finished, once
+    // pass j's accumulators are in LDS (their registers are free by then);
+    // otherwise (the kernels whose main loop leaves too few registers) those
+    // of pass j, as soon as its accumulators are in LDS.
+    constexpr bool IN = EPI == EPI_DGELU || EPI == EPI_RESID;
+    const bool rd = IN && (EPI == EPI_DGELU || ea.beta != 0.f);
+    const T* src = EPI == EPI_DGELU ? ea.aux : ea.c;
+    const long lds = EPI == EPI_DGELU ? ea.ldaux : ea.ldc;
+    auto piece = [&](int s, int& row, long& n) {
+        const int p = 64 * s + l;
+        row = p / (WC / 8);
+        n = nw + 8 * (p % (WC / 8));
+    };
+    auto fetch = [&](int j, t8 (&dst)[NP]) {
+#pragma unroll
+        for (int s = 0; s < NP; ++s) {
+            int row;
+            long n;
+            piece(s, row, n);
+            const long m = mw + 32 * j + row;
+            dst[s] = (m < M && n < N) ? *reinterpret_cast<const t8*>(src + m * lds + n) : t8{};
+        }
+    };
+    t8 inp[2][NP];
+    if (AHEAD && rd && mw < M) fetch(0, inp[0]);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const long r0 = mw + 32 * j;
@@ -260,11 +289,15 @@ __device__ __forceinline__ void epilogue_wave(const EpiArgs<T>& ea, const floatx
                     v[e] = (EPI == EPI_PARTIAL ? 1.f : ea.alpha) * acc[i][j][4 * qd + e];
                 *reinterpret_cast<mf::floatx4*>(wp + ep_off<TNI>(l & 31, col)) = v;
             }
+        if (AHEAD && rd && j + 1 < 4 && r0 + 32 < M) fetch(j + 1, inp[(j + 1) & 1]);
+        if (!AHEAD && rd) fetch(j, inp[j & 1]);
 #pragma unroll
-        for (int s = 0; s < WC / 16; ++s) {
-            const int p = 64 * s + l;
-            const int row = p / (WC / 8), c8 = p % (WC / 8);  // 8-element piece c8 of the row
-            const long m = r0 + row, n = nw + 8 * c8;
+        for (int s = 0; s < NP; ++s) {
+            int row;
+            long n;
+            piece(s, row, n);
+            const int c8 = (int)(n - nw) / 8;
+            const long m = r0 + row;
             const mf::floatx4 v0 =
                 *reinterpret_cast<const mf::floatx4*>(wp + ep_off<TNI>(row, 8 * c8));
             const mf::floatx4 v1 =
@@ -291,16 +324,21 @@ __device__ __forceinline__ void epilogue_wave(const EpiArgs<T>& ea, const floatx
 #pragma unroll
                 for (int e = 0; e < 8; ++e) y[e] = (T)gelu::gelu_f<true>((float)pre[e]);
             } else if constexpr (EPI == EPI_DGELU) {
-                const t8 u = *reinterpret_cast<const t8*>(ea.aux + m * ea.ldaux + n);
+                const t8 u = inp[j & 1][s];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     y[e] = (T)((float)(T)v[e] * gelu::gelu_df<true>((float)u[e]));
                     csum[e] += (float)y[e];
                 }
             } else if constexpr (EPI == EPI_RESID) {
-                const t8 cc = *reinterpret_cast<const t8*>(ea.c + m * ea.ldc + n);
+                if (rd) {
+                    const t8 cc = inp[j & 1][s];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) y[e] = (T)(v[e] + ea.beta * (float)cc[e]);
+                    for (int e = 0; e < 8; ++e) y[e] = (T)(v[e] + ea.beta * (float)cc[e]);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) y[e] = (T)v[e];
+                }
             } else {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) y[e] = (T)v[e];
@@ -498,8 +536,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_fast_kernel(Opnd A, Opnd B, long
         {
             const int le = mf::tid_in((int)it) & 63;
             char* wp = smem + 2 * (buf ^ 1) * TILE_BYTES + (4096 * TNI) * w;
-            epilogue_wave<T, EPI, TNI>(ea, acc, cur.split, (long)cur.m0 + wm, (long)cur.n0 + wn,
-                                       M, N, le, wp);
+            epilogue_wave<T, EPI, TNI, AKC && BKC>(ea, acc, cur.split, (long)cur.m0 + wm,
+                                                    (long)cur.n0 + wn, M, N, le, wp);
         }
         __syncthreads();  // the next item's first copies refill the buffer
         if (!more) break;
