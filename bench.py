@@ -16,8 +16,8 @@ storage with fp32 accumulation.
 
 Timing: W untimed steps, then K timed steps between torch.cuda.synchronize()
 calls, with a hipEvent pair per step on the launch stream; ``ms_per_step`` is
-the median step (median of 50 timed steps after 10 warm-up
-steps, the defaults), ``mean_ms_per_step`` the mean.  The per-kernel split
+the median step (by default the median of 50 timed steps after 10 warm-up
+steps), ``mean_ms_per_step`` the mean.  The per-kernel split
 comes from a separate pass of K steps with the library's launch profiler
 (an event pair around each launch, which would inflate the timed steps).
 

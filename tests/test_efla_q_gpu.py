@@ -118,8 +118,8 @@ def test_nan_inf_stay_in_their_sequence_and_head(oracle):
     """A NaN in one token's k and an Inf in another sequence's v contaminate
     only their own (sequence, head): every other (sequence, head) gets outputs
     and gradients bit-identical to a clean run, and finite; the contaminated
-    ones carry non-finite values from the next chunk on (SURVEY's failure-
-    detection row: NaN/Inf injected into the inputs must propagate)."""
+    ones carry non-finite values from the next chunk on (failure detection:
+    a NaN or Inf injected into the inputs must propagate, and only there)."""
     from ceo_amd.efla import chunk_efla_bwd, chunk_efla_fwd
 
     B, T, H, K, V = 3, 200, 2, 128, 128
