@@ -369,11 +369,12 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     constexpr int NTG = grad_threads<NG>(), NW = NTG / 64;  // threads, waves
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 16 / NG;  // NF key tiles per group
     // K-wide operand tiles (Qs, Ks, h, dh) are kept as K / 64 column halves of
-    // 64 with row stride LDH (72 for K = 128: the same 64 x LDK elements, but
-    // 16-byte row reads of a 64-wide half with a 144-byte stride run about
-    // 1.45x the rate of a 288-byte stride on gfx950); every fragment's k or
-    // line range lies inside one half.  kh(base, c) is the half holding
-    // column c, read at column c % 64.
+    // 64 with row stride LDH (72 for K = 128: the same 64 x LDK elements).  An
+    // LDS probe runs 16-byte row reads of these halves at about half the rate
+    // of the full 288-byte rows, yet the kernel measures 1-1.1 % faster with
+    // the halves than with full rows (its time does not follow its LDS read
+    // rate).  Every fragment's k or line range lies inside one half.
+    // kh(base, c) is the half holding column c, read at column c % 64.
     // (The 8-wave d_v = 256 instantiation keeps [64][LDK] tiles: with the
     // halves, hipcc's register allocation fails on it.)
     constexpr int KH = NG == 4 ? K / 64 : 1, LDH = KH > 1 ? 72 : LDK, HALF = 64 * LDH;

@@ -51,7 +51,12 @@ __device__ __forceinline__ int pim(int tile, int r) {
 }
 
 template <int D>
-constexpr int ldb() {  // bf16 row stride: D + 16 keeps b128, b64 and tr16 reads conflict-free
+// bf16 row stride D + 16: 16-byte row reads (frag_nat, frag_row) and c-order
+// transposing reads (frag_trc) run at the LDS's full rate on it (about 200 B
+// per CU-cycle measured, against about 120 for stride D + 8 with D = 64);
+// natural-order transposing reads (frag_tr: rows r and r + 8 in the same
+// banks) run at about 120 on every 16-byte-aligned stride.
+constexpr int ldb() {
     return D + 16;
 }
 
