@@ -6,8 +6,10 @@
 // ("line-contiguous", LC).  The four combinations cover the forward product
 // (A KC, B LC), dA = dC B^T (both KC) and dB = A^T dC (both LC).
 //
-// Workgroup tile 256 x 256 x 64, four waves each owning 128 x 128 of the
-// output as 4 x 4 tiles of v_mfma_f32_32x32x16 (accumulators in AGPRs).
+// Workgroup tile 256 x 256 x 64.  The library launches eight waves (two per
+// SIMD), each owning 128 x 64 of the output as 4 x 2 tiles of
+// v_mfma_f32_32x32x16; the kernel also compiles for four waves of 128 x 128
+// (4 x 4 tiles).
 // The product is formed transposed, C^T = B^T A^T: B's fragments are the MFMA
 // A operand (rows n) and A's the B operand (columns m), so each lane ends up
 // holding 4 consecutive n of one output row m and writes 8-byte row pieces.
