@@ -10,13 +10,19 @@
 //   Vn = U - W S                       (the chunk's effective values)
 //   O  = Q S + tril(Q K^T) Vn
 //   S' = S + K^T Vn
-// Forward kernels: prep (b, T, W, U; parallel over chunks), state (serial over
-// chunks, one workgroup per (sequence, head, 64-wide value slice), S held in
-// MFMA accumulators), output (parallel over chunks).  The backward recomputes
-// b, W, U and the chunk states, then runs dv_local (tril(QK^T)^T dO), a
-// reverse state scan for dS, dq/dk/dw per chunk, and the WY backward that
-// carries dW, dU through T and b (including the dc/dlambda term of
-// efla.cu:384-451 and dbeta = dc * exp(-beta lambda)).
+// Two kernel sets implement it.  bf16 runs on the gfx950 kernels of
+// efla_q_fast.hpp (prep, forward scan with the output) and efla_q_bwd.hpp
+// (state recompute, reverse state scan, persistent per-chunk gradient
+// kernel); their headers describe them.  fp32 runs on the generic kernels in
+// this file.  Generic forward: prep (b,
+// T, W, U; parallel over chunks), state (serial over chunks, one workgroup
+// per (sequence, head, 64-wide value slice), S held in MFMA accumulators),
+// output (parallel over chunks).  Generic backward: it recomputes b, W, U and
+// the chunk states, then runs dv_local (tril(QK^T)^T dO), a reverse state
+// scan for dS, dq/dk/dw per chunk, and the WY backward that carries dW, dU
+// through T and b (including the dc/dlambda term of efla.cu:384-451 and
+// dbeta = dc * exp(-beta lambda)).  This file also holds the host side:
+// validation, workspace layout and the launches.
 #include <hip/hip_runtime.h>
 #include <stdlib.h>
 
