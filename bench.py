@@ -623,6 +623,15 @@ def main() -> int:
         efla.chunk_efla_fwd(x["q"], x["k"], x["v"], x["beta"], cu_seqlens=cu)
         efla.chunk_efla_bwd(x["q"], x["k"], x["v"], x["beta"], x["do"], cu_seqlens=cu)
 
+    def step_recompute_states():
+        # the forward hands over its per-chunk factors (T, b and the
+        # coefficient derivatives, 5.9 KB per chunk and head) but not the chunk
+        # states or P: the backward recomputes the states
+        efla.chunk_efla_fwd(x["q"], x["k"], x["v"], x["beta"], cu_seqlens=cu, workspace=ws,
+                            save_states=False)
+        efla.chunk_efla_bwd(x["q"], x["k"], x["v"], x["beta"], x["do"], cu_seqlens=cu,
+                            workspace=ws, reuse_forward=True, reuse_states=False)
+
     stream = torch.cuda.current_stream(dev)
 
     def timed(fn, n):
@@ -666,6 +675,12 @@ def main() -> int:
         recompute = median(per_re)
         print(f"[bench] recompute variant: median {recompute:.4f} ms/step", file=sys.stderr,
               flush=True)
+        for _ in range(args.warmup):
+            step_recompute_states()
+        per_rs, _ = timed(step_recompute_states, args.steps)
+        recompute_states = median(per_rs)
+        print(f"[bench] states-only recompute: median {recompute_states:.4f} ms/step",
+              file=sys.stderr, flush=True)
 
     ref_abi = None
     if args.config == "cfg3" and not args.no_ref_abi:
@@ -750,6 +765,14 @@ def main() -> int:
             "ms_per_step": round(recompute, 4),
             "tokens_per_s": round(ntok / (recompute * 1e-3), 1),
             "pct_mfma_peak": round(100 * step_flops / (recompute * 1e-3) / 1e12 / peak, 3),
+            "states_only": {
+                "what": "the forward hands over its per-chunk factors (T, b, dc) but not "
+                        "the chunk states or P; the backward recomputes the states",
+                "ms_per_step": round(recompute_states, 4),
+                "tokens_per_s": round(ntok / (recompute_states * 1e-3), 1),
+                "pct_mfma_peak": round(
+                    100 * step_flops / (recompute_states * 1e-3) / 1e12 / peak, 3),
+            },
         }
 
     cpu = None
