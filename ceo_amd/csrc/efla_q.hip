@@ -50,10 +50,13 @@ constexpr int pad() {
 
 // Sanitise cu_seqlens into [0, ntok] (non-decreasing) and build chunk offsets.
 // One workgroup of 1024 threads; each owns a contiguous run of sequences.
+// With `order` (N <= LPT_MAX_SEQS) it also ranks the sequences by decreasing
+// chunk count, ties in index order, and writes order[rank] = sequence.
 __global__ void __launch_bounds__(1024) chunk_offsets_kernel(const int32_t* __restrict__ cu,
                                                              int N, long ntok,
                                                              int32_t* __restrict__ cu_s,
-                                                             int32_t* __restrict__ coff) {
+                                                             int32_t* __restrict__ coff,
+                                                             int32_t* __restrict__ order) {
     __shared__ int part[1024];
     __shared__ int runmax[1024];
     const int tid = threadIdx.x;
@@ -109,6 +112,22 @@ __global__ void __launch_bounds__(1024) chunk_offsets_kernel(const int32_t* __re
         run += (L + BT - 1) / BT;
     }
     if (tid == 1023) coff[N] = part[1023];
+    if (order && N <= LPT_MAX_SEQS) {
+        __syncthreads();  // every chunk count below is read from part[]
+        int key = 0;
+        if (tid < N) key = (cu_s[tid + 1] - cu_s[tid] + BT - 1) / BT;
+        __syncthreads();  // part[] is free again
+        part[tid] = key;
+        __syncthreads();
+        if (tid < N) {
+            int rank = 0;
+            for (int j = 0; j < N; ++j) {
+                const int kj = part[j];
+                rank += (kj > key || (kj == key && j < tid)) ? 1 : 0;
+            }
+            order[rank] = tid;
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -821,7 +840,7 @@ struct Problem {
 // the forward's factors, and its saved states, in place.
 template <typename T>
 struct FwdWs {
-    int32_t *cu_s, *coff;
+    int32_t *cu_s, *coff, *order;
     T *W, *U;     // generic path
     bf16* Tc;     // bf16 path
     float* bc;    // bf16 path
@@ -834,7 +853,7 @@ struct FwdWs {
 
 template <typename T>
 struct BwdWs {
-    int32_t *cu_s, *coff;
+    int32_t *cu_s, *coff, *order;
     T *W, *U;
     bf16* Tc;
     float* bc;
@@ -850,11 +869,14 @@ struct BwdWs {
 
 // Takes the common prefix; returns with `c` at the end of h (and Vn).
 template <typename T>
-static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** coff, T** W,
-                         T** U, bf16** Tc, float** bc, float** dcc, float** bco, T** h,
-                         bf16** Pc, T** Vn, bool with_h) {
+static void carve_prefix(const Problem& p, Carve& c, int32_t** cu_s, int32_t** coff,
+                         int32_t** order, T** W, T** U, bf16** Tc, float** bc, float** dcc,
+                         float** bco, T** h, bf16** Pc, T** Vn, bool with_h) {
     *cu_s = c.take<int32_t>(p.N + 1);
     *coff = c.take<int32_t>(p.N + 1);
+    // room for the sequence order whenever it can be used (the size queries
+    // do not know whether the call will be varlen)
+    *order = p.N <= LPT_MAX_SEQS ? c.take<int32_t>(p.N) : nullptr;
     *W = *U = nullptr;
     *Tc = nullptr;
     *bc = *dcc = *bco = nullptr;
@@ -883,8 +905,8 @@ template <typename T>
 static size_t carve_fwd(const Problem& p, void* base, FwdWs<T>* out, bool with_states) {
     Carve c(base);
     FwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.dcc, &w.bco, &w.h, &w.Pc,
-                    &w.Vn, with_states);
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.order, &w.W, &w.U, &w.Tc, &w.bc, &w.dcc,
+                    &w.bco, &w.h, &w.Pc, &w.Vn, with_states);
     if (out) *out = w;
     return c.off + 256;
 }
@@ -893,8 +915,8 @@ template <typename T>
 static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
     Carve c(base);
     BwdWs<T> w{};
-    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.W, &w.U, &w.Tc, &w.bc, &w.dcc, &w.bco, &w.h, &w.Pc,
-                    &w.Vn, true);
+    carve_prefix<T>(p, c, &w.cu_s, &w.coff, &w.order, &w.W, &w.U, &w.Tc, &w.bc, &w.dcc,
+                    &w.bco, &w.h, &w.Pc, &w.Vn, true);
     w.dh = c.take<T>((size_t)p.slots * p.H * p.K * p.V);
     if (!__is_same(T, bf16)) {
         w.dvloc = c.take<T>((size_t)p.ntok * p.H * p.V);
@@ -909,10 +931,12 @@ static size_t carve_bwd(const Problem& p, void* base, BwdWs<T>* out) {
 constexpr int VS = 64;  // value slice of the state scans
 constexpr int VO = 64;  // value tile of the per-chunk output kernels
 
-static SeqInfo make_seqinfo(const Problem& p, const int32_t* cu_s, const int32_t* coff) {
+static SeqInfo make_seqinfo(const Problem& p, const int32_t* cu_s, const int32_t* coff,
+                           const int32_t* order) {
     SeqInfo s;
     s.cu = p.varlen ? cu_s : nullptr;
     s.coff = p.varlen ? coff : nullptr;
+    s.order = p.varlen ? order : nullptr;
     s.N = p.N;
     s.T = p.T;
     s.nt = p.nt;
@@ -920,10 +944,10 @@ static SeqInfo make_seqinfo(const Problem& p, const int32_t* cu_s, const int32_t
 }
 
 static int build_offsets(const Problem& p, const int32_t* cu, int32_t* cu_s, int32_t* coff,
-                         hipStream_t st) {
+                         int32_t* order, hipStream_t st) {
     if (!p.varlen) return kSuccess;
     EFLA_LAUNCH("efla_q_chunk_offsets", chunk_offsets_kernel, dim3(1), dim3(1024), st, cu, p.N,
-                p.ntok, cu_s, coff);
+                p.ntok, cu_s, coff, order);
     return (int)hipPeekAtLastError();
 }
 
@@ -933,8 +957,8 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
                    bool save_states, hipStream_t st) {
     FwdWs<T> w;
     carve_fwd<T>(p, ws, &w, save_states);
-    EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, st));
-    const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
+    EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, w.order, st));
+    const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff, w.order);
     const int H = p.H;
     if constexpr (__is_same(T, bf16)) {
         EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
@@ -960,8 +984,8 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
                    bool reuse_states, hipStream_t st) {
     BwdWs<T> w;
     carve_bwd<T>(p, ws, &w);
-    EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, st));
-    const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff);
+    EFLA_CHECK((hipError_t)build_offsets(p, cu, w.cu_s, w.coff, w.order, st));
+    const SeqInfo si = make_seqinfo(p, w.cu_s, w.coff, w.order);
     const int H = p.H;
     // forward recompute: the WY factors unless the forward's are in the
     // workspace (reuse), the chunk states unless the forward saved them

@@ -94,6 +94,7 @@ __global__ void __launch_bounds__(NT) scan_h_kernel(const bf16* __restrict__ k,
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
     int bh, vsl;
     scan_map(blockIdx.x, si.N * H, NVS, bh, vsl);
+    bh = scan_seq_head(si, bh, H);
     const int seq = bh / H, h = bh % H, v0 = vsl * VS;
     long sbos, slen;
     int slot0;
@@ -182,6 +183,7 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
     int bh, vsl;
     scan_map(blockIdx.x, si.N * H, NVS, bh, vsl);
+    bh = scan_seq_head(si, bh, H);
     const int seq = bh / H, h = bh % H, v0 = vsl * VS;
     long sbos, slen;
     int slot0;

@@ -10,14 +10,27 @@ constexpr int BT = 64;  // chunk length
 
 // Where the tokens of each sequence live.  Without cu_seqlens there are N
 // sequences of T tokens back to back; with it, `cu` is a sanitised copy of
-// cu_seqlens and `coff[i]` the index of sequence i's first chunk.
+// cu_seqlens and `coff[i]` the index of sequence i's first chunk.  `order`
+// (varlen, at most LPT_MAX_SEQS sequences; else NULL) lists the sequences by
+// decreasing chunk count, ties in index order: the scans, one chain of
+// dependent chunks per workgroup, take the longest sequences first so that no
+// long chain starts late.
 struct SeqInfo {
     const int32_t* cu;
     const int32_t* coff;
+    const int32_t* order;
     int N;
     long T;
     int nt;  // chunks per sequence (fixed-length case)
 };
+
+constexpr int LPT_MAX_SEQS = 1024;  // one sequence per thread of the offsets kernel
+
+// The scans' (sequence * H + head) index of workgroup id's row, longest
+// sequences first where `order` is given.
+__device__ __forceinline__ int scan_seq_head(const SeqInfo& s, int bh, int H) {
+    return s.order ? s.order[bh / H] * H + bh % H : bh;
+}
 
 __device__ __forceinline__ void seq_bounds(const SeqInfo& s, int seq, long& bos, long& len,
                                            int& slot0) {
