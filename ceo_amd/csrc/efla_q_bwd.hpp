@@ -309,7 +309,7 @@ template <int K, int NG>
 struct GradSmem {
     bf16 Qs[64 * ldb<K>()];
     bf16 Ks[64 * ldb<K>()];
-    bf16 Ps[64 * LD64];  // P[t][t'] (t' <= t)
+    bf16 Ps[64 * LD64];  // P[t][t'] (t' <= t); in the closing, Dm[t][t'] (t' <= t)
     bf16 Tb[64 * LD64];  // bf16(T)[t][t'] (t' <= t), from the WY prep
     // b, dc/dlambda, dc/dbeta per token for items of even / odd position in
     // this workgroup's sequence (the next item's arrive during the closing)
@@ -327,11 +327,12 @@ struct GradSmem {
             bf16 Vn[64 * LD64];  // Vn [t][v]
             bf16 dVn[64 * LD64]; // dVn [t][v]
         } s;
-        struct {  // closing products
-            bf16 Dm[64 * LD64];  // Dm [t][t']
-            bf16 dT[64 * LD64];  // dT [t][t'] (t' < t)
-            bf16 X[64 * LD64];   // dT T^T [t][t'']
-            bf16 dG[64 * LD64];  // dG [i][j] (j < i)
+        struct {  // closing products (Dm lives in Ps meanwhile)
+            bf16 lo[2 * 64 * LD64];  // DR and Vn until the slices end
+            bf16 X[64 * LD64];       // dT T^T [t][t''] (over dVn)
+            bf16 dG[64 * LD64];      // first dT [t][t'] (t' < t), stored before the
+                                     // slices' end (nothing there is read by them),
+                                     // then dG [i][j] (j < i)
         } e;
         struct {  // the item's dq, dk rows on their way out
             bf16 dq[64 * ldb<K>()];
@@ -414,14 +415,17 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         return locate_chunk(si, I.slot, I.bos, I.len);
     };
     // copies into LDS (l: lane); each is issued by all waves
-    auto copy_slice0 = [&](const Item& I, int par, int l) {
+    auto copy_p = [&](const Item& I, int l) {
+        if constexpr (PS)
+            dma_tri<NW>(sm.Ps, Pws + ((long)I.slot * H + I.h) * TRI_ELEMS, 2, l);
+    };
+    auto copy_slice0 = [&](const Item& I, int par, int l, bool with_p) {
         const long cid = (long)I.slot * H + I.h, chb = cid * V * K;
         mf::dma_tile<64, VS, LD64, NW>(sm.V, v + I.bos * ld.v + (long)I.h * V, ld.v, I.len, 0, l);
         mf::dma_tile<64, VS, LD64, NW>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
         kcopy(sm.h, hist + chb, K, 64, 4, l);
         kcopy(sm.dh, dhist + chb, K, 64, 6, l);
-        if constexpr (PS)
-            dma_tri<NW>(sm.Ps, Pws + cid * TRI_ELEMS, 2, l);
+        if (with_p) copy_p(I, l);
         // b (16 chunks of 16 bytes) and dc/dlambda, dc/dbeta (32 chunks)
         if (w8 == NW - 1 && l < 16) mf::dma16(bws + cid * 64, 16u * l, sm.coef[par][0]);
         if (w8 == NW - 2 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
@@ -441,7 +445,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     if (!locate(it, cur)) return;  // uniform over the workgroup
     if constexpr (!PS)  // P's tiles above the diagonal are never written
         for (int i = threadIdx.x; i < 64 * LD64; i += NTG) sm.Ps[i] = (bf16)0.f;
-    copy_slice0(cur, par, mf::lane());
+    copy_slice0(cur, par, mf::lane(), true);
     copy_q(cur, mf::lane());
     copy_t(cur, mf::lane());
     copy_k(cur, mf::lane());
@@ -615,10 +619,14 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     dbp += __shfl_xor(dbp, 16);
     dbp += __shfl_xor(dbp, 32);
     if (g == 0) sm.dbh[hf][t] = dbp;
-    __syncthreads();  // slice buffers are free
 
     // ---- closing products ----
-    // Dm[t][t'] keeps t' <= t, dT[t][t'] keeps t' < t; share both [t][t']
+    // Dm[t][t'] keeps t' <= t, dT[t][t'] keeps t' < t; share both [t][t'].
+    // They go where the last slice phase reads nothing -- Dm into P's tile
+    // (last read by the slice's first phase), dT into dG's slot (beyond the
+    // slice temporaries) -- so one barrier ends the slices and the stores.
+    bf16* const Dm = sm.Ps;
+    bf16* const dTm = sm.u.e.dG;
 #pragma unroll
     for (int e = 0; e < EG; ++e) {
         const int J = EG * hf + e;
@@ -628,16 +636,16 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             if (tp > t) dma[e][i] = 0.f;
             if (tp >= t) dta[e][i] = 0.f;
         }
-        store4(sm.u.e.Dm + t * LD64 + pim(J, 4 * g), dma[e]);
-        store4(sm.u.e.dT + t * LD64 + pim(J, 4 * g), dta[e]);
+        store4(Dm + t * LD64 + pim(J, 4 * g), dma[e]);
+        store4(dTm + t * LD64 + pim(J, 4 * g), dta[e]);
     }
-    __syncthreads();
-    // the next item's first slice, P and coefficients into the free slice
-    // buffers (the closing products touch neither)
-    if (more) copy_slice0(nxt, par ^ 1, l);
+    __syncthreads();  // slice buffers are free; Dm, dT complete
+    // the next item's first slice and coefficients into the free slice
+    // buffers (the closing products touch neither); its P once Dm is read
+    if (more) copy_slice0(nxt, par ^ 1, l, false);
     // X^T[t''][t] = sum_t' T[t''][t'] dT[t][t'] for this group's t'' blocks
     {
-        const bf16x8 d0 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 0), d1 = frag_nat(l, sm.u.e.dT, LD64, 16 * tb, 32);
+        const bf16x8 d0 = frag_nat(l, dTm, LD64, 16 * tb, 0), d1 = frag_nat(l, dTm, LD64, 16 * tb, 32);
 #pragma unroll
         for (int e = 0; e < EG; ++e) {
             const int J = EG * hf + e;
@@ -648,10 +656,10 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     }
     // dq^T += K^T Dm^T (k = t' <= t);  dk^T += Q^T Dm (token t' = t, k = t >= t')
     {
-        const bf16x8 m0 = frag_nat(l, sm.u.e.Dm, LD64, 16 * tb, 0), m1 = frag_nat(l, sm.u.e.Dm, LD64, 16 * tb, 32);
-        const bf16x8 c1 = frag_trc(l, sm.u.e.Dm, LD64, 32, 16 * tb);
+        const bf16x8 m0 = frag_nat(l, Dm, LD64, 16 * tb, 0), m1 = frag_nat(l, Dm, LD64, 16 * tb, 32);
+        const bf16x8 c1 = frag_trc(l, Dm, LD64, 32, 16 * tb);
         bf16x8 c0 = c1;
-        if (nks == 0) c0 = frag_trc(l, sm.u.e.Dm, LD64, 0, 16 * tb);
+        if (nks == 0) c0 = frag_trc(l, Dm, LD64, 0, 16 * tb);
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
@@ -662,7 +670,10 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         }
     }
     __syncthreads();
-    if (more) copy_q(nxt, l);  // Q is not read again in this item
+    if (more) {  // Q and Dm are not read again in this item
+        copy_q(nxt, l);
+        copy_p(nxt, l);
+    }
     // M^T[j][i] = sum_t X[t][j] T[t][i] (i = t owned here, j in this group's
     // blocks, j < i); dA = -M, G recomputed: db += sum_j dA G; dG = b_i dA ->
     // shared [i][j]
