@@ -38,14 +38,20 @@
 // weights for 256 multiply-adds.  Windows longer than 80 take direct kernels
 // that read through the caches.  The weight gradient splits the token tiles
 // over workgroups; each writes a partial, which a second pass sums in a fixed
-// order into grad_weight.  PRISM runs one lane per active channel and one
-// wave per row phase over blocks of 64 rows; columns past head_dim are cleared
-// by a separate 16-byte store pass.  The w_p gradient is summed per workgroup
-// in LDS and added with one float atomic per workgroup and value, so the order
-// of those additions varies between runs.
+// order into grad_weight.  PRISM, for 16-byte rows and up to four iterations
+// (the reference config runs three), takes blocks of 16 rows per workgroup:
+// eight active channels per lane as one 16-byte piece of each input and
+// output, and the columns past head_dim cleared by the same workgroup with
+// 16-byte stores; the w_p gradient of a block is summed in LDS into a
+// per-block partial, and a second kernel adds the partials in block order
+// (the same result on every run).  Other shapes run one lane per active
+// channel and one wave per row phase over blocks of 64 rows, with the columns
+// cleared by a separate pass and the w_p gradient added with one float atomic
+// per workgroup and value (the order of those additions varies between runs).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <initializer_list>
 
 #include "../../include/efla_hip.h"
 #include "common.hpp"
@@ -535,6 +541,177 @@ __global__ void __launch_bounds__(NTH) zero_cols_kernel(bf16* __restrict__ a, bf
     }
 }
 
+// Row-block forms of the PRISM kernels for 16-byte rows (hidden and head_dim
+// multiples of 8, head_dim / 8 dividing NTH, 16-byte aligned activations, at
+// most kFastIter iterations).  A workgroup owns PRR consecutive rows: its
+// threads form the head_dim active channels eight per lane (one 16-byte piece
+// of each input and output per row, the lane's channel group fixed) and clear
+// the rows' columns past head_dim with 16-byte stores, so one launch writes
+// every output byte and each CU keeps several row blocks' accesses in flight
+// (the one-lane-per-channel kernels above keep one 2-byte access per lane).
+constexpr int PRR = 16;
+constexpr int kFastIter = 4;
+constexpr long kMaxFastBlocks = 1L << 20;
+
+__device__ __forceinline__ void zero_row_tails(bf16* __restrict__ a, bf16* __restrict__ b,
+                                               long r0, long rows, int C, int HD) {
+    const int per = (C - HD) / 8;
+    const int n = (int)min((long)PRR, rows - r0) * per;
+    bf16x8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (bf16)0.f;
+    for (int i = threadIdx.x; i < n; i += NTH) {
+        const int rr = i / per;
+        const long off = (r0 + rr) * C + HD + 8 * (i - rr * per);
+        *reinterpret_cast<bf16x8*>(a + off) = z;
+        if (b) *reinterpret_cast<bf16x8*>(b + off) = z;
+    }
+}
+
+// p[l][e] = w_p[l][8 j + e] for l < L, else 0
+__device__ __forceinline__ void load_p8(const WPtrs& wp, int L, int j, float (&p)[kFastIter][8]) {
+#pragma unroll
+    for (int l = 0; l < kFastIter; ++l)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p[l][e] = l < L ? (float)wp.p[l][8 * j + e] : 0.f;
+}
+
+// The forward of prism_fwd_kernel per channel, plus the column clearing of
+// zero_cols_kernel (and of new_state, `extra`, by the first workgroup).
+__global__ void __launch_bounds__(NTH) prism_fwd_rows_kernel(const bf16* __restrict__ u,
+                                                             const bf16* __restrict__ v, WPtrs wp,
+                                                             bf16* __restrict__ out, long rows,
+                                                             int C, int HD, int L,
+                                                             bf16* __restrict__ extra,
+                                                             long extra_n) {
+    if (blockIdx.x == 0)
+        for (long i = threadIdx.x; i < extra_n; i += NTH) extra[i] = (bf16)0.f;
+    const long r0 = (long)blockIdx.x * PRR;
+    const int PH = HD / 8, j = threadIdx.x % PH;
+    float p[kFastIter][8];
+    load_p8(wp, L, j, p);
+    for (int rr = threadIdx.x / PH; rr < PRR; rr += NTH / PH) {
+        const long r = r0 + rr;
+        if (r >= rows) break;
+        const bf16x8 uu = *reinterpret_cast<const bf16x8*>(u + r * C + 8 * j);
+        const bf16x8 vv = *reinterpret_cast<const bf16x8*>(v + r * C + 8 * j);
+        bf16x8 oo;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float res = (float)vv[e] - (float)uu[e];
+            float o = 0.f;
+#pragma unroll
+            for (int l = 0; l < kFastIter; ++l) {
+                if (l < L) {
+                    const float d = gelu_f<true>(p[l][e] * res);
+                    o = (float)(bf16)(o + 0.5f * d);
+                    res -= d;
+                }
+            }
+            oo[e] = (bf16)o;
+        }
+        *reinterpret_cast<bf16x8*>(out + r * C + 8 * j) = oo;
+    }
+    zero_row_tails(out, nullptr, r0, rows, C, HD);
+}
+
+// The backward of prism_bwd_kernel per channel and the column clearing of
+// grad_u and grad_v.  The w_p gradient of the block's rows goes to
+// part[block][l * HD + c], summed over the block's threads in a fixed order;
+// prism_wgrad_sum_kernel then adds the blocks' partials in block order, so the
+// result is the same on every run.
+__global__ void __launch_bounds__(NTH) prism_bwd_rows_kernel(
+    const bf16* __restrict__ go, const bf16* __restrict__ u, const bf16* __restrict__ v, WPtrs wp,
+    bf16* __restrict__ gu, bf16* __restrict__ gv, float* __restrict__ part, long rows, int C,
+    int HD, int L) {
+    __shared__ float red[kFastIter * NTH * 8];
+    const long r0 = (long)blockIdx.x * PRR;
+    const int PH = HD / 8, j = threadIdx.x % PH, k0 = threadIdx.x / PH, KB = NTH / PH;
+    float p[kFastIter][8], dp[kFastIter][8];
+    load_p8(wp, L, j, p);
+#pragma unroll
+    for (int l = 0; l < kFastIter; ++l)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dp[l][e] = 0.f;
+    for (int rr = k0; rr < PRR; rr += KB) {
+        const long r = r0 + rr;
+        if (r >= rows) break;
+        const long off = r * C + 8 * j;
+        const bf16x8 gg = *reinterpret_cast<const bf16x8*>(go + off);
+        const bf16x8 uu = *reinterpret_cast<const bf16x8*>(u + off);
+        const bf16x8 vv = *reinterpret_cast<const bf16x8*>(v + off);
+        bf16x8 ou, ov;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float res[kFastIter], xl[kFastIter];
+            float rv = (float)vv[e] - (float)uu[e];
+            const float gr = (float)gg[e];
+#pragma unroll
+            for (int l = 0; l < kFastIter; ++l) {
+                res[l] = rv;
+                xl[l] = p[l][e] * rv;
+                if (l < L) rv -= gelu_f<true>(xl[l]);
+            }
+            float a = 0.f;
+#pragma unroll
+            for (int l = kFastIter - 1; l >= 0; --l) {
+                if (l < L) {
+                    const float gx = (0.5f * gr - a) * gelu_df<true>(xl[l]);
+                    dp[l][e] = fmaf(gx, res[l], dp[l][e]);
+                    a = fmaf(gx, p[l][e], a);
+                }
+            }
+            ov[e] = (bf16)a;
+            ou[e] = (bf16)(-a);
+        }
+        *reinterpret_cast<bf16x8*>(gv + off) = ov;
+        *reinterpret_cast<bf16x8*>(gu + off) = ou;
+    }
+    zero_row_tails(gu, gv, r0, rows, C, HD);
+    if (!part) return;
+    // red[l][k][c]: thread (k, j) holds channels 8 j .. 8 j + 7 of row set k
+#pragma unroll
+    for (int l = 0; l < kFastIter; ++l)
+        if (l < L)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) red[(l * KB + k0) * HD + 8 * j + e] = dp[l][e];
+    __syncthreads();
+    for (int i = threadIdx.x; i < L * HD; i += NTH) {
+        const int l = i / HD, c = i - l * HD;
+        float t = 0.f;
+        for (int k = 0; k < KB; ++k) t += red[(l * KB + k) * HD + c];
+        part[(long)blockIdx.x * L * HD + i] = t;
+    }
+}
+
+// grad_w_p[l][c] += sum over blocks b (in order) of part[b][l * HD + c];
+// grid (ceil(HD / 16), L): 16 columns per workgroup as 4 lanes of 4 (HD is a
+// multiple of 8), 64 block groups each taking every 64th block with eight
+// 16-byte loads in flight
+__global__ void __launch_bounds__(256) prism_wgrad_sum_kernel(const float* __restrict__ part,
+                                                              int nblk, int HD, int L, GPtrs gw) {
+    __shared__ float acc[64][16 + 1];
+    const int q = threadIdx.x & 3, rg = threadIdx.x >> 2, l = blockIdx.y;
+    const int c0 = blockIdx.x * 16 + 4 * q;
+    const float* base = part + (long)l * HD + c0;
+    const long stride = (long)L * HD;
+    floatx4 s = {0.f, 0.f, 0.f, 0.f};
+    if (c0 < HD)
+#pragma unroll 8
+        for (int b = rg; b < nblk; b += 64)
+            s += *reinterpret_cast<const floatx4*>(base + b * stride);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[rg][4 * q + i] = s[i];
+    __syncthreads();
+    const int c = blockIdx.x * 16 + threadIdx.x;
+    if (threadIdx.x < 16 && c < HD) {
+        float t = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < 64; ++k) t += acc[k][threadIdx.x];
+        gw.p[l][c] += t;
+    }
+}
+
 inline size_t conv_lds_bytes(int W, bool dw) {
     const int Wp = (W + JB - 1) & ~(JB - 1);
     const size_t rows = (size_t)(TT + Wp - 1) + (dw ? TT : 0);
@@ -544,6 +721,18 @@ inline size_t conv_lds_bytes(int W, bool dw) {
 }
 
 inline bool vec_ok(const void* p, int C) { return ((uintptr_t)p & 15) == 0 && C % 8 == 0; }
+
+// whether the row-block kernels take this problem (the pointers are the
+// activations they read and write with 16-byte accesses)
+inline bool rows_form_ok(long rows, size_t C, size_t HD, size_t L,
+                         std::initializer_list<const void*> ptrs) {
+    if (C % 8 != 0 || HD % 8 != 0 || HD == 0 || NTH % (HD / 8) != 0 || L > (size_t)kFastIter)
+        return false;
+    if ((rows + PRR - 1) / PRR > kMaxFastBlocks) return false;
+    for (const void* p : ptrs)
+        if ((uintptr_t)p & 15) return false;
+    return true;
+}
 
 inline unsigned grid_1d(long n) {
     long g = (n + NTH - 1) / NTH;
@@ -734,6 +923,14 @@ extern "C" int prism_forward_hip(const void* u, const void* v, const void* prev_
         return new_state ? fill_zero(new_state, head_dim * head_dim * sizeof(bf16), stream)
                          : kSuccess;
     }
+    if (prism::rows_form_ok(rows, hidden_dim, head_dim, num_iterations, {u, v, output})) {
+        EFLA_LAUNCH("prism_fwd", prism::prism_fwd_rows_kernel,
+                    dim3((unsigned)((rows + prism::PRR - 1) / prism::PRR)), dim3(prism::NTH),
+                    stream, (const bf16*)u, (const bf16*)v, wp, (bf16*)output, rows,
+                    (int)hidden_dim, (int)head_dim, (int)num_iterations, (bf16*)new_state,
+                    new_state ? (long)(head_dim * head_dim) : 0L);
+        return (int)hipPeekAtLastError();
+    }
     const dim3 grid = prism_grid(rows, head_dim);
     EFLA_LAUNCH("prism_fwd", prism::prism_fwd_kernel, grid, dim3(prism::NTH), stream,
                 (const bf16*)u, (const bf16*)v, wp, (bf16*)output, rows, (int)hidden_dim,
@@ -759,6 +956,29 @@ extern "C" int prism_backward_hip(const void* grad_output, const void* u, const 
     for (int l = 0; l < prism::kMaxIter; ++l) {
         gw.p[l] = (grad_w_p && l < L) ? grad_w_p[l] : nullptr;
         if (grad_w_p && l < L && !gw.p[l]) return kInvalidValue;
+    }
+    if (prism::rows_form_ok(rows, hidden_dim, head_dim, num_iterations,
+                            {grad_output, u, v, grad_u, grad_v})) {
+        const long nblk = (rows + prism::PRR - 1) / prism::PRR;
+        float* part = nullptr;
+        WsLease lease;
+        if (grad_w_p && L > 0) {
+            void* ws = nullptr;
+            const int wrc = workspace_acquire((size_t)nblk * L * head_dim * sizeof(float),
+                                              stream, &ws, lease);
+            if (wrc != kSuccess) return wrc;
+            part = (float*)ws;
+        }
+        EFLA_LAUNCH("prism_bwd", prism::prism_bwd_rows_kernel, dim3((unsigned)nblk),
+                    dim3(prism::NTH), stream, (const bf16*)grad_output, (const bf16*)u,
+                    (const bf16*)v, wp, (bf16*)grad_u, (bf16*)grad_v, part, rows,
+                    (int)hidden_dim, (int)head_dim, L);
+        EFLA_CHECK(hipPeekAtLastError());
+        if (part)
+            EFLA_LAUNCH("prism_bwd_wsum", prism::prism_wgrad_sum_kernel,
+                        dim3((unsigned)((head_dim + 15) / 16), (unsigned)L), dim3(256), stream,
+                        (const float*)part, (int)nblk, (int)head_dim, L, gw);
+        return (int)hipPeekAtLastError();
     }
     const dim3 grid = prism_grid(rows, head_dim);
     EFLA_LAUNCH("prism_bwd", prism::prism_bwd_kernel, grid, dim3(prism::NTH), stream,

@@ -77,8 +77,14 @@ def test_shortconv_backward(oracle, B, T, C, W):
     assert torch.equal(dx, dx2)
 
 
+# (2, 64, 256, 64, 3), (1, 1000, 512, 128, 4), (3, 77, 96, 32, 2) and
+# (1, 50, 16, 8, 1) take the 16-row block kernels (16-byte rows, head_dim / 8
+# dividing 256, L <= 4; 1000 rows leave a partial last block); the others the
+# lane-per-channel kernels.
 @pytest.mark.parametrize("B,T,C,HD,L", [(2, 64, 256, 64, 3), (1, 33, 100, 37, 1),
-                                        (2, 16, 64, 64, 16), (1, 8, 300, 128, 0)])
+                                        (2, 16, 64, 64, 16), (1, 8, 300, 128, 0),
+                                        (1, 1000, 512, 128, 4), (3, 77, 96, 32, 2),
+                                        (1, 50, 16, 8, 1)])
 def test_prism_forward(oracle, B, T, C, HD, L):
     from ceo_amd.prism import prism_forward
 
@@ -102,7 +108,9 @@ def test_prism_forward(oracle, B, T, C, HD, L):
     assert not state.float().abs().sum().item()
 
 
-@pytest.mark.parametrize("B,T,C,HD,L", [(2, 64, 256, 64, 3), (1, 33, 100, 37, 2)])
+@pytest.mark.parametrize("B,T,C,HD,L", [(2, 64, 256, 64, 3), (1, 33, 100, 37, 2),
+                                        (1, 1000, 512, 128, 4), (3, 77, 96, 32, 3),
+                                        (1, 50, 16, 8, 1)])
 def test_prism_backward(oracle, B, T, C, HD, L):
     from ceo_amd.prism import prism_backward
 
@@ -124,6 +132,48 @@ def test_prism_backward(oracle, B, T, C, HD, L):
     assert max(errs[2:]) <= 1e-4
     assert not gw[0][HD:].any()
     assert not gu.float()[..., HD:].any() and not gv.float()[..., HD:].any()
+
+
+def _misaligned(t):
+    """A contiguous copy of t whose data starts 2 bytes past a 16-byte
+    boundary (the PRISM entries then take the lane-per-channel kernels)."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=t.device)
+    m = buf[1:].view(t.shape)
+    m.copy_(t)
+    assert m.data_ptr() % 16 == 2
+    return m
+
+
+def test_prism_row_blocks_match_lane_kernels():
+    """The 16-row block kernels and the lane-per-channel kernels compute the
+    same per-channel arithmetic: outputs and input gradients bit-identical,
+    the w_p gradients equal up to summation order; the block kernels' w_p
+    gradient (per-block partials added in block order) is the same on every
+    run."""
+    from ceo_amd.prism import prism_backward, prism_forward
+
+    B, T, C, HD, L = 2, 500, 256, 64, 3
+    announce(f"prism row-block vs lane kernels B={B} T={T} C={C} head_dim={HD} L={L}")
+    rng = np.random.default_rng(5)
+    u = _bf(rng.standard_normal((B, T, C))).cuda()
+    v = _bf(rng.standard_normal((B, T, C)) * 1.5).cuda()
+    g = _bf(rng.standard_normal((B, T, C))).cuda()
+    w_p = [_bf(rng.standard_normal((C, HD)) * 0.7).cuda() for _ in range(L)]
+    um, vm, gm = _misaligned(u), _misaligned(v), _misaligned(g)
+    out_f, _ = prism_forward(u, v, w_p, HD)
+    out_l, _ = prism_forward(um, vm, w_p, HD)
+    gws = [[torch.zeros(C * HD, dtype=torch.float32, device="cuda") for _ in range(L)]
+           for _ in range(3)]
+    gu_f, gv_f = prism_backward(g, u, v, w_p, HD, gws[0])
+    gu_f2, gv_f2 = prism_backward(g, u, v, w_p, HD, gws[1])
+    gu_l, gv_l = prism_backward(gm, um, vm, w_p, HD, gws[2])
+    torch.cuda.synchronize()
+    assert (_bits(out_f) == _bits(out_l)).all()
+    assert (_bits(gu_f) == _bits(gu_l)).all() and (_bits(gv_f) == _bits(gv_l)).all()
+    assert torch.equal(gu_f, gu_f2) and torch.equal(gv_f, gv_f2)
+    for l in range(L):
+        assert torch.equal(gws[0][l], gws[1][l])
+        assert rel_l2(gws[0][l], gws[2][l].cpu().numpy()) <= 1e-5
 
 
 def test_prism_layer_against_torch_autograd():
