@@ -346,8 +346,12 @@ int prism_forward_hip(const void* u, const void* v, const void* prev_state, void
  * the gradient of prism_forward_hip with the bf16 rounding of o passed
  * straight through.  grad_u, grad_v bf16 (full rows; 0 beyond head_dim);
  * grad_w_p a host array of num_iterations fp32 device pointers, each added
- * into over its first head_dim values with float atomics (the summation order
- * varies between runs; may be NULL). */
+ * into over its first head_dim values (may be NULL).  When hidden_dim and
+ * head_dim are multiples of 8, head_dim / 8 divides 256, the activations are
+ * 16-byte aligned and num_iterations <= 4, the sums run in a fixed order
+ * through a cached workspace of 4 * num_iterations * head_dim bytes per 16
+ * rows; otherwise they are added with float atomics and their order varies
+ * between runs. */
 int prism_backward_hip(const void* grad_output, const void* u, const void* v, const void** w_p,
                        void* grad_u, void* grad_v, float** grad_w_p, size_t batch_size,
                        size_t seq_len, size_t hidden_dim, size_t head_dim,
