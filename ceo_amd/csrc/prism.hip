@@ -35,10 +35,15 @@
 // with the token rows and the weights staged as fp32 in LDS: one lane per
 // channel, one wave per 16 tokens.  A lane keeps 16 outputs (or 16 lags) and
 // walks the window in blocks of 16 lags, reading 31 staged values and 16
-// weights for 256 multiply-adds.  Windows longer than 80 take direct kernels
-// that read through the caches.  The weight gradient splits the token tiles
-// over workgroups; each writes a partial, which a second pass sums in a fixed
-// order into grad_weight.  PRISM, for 16-byte rows and up to four iterations
+// weights for 256 multiply-adds.  For 16-byte rows and windows up to 64 the
+// forward and grad_input walk several consecutive token tiles per workgroup
+// (about two workgroups per CU): the upper half of a tile's staged rows is
+// the next tile's lower half, and the next 64 rows are loaded into registers
+// while the tile is formed.  Windows longer than 80 take direct kernels that
+// read through the caches.  The weight gradient splits the token tiles over
+// workgroups (for 16-byte rows, runs of consecutive tiles with the next
+// tile's rows loaded during the current one); each writes a partial, which a
+// second pass sums in a fixed order into grad_weight.  PRISM, for 16-byte rows and up to four iterations
 // (the reference config runs three), takes blocks of 16 rows per workgroup:
 // eight active channels per lane as one 16-byte piece of each input and
 // output, and the columns past head_dim cleared by the same workgroup with
@@ -74,6 +79,7 @@ constexpr int kMaxLagBlocks = kMaxTiledW / JB;
 constexpr int kMaxIter = 16;
 constexpr int PRB = 64;  // PRISM rows per workgroup (16 per wave)
 constexpr long kMaxBlocks = 16384;
+constexpr int kDwPipeBlocks = 512;  // conv_dw_pipe_kernel workgroups (all splits)
 
 struct WPtrs {
     const bf16* p[kMaxIter];
@@ -87,18 +93,19 @@ __device__ __forceinline__ int padded_window(int W) { return (W + JB - 1) & ~(JB
 constexpr int kStageIt = (TT + kMaxTiledW - 1 + 31) / 32;  // 16-byte row chunks per thread
 constexpr int kStageEl = ((TT + kMaxTiledW - 1) * CT + NTH - 1) / NTH;  // scalar elements
 
-// dst[r][c] = src[b, t_lo + r, c0 + c] as fp32 for r < nrows, 0 outside
-// [0, T) x [0, C).  Every load is issued before the first LDS write.  VEC:
-// 16-byte loads of 8 channels (C % 8 == 0 and src 16-byte aligned).
-template <bool VEC>
-__device__ __forceinline__ void stage_rows(float* dst, const bf16* __restrict__ src, long b,
-                                           long t_lo, int nrows, int T, int C, int c0) {
-    if constexpr (VEC) {
+// Rows t_lo .. t_lo + nrows - 1 (nrows <= 32 IT) of channels c0 .. c0 + 63 as
+// 16-byte pieces held in registers (thread: channel group threadIdx % 8, rows
+// threadIdx / 8 + 32 it), 0 outside [0, T) x [0, C); store() writes them to
+// LDS as fp32 [row][CT].
+template <int IT>
+struct RowsVec {
+    bf16x8 v[IT];
+    __device__ __forceinline__ void load(const bf16* __restrict__ src, long b, long t_lo,
+                                         int nrows, int T, int C, int c0) {
         const int q = threadIdx.x & 7, ro = threadIdx.x >> 3;
         const bool cok = c0 + q * 8 < C;
-        bf16x8 v[kStageIt];
 #pragma unroll
-        for (int it = 0; it < kStageIt; ++it) {
+        for (int it = 0; it < IT; ++it) {
             const int r = ro + 32 * it;
             const long t = t_lo + r;
             if (r < nrows && t >= 0 && t < T && cok) {
@@ -108,8 +115,11 @@ __device__ __forceinline__ void stage_rows(float* dst, const bf16* __restrict__ 
                 for (int i = 0; i < 8; ++i) v[it][i] = (bf16)0.f;
             }
         }
+    }
+    __device__ __forceinline__ void store(float* dst, int nrows) const {
+        const int q = threadIdx.x & 7, ro = threadIdx.x >> 3;
 #pragma unroll
-        for (int it = 0; it < kStageIt; ++it) {
+        for (int it = 0; it < IT; ++it) {
             const int r = ro + 32 * it;
             if (r < nrows) {
                 floatx4 lo, hi;
@@ -122,6 +132,19 @@ __device__ __forceinline__ void stage_rows(float* dst, const bf16* __restrict__ 
                 *reinterpret_cast<floatx4*>(&dst[r * CT + q * 8 + 4]) = hi;
             }
         }
+    }
+};
+
+// dst[r][c] = src[b, t_lo + r, c0 + c] as fp32 for r < nrows, 0 outside
+// [0, T) x [0, C).  Every load is issued before the first LDS write.  VEC:
+// 16-byte loads of 8 channels (C % 8 == 0 and src 16-byte aligned).
+template <bool VEC>
+__device__ __forceinline__ void stage_rows(float* dst, const bf16* __restrict__ src, long b,
+                                           long t_lo, int nrows, int T, int C, int c0) {
+    if constexpr (VEC) {
+        RowsVec<kStageIt> rv;
+        rv.load(src, b, t_lo, nrows, T, C, c0);
+        rv.store(dst, nrows);
     } else {
         float v[kStageEl];
 #pragma unroll
@@ -266,6 +289,23 @@ __global__ void __launch_bounds__(NTH) conv_fwd_direct_kernel(const bf16* __rest
     }
 }
 
+// acc[j] = sum over lags w < Wp of ds[g JB + j + w][c] ws[w][c] (the rows past
+// T and the lags past W are staged as zeros)
+__device__ __forceinline__ void conv_dx_lane(float (&acc)[JB], const float* ds, const float* ws,
+                                             int Wp, int g, int c) {
+    for (int w0 = 0; w0 < Wp; w0 += JB) {
+        float dr[2 * JB - 1], wv[JB];
+#pragma unroll
+        for (int m = 0; m < 2 * JB - 1; ++m) dr[m] = ds[(g * JB + w0 + m) * CT + c];
+#pragma unroll
+        for (int k = 0; k < JB; ++k) wv[k] = ws[(w0 + k) * (CT + 1) + c];
+#pragma unroll
+        for (int k = 0; k < JB; ++k)
+#pragma unroll
+            for (int j = 0; j < JB; ++j) acc[j] = fmaf(dr[j + k], wv[k], acc[j]);
+    }
+}
+
 // grad_input for one tile: dx[t] = sum_w dy[t + w] weight[w]
 template <bool VEC>
 __global__ void __launch_bounds__(NTH) conv_dx_kernel(const bf16* __restrict__ dy,
@@ -285,22 +325,91 @@ __global__ void __launch_bounds__(NTH) conv_dx_kernel(const bf16* __restrict__ d
     float acc[JB];
 #pragma unroll
     for (int j = 0; j < JB; ++j) acc[j] = 0.f;
-    for (int w0 = 0; w0 < Wp; w0 += JB) {
-        float dr[2 * JB - 1], wv[JB];
-#pragma unroll
-        for (int m = 0; m < 2 * JB - 1; ++m) dr[m] = ds[(g * JB + w0 + m) * CT + c];
-#pragma unroll
-        for (int k = 0; k < JB; ++k) wv[k] = ws[(w0 + k) * (CT + 1) + c];
-#pragma unroll
-        for (int k = 0; k < JB; ++k)
-#pragma unroll
-            for (int j = 0; j < JB; ++j) acc[j] = fmaf(dr[j + k], wv[k], acc[j]);
-    }
+    conv_dx_lane(acc, ds, ws, Wp, g, c);
     const int tj0 = t0 + g * JB;
     if (c0 + c < C) {
 #pragma unroll
         for (int j = 0; j < JB; ++j)
             if (tj0 + j < T) dx[(b * T + tj0 + j) * C + c0 + c] = (bf16)acc[j];
+    }
+}
+
+// The forward (DX false) or grad_input (DX true) over the token tiles
+// [n0, n0 + tps) of one (channel tile, batch row), for 16-byte rows and
+// windows of at most TT.  Tile n reads 64 + Wp - 1 staged rows, of which the
+// upper 64 are tile n + 1's lower 64: the workgroup keeps 2 TT rows (row i =
+// token t0 + OFF + i, OFF = -TT forward, 0 grad_input), and while a tile is
+// formed each thread loads its share of the next tile's 64 new rows into
+// registers; after the tile, each thread moves the pieces it is about to
+// replace from the upper to the lower half and writes the new rows in their
+// place (no thread touches another's pieces, so two barriers per tile).
+// The per-output arithmetic is that of conv_fwd_kernel / conv_dx_kernel.
+template <bool DX>
+__global__ void __launch_bounds__(NTH) conv_walk_kernel(const bf16* __restrict__ src,
+                                                        const bf16* __restrict__ wt,
+                                                        bf16* __restrict__ dst, int T, int C,
+                                                        int W, int tps) {
+    extern __shared__ float smem[];
+    constexpr int OFF = DX ? 0 : -TT;
+    const int Wp = padded_window(W);
+    float* rows = smem;                // [2 TT][CT]
+    float* ws = smem + 2 * TT * CT;    // [Wp][CT + 1]
+    const long b = blockIdx.y;
+    const int c0 = blockIdx.x * CT;
+    const int n0 = blockIdx.z * tps, n1 = min((T + TT - 1) / TT, n0 + tps);
+    stage_rows<true>(rows, src, b, (long)n0 * TT + OFF, 2 * TT, T, C, c0);
+    stage_weights(ws, wt, W, Wp, C, c0);
+    __syncthreads();
+    const int c = lane_id(), g = __builtin_amdgcn_readfirstlane(wave_id());
+    const int q = threadIdx.x & 7, ro = threadIdx.x >> 3;
+    const bool cok = c0 + 8 * q < C;
+    for (int n = n0; n < n1; ++n) {
+        const int t0 = n * TT;
+        const bool more = n + 1 < n1;
+        bf16x8 nx[2];
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const long t = (long)t0 + OFF + 2 * TT + ro + 32 * it;
+            if (more && cok && t < T) {
+                nx[it] = *reinterpret_cast<const bf16x8*>(src + (b * T + t) * C + c0 + 8 * q);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) nx[it][i] = (bf16)0.f;
+            }
+        }
+        const int tj0 = t0 + g * JB;
+        float acc[JB];
+#pragma unroll
+        for (int j = 0; j < JB; ++j) acc[j] = 0.f;
+        if constexpr (DX)
+            conv_dx_lane(acc, rows, ws, Wp, g, c);
+        else
+            conv_fwd_lane(acc, rows + (TT - (Wp - 1)) * CT, ws, W, Wp, g, c, tj0);
+        if (c0 + c < C) {
+#pragma unroll
+            for (int j = 0; j < JB; ++j)
+                if (tj0 + j < T) dst[(b * T + tj0 + j) * C + c0 + c] = (bf16)acc[j];
+        }
+        if (!more) break;
+        __syncthreads();  // every wave is done with this tile's rows
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            float* up = rows + (TT + ro + 32 * it) * CT + 8 * q;
+            float* lo = rows + (ro + 32 * it) * CT + 8 * q;
+            const floatx4 a0 = *reinterpret_cast<const floatx4*>(up);
+            const floatx4 a1 = *reinterpret_cast<const floatx4*>(up + 4);
+            *reinterpret_cast<floatx4*>(lo) = a0;
+            *reinterpret_cast<floatx4*>(lo + 4) = a1;
+            floatx4 n0v, n1v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                n0v[i] = (float)nx[it][i];
+                n1v[i] = (float)nx[it][4 + i];
+            }
+            *reinterpret_cast<floatx4*>(up) = n0v;
+            *reinterpret_cast<floatx4*>(up + 4) = n1v;
+        }
+        __syncthreads();
     }
 }
 
@@ -368,6 +477,94 @@ __global__ void __launch_bounds__(NTH) conv_dw_kernel(const bf16* __restrict__ d
         }
     }
     // add the four waves' sums: red[w][c], wave 0 writes, waves 1..3 add in turn
+    __syncthreads();
+    float* red = smem;  // [Wp][CT]
+    for (int turn = 0; turn < NTH / kWave; ++turn) {
+        if (g == turn) {
+#pragma unroll
+            for (int q = 0; q < kMaxLagBlocks; ++q) {
+                if (q < nlb) {
+#pragma unroll
+                    for (int k = 0; k < JB; ++k) {
+                        float* r = &red[(q * JB + k) * CT + c];
+                        *r = turn == 0 ? acc[q][k] : *r + acc[q][k];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+    for (int i = threadIdx.x; i < CT * W; i += NTH) {
+        const int cc = i / W, w = i % W;
+        if (c0 + cc < C) part[((long)blockIdx.y * C + c0 + cc) * W + w] = red[w * CT + cc];
+    }
+}
+
+// conv_dw_kernel for 16-byte rows with the token tiles of a split taken in
+// order (tiles [blockIdx.y tpw, (blockIdx.y + 1) tpw) of the B x tiles_t
+// sequence) and the next tile's x and dy rows loaded into registers while the
+// current tile is formed, so the loads' latency is not paid once per tile.
+__global__ void __launch_bounds__(NTH) conv_dw_pipe_kernel(const bf16* __restrict__ dy,
+                                                           const bf16* __restrict__ x,
+                                                           float* __restrict__ part, int B,
+                                                           int T, int C, int W, int tiles_t,
+                                                           int tpw) {
+    extern __shared__ float smem[];
+    const int Wp = padded_window(W);
+    const int nlb = Wp / JB;
+    const int nrx = TT + Wp - 1;
+    float* xs = smem;             // [nrx][CT]: tokens t0 - (Wp-1) ..
+    float* ds = xs + nrx * CT;    // [TT][CT]: tokens t0 ..
+    const int c0 = blockIdx.x * CT;
+    const int c = lane_id(), g = __builtin_amdgcn_readfirstlane(wave_id());
+    float acc[kMaxLagBlocks][JB];
+#pragma unroll
+    for (int q = 0; q < kMaxLagBlocks; ++q)
+#pragma unroll
+        for (int k = 0; k < JB; ++k) acc[q][k] = 0.f;
+    const long ntiles = (long)B * tiles_t;
+    const long tl0 = (long)blockIdx.y * tpw, tl1 = min(ntiles, tl0 + tpw);
+    RowsVec<kStageIt> px;
+    RowsVec<TT / 32> pd;
+    auto load = [&](long tile) {
+        const long b = tile / tiles_t;
+        const int t0 = (int)(tile % tiles_t) * TT;
+        px.load(x, b, (long)t0 - (Wp - 1), nrx, T, C, c0);
+        pd.load(dy, b, t0, TT, T, C, c0);
+    };
+    if (tl0 < tl1) {
+        load(tl0);
+        px.store(xs, nrx);
+        pd.store(ds, TT);
+    }
+    __syncthreads();
+    for (long tile = tl0; tile < tl1; ++tile) {
+        const bool more = tile + 1 < tl1;
+        if (more) load(tile + 1);
+        float dr[JB];
+#pragma unroll
+        for (int j = 0; j < JB; ++j) dr[j] = ds[(g * JB + j) * CT + c];
+#pragma unroll
+        for (int q = 0; q < kMaxLagBlocks; ++q) {
+            if (q < nlb) {
+                const int w0 = q * JB;
+                const int rbase = g * JB - (JB - 1) - w0 + (Wp - 1);
+                float xr[2 * JB - 1];
+#pragma unroll
+                for (int m = 0; m < 2 * JB - 1; ++m) xr[m] = xs[(rbase + m) * CT + c];
+#pragma unroll
+                for (int j = 0; j < JB; ++j)
+#pragma unroll
+                    for (int k = 0; k < JB; ++k) acc[q][k] = fmaf(dr[j], xr[j - k + JB - 1], acc[q][k]);
+            }
+        }
+        if (more) {
+            __syncthreads();
+            px.store(xs, nrx);
+            pd.store(ds, TT);
+            __syncthreads();
+        }
+    }
     __syncthreads();
     float* red = smem;  // [Wp][CT]
     for (int turn = 0; turn < NTH / kWave; ++turn) {
@@ -722,6 +919,22 @@ inline size_t conv_lds_bytes(int W, bool dw) {
 
 inline bool vec_ok(const void* p, int C) { return ((uintptr_t)p & 15) == 0 && C % 8 == 0; }
 
+// Token tiles per workgroup of conv_walk_kernel: enough segments per
+// (channel tile, batch row) for about two workgroups per CU, 1 when the
+// window is too long for its two-tile row buffer or the rows are not 16-byte.
+inline int walk_tiles(int B, int T, int C, int W, bool vec) {
+    if (!vec || W > TT) return 1;
+    const int ttiles = (T + TT - 1) / TT, ctiles = (C + CT - 1) / CT;
+    const long pairs = (long)B * ctiles;
+    const long segs = std::max(1L, std::min((long)ttiles, (512 + pairs - 1) / pairs));
+    return (int)((ttiles + segs - 1) / segs);
+}
+
+inline size_t walk_lds_bytes(int W) {
+    const int Wp = (W + JB - 1) & ~(JB - 1);
+    return (size_t)(2 * TT * CT + Wp * (CT + 1)) * sizeof(float);
+}
+
 // whether the row-block kernels take this problem (the pointers are the
 // activations they read and write with 16-byte accesses)
 inline bool rows_form_ok(long rows, size_t C, size_t HD, size_t L,
@@ -767,7 +980,15 @@ extern "C" int shortconv_forward_hip(const void* input, const void* weight, void
     const bf16* wt = (const bf16*)weight;
     bf16* y = (bf16*)output;
     const int T = (int)seq_len, C = (int)hidden_dim, W = (int)window_size;
-    if (W >= 1 && W <= prism::kMaxTiledW) {
+    const int tps = prism::walk_tiles((int)batch_size, T, C, W, prism::vec_ok(x, C));
+    if (W >= 1 && tps > 1) {
+        const int ttiles = (T + prism::TT - 1) / prism::TT;
+        const dim3 grid((unsigned)((C + prism::CT - 1) / prism::CT), (unsigned)batch_size,
+                        (unsigned)((ttiles + tps - 1) / tps));
+        ::efla::ProfScope ps("shortconv_fwd", stream);
+        hipLaunchKernelGGL(prism::conv_walk_kernel<false>, grid, dim3(prism::NTH),
+                           prism::walk_lds_bytes(W), stream, x, wt, y, T, C, W, tps);
+    } else if (W >= 1 && W <= prism::kMaxTiledW) {
         const dim3 grid((unsigned)((T + prism::TT - 1) / prism::TT),
                         (unsigned)((C + prism::CT - 1) / prism::CT), (unsigned)batch_size);
         ::efla::ProfScope ps("shortconv_fwd", stream);
@@ -806,7 +1027,13 @@ extern "C" int shortconv_backward_hip(const void* grad_output, const void* input
     const int ttiles = (T + prism::TT - 1) / prism::TT;
     if (grad_input) {
         bf16* dx = (bf16*)grad_input;
-        if (tiled) {
+        const int tps = prism::walk_tiles(B, T, C, W, prism::vec_ok(dy, C));
+        if (tps > 1) {
+            const dim3 grid((unsigned)ctiles, (unsigned)B, (unsigned)((ttiles + tps - 1) / tps));
+            ::efla::ProfScope ps("shortconv_dx", stream);
+            hipLaunchKernelGGL(prism::conv_walk_kernel<true>, grid, dim3(prism::NTH),
+                               prism::walk_lds_bytes(W), stream, dy, wt, dx, T, C, W, tps);
+        } else if (tiled) {
             const dim3 grid((unsigned)ttiles, (unsigned)ctiles, (unsigned)B);
             ::efla::ProfScope ps("shortconv_dx", stream);
             if (prism::vec_ok(dy, C))
@@ -824,8 +1051,14 @@ extern "C" int shortconv_backward_hip(const void* grad_output, const void* input
     }
     if (grad_weight) {
         const long cw = (long)C * W;
-        long nsplit;
-        if (tiled) {
+        const bool pipe = tiled && prism::vec_ok(dy, C) && prism::vec_ok(x, C);
+        long nsplit, tpw = 1;
+        if (pipe) {  // about two workgroups per CU, each a run of consecutive tiles
+            const long tiles = (long)B * ttiles;
+            nsplit = std::max(1L, std::min(tiles, (long)prism::kDwPipeBlocks / ctiles));
+            tpw = (tiles + nsplit - 1) / nsplit;
+            nsplit = (tiles + tpw - 1) / tpw;
+        } else if (tiled) {
             const long tiles = (long)B * ttiles;
             nsplit = std::max(1L, std::min({tiles, 256L, 1024L / ctiles}));
         } else {
@@ -836,7 +1069,12 @@ extern "C" int shortconv_backward_hip(const void* grad_output, const void* input
         const int wrc = workspace_acquire((size_t)nsplit * cw * sizeof(float), stream, &ws, lease);
         if (wrc != kSuccess) return wrc;
         float* part = (float*)ws;
-        if (tiled) {
+        if (pipe) {
+            ::efla::ProfScope ps("shortconv_dw", stream);
+            hipLaunchKernelGGL(prism::conv_dw_pipe_kernel, dim3((unsigned)ctiles, (unsigned)nsplit),
+                               dim3(prism::NTH), prism::conv_lds_bytes(W, true), stream, dy, x,
+                               part, B, T, C, W, ttiles, (int)tpw);
+        } else if (tiled) {
             ::efla::ProfScope ps("shortconv_dw", stream);
             const dim3 grid((unsigned)ctiles, (unsigned)nsplit);
             if (prism::vec_ok(dy, C) && prism::vec_ok(x, C))

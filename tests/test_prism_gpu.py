@@ -21,9 +21,12 @@ def _bits(t):
     return (t.view(torch.int16).cpu().numpy().astype(np.int32) & 0xFFFF).astype(np.uint16)
 
 
+# (4, 650, 1024, 64) and (4, 1300, 1024, 37) are large enough in channel tiles x
+# batch rows for the token-walking kernel (two and three tiles per workgroup)
 @pytest.mark.parametrize("B,T,C,W", [(2, 100, 96, 16), (1, 300, 1024, 64), (2, 65, 70, 3),
                                      (1, 50, 64, 80), (1, 40, 32, 100), (1, 8, 16, 1),
-                                     (1, 10, 64, 64), (3, 129, 130, 17)])
+                                     (1, 10, 64, 64), (3, 129, 130, 17), (4, 650, 1024, 64),
+                                     (4, 1300, 1024, 37)])
 def test_shortconv_forward_bit_exact(oracle, B, T, C, W):
     from ceo_amd.prism import shortconv_forward
 
@@ -57,7 +60,7 @@ def test_shortconv_summation_order_known_answer(W):
 
 
 @pytest.mark.parametrize("B,T,C,W", [(2, 100, 96, 16), (1, 256, 1024, 64), (2, 65, 70, 3),
-                                     (1, 40, 32, 100), (1, 10, 64, 64)])
+                                     (1, 40, 32, 100), (1, 10, 64, 64), (4, 650, 1024, 64)])
 def test_shortconv_backward(oracle, B, T, C, W):
     from ceo_amd.prism import shortconv_backward
 
@@ -75,6 +78,28 @@ def test_shortconv_backward(oracle, B, T, C, W):
     print(f"  rel-L2 dx={e_dx:.2e} dw(2 calls)={e_dw:.2e}", flush=True)
     assert e_dx <= 1e-2 and e_dw <= 1e-5
     assert torch.equal(dx, dx2)
+
+
+@pytest.mark.parametrize("B,T,C,W", [(4, 650, 1024, 64), (4, 1300, 1024, 37),
+                                     (8, 333, 1024, 16)])
+def test_shortconv_walk_matches_tiles(B, T, C, W):
+    """The token-walking kernel (rows handed from one tile to the next) and the
+    one-tile kernels (taken for rows that are not 16-byte aligned) give
+    bit-identical outputs and input gradients."""
+    from ceo_amd.prism import shortconv_backward, shortconv_forward
+
+    announce(f"shortconv walk vs tiles B={B} T={T} C={C} W={W}")
+    g = torch.Generator().manual_seed(B + T + W)
+    x = torch.randn(B, T, C, generator=g).to(torch.bfloat16).cuda()
+    dy = torch.randn(B, T, C, generator=g).to(torch.bfloat16).cuda()
+    w = (torch.randn(C, W, generator=g) / W ** 0.5).to(torch.bfloat16).cuda()
+    y_w = shortconv_forward(x, w)
+    y_t = shortconv_forward(_misaligned(x), w)
+    dx_w, _ = shortconv_backward(dy, x, w)
+    dx_t, _ = shortconv_backward(_misaligned(dy), x, w)
+    torch.cuda.synchronize()
+    assert (_bits(y_w) == _bits(y_t)).all()
+    assert (_bits(dx_w) == _bits(dx_t)).all()
 
 
 # (2, 64, 256, 64, 3), (1, 1000, 512, 128, 4), (3, 77, 96, 32, 2) and
