@@ -199,11 +199,17 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
     }
     const long waves = (long)gridDim.x * (NTH / kWave);
     long row = (long)blockIdx.x * (NTH / kWave) + wv;
-    // the next two rows' x, dy (and the residual gradient) are in flight while
-    // this one computes: with one row a wave kept too few bytes in flight to
-    // cover the loaded memory latency
+    // the next two rows' x, dy (and the residual gradient) and their mean and
+    // rstd are in flight while this one computes: with one row a wave kept too
+    // few bytes in flight to cover the loaded memory latency.  The statistics
+    // travel with the rows: loaded at their use, after the prefetch, their
+    // wait (one in-order counter for all vector-memory loads) would also wait
+    // for the rows just prefetched.
     bf16x8 xn[2][NV], gn[2][NV], rn[2][NV] = {};
+    float mun[2] = {0.f, 0.f}, rsn[2] = {0.f, 0.f};
     auto fetch = [&](long r, int sl) {
+        mun[sl] = mean[r];
+        rsn[sl] = rstd[r];
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             xn[sl][j] = *reinterpret_cast<const bf16x8*>(x + r * D + (j * 64 + lane) * 8);
@@ -224,8 +230,10 @@ __global__ void __launch_bounds__(NTH) bwd_reg_kernel(const bf16* __restrict__ d
             gn[0][j] = gn[1][j];
             rn[0][j] = rn[1][j];
         }
+        const float mu = mun[0], rs = rsn[0];
+        mun[0] = mun[1];
+        rsn[0] = rsn[1];
         if (row + 2 * waves < rows) fetch(row + 2 * waves, 1);
-        const float mu = mean[row], rs = rstd[row];
         float sg = 0.f, sgx = 0.f;
 #pragma unroll
         for (int j = 0; j < NV; ++j)
