@@ -15,7 +15,10 @@
 // and the state gradient runs backwards as dS_n = dS_{n+1} + Q^T dO - K^T D Y
 // (= dS_{n+1} + Q^T dO - W^T dVn with W = T D K).  These restate the BPTT of
 // kernels/cuda/efla.cu:315-454 chunk-wise (including its dc/dlambda term of
-// efla.cu:384-451) for the query readout.
+// efla.cu:384-451) for the query readout.  Since
+// T^T dT T^T = (T^T dVn)(T D R)^T = Y Vn^T, the gradient kernel forms
+//   dA = -strict_lower(Y Vn^T)
+// as a sum over the value slices, like Dm, and never forms dT.
 //
 // scan_h_kernel   (forward recompute, grid: sequences x H x V/64)
 //   S through the chunks as in scan_o_kernel; writes each chunk's start state
@@ -323,17 +326,11 @@ struct GradSmem {
     bf16 dh[64 * ldb<K>()];  // dh[v][f]
     union {
         struct {  // one 64-wide value slice
-            bf16 DR[64 * LD64];  // D R [t][v]
+            bf16 DR[64 * LD64];  // D R [t][v]; after the last slice, dG [i][j] (j < i)
             bf16 Vn[64 * LD64];  // Vn [t][v]
             bf16 dVn[64 * LD64]; // dVn [t][v]
+            bf16 Y[64 * LD64];   // Y [t][v]
         } s;
-        struct {  // closing products (Dm lives in Ps meanwhile)
-            bf16 lo[2 * 64 * LD64];  // DR and Vn until the slices end
-            bf16 X[64 * LD64];       // dT T^T [t][t''] (over dVn)
-            bf16 dG[64 * LD64];      // first dT [t][t'] (t' < t), stored before the
-                                     // slices' end (nothing there is read by them),
-                                     // then dG [i][j] (j < i)
-        } e;
         struct {  // the item's dq, dk rows on their way out
             bf16 dq[64 * ldb<K>()];
             bf16 dk[64 * ldb<K>()];
@@ -351,11 +348,10 @@ struct GradSmem {
 // b + gridDim.x, ... in heads-fastest order (the heads of one chunk are
 // neighbouring row pieces of the same token rows).  An item's inputs are
 // copied straight into LDS (global_load_lds) while the previous item runs its
-// closing products: its first value slice (v, dO, h, dh), P and the per-token
-// coefficients as soon as the slice buffers are free, q once the closing no
-// longer reads Q, T once it no longer reads T, and k after the last product
-// that reads K.  Nothing of the next item passes through registers, so the
-// copies never make a wave wait.
+// closing products: its first value slice (v, dO, h, dh), T and the per-token
+// coefficients as soon as the slices end (the closing reads none of them),
+// q, P and k after the closing's last product.  Nothing of the next item
+// passes through registers, so the copies never make a wave wait.
 template <int NG>
 constexpr int grad_threads() {
     return 256 * NG;
@@ -514,11 +510,11 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     const float bt = cf[t];
 
     // ---- value slices ----
-    floatx4 dqa[NF], dka[NF], dma[EG], dta[EG];
+    floatx4 dqa[NF], dka[NF], dma[EG], dya[EG];
 #pragma unroll
     for (int fb = 0; fb < NF; ++fb) dqa[fb] = dka[fb] = zero4();
 #pragma unroll
-    for (int e = 0; e < EG; ++e) dma[e] = dta[e] = zero4();
+    for (int e = 0; e < EG; ++e) dma[e] = dya[e] = zero4();
     // this group's t' blocks reach t' <= t: block J holds tokens of
     // 32 (J >> 1) .. 32 (J >> 1) + 31 (pim interleaves J and J ^ 1)
     const bool jlive = 32 * ((EG * hf) >> 1) <= 16 * tb + 15;
@@ -566,7 +562,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             store4(sm.u.s.dVn + t * LD64 + 16 * vb + 4 * g, da);
         }
         __syncthreads();
-        // Vn^T = (D R)^T T^T; Y^T = dVn^T T; db += sum_v Y R; D Y -> V (and dv)
+        // Vn^T = (D R)^T T^T; Y^T = dVn^T T; db += sum_v Y R; Y -> Y, D Y -> V (and dv)
 #pragma unroll
         for (int e = 0; e < EG; ++e) {
             const int vb = EG * hf + e;
@@ -579,6 +575,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             y = mma(frag_trc(l, sm.u.s.dVn, LD64, 32, 16 * vb), frag_trc(l, sm.Tb, LD64, 32, 16 * tb), y);
 #pragma unroll
             for (int i = 0; i < 4; ++i) dbp += y[i] * rT[e][i];
+            store4(sm.u.s.Y + t * LD64 + 16 * vb + 4 * g, y);
             store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
         __syncthreads();
@@ -590,7 +587,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
                     *reinterpret_cast<const bf16x8*>(sm.V + tt * LD64 + f);
         }
         // dq^T += h^T dO^T; dk^T += dh^T Vn^T - h^T (D Y)^T  (key tiles f0 .. f0+NF-1)
-        // dT^T[t'][t] += sum_v D R[t'] dVn[t]; Dm^T[t'][t] += sum_v Vn[t'] dO[t]
+        // (Y Vn^T)^T[t'][t] += sum_v Vn[t'] Y[t]; Dm^T[t'][t] += sum_v Vn[t'] dO[t]
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             const bf16x8 dob = frag_nat(l, sm.dO, LD64, 16 * tb, 32 * ks);
@@ -605,54 +602,61 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
                 dka[fb] = mma(frag_tr(l, kh(sm.dh, fcl), LDH, 32 * ks, kcol(fcl)), vnb, dka[fb]);
             }
             if (jlive) {
-                const bf16x8 dvb = frag_nat(l, sm.u.s.dVn, LD64, 16 * tb, 32 * ks);
+                const bf16x8 yb = frag_nat(l, sm.u.s.Y, LD64, 16 * tb, 32 * ks);
 #pragma unroll
                 for (int e = 0; e < EG; ++e) {
                     const int J = EG * hf + e;
-                    dta[e] = mma(frag_row(l, sm.u.s.DR, LD64, pim(J, r), 32 * ks), dvb, dta[e]);
-                    dma[e] = mma(frag_row(l, sm.u.s.Vn, LD64, pim(J, r), 32 * ks), dob, dma[e]);
+                    const bf16x8 vr = frag_row(l, sm.u.s.Vn, LD64, pim(J, r), 32 * ks);
+                    dya[e] = mma(vr, yb, dya[e]);
+                    dma[e] = mma(vr, dob, dma[e]);
                 }
             }
         }
     }
-    // db from Y o R: sum over the 4 lane groups holding token t, then the halves
-    dbp += __shfl_xor(dbp, 16);
-    dbp += __shfl_xor(dbp, 32);
-    if (g == 0) sm.dbh[hf][t] = dbp;
-
     // ---- closing products ----
-    // Dm[t][t'] keeps t' <= t, dT[t][t'] keeps t' < t; share both [t][t'].
-    // They go where the last slice phase reads nothing -- Dm into P's tile
-    // (last read by the slice's first phase), dT into dG's slot (beyond the
-    // slice temporaries) -- so one barrier ends the slices and the stores.
+    // dA[t][j] = -sum_v Y[t][v] Vn[j][v] (j < t) is complete in this wave's
+    // tiles; with G recomputed, db += sum_j dA G and dG = b dA.  Dm (j <= t)
+    // goes into P's tile (last read by the slices' first phase), dG into D R's
+    // (last read by their second), so one barrier ends the slices and the stores.
     bf16* const Dm = sm.Ps;
-    bf16* const dTm = sm.u.e.dG;
+    bf16* const dGm = sm.u.s.DR;
+    float dbg = 0.f;
 #pragma unroll
     for (int e = 0; e < EG; ++e) {
         const int J = EG * hf + e;
+        floatx4 dg = zero4();
+        if (jlive) {
+            floatx4 gg = zero4();
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int tp = pim(J, 4 * g + i);
-            if (tp > t) dma[e][i] = 0.f;
-            if (tp >= t) dta[e][i] = 0.f;
+            for (int k0 = 0; k0 < K; k0 += 32)
+                gg = mma(frag_row(l, kh(sm.Ks, k0), LDH, pim(J, r), kcol(k0)),
+                         frag_nat(l, kh(sm.Ks, k0), LDH, 16 * tb, kcol(k0)), gg);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = pim(J, 4 * g + i);
+                const float da = (j < t) ? -dya[e][i] : 0.f;
+                dbg += da * gg[i];
+                dg[i] = bt * da;
+            }
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            if (pim(J, 4 * g + i) > t) dma[e][i] = 0.f;
         store4(Dm + t * LD64 + pim(J, 4 * g), dma[e]);
-        store4(dTm + t * LD64 + pim(J, 4 * g), dta[e]);
+        store4(dGm + t * LD64 + pim(J, 4 * g), dg);
     }
-    __syncthreads();  // slice buffers are free; Dm, dT complete
-    // the next item's first slice and coefficients into the free slice
-    // buffers (the closing products touch neither); its P once Dm is read
-    if (more) copy_slice0(nxt, par ^ 1, l, false);
-    // X^T[t''][t] = sum_t' T[t''][t'] dT[t][t'] for this group's t'' blocks
-    {
-        const bf16x8 d0 = frag_nat(l, dTm, LD64, 16 * tb, 0), d1 = frag_nat(l, dTm, LD64, 16 * tb, 32);
-#pragma unroll
-        for (int e = 0; e < EG; ++e) {
-            const int J = EG * hf + e;
-            floatx4 x = mma(frag_nat(l, sm.Tb, LD64, 16 * J, 0), d0, zero4());
-            x = mma(frag_nat(l, sm.Tb, LD64, 16 * J, 32), d1, x);
-            store4(sm.u.e.X + t * LD64 + 16 * J + 4 * g, x);
-        }
+    // db from Y o R and dA o G: sum over the 4 lane groups holding token t,
+    // then over the groups
+    dbp += dbg;
+    dbp += __shfl_xor(dbp, 16);
+    dbp += __shfl_xor(dbp, 32);
+    if (g == 0) sm.dbh[hf][t] = dbp;
+    __syncthreads();  // slice buffers are free; Dm, dG, db complete
+    // the next item's first slice, T and coefficients into the free buffers
+    // (the closing products read none of them)
+    if (more) {
+        copy_slice0(nxt, par ^ 1, l, false);
+        copy_t(nxt, l);
     }
     // dq^T += K^T Dm^T (k = t' <= t);  dk^T += Q^T Dm (token t' = t, k = t >= t')
     {
@@ -669,50 +673,12 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             dka[fb] = mma(frag_trc(l, kh(sm.Qs, fc), LDH, 32, kcol(fc)), c1, dka[fb]);
         }
     }
-    __syncthreads();
-    if (more) {  // Q and Dm are not read again in this item
-        copy_q(nxt, l);
-        copy_p(nxt, l);
-    }
-    // M^T[j][i] = sum_t X[t][j] T[t][i] (i = t owned here, j in this group's
-    // blocks, j < i); dA = -M, G recomputed: db += sum_j dA G; dG = b_i dA ->
-    // shared [i][j]
-    float dbg = 0.f;
-#pragma unroll
-    for (int e = 0; e < EG; ++e) {
-        const int J = EG * hf + e;
-        floatx4 dg = zero4();
-        if (jlive) {
-            const int c0 = 32 * (J >> 1) + 4 * (J & 1);
-            floatx4 m = zero4();
-            if (nks == 0) m = mma(frag_trc(l, sm.u.e.X, LD64, 0, c0, 8), frag_trc(l, sm.Tb, LD64, 0, 16 * tb), m);
-            m = mma(frag_trc(l, sm.u.e.X, LD64, 32, c0, 8), frag_trc(l, sm.Tb, LD64, 32, 16 * tb), m);
-            floatx4 gg = zero4();
-#pragma unroll
-            for (int k0 = 0; k0 < K; k0 += 32)
-                gg = mma(frag_row(l, kh(sm.Ks, k0), LDH, pim(J, r), kcol(k0)),
-                         frag_nat(l, kh(sm.Ks, k0), LDH, 16 * tb, kcol(k0)), gg);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = pim(J, 4 * g + i);
-                const float da = (j < t) ? -m[i] : 0.f;
-                dbg += da * gg[i];
-                dg[i] = bt * da;
-            }
-        }
-        store4(sm.u.e.dG + t * LD64 + pim(J, 4 * g), dg);
-    }
-    dbg += __shfl_xor(dbg, 16);
-    dbg += __shfl_xor(dbg, 32);
-    __syncthreads();
-    if (more) copy_t(nxt, l);  // nor T
-    if (g == 0) sm.dbh[hf][t] += dbg;
     // dk^T += K^T dG^T (k = j < i = t) + K^T dG (token j = t, k = i > j)
     {
-        const bf16x8 a0 = frag_nat(l, sm.u.e.dG, LD64, 16 * tb, 0), a1 = frag_nat(l, sm.u.e.dG, LD64, 16 * tb, 32);
-        const bf16x8 b1 = frag_tr(l, sm.u.e.dG, LD64, 32, 16 * tb);
+        const bf16x8 a0 = frag_nat(l, dGm, LD64, 16 * tb, 0), a1 = frag_nat(l, dGm, LD64, 16 * tb, 32);
+        const bf16x8 b1 = frag_tr(l, dGm, LD64, 32, 16 * tb);
         bf16x8 b0 = b1;
-        if (nks == 0) b0 = frag_tr(l, sm.u.e.dG, LD64, 0, 16 * tb);
+        if (nks == 0) b0 = frag_tr(l, dGm, LD64, 0, 16 * tb);
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
@@ -731,7 +697,11 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         kfin[fb] = *reinterpret_cast<const bf16x4*>(kh(sm.Ks, 16 * (f0 + fb)) + t * LDH +
                                                     kcol(16 * (f0 + fb)) + 4 * g);
     __syncthreads();
-    if (more) copy_k(nxt, l);
+    if (more) {  // Q, Dm (in P's tile) and K are not read again in this item
+        copy_q(nxt, l);
+        copy_p(nxt, l);
+        copy_k(nxt, l);
+    }
     float dbt = sm.dbh[0][t];  // dL/db for token t
 #pragma unroll
     for (int gg = 1; gg < NG; ++gg) dbt += sm.dbh[gg][t];
