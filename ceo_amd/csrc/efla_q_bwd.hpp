@@ -352,6 +352,36 @@ struct GradSmem {
 // coefficients as soon as the slices end (the closing reads none of them),
 // q, P and k after the closing's last product.  Nothing of the next item
 // passes through registers, so the copies never make a wave wait.
+// A 64 x K bf16 LDS tile: one [64][ldb<K>()] block, or (SPLIT_, K > 64)
+// K / 64 column halves of 64 with row stride 72.  at(base, c) is the block
+// holding column c, read at column col(c).
+template <int K, bool SPLIT_>
+struct KTile {
+    static constexpr bool SPLIT = SPLIT_ && K > 64;
+    static constexpr int KH = SPLIT ? K / 64 : 1, LD = SPLIT ? 72 : ldb<K>(), HALF = 64 * LD;
+    static_assert(K % 64 == 0 && KH * HALF <= 64 * ldb<K>(), "K = 64 or 128");
+    static __device__ __forceinline__ const bf16* at(const bf16* base, int c) {
+        return SPLIT ? base + (c >> 6) * HALF : base;
+    }
+    static __device__ __forceinline__ int col(int c) { return SPLIT ? (c & 63) : c; }
+    // every 16-byte piece of the 64 x K tile at src (row stride ld) into dst
+    template <int NW>
+    static __device__ __forceinline__ void copy(bf16* dst, const bf16* src, long ld, int nvalid,
+                                                int rot, int l) {
+        if constexpr (!SPLIT) {
+            mf::dma_tile<64, K, ldb<K>(), NW>(dst, src, ld, nvalid, rot, l);
+        } else {
+#pragma unroll
+            for (int hh = 0; hh < KH; ++hh)
+                mf::dma_tile<64, 64, LD, NW>(dst + hh * HALF, src + 64 * hh, ld, nvalid, rot + hh, l);
+        }
+    }
+    // offset of element (row, c) (c a multiple of 8)
+    static __device__ __forceinline__ int off(int row, int c) {
+        return (SPLIT ? (c >> 6) * HALF : 0) + row * LD + col(c);
+    }
+};
+
 template <int NG>
 constexpr int grad_threads() {
     return 256 * NG;
@@ -367,28 +397,26 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     bf16* __restrict__ dbeta, TokLd ld) {
     constexpr int NTG = grad_threads<NG>(), NW = NTG / 64;  // threads, waves
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 16 / NG;  // NF key tiles per group
-    // K-wide operand tiles (Qs, Ks, h, dh) are kept as K / 64 column halves of
-    // 64 with row stride LDH (72 for K = 128: the same 64 x LDK elements).  An
-    // LDS probe runs 16-byte row reads of these halves at about half the rate
-    // of the full 288-byte rows, yet the kernel measures 1-1.1 % faster with
-    // the halves than with full rows (its time does not follow its LDS read
-    // rate).  Every fragment's k or line range lies inside one half.
-    // kh(base, c) is the half holding column c, read at column c % 64.
-    // (The 8-wave d_v = 256 instantiation keeps [64][LDK] tiles: with the
-    // halves, hipcc's register allocation fails on it.)
-    constexpr int KH = NG == 4 ? K / 64 : 1, LDH = KH > 1 ? 72 : LDK, HALF = 64 * LDH;
-    static_assert(K % 64 == 0 && KH * HALF <= 64 * LDK, "K = 64 or 128");
-    auto kh = [](const bf16* base, int c) { return KH > 1 ? base + (c >> 6) * HALF : base; };
-    auto kcol = [](int c) { return KH > 1 ? (c & 63) : c; };
-    auto kcopy = [&](bf16* dst, const bf16* src, long ld, int nvalid, int rot, int l) {
-        if constexpr (KH == 1) {
-            mf::dma_tile<64, K, LDK, NW>(dst, src, ld, nvalid, rot, l);
-        } else {
-#pragma unroll
-            for (int hh = 0; hh < KH; ++hh)
-                mf::dma_tile<64, 64, LDH, NW>(dst + hh * HALF, src + 64 * hh, ld, nvalid, rot + hh, l);
-        }
-    };
+    // K-wide operand tiles (Qs, Ks, h, dh) are kept either as one [64][LDK]
+    // block or as K / 64 column halves of 64 with row stride 72 (the same
+    // 64 x LDK elements); every fragment's k or line range lies inside one
+    // half.  Lk describes Qs and Ks, Lh describes h and dh.  (The 8-wave
+    // d_v = 256 instantiation keeps [64][LDK] tiles: with the halves, hipcc's
+    // register allocation fails on it.)
+#ifndef GRAD_SPLIT_K
+#define GRAD_SPLIT_K 0
+#endif
+#ifndef GRAD_SPLIT_H
+#define GRAD_SPLIT_H 1
+#endif
+    using Lk = KTile<K, NG == 4 && GRAD_SPLIT_K>;
+    using Lh = KTile<K, NG == 4 && GRAD_SPLIT_H>;
+    auto kh = [](const bf16* base, int c) { return Lk::at(base, c); };
+    auto kcol = [](int c) { return Lk::col(c); };
+    constexpr int LDH = Lk::LD;
+    auto hh_ = [](const bf16* base, int c) { return Lh::at(base, c); };
+    auto hcol = [](int c) { return Lh::col(c); };
+    constexpr int LDS_H = Lh::LD;
     constexpr int EG = 4 / NG;  // value tiles / 16-token blocks per group
     // threads holding the v, dO slice and the h, dh slice prefetches (one
     // 16-byte piece each at most)
@@ -419,21 +447,21 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         const long cid = (long)I.slot * H + I.h, chb = cid * V * K;
         mf::dma_tile<64, VS, LD64, NW>(sm.V, v + I.bos * ld.v + (long)I.h * V, ld.v, I.len, 0, l);
         mf::dma_tile<64, VS, LD64, NW>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
-        kcopy(sm.h, hist + chb, K, 64, 4, l);
-        kcopy(sm.dh, dhist + chb, K, 64, 6, l);
+        Lh::template copy<NW>(sm.h, hist + chb, K, 64, 4, l);
+        Lh::template copy<NW>(sm.dh, dhist + chb, K, 64, 6, l);
         if (with_p) copy_p(I, l);
         // b (16 chunks of 16 bytes) and dc/dlambda, dc/dbeta (32 chunks)
         if (w8 == NW - 1 && l < 16) mf::dma16(bws + cid * 64, 16u * l, sm.coef[par][0]);
         if (w8 == NW - 2 && l < 32) mf::dma16(dcws + cid * 128, 16u * l, sm.coef[par][1]);
     };
     auto copy_q = [&](const Item& I, int l) {
-        kcopy(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
+        Lk::template copy<NW>(sm.Qs, q + I.bos * ld.q + (long)I.h * K, ld.q, I.len, 3, l);
     };
     auto copy_t = [&](const Item& I, int l) {
         dma_tri<NW>(sm.Tb, Tws + ((long)I.slot * H + I.h) * TRI_ELEMS, 5, l);
     };
     auto copy_k = [&](const Item& I, int l) {
-        kcopy(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);
+        Lk::template copy<NW>(sm.Ks, k + I.bos * ld.k + (long)I.h * K, ld.k, I.len, 1, l);
     };
 
     int it = blockIdx.x, par = 0;
@@ -478,7 +506,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     if (len < 64) {  // a sequence's last chunk: token rows past its end read as zero
         for (int i = tid; i < (64 - len) * (K / 8); i += NTG) {
             const int c = 8 * (i % (K / 8));
-            const int o = (KH > 1 ? (c >> 6) * HALF : 0) + (len + i / (K / 8)) * LDH + kcol(c);
+            const int o = Lk::off(len + i / (K / 8), c);
             *reinterpret_cast<bf16x8*>(sm.Qs + o) = bf16x8{};
             *reinterpret_cast<bf16x8*>(sm.Ks + o) = bf16x8{};
         }
@@ -508,6 +536,14 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     // B operand (line t, k = t') of T
     const bf16x8 tfr0 = frag_nat(l, sm.Tb, LD64, 16 * tb, 0), tfr1 = frag_nat(l, sm.Tb, LD64, 16 * tb, 32);
     const float bt = cf[t];
+#ifndef GRAD_DB_VN
+#define GRAD_DB_VN 1
+#endif
+    // dL/db: (I + D strict_lower(G)) Vn = D R gives strict_lower(G) Vn =
+    // R - D^-1 Vn, so rowsum(Y o R) + rowsum(dA o G) = rowsum(Y o Vn) / b, with
+    // no G.  A 16-token block holding a b near 0 takes the explicit sum
+    // instead (wave-uniform: every wave of the block sees the same 16 b).
+    const bool dbx = !GRAD_DB_VN || __any(t < len && !(fabsf(bt) >= 1e-20f));
 
     // ---- value slices ----
     floatx4 dqa[NF], dka[NF], dma[EG], dya[EG];
@@ -528,12 +564,12 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
                 rd.store_rows(sm.dO, LD64);
             }
             if (NTH == NTG || tid < NTH) {
-                if constexpr (KH > 1) {
-                    rh.store_rows_split(sm.h, LDH, HALF);
-                    rdh.store_rows_split(sm.dh, LDH, HALF);
+                if constexpr (Lh::KH > 1) {
+                    rh.store_rows_split(sm.h, Lh::LD, Lh::HALF);
+                    rdh.store_rows_split(sm.dh, Lh::LD, Lh::HALF);
                 } else {
-                    rh.store_rows(sm.h, LDK);
-                    rdh.store_rows(sm.dh, LDK);
+                    rh.store_rows(sm.h, Lh::LD);
+                    rdh.store_rows(sm.dh, Lh::LD);
                 }
             }
             __syncthreads();
@@ -541,7 +577,6 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         if (s + 1 < NS) prefetch(s + 1);
         // R^T = V^T - h K^T and dVn^T = dO^T P + dh K^T for value tiles
         // EG hf .. EG hf + EG - 1: tile (value 16vb + 4g + i, token t)
-        floatx4 rT[EG];
 #pragma unroll
         for (int e = 0; e < EG; ++e) {
             const int vb = EG * hf + e;
@@ -551,15 +586,16 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             for (int kb = 0; kb < K / 32; ++kb) {
                 const int kc = 32 * kb;
                 const bf16x8 kt = frag_nat(l, kh(sm.Ks, kc), LDH, 16 * tb, kcol(kc));
-                ra = mma(frag_nat(l, kh(sm.h, kc), LDH, 16 * vb, kcol(kc)), mf::neg(kt), ra);
-                da = mma(frag_nat(l, kh(sm.dh, kc), LDH, 16 * vb, kcol(kc)), kt, da);
+                ra = mma(frag_nat(l, hh_(sm.h, kc), LDS_H, 16 * vb, hcol(kc)), mf::neg(kt), ra);
+                da = mma(frag_nat(l, hh_(sm.dh, kc), LDS_H, 16 * vb, hcol(kc)), kt, da);
             }
             // (both operands transposed: c-order rows, see mf::frag_trc)
             if (nks == 0) da = mma(frag_trc(l, sm.dO, LD64, 0, 16 * vb), frag_trc(l, sm.Ps, LD64, 0, 16 * tb), da);
             da = mma(frag_trc(l, sm.dO, LD64, 32, 16 * vb), frag_trc(l, sm.Ps, LD64, 32, 16 * tb), da);
-            rT[e] = ra;
             store4s(sm.u.s.DR + t * LD64 + 16 * vb + 4 * g, ra, bt);
             store4(sm.u.s.dVn + t * LD64 + 16 * vb + 4 * g, da);
+            // the explicit db needs R itself: parked where this wave's Y goes
+            if (dbx) store4(sm.u.s.Y + t * LD64 + 16 * vb + 4 * g, ra);
         }
         __syncthreads();
         // Vn^T = (D R)^T T^T; Y^T = dVn^T T; db += sum_v Y R; Y -> Y, D Y -> V (and dv)
@@ -573,8 +609,14 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             if (nks == 0)
                 y = mma(frag_trc(l, sm.u.s.dVn, LD64, 0, 16 * vb), frag_trc(l, sm.Tb, LD64, 0, 16 * tb), y);
             y = mma(frag_trc(l, sm.u.s.dVn, LD64, 32, 16 * vb), frag_trc(l, sm.Tb, LD64, 32, 16 * tb), y);
+            if (dbx) {
+                const floatx4 ra = load4(sm.u.s.Y + t * LD64 + 16 * vb + 4 * g);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dbp += y[i] * rT[e][i];
+                for (int i = 0; i < 4; ++i) dbp += y[i] * ra[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dbp += y[i] * vn[i];
+            }
             store4(sm.u.s.Y + t * LD64 + 16 * vb + 4 * g, y);
             store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
@@ -596,10 +638,10 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
 #pragma unroll
             for (int fb = 0; fb < NF; ++fb) {
                 const int fcl = 16 * (f0 + fb);
-                const bf16x8 ha = frag_tr(l, kh(sm.h, fcl), LDH, 32 * ks, kcol(fcl));
+                const bf16x8 ha = frag_tr(l, hh_(sm.h, fcl), LDS_H, 32 * ks, hcol(fcl));
                 dqa[fb] = mma(ha, dob, dqa[fb]);
                 dka[fb] = mma(ha, dyb, dka[fb]);
-                dka[fb] = mma(frag_tr(l, kh(sm.dh, fcl), LDH, 32 * ks, kcol(fcl)), vnb, dka[fb]);
+                dka[fb] = mma(frag_tr(l, hh_(sm.dh, fcl), LDS_H, 32 * ks, hcol(fcl)), vnb, dka[fb]);
             }
             if (jlive) {
                 const bf16x8 yb = frag_nat(l, sm.u.s.Y, LD64, 16 * tb, 32 * ks);
@@ -615,7 +657,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     }
     // ---- closing products ----
     // dA[t][j] = -sum_v Y[t][v] Vn[j][v] (j < t) is complete in this wave's
-    // tiles; with G recomputed, db += sum_j dA G and dG = b dA.  Dm (j <= t)
+    // tiles; dG = b dA (and, in blocks taking the explicit db, G recomputed
+    // and db += sum_j dA G).  Dm (j <= t)
     // goes into P's tile (last read by the slices' first phase), dG into D R's
     // (last read by their second), so one barrier ends the slices and the stores.
     bf16* const Dm = sm.Ps;
@@ -626,18 +669,19 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         const int J = EG * hf + e;
         floatx4 dg = zero4();
         if (jlive) {
-            floatx4 gg = zero4();
 #pragma unroll
-            for (int k0 = 0; k0 < K; k0 += 32)
-                gg = mma(frag_row(l, kh(sm.Ks, k0), LDH, pim(J, r), kcol(k0)),
-                         frag_nat(l, kh(sm.Ks, k0), LDH, 16 * tb, kcol(k0)), gg);
+            for (int i = 0; i < 4; ++i) dg[i] = (pim(J, 4 * g + i) < t) ? -dya[e][i] : 0.f;  // dA
+            if (dbx) {
+                floatx4 gg = zero4();
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = pim(J, 4 * g + i);
-                const float da = (j < t) ? -dya[e][i] : 0.f;
-                dbg += da * gg[i];
-                dg[i] = bt * da;
+                for (int k0 = 0; k0 < K; k0 += 32)
+                    gg = mma(frag_row(l, kh(sm.Ks, k0), LDH, pim(J, r), kcol(k0)),
+                             frag_nat(l, kh(sm.Ks, k0), LDH, 16 * tb, kcol(k0)), gg);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) dbg += dg[i] * gg[i];
             }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dg[i] *= bt;
         }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -645,9 +689,9 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         store4(Dm + t * LD64 + pim(J, 4 * g), dma[e]);
         store4(dGm + t * LD64 + pim(J, 4 * g), dg);
     }
-    // db from Y o R and dA o G: sum over the 4 lane groups holding token t,
-    // then over the groups
-    dbp += dbg;
+    // db: sum over the 4 lane groups holding token t, then over the groups
+    // (rows past the sequence's end have b = 0 and are never written)
+    dbp = dbx ? dbp + dbg : (t < len ? dbp / bt : 0.f);
     dbp += __shfl_xor(dbp, 16);
     dbp += __shfl_xor(dbp, 32);
     if (g == 0) sm.dbh[hf][t] = dbp;

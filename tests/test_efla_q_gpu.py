@@ -114,6 +114,22 @@ def test_small_lambda_bf16_fast_kernels(oracle, K, V):
           xform=small_lambda)
 
 
+def zero_beta(oracle, x, bf16):
+    """beta = 0 on a few tokens inside the sequences (b = c(0, lambda) = 0):
+    the bf16 gradient kernel then forms dL/db of those 16-token blocks from
+    rowsum(Y o R) + rowsum(dA o G) instead of rowsum(Y o Vn) / b."""
+    beta = x["beta"].copy()
+    beta[[5, 81, 150, 263, 300]] = 0.0
+    x = dict(x)
+    x["beta"] = beta
+    return x
+
+
+@pytest.mark.parametrize("K,V", [(128, 128), (64, 64)])
+def test_zero_beta_tokens_bf16_fast_kernels(oracle, K, V):
+    _case(oracle, 0x0B0 + K, 2, 200, 2, K, V, torch.bfloat16, s0=True, dst=True, xform=zero_beta)
+
+
 def test_nan_inf_stay_in_their_sequence_and_head(oracle):
     """A NaN in one token's k and an Inf in another sequence's v contaminate
     only their own (sequence, head): every other (sequence, head) gets outputs
