@@ -312,7 +312,7 @@ template <int K, int NG>
 struct GradSmem {
     bf16 Qs[64 * ldb<K>()];
     bf16 Ks[64 * ldb<K>()];
-    bf16 Ps[64 * LD64];  // P[t][t'] (t' <= t); in the closing, Dm[t][t'] (t' <= t)
+    bf16 Ps[64 * LD64];  // P[t][t'] (t' <= t)
     bf16 Tb[64 * LD64];  // bf16(T)[t][t'] (t' <= t), from the WY prep
     // b, dc/dlambda, dc/dbeta per token for items of even / odd position in
     // this workgroup's sequence (the next item's arrive during the closing)
@@ -328,7 +328,7 @@ struct GradSmem {
         struct {  // one 64-wide value slice
             bf16 DR[64 * LD64];  // D R [t][v]; after the last slice, dG [i][j] (j < i)
             bf16 Vn[64 * LD64];  // Vn [t][v]
-            bf16 dVn[64 * LD64]; // dVn [t][v]
+            bf16 dVn[64 * LD64]; // dVn [t][v]; after the last slice, Dm [t][t'] (t' <= t)
             bf16 Y[64 * LD64];   // Y [t][v]
         } s;
         struct {  // the item's dq, dk rows on their way out
@@ -338,20 +338,6 @@ struct GradSmem {
     } u;
 };
 
-// Wave (tb, gq): tb = wave & 3 owns tokens 16tb .. 16tb+15 (the columns of
-// every transposed tile it computes); gq = wave >> 2 picks one of NG groups of
-// the value tiles (slice phase), of the key tiles (dq / dk) and of the 16-token
-// blocks of the 64 x 64 chunk matrices: 4 / NG of each.  NG = 2 is 8 waves, NG
-// = 4 is 16 (four per SIMD, half the tiles per wave).
-//
-// Persistent: workgroup b (one per CU) takes the (chunk, head) items b,
-// b + gridDim.x, ... in heads-fastest order (the heads of one chunk are
-// neighbouring row pieces of the same token rows).  An item's inputs are
-// copied straight into LDS (global_load_lds) while the previous item runs its
-// closing products: its first value slice (v, dO, h, dh), T and the per-token
-// coefficients as soon as the slices end (the closing reads none of them),
-// q, P and k after the closing's last product.  Nothing of the next item
-// passes through registers, so the copies never make a wave wait.
 // A 64 x K bf16 LDS tile: one [64][ldb<K>()] block, or (SPLIT_, K > 64)
 // K / 64 column halves of 64 with row stride 72.  at(base, c) is the block
 // holding column c, read at column col(c).
@@ -382,6 +368,21 @@ struct KTile {
     }
 };
 
+// Wave (tb, gq): tb = wave & 3 owns tokens 16tb .. 16tb+15 (the columns of
+// every transposed tile it computes); gq = wave >> 2 picks one of NG groups of
+// the value tiles (slice phase), of the key tiles (dq / dk) and of the 16-token
+// blocks of the 64 x 64 chunk matrices: 4 / NG of each.  NG = 2 is 8 waves, NG
+// = 4 is 16 (four per SIMD, half the tiles per wave).
+//
+// Persistent: workgroup b (one per CU) takes the (chunk, head) items b,
+// b + gridDim.x, ... in heads-fastest order (the heads of one chunk are
+// neighbouring row pieces of the same token rows).  An item's inputs are
+// copied straight into LDS (global_load_lds) while the previous item ends:
+// P once the last value slice's first phase is done, T after its second, the
+// first value slice (v, dO, h, dh) and the per-token coefficients as soon as
+// the slices end (the closing reads none of them), q after the closing's Dm
+// products and k after the last product that reads K.  Nothing of the next
+// item passes through registers, so the copies never make a wave wait.
 template <int NG>
 constexpr int grad_threads() {
     return 256 * NG;
@@ -397,20 +398,15 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     bf16* __restrict__ dbeta, TokLd ld) {
     constexpr int NTG = grad_threads<NG>(), NW = NTG / 64;  // threads, waves
     constexpr int LDK = ldb<K>(), NS = V / VS, NF = K / 16 / NG;  // NF key tiles per group
-    // K-wide operand tiles (Qs, Ks, h, dh) are kept either as one [64][LDK]
-    // block or as K / 64 column halves of 64 with row stride 72 (the same
-    // 64 x LDK elements); every fragment's k or line range lies inside one
-    // half.  Lk describes Qs and Ks, Lh describes h and dh.  (The 8-wave
-    // d_v = 256 instantiation keeps [64][LDK] tiles: with the halves, hipcc's
-    // register allocation fails on it.)
-#ifndef GRAD_SPLIT_K
-#define GRAD_SPLIT_K 0
-#endif
-#ifndef GRAD_SPLIT_H
-#define GRAD_SPLIT_H 1
-#endif
-    using Lk = KTile<K, NG == 4 && GRAD_SPLIT_K>;
-    using Lh = KTile<K, NG == 4 && GRAD_SPLIT_H>;
+    // K-wide operand tiles: Qs and Ks are one [64][LDK] block each (Lk); the
+    // 16-wave kernel keeps h and dh as K / 64 column halves of 64 with row
+    // stride 72 (Lh; the same 64 x LDK elements), every fragment's k or line
+    // range inside one half.  Measured at cfg3 against the other three
+    // combinations, this one is 1-3 % faster.  (The 8-wave d_v = 256
+    // instantiation keeps [64][LDK] tiles: with the halves, hipcc's register
+    // allocation fails on it.)
+    using Lk = KTile<K, false>;
+    using Lh = KTile<K, NG == 4>;
     auto kh = [](const bf16* base, int c) { return Lk::at(base, c); };
     auto kcol = [](int c) { return Lk::col(c); };
     constexpr int LDH = Lk::LD;
@@ -536,14 +532,11 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     // B operand (line t, k = t') of T
     const bf16x8 tfr0 = frag_nat(l, sm.Tb, LD64, 16 * tb, 0), tfr1 = frag_nat(l, sm.Tb, LD64, 16 * tb, 32);
     const float bt = cf[t];
-#ifndef GRAD_DB_VN
-#define GRAD_DB_VN 1
-#endif
     // dL/db: (I + D strict_lower(G)) Vn = D R gives strict_lower(G) Vn =
     // R - D^-1 Vn, so rowsum(Y o R) + rowsum(dA o G) = rowsum(Y o Vn) / b, with
     // no G.  A 16-token block holding a b near 0 takes the explicit sum
     // instead (wave-uniform: every wave of the block sees the same 16 b).
-    const bool dbx = !GRAD_DB_VN || __any(t < len && !(fabsf(bt) >= 1e-20f));
+    const bool dbx = __any(t < len && !(fabsf(bt) >= 1e-20f));
 
     // ---- value slices ----
     floatx4 dqa[NF], dka[NF], dma[EG], dya[EG];
@@ -598,6 +591,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             if (dbx) store4(sm.u.s.Y + t * LD64 + 16 * vb + 4 * g, ra);
         }
         __syncthreads();
+        // the last slice no longer reads P: the next item's P goes in now
+        if (s == NS - 1 && more) copy_p(nxt, l);
         // Vn^T = (D R)^T T^T; Y^T = dVn^T T; db += sum_v Y R; Y -> Y, D Y -> V (and dv)
 #pragma unroll
         for (int e = 0; e < EG; ++e) {
@@ -621,6 +616,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             store4s(sm.V + t * LD64 + 16 * vb + 4 * g, y, bt);
         }
         __syncthreads();
+        // nor T (its fragments for Vn are in registers since the item start)
+        if (s == NS - 1 && more) copy_t(nxt, l);
         if (NTV == NTG || tid < NTV) {  // dv = D Y of this slice from its bf16 copy in V, as whole 16-byte row pieces
             static_assert(NTV == 64 * (VS / 8), "one piece per thread");
             const int tt = tid / (VS / 8), f = 8 * (tid % (VS / 8));
@@ -659,9 +656,9 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     // dA[t][j] = -sum_v Y[t][v] Vn[j][v] (j < t) is complete in this wave's
     // tiles; dG = b dA (and, in blocks taking the explicit db, G recomputed
     // and db += sum_j dA G).  Dm (j <= t)
-    // goes into P's tile (last read by the slices' first phase), dG into D R's
-    // (last read by their second), so one barrier ends the slices and the stores.
-    bf16* const Dm = sm.Ps;
+    // goes into dVn's tile, dG into D R's (both last read by the slices' second
+    // phase), so one barrier ends the slices and the stores.
+    bf16* const Dm = sm.u.s.dVn;
     bf16* const dGm = sm.u.s.DR;
     float dbg = 0.f;
 #pragma unroll
@@ -700,7 +697,6 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     // (the closing products read none of them)
     if (more) {
         copy_slice0(nxt, par ^ 1, l, false);
-        copy_t(nxt, l);
     }
     // dq^T += K^T Dm^T (k = t' <= t);  dk^T += Q^T Dm (token t' = t, k = t >= t')
     {
@@ -717,6 +713,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             dka[fb] = mma(frag_trc(l, kh(sm.Qs, fc), LDH, 32, kcol(fc)), c1, dka[fb]);
         }
     }
+    __syncthreads();  // Q is read
+    if (more) copy_q(nxt, l);
     // dk^T += K^T dG^T (k = j < i = t) + K^T dG (token j = t, k = i > j)
     {
         const bf16x8 a0 = frag_nat(l, dGm, LD64, 16 * tb, 0), a1 = frag_nat(l, dGm, LD64, 16 * tb, 32);
@@ -741,11 +739,7 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         kfin[fb] = *reinterpret_cast<const bf16x4*>(kh(sm.Ks, 16 * (f0 + fb)) + t * LDH +
                                                     kcol(16 * (f0 + fb)) + 4 * g);
     __syncthreads();
-    if (more) {  // Q, Dm (in P's tile) and K are not read again in this item
-        copy_q(nxt, l);
-        copy_p(nxt, l);
-        copy_k(nxt, l);
-    }
+    if (more) copy_k(nxt, l);  // nor K
     float dbt = sm.dbh[0][t];  // dL/db for token t
 #pragma unroll
     for (int gg = 1; gg < NG; ++gg) dbt += sm.dbh[gg][t];
