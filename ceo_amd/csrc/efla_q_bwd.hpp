@@ -379,9 +379,9 @@ struct KTile {
 // neighbouring row pieces of the same token rows).  An item's inputs are
 // copied straight into LDS (global_load_lds) while the previous item ends:
 // P once the last value slice's first phase is done, T after its second, the
-// first value slice (v, dO, h, dh) and the per-token coefficients as soon as
-// the slices end (the closing reads none of them), q after the closing's Dm
-// products and k after the last product that reads K.  Nothing of the next
+// first value slice's v, dO, h and the per-token coefficients as soon as the
+// slices end (the closing reads none of them), q and dh after the closing's
+// Q^T Dm product and k after the last product that reads K.  Nothing of the next
 // item passes through registers, so the copies never make a wave wait.
 template <int NG>
 constexpr int grad_threads() {
@@ -439,12 +439,15 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
         if constexpr (PS)
             dma_tri<NW>(sm.Ps, Pws + ((long)I.slot * H + I.h) * TRI_ELEMS, 2, l);
     };
-    auto copy_slice0 = [&](const Item& I, int par, int l, bool with_p) {
+    auto copy_dh0 = [&](const Item& I, int l) {
+        Lh::template copy<NW>(sm.dh, dhist + ((long)I.slot * H + I.h) * V * K, K, 64, 6, l);
+    };
+    auto copy_slice0 = [&](const Item& I, int par, int l, bool with_p, bool with_dh = true) {
         const long cid = (long)I.slot * H + I.h, chb = cid * V * K;
         mf::dma_tile<64, VS, LD64, NW>(sm.V, v + I.bos * ld.v + (long)I.h * V, ld.v, I.len, 0, l);
         mf::dma_tile<64, VS, LD64, NW>(sm.dO, dO + (I.bos * H + I.h) * V, (long)H * V, I.len, 2, l);
         Lh::template copy<NW>(sm.h, hist + chb, K, 64, 4, l);
-        Lh::template copy<NW>(sm.dh, dhist + chb, K, 64, 6, l);
+        if (with_dh) copy_dh0(I, l);
         if (with_p) copy_p(I, l);
         // b (16 chunks of 16 bytes) and dc/dlambda, dc/dbeta (32 chunks)
         if (w8 == NW - 1 && l < 16) mf::dma16(bws + cid * 64, 16u * l, sm.coef[par][0]);
@@ -693,30 +696,30 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
     dbp += __shfl_xor(dbp, 32);
     if (g == 0) sm.dbh[hf][t] = dbp;
     __syncthreads();  // slice buffers are free; Dm, dG, db complete
-    // the next item's first slice, T and coefficients into the free buffers
-    // (the closing products read none of them)
-    if (more) {
-        copy_slice0(nxt, par ^ 1, l, false);
-    }
-    // dq^T += K^T Dm^T (k = t' <= t);  dk^T += Q^T Dm (token t' = t, k = t >= t')
+    // the next item's v, dO and h slices and coefficients into the free
+    // buffers (the closing products read none of them); its dh below
+    if (more) copy_slice0(nxt, par ^ 1, l, false, false);
+    // dk^T += Q^T Dm (token t' = t, k = t >= t'), first, so Q is free early
     {
-        const bf16x8 m0 = frag_nat(l, Dm, LD64, 16 * tb, 0), m1 = frag_nat(l, Dm, LD64, 16 * tb, 32);
         const bf16x8 c1 = frag_trc(l, Dm, LD64, 32, 16 * tb);
         bf16x8 c0 = c1;
         if (nks == 0) c0 = frag_trc(l, Dm, LD64, 0, 16 * tb);
 #pragma unroll
         for (int fb = 0; fb < NF; ++fb) {
             const int fc = 16 * (f0 + fb);
-            dqa[fb] = mma(frag_tr(l, kh(sm.Ks, fc), LDH, 0, kcol(fc)), m0, dqa[fb]);
-            if (tb >= 2) dqa[fb] = mma(frag_tr(l, kh(sm.Ks, fc), LDH, 32, kcol(fc)), m1, dqa[fb]);
             if (nks == 0) dka[fb] = mma(frag_trc(l, kh(sm.Qs, fc), LDH, 0, kcol(fc)), c0, dka[fb]);
             dka[fb] = mma(frag_trc(l, kh(sm.Qs, fc), LDH, 32, kcol(fc)), c1, dka[fb]);
         }
     }
     __syncthreads();  // Q is read
-    if (more) copy_q(nxt, l);
-    // dk^T += K^T dG^T (k = j < i = t) + K^T dG (token j = t, k = i > j)
+    if (more) {
+        copy_q(nxt, l);
+        copy_dh0(nxt, l);
+    }
+    // dq^T += K^T Dm^T (k = t' <= t); dk^T += K^T dG^T (k = j < i = t) +
+    // K^T dG (token j = t, k = i > j): the K fragments serve both
     {
+        const bf16x8 m0 = frag_nat(l, Dm, LD64, 16 * tb, 0), m1 = frag_nat(l, Dm, LD64, 16 * tb, 32);
         const bf16x8 a0 = frag_nat(l, dGm, LD64, 16 * tb, 0), a1 = frag_nat(l, dGm, LD64, 16 * tb, 32);
         const bf16x8 b1 = frag_tr(l, dGm, LD64, 32, 16 * tb);
         bf16x8 b0 = b1;
@@ -726,6 +729,8 @@ __global__ void __launch_bounds__(grad_threads<NG>()) grad_kernel(
             const int fc = 16 * (f0 + fb);
             const bf16x8 k0 = frag_tr(l, kh(sm.Ks, fc), LDH, 0, kcol(fc)),
                          k1 = frag_tr(l, kh(sm.Ks, fc), LDH, 32, kcol(fc));
+            dqa[fb] = mma(k0, m0, dqa[fb]);
+            if (tb >= 2) dqa[fb] = mma(k1, m1, dqa[fb]);
             dka[fb] = mma(k0, a0, dka[fb]);
             if (tb >= 2) dka[fb] = mma(k1, a1, dka[fb]);
             if (nks == 0) dka[fb] = mma(k0, b0, dka[fb]);
