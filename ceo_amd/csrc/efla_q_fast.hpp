@@ -90,6 +90,34 @@ __device__ __forceinline__ void tri_store_piece(bf16* __restrict__ base, int row
     }
 }
 
+// Buffer stores whose out-of-range lanes the hardware drops.  A store written
+// as `if (cond) *p = x` becomes a branch around the instruction, and the
+// compiler's wait counts at the join assume the path without it: a later
+// wait for a load issued before the store then also waits for the store (one
+// in-order counter for loads and stores).  Every lane of a wave issuing the
+// instruction, with the condition folded into the offset or into the
+// resource's byte count, keeps the count the same on every path.
+constexpr unsigned BUF_OOB = 0x40000000u;  // an offset past every resource used here
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+__device__ __forceinline__ void bstore8(bf16x4 x, __amdgpu_buffer_rsrc_t r, unsigned off) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(mf::int2v, x), r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void bstore16(bf16x8 x, __amdgpu_buffer_rsrc_t r, unsigned off) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(mf::int4v, x), r, (int)off, 0, 0);
+}
+// tri_store_piece through a resource over one packed matrix (no store when
+// the resource holds 0 bytes)
+__device__ __forceinline__ void tri_store_piece(__amdgpu_buffer_rsrc_t r, int row, int J,
+                                                const bf16x8& lo, const bf16x8& hi) {
+    const bool tile = J <= (row >> 4), stub = row == 0 && J == 1;
+    const unsigned off = tile ? 2u * tri_off(row, 2 * J) : stub ? 2u * TRI_ZERO : BUF_OOB;
+    bstore16(tile ? lo : bf16x8{}, r, off);
+    bstore16(tile ? hi : bf16x8{}, r, off + 16);
+}
+
 // A packed matrix into the registers of a 64 x 64 tile loader, as
 // TileRegs::load would hold the full matrix (upper pieces read as zeros).
 template <int NT>
@@ -113,6 +141,13 @@ __device__ __forceinline__ void store_state_frag(bf16* __restrict__ hist, const 
     bf16* p = hist + (long)vcol * K + 8 * (mf::lane() >> 4);
 #pragma unroll
     for (int kb = 0; kb < K / 32; ++kb) *reinterpret_cast<bf16x8*>(p + 32 * kb) = sb[kb];
+}
+// the same through a resource over the K x V block (no store when it holds 0 bytes)
+template <int K>
+__device__ __forceinline__ void store_state_frag(__amdgpu_buffer_rsrc_t r, const bf16x8* sb, int vcol) {
+    const unsigned o = 2u * (unsigned)(vcol * K + 8 * (mf::lane() >> 4));
+#pragma unroll
+    for (int kb = 0; kb < K / 32; ++kb) bstore16(sb[kb], r, o + 64u * kb);
 }
 
 // ---------------------------------------------------------------------------
@@ -329,7 +364,7 @@ struct ChunkRegs {
         rk.load(k + bos * lk + (long)h * K, lk, len);
         rv.load(vsl + bos * lv + (long)h * V + v0, lv, len);
         load_tri(rt, Tc + cid * TRI_ELEMS);
-        if (threadIdx.x < 64) b = bc[cid * 64 + threadIdx.x];
+        b = bc[cid * 64 + (threadIdx.x & 63)];  // every lane: no branch around the load
     }
     template <typename Buf>
     __device__ __forceinline__ void stage(Buf& bf) {
@@ -426,6 +461,17 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         pre.stage(sm.buf[0]);
         if (nch > 1) prefetch(1);
     }
+    {
+        // as many stores as a chunk issues after its prefetch (P hand-over,
+        // output rows), all dropped: the loop is entered with the same count
+        // of stores behind the prefetch as each iteration leaves, so the
+        // staging's waits need not drain the previous chunk's stores
+        const __amdgpu_buffer_rsrc_t none = out_rsrc(o, 0u);
+        bstore16(bf16x8{}, none, 0u);
+        bstore16(bf16x8{}, none, 16u);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) bstore8(bf16x4{}, none, 8u * tb);
+    }
     for (int n = 0; n < nch; ++n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
@@ -448,7 +494,9 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(S[2 * kb], S[2 * kb + 1]);
-        if (hist) store_state_frag<K>(hist + ((long)(slot0 + n) * H + h) * V * K, sb, vcol);
+        store_state_frag<K>(out_rsrc(hist ? hist + ((long)(slot0 + n) * H + h) * V * K : o,
+                                     hist ? 2u * V * K : 0u),
+                            sb, vcol);
         floatx4 vn[4];
         chunk_vn<K>(cb, w, sb, vn);
         // stage chunk n + 1 (its loads were issued one chunk ago), fetch n + 2
@@ -457,16 +505,21 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
             if (n + 2 < nch) prefetch(n + 2);
         }
         __syncthreads();  // P complete
-        if (pout && vsl == 0) {
-            // hand P to the backward (packed lower tiles)
+        {
+            // hand P to the backward (packed lower tiles; slice 0 only)
             const int tr = threadIdx.x >> 2, J = threadIdx.x & 3;
-            tri_store_piece(pout + ((long)(slot0 + n) * H + h) * TRI_ELEMS, tr, J,
-                            *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + 16 * J),
+            const bool put = pout && vsl == 0;
+            tri_store_piece(out_rsrc(put ? pout + ((long)(slot0 + n) * H + h) * TRI_ELEMS : o,
+                                     put ? 2u * TRI_ELEMS : 0u),
+                            tr, J, *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + 16 * J),
                             *reinterpret_cast<const bf16x8*>(sm.P + tr * LDP + 16 * J + 8));
         }
         const bf16x8 vb0 = frag_from_c(vn[0], vn[1]), vb1 = frag_from_c(vn[2], vn[3]);
         // o^T = S^T Q^T + Vn^T P^T: tile tb holds (value 16w + 4g + i, token 16tb + r)
-        bf16* orow = o + (bos * H + h) * V + v0 + 16 * w + 4 * g;
+        // the chunk's output rows; lanes of rows past the sequence's end fall
+        // outside the resource
+        const __amdgpu_buffer_rsrc_t orr = out_rsrc(o + bos * H * V, 2u * (unsigned)len * H * V);
+        const unsigned ocol = 2u * (unsigned)(h * V + v0 + 16 * w + 4 * g);
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
             floatx4 acc = zero4();
@@ -476,9 +529,8 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
             acc = mma(vb0, frag_nat(sm.P, LDP, 16 * tb, 0), acc);
             if (tb >= 2) acc = mma(vb1, frag_nat(sm.P, LDP, 16 * tb, 32), acc);
             const int t = 16 * tb + r;
-            if (t < len)
-                *reinterpret_cast<bf16x4*>(orow + (long)t * H * V) =
-                    bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+            bstore8(bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]}, orr,
+                    2u * (unsigned)(t * H * V) + ocol);
         }
         // S <- S + K^T Vn; A rows follow the state's key map pim(fb, r)
 #pragma unroll
