@@ -21,8 +21,12 @@ cross-entropy (lm.hip).  torch provides memory and views.
 
 Parameters live in flat buffers: fp32 master weights, fp32 AdamW moments, a
 bf16 copy that the GEMMs read (each weight a contiguous view into it) and a
-bf16 gradient buffer the backward writes into, so the optimizer step is one
-``adamw_step_master`` launch over every parameter.
+bf16 gradient buffer the backward writes into.  ``update`` is one
+``adamw_step_master`` launch over every parameter; ``train_step`` instead
+updates each contiguous group of parameters (the LM head and final LayerNorm,
+each block, the embedding) on a second stream as soon as the backward has
+written its gradients, so the memory-bound optimizer runs beside the rest of
+the backward.  AdamW is elementwise: the results are bit-identical.
 """
 from __future__ import annotations
 
@@ -104,6 +108,13 @@ class EflaLM:
         self.embed_grad = torch.zeros(V, D, dtype=torch.float32, device=dev)
         self._ws = None
         self._ws_key = None
+        # contiguous parameter groups in the order the backward completes them
+        first = [self.offsets[f"l{i}.ln1.w"][0] for i in range(cfg.n_layers)]
+        first.append(self.offsets["lnf.w"][0])
+        self._groups = {"tail": (first[-1], off), "embed": (0, first[0])}
+        for i in range(cfg.n_layers):
+            self._groups[i] = (first[i], first[i + 1])
+        self._upd_stream = None
 
     # -- parameter views ------------------------------------------------------
     def _view(self, buf: torch.Tensor, name: str) -> torch.Tensor:
@@ -187,9 +198,30 @@ class EflaLM:
         return loss_rows.sum(), saved
 
     # -- backward -------------------------------------------------------------
-    def backward(self, saved) -> None:
-        """Gradients of the mean loss into self.grads (bf16) / self.embed_grad."""
+    def _update_group(self, key) -> None:
+        """AdamW over one contiguous parameter group on the update stream, after
+        everything the current stream has queued so far (its gradients)."""
         cfg = self.cfg
+        lo, hi = self._groups[key]
+        cur = torch.cuda.current_stream(self.device)
+        self._upd_stream.wait_stream(cur)
+        with torch.cuda.stream(self._upd_stream):
+            nn.adamw_step_master(self.master[lo:hi], self.grads[lo:hi], self.exp_avg[lo:hi],
+                                 self.exp_avg_sq[lo:hi], cfg.lr, cfg.beta1, cfg.beta2,
+                                 cfg.adam_eps, cfg.weight_decay, self.step_count,
+                                 param_bf16=self.weights[lo:hi])
+
+    def backward(self, saved, update: bool = False) -> None:
+        """Gradients of the mean loss into self.grads (bf16) / self.embed_grad;
+        with ``update`` also the AdamW step, group by group on the update stream
+        (the caller makes its stream wait for that one before reading the
+        weights again, as ``train_step`` does)."""
+        cfg = self.cfg
+        if update:
+            if self._upd_stream is None:
+                self._upd_stream = torch.cuda.Stream(self.device)
+            self.step_count += 1
+        upd = self._update_group if update else (lambda key: None)
         B, T = saved["tokens"].shape
         N, D, H, dh = B * T, cfg.d_model, cfg.n_heads, cfg.head_dim
         HD = H * dh
@@ -207,6 +239,7 @@ class EflaLM:
             daf, saved["x"], self.w("lnf.w"), saved["mf"], saved["rf"],
             out_dx_colsum=self.gr(f"l{top}.b_down") if top >= 0 else None,
             out_dw=self.gr("lnf.w"), out_db=self.gr("lnf.b"))
+        upd("tail")  # the LM head and final LayerNorm are read no more
         for i in reversed(range(cfg.n_layers)):
             L = f"l{i}."
             s = saved["layers"][i]
@@ -242,9 +275,11 @@ class EflaLM:
                 out_dx_colsum=self.gr(f"l{i - 1}.b_down") if i > 0 else None,
                 out_dw=self.gr(L + "ln1.w"), out_db=self.gr(L + "ln1.b"))
             saved["layers"][i] = None
+            upd(i)  # block i's gradients are complete (b_down's came from block i + 1)
         self.embed_grad.zero_()
         nn.embedding_backward(dx, saved["tokens"].reshape(-1), self.embed_grad)
         self.gr("embed").copy_(self.embed_grad)
+        upd("embed")
 
     # -- update ---------------------------------------------------------------
     def update(self) -> None:
@@ -256,10 +291,11 @@ class EflaLM:
                              self.step_count, param_bf16=self.weights)
 
     def train_step(self, tokens: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
-        """forwardStep, backwardStep, updateStep; returns the loss (device scalar)."""
+        """forwardStep, backwardStep, updateStep; returns the loss (device scalar).
+        The update runs group by group beside the backward (see ``backward``)."""
         loss, saved = self.forward(tokens, targets)
-        self.backward(saved)
-        self.update()
+        self.backward(saved, update=True)
+        torch.cuda.current_stream(self.device).wait_stream(self._upd_stream)
         return loss
 
 

@@ -165,3 +165,30 @@ def test_eval_forward_keeps_logits():
     assert abs(ref.item() - loss_e.item()) <= 1e-3 * abs(ref.item())
     # the training forward's rows hold dL/dlogits instead: each sums to ~0
     assert saved_t["dlogits"].float().sum(-1).abs().max().item() < 1e-2
+
+
+def test_overlapped_update_matches_single_launch():
+    """train_step's group-by-group AdamW on the update stream (beside the
+    backward) leaves master weights, moments and the bf16 copy bit-identical
+    to backward() followed by the single-launch update()."""
+    from ceo_amd.lm_step import EflaLM, synthetic_batch
+
+    announce("lm step: overlapped AdamW groups vs one launch")
+    cfg = _small()
+    cfg.lr = 3e-3
+    tokens, targets = synthetic_batch(cfg, 2, 128, seed=11)
+    runs = []
+    for overlap in (True, False):
+        model = EflaLM(cfg, seed=9)
+        for _ in range(3):
+            if overlap:
+                model.train_step(tokens, targets)
+            else:
+                _, saved = model.forward(tokens, targets)
+                model.backward(saved)
+                model.update()
+        torch.cuda.synchronize()
+        runs.append((model.master, model.exp_avg, model.exp_avg_sq, model.weights))
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+    assert not torch.equal(runs[0][0], EflaLM(cfg, seed=9).master)  # the steps did update
