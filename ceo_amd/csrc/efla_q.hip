@@ -964,7 +964,7 @@ static int run_fwd(const Problem& p, const T* q, const T* k, const T* v, const T
         EFLA_LAUNCH("efla_q_fwd_prep", (fast::prep_kernel<K>), dim3(H, p.slots),
                     dim3(fast::NT), st, k, beta, si, H, w.Tc, w.bc, w.dcc, p.ld.k);
         EFLA_LAUNCH("efla_q_fwd_scan", (fast::scan_o_kernel<K, V>),
-                    dim3(p.N * H * (V / fast::VS)), dim3(fast::NT), st, q, k, v, w.Tc, w.bc, si,
+                    dim3(p.N * H * (V / fast::VS)), dim3(fast::NTS), st, q, k, v, w.Tc, w.bc, si,
                     H, S0, ST, o, w.h, w.Pc, p.ld);
         return (int)hipPeekAtLastError();
     }
@@ -1015,7 +1015,7 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
         constexpr int NG = V <= 128 ? 4 : 2;
         if (reuse_states) {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, true>), scan_grid,
-                        dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        dim3(fast::NTS), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)w.Pc, si, H, dST, dS0, w.dh, p.ld);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true, NG>), grad_grid,
                         dim3(fast::grad_threads<NG>()), st, q, k, v, dO, (const bf16*)w.Tc,
@@ -1023,7 +1023,7 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
                         si, H, nitems, dq, dk, dv, dbeta, p.ld);
         } else {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, false>), scan_grid,
-                        dim3(fast::NT), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        dim3(fast::NTS), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)nullptr, si, H, dST, dS0, w.dh, p.ld);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false, NG>), grad_grid,
                         dim3(fast::grad_threads<NG>()), st, q, k, v, dO, (const bf16*)w.Tc,

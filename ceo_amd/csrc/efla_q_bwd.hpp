@@ -42,21 +42,6 @@ using mf::frag_tr;
 using mf::frag_trc;
 using mf::tr_rows4;
 
-constexpr int LD64 = ldb<64>();
-
-// A packed lower-triangular matrix (tri_off) straight into a [64][LD64] LDS
-// tile, as mf::dma_tile copies a full one: every 16-byte LDS chunk is written,
-// the upper and pad chunks from the zero stub.
-template <int NW>
-__device__ __forceinline__ void dma_tri(bf16* lds, const bf16* src, int rot, int l) {
-    constexpr int CPR = LD64 / 8, NI = 64 * CPR / 64;
-    const int w = mf::wave();
-    for (int i = (w + NW - rot % NW) % NW; i < NI; i += NW) {
-        const int c = 64 * i + l, row = c / CPR, col = c - row * CPR;
-        mf::dma16(src, (unsigned)(col < 8 ? tri_off(row, col) : TRI_ZERO) * 2u, lds + 512 * i);
-    }
-}
-
 __device__ __forceinline__ void store4s(bf16* p, floatx4 a, float s) {
     *reinterpret_cast<bf16x4*>(p) =
         bf16x4{(bf16)(a[0] * s), (bf16)(a[1] * s), (bf16)(a[2] * s), (bf16)(a[3] * s)};
@@ -171,16 +156,19 @@ struct ScanDhSmem {
     bf16 P[PS ? 8 : 64 * LD64];  // P [t][t'] computed here (not PS)
 };
 
+// Waves 0..3 compute, waves 4..7 write chunk n - 1 into LDS during chunk n
+// (as in scan_o_kernel, one register set: more loads in flight measured
+// slower here).
 template <int K, int V, bool PS>
-__global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
-                                                     const bf16* __restrict__ k,
-                                                     const bf16* __restrict__ dO,
-                                                     const bf16* __restrict__ Tc,
-                                                     const float* __restrict__ bc,
-                                                     const bf16* __restrict__ Pc, SeqInfo si,
-                                                     int H, const float* __restrict__ dST,
-                                                     float* __restrict__ dS0,
-                                                     bf16* __restrict__ dhist, TokLd ld) {
+__global__ void __launch_bounds__(NTS) scan_dh_kernel(const bf16* __restrict__ q,
+                                                      const bf16* __restrict__ k,
+                                                      const bf16* __restrict__ dO,
+                                                      const bf16* __restrict__ Tc,
+                                                      const float* __restrict__ bc,
+                                                      const bf16* __restrict__ Pc, SeqInfo si,
+                                                      int H, const float* __restrict__ dST,
+                                                      float* __restrict__ dS0,
+                                                      bf16* __restrict__ dhist, TokLd ld) {
     constexpr int LDK = ldb<K>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanDhSmem<K, PS> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
@@ -192,6 +180,40 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
     int slot0;
     seq_bounds(si, seq, sbos, slen, slot0);
     const int nch = (int)((slen + 63) / 64);
+    if (w >= NCW) {  // copy waves: chunk n - 1 into buf[(n - 1) & 1] during chunk n
+        const int ct = (int)threadIdx.x - NT;
+        struct Regs {
+            ChunkRegs<K, true, true> c;
+            mf::TileRegs<64, 64, NT> p;  // PS: the chunk's P
+        };
+        // chunk n's loads (clamped to chunk 0, so every iteration issues the
+        // same loads and the staging's waits stay exact)
+        auto load = [&](Regs& R, int n) {
+            n = max(n, 0);
+            const long bos = sbos + (long)n * 64;
+            const int len = (int)min((long)64, slen - (long)n * 64);
+            const long cid = (long)(slot0 + n) * H + h;
+            R.c.load(q, k, dO, Tc, bc, bos, len, h, V, v0, cid, ld.q, ld.k, (long)H * V, ct);
+            if constexpr (PS) load_tri(R.p, Pc + cid * TRI_ELEMS, ct);
+        };
+        auto stage = [&](Regs& R, ScanDhBuf<K, PS>& bf) {
+            R.c.stage(bf);
+            if constexpr (PS) R.p.store_rows(bf.P, LD64);
+        };
+        Regs ra;
+        if (nch > 0) {
+            load(ra, nch - 1);
+            stage(ra, sm.buf[(nch - 1) & 1]);
+            load(ra, nch - 2);
+        }
+        for (int n = nch - 1; n >= 0; --n) {
+            __syncthreads();  // chunk n staged; everyone is done with chunk n + 1
+            if (n > 0) stage(ra, sm.buf[(n - 1) & 1]);
+            load(ra, n - 2);
+            if constexpr (!PS) __syncthreads();  // the compute waves' P complete
+        }
+        return;
+    }
     const long sbase = (long)bh * K * V;
     const int vcol = v0 + 16 * w + r;
     floatx4 dS[K / 16];
@@ -206,24 +228,6 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
     }
     if constexpr (!PS)
         for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;
-    ChunkRegs<K, true, true> pre;
-    mf::TileRegs<64, 64, NT> rp;  // PS: the chunk's P
-    auto prefetch = [&](int n) {
-        const long bos = sbos + (long)n * 64;
-        const int len = (int)min((long)64, slen - (long)n * 64);
-        const long cid = (long)(slot0 + n) * H + h;
-        pre.load(q, k, dO, Tc, bc, bos, len, h, V, v0, cid, ld.q, ld.k, (long)H * V);
-        if constexpr (PS) load_tri(rp, Pc + cid * TRI_ELEMS);
-    };
-    auto stage = [&](ScanDhBuf<K, PS>& bf) {
-        pre.stage(bf);
-        if constexpr (PS) rp.store_rows(bf.P, LD64);
-    };
-    if (nch > 0) {
-        prefetch(nch - 1);
-        stage(sm.buf[(nch - 1) & 1]);
-        if (nch > 1) prefetch(nch - 2);
-    }
     for (int n = nch - 1; n >= 0; --n) {
         const ScanDhBuf<K, PS>& cb = sm.buf[n & 1];
         const bf16* Pm = PS ? cb.P : sm.P;
@@ -258,10 +262,6 @@ __global__ void __launch_bounds__(NT) scan_dh_kernel(const bf16* __restrict__ q,
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb) acc = mma(frag_row(cb.Kr, LDK, row, 32 * kb), sb[kb], acc);
             dvn[tb] = acc;
-        }
-        if (n > 0) {
-            stage(sm.buf[(n - 1) & 1]);
-            if (n > 1) prefetch(n - 2);
         }
         if constexpr (!PS) __syncthreads();  // P complete
 #pragma unroll

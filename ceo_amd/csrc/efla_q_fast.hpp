@@ -121,12 +121,28 @@ __device__ __forceinline__ void tri_store_piece(__amdgpu_buffer_rsrc_t r, int ro
 // A packed matrix into the registers of a 64 x 64 tile loader, as
 // TileRegs::load would hold the full matrix (upper pieces read as zeros).
 template <int NT>
-__device__ __forceinline__ void load_tri(mf::TileRegs<64, 64, NT>& r, const bf16* __restrict__ src) {
-    r.tid = (int)threadIdx.x;
+__device__ __forceinline__ void load_tri(mf::TileRegs<64, 64, NT>& r, const bf16* __restrict__ src,
+                                         int thread = (int)threadIdx.x) {
+    r.tid = thread;
     r.valid = 64;
     const int f = r.fg(), t = r.t0();
 #pragma unroll
     for (int j = 0; j < r.TPT; ++j) r.x[j] = *reinterpret_cast<const bf16x8*>(src + tri_off(t + j, f));
+}
+
+constexpr int LD64 = ldb<64>();
+
+// A packed lower-triangular matrix (tri_off) straight into a [64][LD64] LDS
+// tile, as mf::dma_tile copies a full one: every 16-byte LDS chunk is written,
+// the upper and pad chunks from the zero stub.
+template <int NW>
+__device__ __forceinline__ void dma_tri(bf16* lds, const bf16* src, int rot, int l) {
+    constexpr int CPR = LD64 / 8, NI = 64 * CPR / 64;
+    const int w = mf::wave();
+    for (int i = (w + NW - rot % NW) % NW; i < NI; i += NW) {
+        const int c = 64 * i + l, row = c / CPR, col = c - row * CPR;
+        mf::dma16(src, (unsigned)(col < 8 ? tri_off(row, col) : TRI_ZERO) * 2u, lds + 512 * i);
+    }
 }
 
 __device__ __forceinline__ void store4(bf16* p, floatx4 a) {
@@ -355,16 +371,18 @@ struct ChunkRegs {
     mf::TileRegs<64, K, NT> rq, rk;
     mf::TileRegs<64, VS, NT> rv;  // v (VALUES) or dO slice
     mf::TileRegs<64, 64, NT> rt;
-    float b;                      // thread < 64: b of token threadIdx.x
+    float b;                      // b of token thread & 63
+    int thread;                   // index among the NT threads that load and stage
     __device__ __forceinline__ void load(const bf16* q, const bf16* k, const bf16* vsl,
                                          const bf16* Tc, const float* bc, long bos, int len,
                                          int h, int V, int v0, long cid, long lq, long lk,
-                                         long lv) {
-        if (WITH_Q) rq.load(q + bos * lq + (long)h * K, lq, len);
-        rk.load(k + bos * lk + (long)h * K, lk, len);
-        rv.load(vsl + bos * lv + (long)h * V + v0, lv, len);
-        load_tri(rt, Tc + cid * TRI_ELEMS);
-        b = bc[cid * 64 + (threadIdx.x & 63)];  // every lane: no branch around the load
+                                         long lv, int th = (int)threadIdx.x) {
+        thread = th;
+        if (WITH_Q) rq.load(q + bos * lq + (long)h * K, lq, len, th);
+        rk.load(k + bos * lk + (long)h * K, lk, len, th);
+        rv.load(vsl + bos * lv + (long)h * V + v0, lv, len, th);
+        load_tri(rt, Tc + cid * TRI_ELEMS, th);
+        b = bc[cid * 64 + (th & 63)];  // every lane: no branch around the load
     }
     template <typename Buf>
     __device__ __forceinline__ void stage(Buf& bf) {
@@ -372,7 +390,7 @@ struct ChunkRegs {
         rk.store_rows(bf.Kr, ldb<K>());
         rv.store_rows(bf.Vs, ldb<VS>());
         rt.store_rows(bf.T, ldb<64>());
-        if (threadIdx.x < 64) bf.b[threadIdx.x] = b;
+        bf.b[thread & 63] = b;  // every lane (the same values): no branch around the write
     }
 };
 
@@ -410,17 +428,27 @@ __device__ __forceinline__ void chunk_vn(const Buf& cb, int w, const bf16x8* sb,
     }
 }
 
+// Scan workgroups with copy waves: waves 0..3 compute (NT threads), waves
+// 4..7 load the inputs of the next chunks into registers and write them to
+// the chunk's LDS buffer while the compute waves work on the current one, so
+// no compute wave waits for a load or spends time staging.  Both kinds pass
+// the same barriers per chunk.  Two waves per SIMD: the kernel's registers
+// stay at 256 per lane or fewer (launch bounds).  Copies straight into LDS
+// (global_load_lds) by the copy waves measured slower than the register path.
+constexpr int NTS = 2 * NT;
+constexpr int NCW = NT / 64;  // copy waves
+
 template <int K, int V>
-__global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
-                                                    const bf16* __restrict__ k,
-                                                    const bf16* __restrict__ v,
-                                                    const bf16* __restrict__ Tc,
-                                                    const float* __restrict__ bc, SeqInfo si,
-                                                    int H, const float* __restrict__ S0,
-                                                    float* __restrict__ ST,
-                                                    bf16* __restrict__ o,
-                                                    bf16* __restrict__ hist,
-                                                    bf16* __restrict__ pout, TokLd ld) {
+__global__ void __launch_bounds__(NTS) scan_o_kernel(const bf16* __restrict__ q,
+                                                     const bf16* __restrict__ k,
+                                                     const bf16* __restrict__ v,
+                                                     const bf16* __restrict__ Tc,
+                                                     const float* __restrict__ bc, SeqInfo si,
+                                                     int H, const float* __restrict__ S0,
+                                                     float* __restrict__ ST,
+                                                     bf16* __restrict__ o,
+                                                     bf16* __restrict__ hist,
+                                                     bf16* __restrict__ pout, TokLd ld) {
     constexpr int LDK = ldb<K>(), LDP = ldb<64>(), NVS = V / VS;
     __shared__ __attribute__((aligned(16))) ScanSmem<K> sm;
     const int w = mf::wave(), l = mf::lane(), g = l >> 4, r = l & 15;
@@ -432,6 +460,40 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
     int slot0;
     seq_bounds(si, seq, sbos, slen, slot0);
     const int nch = (int)((slen + 63) / 64);
+    if (w >= NCW) {
+        // copy waves: two register sets, ra and rb, each a chunk ahead of the
+        // other; chunk n + 1 is written to buf[(n + 1) & 1] during chunk n,
+        // while chunk n + 2's loads are still in flight
+        const int ct = (int)threadIdx.x - NT;
+        // chunk n's loads (clamped to the last chunk, so every iteration
+        // issues the same loads and the staging's waits stay exact)
+        auto load = [&](ChunkRegs<K, true, true>& R, int n) {
+            n = min(n, nch - 1);
+            const long bos = sbos + (long)n * 64;
+            const int len = (int)min((long)64, slen - (long)n * 64);
+            R.load(q, k, v, Tc, bc, bos, len, h, V, v0, (long)(slot0 + n) * H + h, ld.q, ld.k,
+                   ld.v, ct);
+        };
+        ChunkRegs<K, true, true> ra, rb;
+        if (nch > 0) {
+            load(ra, 0);
+            ra.stage(sm.buf[0]);
+            load(ra, 1);
+            load(rb, 2);
+        }
+        for (int n = 0; n < nch; n += 2) {  // ra holds chunk n + 1, rb chunk n + 2
+            __syncthreads();  // chunk n staged; everyone is done with chunk n - 1
+            if (n + 1 < nch) ra.stage(sm.buf[(n + 1) & 1]);
+            load(ra, n + 3);
+            __syncthreads();  // the compute waves' P complete
+            if (n + 1 >= nch) break;
+            __syncthreads();  // chunk n + 1 staged
+            if (n + 2 < nch) rb.stage(sm.buf[n & 1]);
+            load(rb, n + 4);
+            __syncthreads();
+        }
+        return;
+    }
     const long sbase = (long)bh * K * V;
     const int vcol = v0 + 16 * w + r;  // this lane's state column
     floatx4 S[K / 16];
@@ -449,29 +511,6 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
     }
     for (int i = threadIdx.x; i < 64 * LDP; i += NT) sm.P[i] = (bf16)0.f;
 
-    ChunkRegs<K, true, true> pre;
-    auto prefetch = [&](int n) {
-        const long bos = sbos + (long)n * 64;
-        const int len = (int)min((long)64, slen - (long)n * 64);
-        pre.load(q, k, v, Tc, bc, bos, len, h, V, v0, (long)(slot0 + n) * H + h, ld.q, ld.k,
-                 ld.v);
-    };
-    if (nch > 0) {
-        prefetch(0);
-        pre.stage(sm.buf[0]);
-        if (nch > 1) prefetch(1);
-    }
-    {
-        // as many stores as a chunk issues after its prefetch (P hand-over,
-        // output rows), all dropped: the loop is entered with the same count
-        // of stores behind the prefetch as each iteration leaves, so the
-        // staging's waits need not drain the previous chunk's stores
-        const __amdgpu_buffer_rsrc_t none = out_rsrc(o, 0u);
-        bstore16(bf16x8{}, none, 0u);
-        bstore16(bf16x8{}, none, 16u);
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) bstore8(bf16x4{}, none, 8u * tb);
-    }
     for (int n = 0; n < nch; ++n) {
         const long bos = sbos + (long)n * 64;
         const int len = (int)min((long)64, slen - (long)n * 64);
@@ -499,11 +538,6 @@ __global__ void __launch_bounds__(NT) scan_o_kernel(const bf16* __restrict__ q,
                             sb, vcol);
         floatx4 vn[4];
         chunk_vn<K>(cb, w, sb, vn);
-        // stage chunk n + 1 (its loads were issued one chunk ago), fetch n + 2
-        if (n + 1 < nch) {
-            pre.stage(sm.buf[(n + 1) & 1]);
-            if (n + 2 < nch) prefetch(n + 2);
-        }
         __syncthreads();  // P complete
         {
             // hand P to the backward (packed lower tiles; slice 0 only)
