@@ -1015,7 +1015,7 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
         constexpr int NG = V <= 128 ? 4 : 2;
         if (reuse_states) {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, true>), scan_grid,
-                        dim3(fast::NTS), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        dim3(fast::dh_threads<K>()), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)w.Pc, si, H, dST, dS0, w.dh, p.ld);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, true, NG>), grad_grid,
                         dim3(fast::grad_threads<NG>()), st, q, k, v, dO, (const bf16*)w.Tc,
@@ -1023,7 +1023,7 @@ static int run_bwd(const Problem& p, const T* q, const T* k, const T* v, const T
                         si, H, nitems, dq, dk, dv, dbeta, p.ld);
         } else {
             EFLA_LAUNCH("efla_q_bwd_state", (fast::scan_dh_kernel<K, V, false>), scan_grid,
-                        dim3(fast::NTS), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
+                        dim3(fast::dh_threads<K>()), st, q, k, dO, (const bf16*)w.Tc, (const float*)w.bc,
                         (const bf16*)nullptr, si, H, dST, dS0, w.dh, p.ld);
             EFLA_LAUNCH("efla_q_bwd_grad", (fast::grad_kernel<K, V, false, NG>), grad_grid,
                         dim3(fast::grad_threads<NG>()), st, q, k, v, dO, (const bf16*)w.Tc,

@@ -156,11 +156,20 @@ struct ScanDhSmem {
     bf16 P[PS ? 8 : 64 * LD64];  // P [t][t'] computed here (not PS)
 };
 
-// Waves 0..3 compute, waves 4..7 write chunk n - 1 into LDS during chunk n
-// (as in scan_o_kernel, one register set: more loads in flight measured
-// slower here).
+// d_k = 128: waves 0..3 compute, waves 4..7 write chunk n - 1 into LDS during
+// chunk n (as in scan_o_kernel, one register set: more loads in flight
+// measured slower here).  d_k = 64: four waves that also stage the next
+// chunk themselves (copy waves measured 1.14x slower at that size).
+template <int K>
+constexpr bool dh_copy_waves() {
+    return K > 64;
+}
+template <int K>
+constexpr int dh_threads() {
+    return dh_copy_waves<K>() ? NTS : NT;
+}
 template <int K, int V, bool PS>
-__global__ void __launch_bounds__(NTS) scan_dh_kernel(const bf16* __restrict__ q,
+__global__ void __launch_bounds__(dh_threads<K>()) scan_dh_kernel(const bf16* __restrict__ q,
                                                       const bf16* __restrict__ k,
                                                       const bf16* __restrict__ dO,
                                                       const bf16* __restrict__ Tc,
@@ -180,7 +189,8 @@ __global__ void __launch_bounds__(NTS) scan_dh_kernel(const bf16* __restrict__ q
     int slot0;
     seq_bounds(si, seq, sbos, slen, slot0);
     const int nch = (int)((slen + 63) / 64);
-    if (w >= NCW) {  // copy waves: chunk n - 1 into buf[(n - 1) & 1] during chunk n
+    constexpr bool CW = dh_copy_waves<K>();
+    if (CW && w >= NCW) {  // copy waves: chunk n - 1 into buf[(n - 1) & 1] during chunk n
         const int ct = (int)threadIdx.x - NT;
         struct Regs {
             ChunkRegs<K, true, true> c;
@@ -228,6 +238,26 @@ __global__ void __launch_bounds__(NTS) scan_dh_kernel(const bf16* __restrict__ q
     }
     if constexpr (!PS)
         for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;
+    // without copy waves: chunk n - 1 staged from registers during chunk n,
+    // chunk n - 2's loads issued right after
+    ChunkRegs<K, true, true> pre;
+    mf::TileRegs<64, 64, NT> rp;  // PS: the chunk's P
+    auto prefetch = [&](int n) {
+        const long bos = sbos + (long)n * 64;
+        const int len = (int)min((long)64, slen - (long)n * 64);
+        const long cid = (long)(slot0 + n) * H + h;
+        pre.load(q, k, dO, Tc, bc, bos, len, h, V, v0, cid, ld.q, ld.k, (long)H * V);
+        if constexpr (PS) load_tri(rp, Pc + cid * TRI_ELEMS);
+    };
+    auto stage = [&](ScanDhBuf<K, PS>& bf) {
+        pre.stage(bf);
+        if constexpr (PS) rp.store_rows(bf.P, LD64);
+    };
+    if (!CW && nch > 0) {
+        prefetch(nch - 1);
+        stage(sm.buf[(nch - 1) & 1]);
+        if (nch > 1) prefetch(nch - 2);
+    }
     for (int n = nch - 1; n >= 0; --n) {
         const ScanDhBuf<K, PS>& cb = sm.buf[n & 1];
         const bf16* Pm = PS ? cb.P : sm.P;
@@ -262,6 +292,10 @@ __global__ void __launch_bounds__(NTS) scan_dh_kernel(const bf16* __restrict__ q
 #pragma unroll
             for (int kb = 0; kb < K / 32; ++kb) acc = mma(frag_row(cb.Kr, LDK, row, 32 * kb), sb[kb], acc);
             dvn[tb] = acc;
+        }
+        if (!CW && n > 0) {
+            stage(sm.buf[(n - 1) & 1]);
+            if (n > 1) prefetch(n - 2);
         }
         if constexpr (!PS) __syncthreads();  // P complete
 #pragma unroll
