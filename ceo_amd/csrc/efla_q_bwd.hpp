@@ -152,9 +152,32 @@ struct ScanDhBuf {
 
 template <int K, bool PS>
 struct ScanDhSmem {
-    ScanDhBuf<K, PS> buf[2];     // chunk n in buf[n & 1]
-    bf16 P[PS ? 8 : 64 * LD64];  // P [t][t'] computed here (not PS)
+    ScanDhBuf<K, PS> buf[2];  // chunk n in buf[n & 1]
+    // P [t][t'] computed here (not PS): with copy waves chunk n's in P + (n & 1) *
+    // 64 * LD64, formed by the copy waves during chunk n + 1
+    bf16 P[PS ? 8 : (K > 64 ? 2 : 1) * 64 * LD64];
 };
+
+// P = tril(Q K^T) of a staged chunk into P [t][t'] (row stride LD64): lower
+// 16x16 tiles nt0, nt0 + 4, ... of 10 (I = t block, J = t' block), computed
+// transposed so each lane writes 4 consecutive t'; upper tiles untouched.
+template <int K, typename Buf>
+__device__ __forceinline__ void chunk_p_tiles(const Buf& cb, bf16* P, int nt0) {
+    constexpr int LDK = ldb<K>();
+    const int l = mf::lane(), g = l >> 4, r = l & 15;
+    for (int nt = nt0; nt < 10; nt += 4) {
+        int I, J;
+        lower_tile(nt, I, J);
+        floatx4 acc = zero4();
+#pragma unroll
+        for (int k0 = 0; k0 < K; k0 += 32)
+            acc = mma(frag_nat(cb.Kr, LDK, 16 * J, k0), frag_nat(cb.Q, LDK, 16 * I, k0), acc);
+        const int tq = 16 * I + r, tk = 16 * J + 4 * g;
+        *reinterpret_cast<bf16x4*>(P + tq * LD64 + tk) =
+            bf16x4{(bf16)(tk + 0 <= tq ? acc[0] : 0.f), (bf16)(tk + 1 <= tq ? acc[1] : 0.f),
+                   (bf16)(tk + 2 <= tq ? acc[2] : 0.f), (bf16)(tk + 3 <= tq ? acc[3] : 0.f)};
+    }
+}
 
 // d_k = 128: waves 0..3 compute, waves 4..7 write chunk n - 1 into LDS during
 // chunk n (as in scan_o_kernel, one register set: more loads in flight
@@ -210,17 +233,28 @@ __global__ void __launch_bounds__(dh_threads<K>()) scan_dh_kernel(const bf16* __
             R.c.stage(bf);
             if constexpr (PS) R.p.store_rows(bf.P, LD64);
         };
+        // not PS: the copy waves also form each chunk's P once it is staged
+        auto ptiles = [&](int m) {
+            chunk_p_tiles<K>(sm.buf[m & 1], sm.P + (m & 1) * 64 * LD64, w - NCW);
+        };
         Regs ra;
         if (nch > 0) {
             load(ra, nch - 1);
             stage(ra, sm.buf[(nch - 1) & 1]);
             load(ra, nch - 2);
+            if constexpr (!PS) {
+                __syncthreads();  // chunk nch - 1 staged
+                ptiles(nch - 1);
+            }
         }
         for (int n = nch - 1; n >= 0; --n) {
             __syncthreads();  // chunk n staged; everyone is done with chunk n + 1
             if (n > 0) stage(ra, sm.buf[(n - 1) & 1]);
             load(ra, n - 2);
-            if constexpr (!PS) __syncthreads();  // the compute waves' P complete
+            if constexpr (!PS) {
+                __syncthreads();  // chunk n - 1 staged
+                if (n > 0) ptiles(n - 1);
+            }
         }
         return;
     }
@@ -236,8 +270,10 @@ __global__ void __launch_bounds__(dh_threads<K>()) scan_dh_kernel(const bf16* __
             for (int i = 0; i < 4; ++i) dS[fb][i] = dST[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
         mf::dma_wait();  // retired here, not by a vmcnt(0) inside the chunk loop
     }
-    if constexpr (!PS)
-        for (int i = threadIdx.x; i < 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;
+    if constexpr (!PS) {
+        for (int i = threadIdx.x; i < (CW ? 2 : 1) * 64 * LD64; i += NT) sm.P[i] = (bf16)0.f;
+        if (CW && nch > 0) __syncthreads();  // zeros in place before the copy waves' P tiles
+    }
     // without copy waves: chunk n - 1 staged from registers during chunk n,
     // chunk n - 2's loads issued right after
     ChunkRegs<K, true, true> pre;
@@ -260,22 +296,9 @@ __global__ void __launch_bounds__(dh_threads<K>()) scan_dh_kernel(const bf16* __
     }
     for (int n = nch - 1; n >= 0; --n) {
         const ScanDhBuf<K, PS>& cb = sm.buf[n & 1];
-        const bf16* Pm = PS ? cb.P : sm.P;
+        const bf16* Pm = PS ? cb.P : sm.P + (CW ? (n & 1) * 64 * LD64 : 0);
         __syncthreads();  // chunk n staged; everyone is done with chunk n + 1
-        if constexpr (!PS) {
-            for (int nt = w; nt < 10; nt += 4) {
-                int I, J;
-                lower_tile(nt, I, J);
-                floatx4 acc = zero4();
-#pragma unroll
-                for (int k0 = 0; k0 < K; k0 += 32)
-                    acc = mma(frag_nat(cb.Kr, LDK, 16 * J, k0), frag_nat(cb.Q, LDK, 16 * I, k0), acc);
-                const int tq = 16 * I + r, tk = 16 * J + 4 * g;
-                *reinterpret_cast<bf16x4*>(sm.P + tq * LD64 + tk) =
-                    bf16x4{(bf16)(tk + 0 <= tq ? acc[0] : 0.f), (bf16)(tk + 1 <= tq ? acc[1] : 0.f),
-                           (bf16)(tk + 2 <= tq ? acc[2] : 0.f), (bf16)(tk + 3 <= tq ? acc[3] : 0.f)};
-            }
-        }
+        if (!PS && !CW) chunk_p_tiles<K>(cb, sm.P, w);
         bf16x8 sb[K / 32];
 #pragma unroll
         for (int kb = 0; kb < K / 32; ++kb) sb[kb] = frag_from_c(dS[2 * kb], dS[2 * kb + 1]);
@@ -297,7 +320,9 @@ __global__ void __launch_bounds__(dh_threads<K>()) scan_dh_kernel(const bf16* __
             stage(sm.buf[(n - 1) & 1]);
             if (n > 1) prefetch(n - 2);
         }
-        if constexpr (!PS) __syncthreads();  // P complete
+        // not PS: P complete (without copy waves); chunk n - 1 staged for the
+        // copy waves' P tiles (with them)
+        if constexpr (!PS) __syncthreads();
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
             const int c0 = 32 * (tb >> 1) + 4 * (tb & 1);
