@@ -13,7 +13,8 @@
 //   diagonal) and fp32 b [64].
 // scan_o_kernel (grid: sequences x H x V/64, one 64-wide value slice each)
 //   carries S[:, slice] (K x 64, fp32) through the chunks of one sequence in
-//   MFMA accumulators (wave w owns value columns 16w..16w+15) and per chunk
+//   MFMA accumulators (compute wave w owns value columns 16w..16w+15; four
+//   more waves stage the next chunks' inputs in LDS) and per chunk
 //     R = V - K S,  Vn = T D R,  o = Q S + tril(Q K^T) Vn,  S <- S + K^T Vn;
 //   optionally writes each chunk's start state to `hist` (bf16 [chunk][head]
 //   [v][f], as the backward reads it) so the backward need not recompute it.
@@ -506,7 +507,7 @@ __global__ void __launch_bounds__(NTS) scan_o_kernel(const bf16* __restrict__ q,
             for (int i = 0; i < 4; ++i) S[fb][i] = S0[sbase + (long)pim(fb, 4 * g + i) * V + vcol];
         // retire these loads here: left pending, their waits land inside the
         // chunk loop as vmcnt(0), which every chunk would then pay for the
-        // next chunk's prefetch and the last chunk's stores
+        // previous chunk's stores
         mf::dma_wait();
     }
     for (int i = threadIdx.x; i < 64 * LDP; i += NT) sm.P[i] = (bf16)0.f;
