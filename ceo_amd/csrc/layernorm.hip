@@ -16,9 +16,12 @@
 // to 2048 the rows of x and dy stay in registers (16-byte loads, one HBM pass)
 // and each lane accumulates dw/db for its own columns in registers across its
 // rows; the 4 waves of a workgroup combine theirs in LDS and write one partial
-// row.  Other widths loop over the row and accumulate with LDS atomics.  A
-// second kernel sums the per-workgroup partials, 16 row groups per column
-// block (D <= 8192 when dw/db are wanted).
+// row.  Other widths loop over the row; up to D = 2048 each wave accumulates
+// dw/db in an LDS slice of its own (a column belongs to one lane of the wave)
+// and the four slices are added in wave order, so the sums do not depend on
+// timing; wider rows accumulate with LDS atomics (order-dependent in the last
+// bits).  A second kernel sums the per-workgroup partials, 16 row groups per
+// column block (D <= 8192 when dw/db are wanted).
 #include <hip/hip_runtime.h>
 
 #include "../../include/efla_hip.h"
@@ -122,8 +125,10 @@ __global__ void __launch_bounds__(NTH) fwd_loop_kernel(const bf16* __restrict__ 
     }
 }
 
-// dx per row; dw/db partials per workgroup in LDS (2*D floats), written to
-// part[blockIdx.x][0..D) (dw) and part[blockIdx.x][D..2D) (db).
+// dx per row; dw/db partials per workgroup in LDS, written to
+// part[blockIdx.x][0..D) (dw) and part[blockIdx.x][D..2D) (db): per wave
+// (4 * 2D floats, added in wave order) when per_wave, else one 2D block
+// updated with atomics.
 __global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
                                                   const bf16* __restrict__ x,
                                                   const bf16* __restrict__ w,
@@ -132,11 +137,13 @@ __global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
                                                   const bf16* __restrict__ res,
                                                   bf16* __restrict__ dx,
                                                   float* __restrict__ part, long rows, int D,
-                                                  int want_params) {
-    extern __shared__ float acc[];  // 2*D when want_params
+                                                  int want_params, int per_wave) {
+    extern __shared__ float acc[];  // 2*D (4 * 2*D per_wave) when want_params
     const int lane = lane_id();
+    const int nacc = per_wave ? (NTH / kWave) * 2 * D : 2 * D;
+    float* wacc = acc + (per_wave ? wave_id() * 2 * D : 0);
     if (want_params)
-        for (int i = threadIdx.x; i < 2 * D; i += NTH) acc[i] = 0.f;
+        for (int i = threadIdx.x; i < nacc; i += NTH) acc[i] = 0.f;
     __syncthreads();
     const long waves = (long)gridDim.x * (NTH / kWave);
     for (long row = (long)blockIdx.x * (NTH / kWave) + wave_id(); row < rows; row += waves) {
@@ -160,15 +167,25 @@ __global__ void __launch_bounds__(NTH) bwd_kernel(const bf16* __restrict__ dy,
             const float add = res ? (float)res[row * D + c] : 0.f;
             dxr[c] = (bf16)(rs * (g - sg - xh * sgx) + add);
             if (want_params) {
-                atomicAdd(&acc[c], gy * xh);
-                atomicAdd(&acc[D + c], gy);
+                if (per_wave) {  // column c is this lane's alone within the wave
+                    wacc[c] += gy * xh;
+                    wacc[D + c] += gy;
+                } else {
+                    atomicAdd(&acc[c], gy * xh);
+                    atomicAdd(&acc[D + c], gy);
+                }
             }
         }
     }
     if (!want_params) return;
     __syncthreads();
     float* pr = part + (long)blockIdx.x * 2 * D;
-    for (int i = threadIdx.x; i < 2 * D; i += NTH) pr[i] = acc[i];
+    for (int i = threadIdx.x; i < 2 * D; i += NTH) {
+        float v = acc[i];
+        if (per_wave)
+            for (int ww = 1; ww < NTH / kWave; ++ww) v += acc[ww * 2 * D + i];
+        pr[i] = v;
+    }
 }
 
 // Register-resident backward for D = NV * 512 (NV <= 4): lane owns columns
@@ -447,10 +464,14 @@ static int ln_backward(const void* grad_output, const void* input, const void* w
         LN_BWD_CASE(1, 3) LN_BWD_CASE(2, 3) LN_BWD_CASE(3, 3) LN_BWD_CASE(4, 3)
 #undef LN_BWD_CASE
         default: {
-            const size_t smem = params ? 2 * D * sizeof(float) : 0;
+            // per-wave dw/db slices (timing-independent sums) while they fit
+            // in 64 KB of LDS
+            const bool per_wave = params && D <= 2048;
+            const size_t smem =
+                params ? (per_wave ? (ln::NTH / kWave) : 1) * 2 * D * sizeof(float) : 0;
             ::efla::ProfScope ps("layernorm_bwd_loop", stream);
             hipLaunchKernelGGL(ln::bwd_kernel, grid, block, smem, stream, g, x, w, mean, rstd, res,
-                               dx, part, (long)rows, (int)D, params ? 1 : 0);
+                               dx, part, (long)rows, (int)D, params ? 1 : 0, per_wave ? 1 : 0);
         }
     }
     EFLA_CHECK(hipPeekAtLastError());

@@ -151,11 +151,17 @@ __global__ void __launch_bounds__(NTH) bwd_loop_kernel(const bf16* __restrict__ 
                                                        const bf16* __restrict__ w,
                                                        bf16* __restrict__ dx,
                                                        float* __restrict__ part, long rows,
-                                                       int D, float eps, int want_w) {
-    extern __shared__ float acc[];  // D when want_w
+                                                       int D, float eps, int want_w,
+                                                       int per_wave) {
+    // dw partials: one D-float slice per wave (column c belongs to one lane of
+    // the wave; the slices are added in wave order, so the sums do not depend
+    // on timing) when per_wave, else one slice updated with atomics
+    extern __shared__ float acc[];
     const int lane = lane_id();
+    const int nacc = per_wave ? RPB * D : D;
+    float* wacc = acc + (per_wave ? wave_id() * D : 0);
     if (want_w)
-        for (int i = threadIdx.x; i < D; i += NTH) acc[i] = 0.f;
+        for (int i = threadIdx.x; i < nacc; i += NTH) acc[i] = 0.f;
     __syncthreads();
     const long waves = (long)gridDim.x * RPB;
     for (long row = (long)blockIdx.x * RPB + wave_id(); row < rows; row += waves) {
@@ -172,12 +178,22 @@ __global__ void __launch_bounds__(NTH) bwd_loop_kernel(const bf16* __restrict__ 
         for (int c = lane; c < D; c += kWave) {
             const float xf = (float)xr[c], gy = (float)gr[c];
             dx[row * D + c] = (bf16)(rs * gy * (float)w[c] - xf * c2);
-            if (want_w) atomicAdd(&acc[c], gy * xf * rs);
+            if (want_w) {
+                if (per_wave)
+                    wacc[c] += gy * xf * rs;
+                else
+                    atomicAdd(&acc[c], gy * xf * rs);
+            }
         }
     }
     if (!want_w) return;
     __syncthreads();
-    for (int i = threadIdx.x; i < D; i += NTH) part[(long)blockIdx.x * D + i] = acc[i];
+    for (int i = threadIdx.x; i < D; i += NTH) {
+        float v = acc[i];
+        if (per_wave)
+            for (int ww = 1; ww < RPB; ++ww) v += acc[ww * D + i];
+        part[(long)blockIdx.x * D + i] = v;
+    }
 }
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -254,9 +270,13 @@ extern "C" int rmsnorm_backward_hip(const void* grad_output, const void* input,
         RMS_BWD(1) RMS_BWD(2) RMS_BWD(3) RMS_BWD(4)
 #undef RMS_BWD
         default: {
+            // per-wave dw slices (timing-independent sums) while they fit in
+            // 64 KB of LDS
+            const bool per_wave = want && D * rms::RPB <= 16384;
             ::efla::ProfScope ps("rmsnorm_bwd_loop", stream);
-            hipLaunchKernelGGL(rms::bwd_loop_kernel, grid, block, want ? D * sizeof(float) : 0,
-                               stream, g, x, w, dx, part, (long)rows, (int)D, eps, want);
+            hipLaunchKernelGGL(rms::bwd_loop_kernel, grid, block,
+                               want ? (per_wave ? rms::RPB : 1) * D * sizeof(float) : 0, stream, g,
+                               x, w, dx, part, (long)rows, (int)D, eps, want, per_wave ? 1 : 0);
         }
     }
     EFLA_CHECK(hipPeekAtLastError());

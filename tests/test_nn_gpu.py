@@ -79,6 +79,31 @@ def test_rmsnorm_forward(oracle, rows, D):
     assert np.abs(ms - 1).max() < 1e-2
 
 
+@pytest.mark.parametrize("D", [96, 128, 1000, 2048])
+def test_norm_backward_weight_grads_repeat_bit_for_bit(D):
+    # widths off the register path loop over the row; up to D = 2048 each wave
+    # sums its dw (and db) columns in an LDS slice of its own and the slices
+    # are added in wave order, so repeated calls give the same bits (LDS
+    # atomics across the waves would not).  Enough rows for several per wave.
+    from ceo_amd.nn import layernorm_backward, layernorm_forward, rmsnorm_backward
+
+    announce(f"norm backward repeatability D={D}")
+    rows = 4099
+    rng = np.random.default_rng(5 + D)
+    x = _bf(rng.standard_normal((rows, D))).cuda()
+    w = _bf(1 + 0.1 * rng.standard_normal(D)).cuda()
+    dy = _bf(rng.standard_normal((rows, D))).cuda()
+    _, mean, rstd = layernorm_forward(x, w, None, 1e-5, save_stats=True)
+    ln = [layernorm_backward(dy, x, w, mean, rstd) for _ in range(4)]
+    rms = [rmsnorm_backward(dy, x, w, 1e-6) for _ in range(4)]
+    torch.cuda.synchronize()
+    for i in range(1, 4):
+        for a, b in zip(ln[0], ln[i]):
+            assert torch.equal(a, b)
+        for a, b in zip(rms[0], rms[i]):
+            assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("rows,D", [(64, 1024), (50, 96), (5000, 1024), (33, 1536), (300, 2048),
                                     (17, 4096), (6, 16384), (4, 20000)])
 def test_rmsnorm_backward(oracle, rows, D):
