@@ -462,9 +462,9 @@ __global__ void __launch_bounds__(NTS) scan_o_kernel(const bf16* __restrict__ q,
     seq_bounds(si, seq, sbos, slen, slot0);
     const int nch = (int)((slen + 63) / 64);
     if (w >= NCW) {
-        // copy waves: two register sets, ra and rb, each a chunk ahead of the
-        // other; chunk n + 1 is written to buf[(n + 1) & 1] during chunk n,
-        // while chunk n + 2's loads are still in flight
+        // copy waves: three register sets, ra, rb and rc, each a chunk ahead
+        // of the one before; chunk n + 1 is written to buf[(n + 1) & 1] during
+        // chunk n, while the loads of chunks n + 2 and n + 3 are in flight
         const int ct = (int)threadIdx.x - NT;
         // chunk n's loads (clamped to the last chunk, so every iteration
         // issues the same loads and the staging's waits stay exact)
@@ -475,22 +475,28 @@ __global__ void __launch_bounds__(NTS) scan_o_kernel(const bf16* __restrict__ q,
             R.load(q, k, v, Tc, bc, bos, len, h, V, v0, (long)(slot0 + n) * H + h, ld.q, ld.k,
                    ld.v, ct);
         };
-        ChunkRegs<K, true, true> ra, rb;
+        ChunkRegs<K, true, true> ra, rb, rc;
         if (nch > 0) {
             load(ra, 0);
             ra.stage(sm.buf[0]);
             load(ra, 1);
             load(rb, 2);
+            load(rc, 3);
         }
-        for (int n = 0; n < nch; n += 2) {  // ra holds chunk n + 1, rb chunk n + 2
+        for (int n = 0; n < nch; n += 3) {  // ra holds chunk n + 1, rb n + 2, rc n + 3
             __syncthreads();  // chunk n staged; everyone is done with chunk n - 1
             if (n + 1 < nch) ra.stage(sm.buf[(n + 1) & 1]);
-            load(ra, n + 3);
+            load(ra, n + 4);
             __syncthreads();  // the compute waves' P complete
             if (n + 1 >= nch) break;
             __syncthreads();  // chunk n + 1 staged
             if (n + 2 < nch) rb.stage(sm.buf[n & 1]);
-            load(rb, n + 4);
+            load(rb, n + 5);
+            __syncthreads();
+            if (n + 2 >= nch) break;
+            __syncthreads();  // chunk n + 2 staged
+            if (n + 3 < nch) rc.stage(sm.buf[(n + 1) & 1]);
+            load(rc, n + 6);
             __syncthreads();
         }
         return;
